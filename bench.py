@@ -1,0 +1,230 @@
+#!/usr/bin/env python3
+"""Benchmark of the MTC quantized-weight matmul on one MI355X.
+
+Headline (the `value`): packed-weight GB/s of the fp32 decode kernel at M = 1
+on workload c2 (4096 x 4096 Student-t weights, PermutedQuadtreeRD (32,16,8,4)
+@ 4.25 bits/weight), i.e. allocator-accounted packed bytes (alloc.total_bits/8)
+per call divided by the per-call time. One step = one Y = X * W_hat call at
+M = 1 on one rotating copy of the packed weight; >= 1 GiB of distinct copies
+rotate so the weight is read from HBM, not the 256 MB Infinity Cache. The K
+timed calls are replayed from a HIP graph (launch-bound decode loops are
+graph-captured in serving too) between a synchronize on both sides.
+
+Also reported in the same JSON line: M = 16 on c2 (fp32-VALU bound) and the
+prefill kernel (bf16 MFMA) on c4 (8192 x 8192, QuadtreeRD @ 4.5, M = 4096),
+and the CPU baseline (C/OpenMP port of the reference block loop) on a bounded
+sample of the c2 M = 1 workload.
+
+    python bench.py [--steps K] [--warmup W] [--no-prefill] [--no-cpu-baseline]
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2400)
+    ap.add_argument("--warmup", type=int, default=240)
+    ap.add_argument("--rotate-gib", type=float, default=1.0)
+    ap.add_argument("--prefill-steps", type=int, default=10)
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-m16", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--graph", type=int, default=1, help="replay the timed calls from a HIP graph")
+    return ap.parse_args()
+
+
+def timed_calls(torch, launch_list, steps, warmup, use_graph):
+    """Time exactly `steps` calls cycling over launch_list; returns (seconds, per-call ms)."""
+    n = len(launch_list)
+    stream = torch.cuda.current_stream()
+    if use_graph:
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(g, stream=side):
+                for f in launch_list:
+                    f()
+        stream.wait_stream(side)
+        tail = steps % n
+        gt = None
+        if tail:
+            gt = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(side):
+                with torch.cuda.graph(gt, stream=side):
+                    for f in launch_list[:tail]:
+                        f()
+            stream.wait_stream(side)
+        for _ in range(max(1, warmup // n)):
+            g.replay()
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(steps // n):
+            g.replay()
+        if gt is not None:
+            gt.replay()
+        stop.record(stream)
+        torch.cuda.synchronize()
+    else:
+        for i in range(warmup):
+            launch_list[i % n]()
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for i in range(steps):
+            launch_list[i % n]()
+        stop.record(stream)
+        torch.cuda.synchronize()
+    ms = start.elapsed_time(stop)
+    return ms / 1e3, ms / steps
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from tensorpack_amd import workloads
+    from tensorpack_amd.kernels.gemm import MTCMatrix, GEMM_CHUNK_ROWS
+    from tensorpack_amd.device import require_gpu
+
+    dev = require_gpu()
+    torch.cuda.set_device(dev)
+    res = {}
+
+    # ---------------- c2 decode ----------------
+    wl = workloads.c2()
+    t0 = time.time()
+    alloc = wl.allocate()
+    log(f"c2 allocation {time.time() - t0:.1f}s, {alloc.bits_per_element:.4f} b/w")
+    m = MTCMatrix.from_quadtree(alloc, wl.W)
+    t0 = time.time()
+    ds = m.device_stream()
+    log(f"c2 packed in {time.time() - t0:.1f}s: chunk_rows={ds.host.chunk_rows} stream {ds.device_bytes()} B, "
+        f"accounted {m.packed_bytes:.0f} B")
+    packed = m.packed_bytes
+    per_copy = ds.device_bytes()
+    n_copies = max(1, int(np.ceil(args.rotate_gib * (1 << 30) / per_copy)))
+    copies = [ds] + [ds.clone() for _ in range(n_copies - 1)]
+    X1 = torch.from_numpy(wl.activations(1)).to(dev)
+    Y1 = torch.empty((1, wl.W.shape[1]), dtype=torch.float32, device=dev)
+    for c in copies:
+        c.workspace(1)
+        c.gemv_f32(X1, out=Y1)
+    torch.cuda.synchronize()
+    launches = [lambda c=c: c.gemv_f32(X1, out=Y1) for c in copies]
+    secs, ms = timed_calls(torch, launches, args.steps, args.warmup, bool(args.graph))
+    gbs = packed / (ms * 1e-3) / 1e9
+    log(f"c2 M=1: {ms * 1e3:.2f} us/call, {gbs:.1f} GB/s packed ({n_copies} copies)")
+    y_gpu = Y1.cpu().numpy().copy()
+
+    if not args.no_m16:
+        X16 = torch.from_numpy(wl.activations(16)).to(dev)
+        Y16 = torch.empty((16, wl.W.shape[1]), dtype=torch.float32, device=dev)
+        for c in copies:
+            c.workspace(16)
+        l16 = [lambda c=c: c.gemv_f32(X16, out=Y16) for c in copies]
+        s16, ms16 = timed_calls(torch, l16, max(args.steps // 4, len(copies)), args.warmup // 4, bool(args.graph))
+        flop16 = 2.0 * 16 * wl.W.shape[0] * wl.W.shape[1]
+        res["c2_m16"] = {"us_per_call": ms16 * 1e3, "packed_GBps": packed / (ms16 * 1e-3) / 1e9,
+                         "TFLOPs": flop16 / (ms16 * 1e-3) / 1e12,
+                         "frac_fp32_peak": flop16 / (ms16 * 1e-3) / 1e12 / FP32_PEAK_TFLOPS}
+        log(f"c2 M=16: {ms16 * 1e3:.2f} us/call, {res['c2_m16']['TFLOPs']:.2f} TFLOP/s")
+
+    # ---------------- CPU baseline (bounded sample) ----------------
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import mtc_oracle as O
+        inner = alloc.inner
+        la = O.LeafArena(inner.weights, inner.sizes, inner.leaf, inner.modes, inner.scales,
+                         alloc.row_perm, alloc.col_perm)
+        x = wl.activations(1)
+        y_cpu = O.cpu_qt_gemm(x, la)
+        calls, t0 = 0, time.time()
+        while True:
+            O.cpu_qt_gemm(x, la)
+            calls += 1
+            if time.time() - t0 >= args.cpu_seconds and calls >= 3:
+                break
+        el = time.time() - t0
+        cores = int(O.cpu_lib().oracle_threads())
+        cpu = {"value": packed * calls / el / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+               "sample": f"{calls} calls of c2 M=1 (full 4096x4096 matrix) in {el:.1f}s, C/OpenMP port of the "
+                         f"reference block loop (gemm.py:124-210)",
+               "gpu_vs_cpu_rel_frobenius": O.relative_frobenius_error(y_cpu, y_gpu)}
+        log(f"cpu baseline {cpu['value']:.3f} GB/s on {cores} threads; gpu-vs-cpu rel {cpu['gpu_vs_cpu_rel_frobenius']:.2e}")
+
+    # ---------------- c4 prefill ----------------
+    if not args.no_prefill:
+        wl4 = workloads.c4()
+        t0 = time.time()
+        a4 = wl4.allocate()
+        log(f"c4 allocation {time.time() - t0:.1f}s, {a4.bits_per_element:.4f} b/w")
+        m4 = MTCMatrix.from_quadtree(a4, wl4.W)
+        t0 = time.time()
+        g4 = m4.device_stream(GEMM_CHUNK_ROWS)
+        log(f"c4 packed in {time.time() - t0:.1f}s")
+        M4 = 4096
+        X4 = torch.from_numpy(wl4.activations(M4)).to(dev).to(torch.bfloat16)
+        Y4 = torch.empty((M4, wl4.W.shape[1]), dtype=torch.float32, device=dev)
+        g4.gemm_bf16(X4, out=Y4)
+        torch.cuda.synchronize()
+        s4, ms4 = timed_calls(torch, [lambda: g4.gemm_bf16(X4, out=Y4)], args.prefill_steps, 2, False)
+        flop4 = 2.0 * M4 * wl4.W.shape[0] * wl4.W.shape[1]
+        tf = flop4 / (ms4 * 1e-3) / 1e12
+        res["c4_prefill"] = {"M": M4, "ms_per_call": ms4, "TFLOPs": tf, "frac_bf16_peak": tf / BF16_PEAK_TFLOPS,
+                             "packed_bytes": m4.packed_bytes}
+        log(f"c4 M=4096: {ms4:.3f} ms/call, {tf:.1f} TFLOP/s ({100 * tf / BF16_PEAK_TFLOPS:.1f}% of bf16 peak)")
+
+    K, N = wl.W.shape
+    out = {
+        "metric": "packed-weight GB/s at M=1 (fp32 decode kernel)",
+        "value": gbs,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded np.random.RandomState weights/activations, random-init)",
+        "config": {"workload": wl.name + " M=1", "K": K, "N": N, "M": 1, "budget_bits": wl.budget,
+                   "bits_per_weight": alloc.bits_per_element, "packed_bytes": packed,
+                   "stream_bytes": per_copy, "rotating_copies": n_copies,
+                   "chunk_rows": ds.host.chunk_rows, "graph_replay": bool(args.graph)},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": gbs / HBM_PEAK_GBS, "traffic": None, "kernel": "k_gemv<1>",
+                     "stream_GBps": per_copy / (ms * 1e-3) / 1e9},
+        "cpu_baseline": cpu,
+        "extra": res,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

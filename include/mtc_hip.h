@@ -1,0 +1,123 @@
+/*
+ * C-ABI of libmtc_hip.so: MI355X (gfx950) kernels for Y = X * W_hat, where
+ * W_hat is a quadtree-tiled, per-leaf mixed-precision weight packed into a
+ * device-resident "panel stream" (format below).
+ *
+ * Plain C types only; every device buffer is caller-owned; no entry point
+ * allocates device memory. Launches are asynchronous on the given HIP stream
+ * (NULL = default stream). Functions return 0 on success and a negative
+ * MTC_E* code on failure; mtc_last_error() returns a thread-local message.
+ * Calls that share one GEMV workspace must not overlap in time.
+ *
+ * Reference interfaces replaced (Sharexi/TensorPack, Python + numba, no FFI):
+ *   mtc_gemv_f32   <- mtc/kernels/gemm.py:124-210 (mtc_gemm_core_kernel) as
+ *                     driven by mtc_gemm, gemm.py:541-574, for decode shapes
+ *   mtc_gemm_bf16  <- same kernel/entry point, prefill shapes (bf16 MFMA)
+ *   mtc_dequant    <- MTCMatrix.to_array, gemm.py:510-538, and
+ *                     qt_dequant / permuted_qt_dequant, mtc/core/quadtree.py:157-171,
+ *                     mtc/core/permutation.py:76-79
+ *   mtc_rd_search  (libmtc_rd.so, host) <- _search_kernel, mtc/core/allocation.py:106-136
+ */
+#ifndef MTC_HIP_H
+#define MTC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MTC_ABI_VERSION 1
+
+enum {
+  MTC_OK = 0,
+  MTC_E_NULL = -1,        /* a required pointer is NULL */
+  MTC_E_DESC = -2,        /* malformed stream descriptor */
+  MTC_E_SHAPE = -3,       /* M / leading dimension / chunk geometry not supported */
+  MTC_E_DTYPE = -4,       /* unsupported dtype code */
+  MTC_E_WORKSPACE = -5,   /* workspace missing or too small */
+  MTC_E_LAUNCH = -6,      /* HIP launch / runtime error */
+  MTC_E_VERSION = -7      /* descriptor from another ABI version */
+};
+
+enum { MTC_DTYPE_F32 = 0, MTC_DTYPE_BF16 = 1 };
+
+/* Descriptor flags */
+#define MTC_FLAG_FP32_SCALES 0x1u   /* leaf scales come from `leaf_scale`, not the descriptor word */
+
+/*
+ * Panel stream. The (permuted) weight Wp is K x N (reduction x output). It is
+ * cut into work units u = panel * n_chunks + chunk: panel = 32 output columns,
+ * chunk = `chunk_rows` reduction rows. Within a unit, non-P0 leaves are grouped
+ * into buckets of equal (leaf size S in {4,8,16,32}, code width P in
+ * {2,3,4,5,6,8,16}).
+ *
+ *  unit_buckets[u] .. unit_buckets[u+1]-1 : bucket indices of unit u
+ *  buckets[4*b + 0] : payload offset of the bucket, in dwords (multiple of 4)
+ *  buckets[4*b + 1] : index of the bucket's first leaf word
+ *  buckets[4*b + 2] : number of 32-code lane chunks
+ *  buckets[4*b + 3] : log2(S) | P << 8
+ *  leaf_word[l]     : bits 0-7 row offset in the unit / 4, bits 8-10 column
+ *                     offset in the panel / 4, bit 11 pad leaf (ignored),
+ *                     bits 16-31 bf16 scale
+ *  leaf_scale[l]    : fp32 scale (only with MTC_FLAG_FP32_SCALES)
+ *
+ * A lane chunk is 32 codes in P dwords: code i occupies bits [i*P, i*P+P) of
+ * the little-endian bit string (two's complement). Codes of a leaf are in
+ * column-major order; a chunk holds 32/S columns of one leaf for S >= 8, and
+ * two whole 4x4 leaves (2j, 2j+1) for S = 4 (odd buckets end with a pad leaf
+ * whose codes are zero).
+ *
+ * Y[:, col_perm[n]] = X[:, row_perm] * Wp[:, n]; NULL perms mean identity.
+ */
+typedef struct mtc_stream_desc {
+  uint32_t abi_version;
+  uint32_t flags;
+  int32_t K;
+  int32_t N;
+  int32_t chunk_rows;
+  int32_t n_panels;
+  int32_t n_chunks;
+  int32_t n_buckets;
+  int64_t n_leaves;
+  int64_t payload_dwords;
+  const uint32_t* payload;
+  const uint32_t* buckets;
+  const int32_t* unit_buckets;
+  const uint32_t* leaf_word;
+  const float* leaf_scale;
+  const int32_t* row_perm;
+  const int32_t* col_perm;
+} mtc_stream_desc;
+
+int mtc_abi_version(void);
+const char* mtc_last_error(void);
+
+/* Host-side validation of a descriptor (pointer presence and geometry only). */
+int mtc_check_desc(const mtc_stream_desc* d);
+
+/* W_out (K x N fp32, row-major, ORIGINAL channel order) = W_hat, bit-exact,
+ * with +0.0 wherever a P0 leaf lies. */
+int mtc_dequant(const mtc_stream_desc* d, float* W_out, void* hip_stream);
+
+/* Bytes of GEMV workspace needed for M rows (0 if the stream has one chunk).
+ * The workspace must be zero-filled once before first use; the kernels leave
+ * its counters at zero again after every call. */
+size_t mtc_gemv_workspace_bytes(const mtc_stream_desc* d, int M);
+
+/* fp32 path: Y (M x N fp32, leading dim ldy) = X (M x K fp32, leading dim ldx) * W_hat.
+ * Any M >= 1; tuned for decode (M <= 16). Deterministic. */
+int mtc_gemv_f32(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y, int64_t ldy, int M,
+                 void* workspace, size_t workspace_bytes, void* hip_stream);
+
+/* bf16 MFMA path (prefill): X is fp32 (rounded to bf16 on load) or bf16; Y is
+ * fp32 or bf16; fp32 accumulation. Requires a stream with chunk_rows == 64. */
+int mtc_gemm_bf16(const mtc_stream_desc* d, const void* X, int x_dtype, int64_t ldx, void* Y, int y_dtype,
+                  int64_t ldy, int M, void* hip_stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MTC_HIP_H */

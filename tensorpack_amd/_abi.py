@@ -1,0 +1,72 @@
+"""ctypes mirror of include/mtc_hip.h (struct layout, constants, prototypes)."""
+
+import ctypes
+
+ABI_VERSION = 1
+
+MTC_OK = 0
+MTC_DTYPE_F32 = 0
+MTC_DTYPE_BF16 = 1
+MTC_FLAG_FP32_SCALES = 0x1
+
+ERROR_NAMES = {
+    -1: "MTC_E_NULL", -2: "MTC_E_DESC", -3: "MTC_E_SHAPE", -4: "MTC_E_DTYPE",
+    -5: "MTC_E_WORKSPACE", -6: "MTC_E_LAUNCH", -7: "MTC_E_VERSION",
+}
+
+EXPORTED = ("mtc_abi_version", "mtc_last_error", "mtc_check_desc", "mtc_dequant",
+            "mtc_gemv_workspace_bytes", "mtc_gemv_f32", "mtc_gemm_bf16")
+
+
+class MtcStreamDesc(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
+        ("K", ctypes.c_int32),
+        ("N", ctypes.c_int32),
+        ("chunk_rows", ctypes.c_int32),
+        ("n_panels", ctypes.c_int32),
+        ("n_chunks", ctypes.c_int32),
+        ("n_buckets", ctypes.c_int32),
+        ("n_leaves", ctypes.c_int64),
+        ("payload_dwords", ctypes.c_int64),
+        ("payload", ctypes.c_void_p),
+        ("buckets", ctypes.c_void_p),
+        ("unit_buckets", ctypes.c_void_p),
+        ("leaf_word", ctypes.c_void_p),
+        ("leaf_scale", ctypes.c_void_p),
+        ("row_perm", ctypes.c_void_p),
+        ("col_perm", ctypes.c_void_p),
+    ]
+
+
+DescP = ctypes.POINTER(MtcStreamDesc)
+
+
+def declare(lib: ctypes.CDLL) -> None:
+    vp, i32, i64, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
+    lib.mtc_abi_version.restype = i32
+    lib.mtc_abi_version.argtypes = []
+    lib.mtc_last_error.restype = ctypes.c_char_p
+    lib.mtc_last_error.argtypes = []
+    lib.mtc_check_desc.restype = i32
+    lib.mtc_check_desc.argtypes = [DescP]
+    lib.mtc_dequant.restype = i32
+    lib.mtc_dequant.argtypes = [DescP, vp, vp]
+    lib.mtc_gemv_workspace_bytes.restype = sz
+    lib.mtc_gemv_workspace_bytes.argtypes = [DescP, i32]
+    lib.mtc_gemv_f32.restype = i32
+    lib.mtc_gemv_f32.argtypes = [DescP, vp, i64, vp, i64, i32, vp, sz, vp]
+    lib.mtc_gemm_bf16.restype = i32
+    lib.mtc_gemm_bf16.argtypes = [DescP, vp, i32, i64, vp, i32, i64, i32, vp]
+
+
+class MtcError(RuntimeError):
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} failed with {ERROR_NAMES.get(code, code)}: {msg}")
+        self.code = code
+
+
+def check(lib: ctypes.CDLL, fn: str, code: int) -> None:
+    if code != MTC_OK:
+        raise MtcError(fn, code, (lib.mtc_last_error() or b"").decode(errors="replace"))

@@ -1,0 +1,156 @@
+"""Device residency of a panel stream and thin launch wrappers over the C-ABI.
+
+PyTorch is used only as the device allocator and for the current HIP stream;
+every computation goes through libmtc_hip.so. There is no CPU fallback: with
+no GPU or no built library these functions raise.
+"""
+
+import ctypes
+from typing import Dict, Optional, Tuple
+
+import numpy as np
+
+from . import _abi, _native
+from .packer import PanelStream
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def require_gpu(device=None):
+    torch = _torch()
+    if not torch.cuda.is_available():
+        raise RuntimeError("mtc GPU path needs a ROCm GPU (torch.cuda.is_available() is False)")
+    return torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+
+
+def current_stream_handle(device) -> int:
+    torch = _torch()
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class DeviceStream:
+    """A PanelStream uploaded to one GPU, plus its ctypes descriptor."""
+
+    def __init__(self, ps: PanelStream, device=None):
+        torch = _torch()
+        self.device = require_gpu(device)
+        self.host = ps
+        self.lib = _native.hip_lib()
+
+        def up(a: Optional[np.ndarray], dtype):
+            if a is None:
+                return None
+            return torch.from_numpy(np.ascontiguousarray(a).view(dtype)).to(self.device)
+
+        self.payload = up(ps.payload.view(np.int32), np.int32)
+        self.buckets = up(ps.buckets.reshape(-1).view(np.int32), np.int32)
+        self.unit_buckets = up(ps.unit_buckets, np.int32)
+        self.leaf_word = up(ps.leaf_word.view(np.int32), np.int32)
+        self.leaf_scale = up(ps.leaf_scale, np.float32)
+        self.row_perm = up(ps.row_perm, np.int32)
+        self.col_perm = up(ps.col_perm, np.int32)
+
+        d = _abi.MtcStreamDesc()
+        d.abi_version = _abi.ABI_VERSION
+        d.flags = _abi.MTC_FLAG_FP32_SCALES if ps.leaf_scale is not None else 0
+        d.K, d.N, d.chunk_rows = ps.K, ps.N, ps.chunk_rows
+        d.n_panels, d.n_chunks = ps.n_panels, ps.n_chunks
+        d.n_buckets = int(ps.unit_buckets[-1])
+        d.n_leaves = int(ps.leaf_word.size)
+        d.payload_dwords = int(ps.payload.size)
+        ptr = lambda t: None if t is None else t.data_ptr()
+        d.payload, d.buckets, d.unit_buckets = ptr(self.payload), ptr(self.buckets), ptr(self.unit_buckets)
+        d.leaf_word, d.leaf_scale = ptr(self.leaf_word), ptr(self.leaf_scale)
+        d.row_perm, d.col_perm = ptr(self.row_perm), ptr(self.col_perm)
+        self.desc = d
+        _abi.check(self.lib, "mtc_check_desc", self.lib.mtc_check_desc(ctypes.byref(d)))
+        self._ws: Dict[int, "object"] = {}
+
+    def clone(self) -> "DeviceStream":
+        """A second device copy of the same stream (distinct buffers, same contents)."""
+        other = object.__new__(DeviceStream)
+        other.device, other.host, other.lib = self.device, self.host, self.lib
+        for name in ("payload", "buckets", "unit_buckets", "leaf_word", "leaf_scale", "row_perm", "col_perm"):
+            t = getattr(self, name)
+            setattr(other, name, None if t is None else t.clone())
+        d = _abi.MtcStreamDesc.from_buffer_copy(self.desc)
+        ptr = lambda t: None if t is None else t.data_ptr()
+        d.payload, d.buckets, d.unit_buckets = ptr(other.payload), ptr(other.buckets), ptr(other.unit_buckets)
+        d.leaf_word, d.leaf_scale = ptr(other.leaf_word), ptr(other.leaf_scale)
+        d.row_perm, d.col_perm = ptr(other.row_perm), ptr(other.col_perm)
+        other.desc = d
+        other._ws = {}
+        return other
+
+    def device_bytes(self) -> int:
+        n = 0
+        for name in ("payload", "buckets", "unit_buckets", "leaf_word", "leaf_scale", "row_perm", "col_perm"):
+            t = getattr(self, name)
+            if t is not None:
+                n += t.numel() * t.element_size()
+        return n
+
+    @property
+    def K(self) -> int:
+        return self.host.K
+
+    @property
+    def N(self) -> int:
+        return self.host.N
+
+    def nbytes(self) -> int:
+        return self.host.nbytes()
+
+    def workspace(self, M: int):
+        """Zero-initialised GEMV workspace for M rows (cached; counters self-reset)."""
+        need = int(self.lib.mtc_gemv_workspace_bytes(ctypes.byref(self.desc), int(M)))
+        if need == 0:
+            return None, 0
+        ws = self._ws.get(need)
+        if ws is None:
+            torch = _torch()
+            ws = torch.zeros(need, dtype=torch.uint8, device=self.device)
+            self._ws = {need: ws}
+        return ws, need
+
+    # ---- launches -------------------------------------------------------------------
+    def dequant(self, out=None):
+        torch = _torch()
+        if out is None:
+            out = torch.empty((self.K, self.N), dtype=torch.float32, device=self.device)
+        assert out.is_contiguous() and out.dtype == torch.float32 and tuple(out.shape) == (self.K, self.N)
+        rc = self.lib.mtc_dequant(ctypes.byref(self.desc), out.data_ptr(), current_stream_handle(self.device))
+        _abi.check(self.lib, "mtc_dequant", rc)
+        return out
+
+    def gemv_f32(self, X, out=None):
+        torch = _torch()
+        assert X.dim() == 2 and X.dtype == torch.float32 and X.stride(1) == 1, "X must be (M, K) fp32 row-major"
+        M = X.shape[0]
+        if out is None:
+            out = torch.empty((M, self.N), dtype=torch.float32, device=self.device)
+        assert out.dtype == torch.float32 and out.stride(1) == 1
+        ws, nbytes = self.workspace(M)
+        rc = self.lib.mtc_gemv_f32(ctypes.byref(self.desc), X.data_ptr(), X.stride(0), out.data_ptr(), out.stride(0),
+                                   M, None if ws is None else ws.data_ptr(), nbytes,
+                                   current_stream_handle(self.device))
+        _abi.check(self.lib, "mtc_gemv_f32", rc)
+        return out
+
+    def gemm_bf16(self, X, out=None, out_dtype=None):
+        torch = _torch()
+        assert X.dim() == 2 and X.stride(1) == 1 and X.dtype in (torch.float32, torch.bfloat16)
+        M = X.shape[0]
+        out_dtype = out_dtype or torch.float32
+        if out is None:
+            out = torch.empty((M, self.N), dtype=out_dtype, device=self.device)
+        assert out.dtype in (torch.float32, torch.bfloat16) and out.stride(1) == 1
+        xdt = _abi.MTC_DTYPE_BF16 if X.dtype == torch.bfloat16 else _abi.MTC_DTYPE_F32
+        ydt = _abi.MTC_DTYPE_BF16 if out.dtype == torch.bfloat16 else _abi.MTC_DTYPE_F32
+        rc = self.lib.mtc_gemm_bf16(ctypes.byref(self.desc), X.data_ptr(), xdt, X.stride(0), out.data_ptr(), ydt,
+                                    out.stride(0), M, current_stream_handle(self.device))
+        _abi.check(self.lib, "mtc_gemm_bf16", rc)
+        return out

@@ -1,0 +1,331 @@
+"""Drop-in `MTCMatrix` and `mtc_gemm` (mtc/kernels/gemm.py) executing on MI355X.
+
+Two weight forms share one device format (the panel stream, include/mtc_hip.h):
+
+- quadtree (QuadtreeRD / PermutedQuadtreeRD allocations): the north-star form,
+  leaves 32x32 .. 4x4, bf16 scales, optional row/column permutation folded into
+  an X gather and a Y scatter;
+- uniform blocks (the reference's `from_allocation` arena, gemm.py:432-488):
+  one leaf level of size Bs with fp32 scales. The host arena keeps the
+  reference byte layout so `arena`, `offsets`, `total_bytes_allocated` mean
+  what they mean in the reference.
+
+`mtc_gemm(X, W)` with a dense X (numpy or torch, (M, K) or (K,)) is the
+north-star overload; `mtc_gemm(A, B)` with two MTCMatrix keeps the reference
+semantics (gemm.py:541-574): C = A_hat @ B_hat in fp32.
+
+All arithmetic runs in libmtc_hip.so; without a GPU these calls raise.
+"""
+
+from math import ceil
+from typing import Dict, Optional, Tuple
+
+import numpy as np
+
+from ..core.allocation import QRANGE, quantize_blocks, rd_allocate_pair, to_blocks
+from ..core.arena import MemoryArena
+from ..core.permutation import PermutedQTAllocation
+from ..core.quadtree import QTAllocation
+from ..packer import PanelStream, pack_levels, weight_codes
+
+GEMM_CHUNK_ROWS = 64          # K step of the bf16 MFMA kernel
+DECODE_MAX_M = 16             # M at or below this takes the fp32 decode kernel under compute="auto"
+GEMV_TARGET_UNITS = 1024      # work units wanted per decode launch (256 CUs x 4)
+
+
+def gemv_chunk_rows(K: int, N: int) -> int:
+    """Rows per decode work unit: enough units to fill the chip, 64..512 rows each."""
+    panels = max(N // 32, 1)
+    chunks = max(1, -(-GEMV_TARGET_UNITS // panels))
+    rows = -(-K // chunks)
+    rows = -(-rows // 32) * 32
+    return int(min(max(rows, 64), 512))
+
+
+# ---------------------------------------------------------------------------------------
+# reference arena byte layout (gemm.py:457-478 writes it, gemm.py:29-117 reads it)
+# ---------------------------------------------------------------------------------------
+def arena_encode(codes: np.ndarray, mode: int) -> np.ndarray:
+    """(n, Bs*Bs) row-major codes -> (n, mode*Bs*Bs/8) bytes in the reference layout."""
+    q = np.asarray(codes).astype(np.int32)
+    n = q.shape[0]
+    if mode == 8:
+        return q.astype(np.int8).view(np.uint8).reshape(n, -1)
+    if mode == 16:
+        return q.astype("<i2").view(np.uint8).reshape(n, -1)
+    if mode in (2, 4):
+        per = 8 // mode
+        u = (q & ((1 << mode) - 1)).reshape(n, -1, per)
+        out = np.zeros(u.shape[:2], dtype=np.int32)
+        for i in range(per):
+            out |= u[..., i] << (mode * i)
+        return out.astype(np.uint8)
+    u = (q & ((1 << mode) - 1)).astype(np.uint32)
+    bits = ((u[..., None] >> np.arange(mode, dtype=np.uint32)) & 1).astype(np.uint8)
+    return np.packbits(bits.reshape(n, -1), axis=1, bitorder="little")
+
+
+def arena_decode(data: np.ndarray, mode: int, count: int) -> np.ndarray:
+    """(n, bytes) in the reference layout -> (n, count) signed codes (row-major)."""
+    b = np.asarray(data, dtype=np.uint8)
+    n = b.shape[0]
+    if mode == 8:
+        return b.view(np.int8).astype(np.int32).reshape(n, count)
+    if mode == 16:
+        return np.ascontiguousarray(b).view("<i2").astype(np.int32).reshape(n, count)
+    bits = np.unpackbits(b, axis=1, bitorder="little")[:, : count * mode].reshape(n, count, mode).astype(np.int32)
+    v = (bits << np.arange(mode, dtype=np.int32)).sum(axis=2)
+    return np.where(v >= (1 << (mode - 1)), v - (1 << mode), v).astype(np.int32)
+
+
+class _Levels:
+    """Leaf description handed to the packer."""
+
+    def __init__(self, shape, sizes, leaf, modes, scales, codes_of, scale_format, row_perm=None, col_perm=None):
+        self.shape = (int(shape[0]), int(shape[1]))
+        self.sizes, self.leaf, self.modes, self.scales = tuple(sizes), leaf, modes, scales
+        self.codes_of, self.scale_format = codes_of, scale_format
+        self.row_perm, self.col_perm = row_perm, col_perm
+
+
+class MTCMatrix:
+    """A packed (K x N) matrix: reduction along rows, as the right operand of Y = X * W."""
+
+    def __init__(self, shape: Tuple[int, int], block_size: int, arena: MemoryArena, offsets: np.ndarray,
+                 precisions: np.ndarray, scales: np.ndarray, pointer_tensor=None):
+        """Uniform-block matrix over a reference-layout arena (gemm.py:222-238)."""
+        self.shape = (int(shape[0]), int(shape[1]))
+        self.block_size = int(block_size)
+        self.arena = arena
+        self.offsets = offsets
+        self.precisions = precisions
+        self.scales = scales
+        self.pointer_tensor = pointer_tensor
+        self.allocation = None
+        self._levels: Optional[_Levels] = None
+        self._host: Dict[int, PanelStream] = {}
+        self._dev: Dict[Tuple[str, int], object] = {}
+
+    # ---- constructors ------------------------------------------------------------------
+    @classmethod
+    def from_quadtree(cls, alloc, matrix: Optional[np.ndarray] = None) -> "MTCMatrix":
+        """Pack a QTAllocation / PermutedQTAllocation (matrix = the ORIGINAL W; optional)."""
+        if isinstance(alloc, PermutedQTAllocation):
+            inner, pr, pc = alloc.inner, np.asarray(alloc.row_perm), np.asarray(alloc.col_perm)
+            if matrix is not None:
+                Wp = np.asarray(matrix, dtype=np.float32)[pr][:, pc]
+            else:
+                Wp = inner.weights
+        elif isinstance(alloc, QTAllocation):
+            inner, pr, pc = alloc, None, None
+            Wp = np.asarray(matrix, dtype=np.float32) if matrix is not None else alloc.weights
+        else:
+            raise TypeError(f"expected QTAllocation or PermutedQTAllocation, got {type(alloc).__name__}")
+        if Wp is None:
+            raise ValueError("the allocation carries no weights; pass the original matrix")
+        if tuple(Wp.shape) != tuple(inner.shape):
+            raise ValueError(f"matrix shape {Wp.shape} != allocation shape {inner.shape}")
+        K, N = inner.shape
+        m = cls.__new__(cls)
+        m.shape = (K, N)
+        m.block_size = inner.sizes[0]
+        m.arena = None
+        m.offsets = None
+        m.precisions = None
+        m.scales = None
+        m.pointer_tensor = None
+        m.allocation = alloc
+        m._levels = _Levels((K, N), inner.sizes, inner.leaf, inner.modes, inner.scales, weight_codes(Wp), "bf16",
+                            pr, pc)
+        m._host, m._dev = {}, {}
+        return m
+
+    @classmethod
+    def from_allocation(cls, matrix: np.ndarray, modes, scales: Optional[np.ndarray] = None,
+                        block_size: Optional[int] = None) -> "MTCMatrix":
+        """Reference form `from_allocation(matrix, modes, scales, block_size)` packs uniform
+        blocks into the arena (gemm.py:432-488); `from_allocation(matrix, qt_alloc)` packs a
+        quadtree allocation."""
+        if isinstance(modes, (QTAllocation, PermutedQTAllocation)):
+            return cls.from_quadtree(modes, matrix)
+        if scales is None or block_size is None:
+            raise TypeError("uniform form needs modes, scales and block_size")
+        arr = np.asarray(matrix, dtype=np.float32)
+        H, W = arr.shape
+        Bs = int(block_size)
+        assert H % Bs == 0 and W % Bs == 0, f"Dimensions ({H}, {W}) must be divisible by block_size {Bs}"
+        blocks = to_blocks(arr, Bs)
+        nbh, nbw = blocks.shape[:2]
+        modes = np.asarray(modes, dtype=np.uint8).reshape(nbh, nbw)
+        scales = np.asarray(scales, dtype=np.float32).reshape(nbh, nbw)
+        nbytes = (modes.astype(np.int64) * Bs * Bs) // 8
+        starts = np.concatenate([[0], np.cumsum(nbytes.ravel())[:-1]])
+        total = int(nbytes.sum())
+        arena = MemoryArena(capacity_bytes=max(total, 1))
+        base = arena.allocate(total, alignment=2)
+        offsets = (starts + base).astype(np.uint32).reshape(nbh, nbw)
+        buf = arena.raw_buffer
+        for m in QRANGE:
+            sel = modes == m
+            if not sel.any():
+                continue
+            q = quantize_blocks(blocks[sel][None], m, scales[sel][None])[0]
+            packed = arena_encode(q.reshape(q.shape[0], Bs * Bs), m)
+            buf[offsets[sel].astype(np.int64)[:, None] + np.arange(packed.shape[1])] = packed
+        return cls((H, W), Bs, arena, offsets, modes.copy(), np.where(modes == 0, 0.0, scales).astype(np.float32))
+
+    @classmethod
+    def from_numpy_rd_pair(cls, matrix_a: np.ndarray, matrix_b: np.ndarray, bits_per_element: float,
+                           block_size: int = 16) -> Tuple["MTCMatrix", "MTCMatrix"]:
+        """Joint RD allocation of C = A @ B packed into real arenas (gemm.py:490-508)."""
+        a, b = rd_allocate_pair(matrix_a, matrix_b, bits_per_element, block_size)
+        return (cls.from_allocation(matrix_a, a.modes, a.scales, block_size),
+                cls.from_allocation(matrix_b, b.modes, b.scales, block_size))
+
+    # ---- reference properties ------------------------------------------------------------
+    @property
+    def is_quadtree(self) -> bool:
+        return self.allocation is not None
+
+    @property
+    def num_blocks(self) -> Tuple[int, int]:
+        if self.offsets is not None:
+            return self.offsets.shape
+        return (self.shape[0] // self.block_size, self.shape[1] // self.block_size)
+
+    @property
+    def total_bits(self) -> int:
+        """Allocator-accounted bits: payload + per-leaf metadata (+ split flags, permutation indices)."""
+        if self.is_quadtree:
+            return int(self.allocation.total_bits)
+        return int(self.arena.bytes_allocated * 8)
+
+    @property
+    def total_bytes_allocated(self) -> int:
+        if self.arena is not None:
+            return self.arena.bytes_allocated
+        return int(ceil(self.total_bits / 8))
+
+    @property
+    def packed_bytes(self) -> float:
+        return self.total_bits / 8.0
+
+    @property
+    def average_bits_per_element(self) -> float:
+        n = self.shape[0] * self.shape[1]
+        return 0.0 if n == 0 else self.total_bytes_allocated * 8.0 / n
+
+    # ---- packing ---------------------------------------------------------------------------
+    def _uniform_levels(self) -> _Levels:
+        Bs = self.block_size
+        buf = self.arena.raw_buffer
+
+        def codes_of(S, P, ii, jj, sc):
+            nb = P * Bs * Bs // 8
+            raw = buf[self.offsets[ii, jj].astype(np.int64)[:, None] + np.arange(nb)]
+            return arena_decode(raw, P, Bs * Bs).reshape(-1, Bs, Bs)
+
+        leaf = {Bs: np.ones(self.precisions.shape, dtype=bool)}
+        return _Levels(self.shape, (Bs,), leaf, {Bs: self.precisions}, {Bs: self.scales}, codes_of, "fp32")
+
+    def panel_stream(self, chunk_rows: int) -> PanelStream:
+        ps = self._host.get(chunk_rows)
+        if ps is None:
+            lv = self._levels if self._levels is not None else self._uniform_levels()
+            ps = pack_levels(lv.shape, lv.sizes, lv.leaf, lv.modes, lv.scales, lv.codes_of, chunk_rows,
+                             lv.scale_format, lv.row_perm, lv.col_perm)
+            self._host[chunk_rows] = ps
+        return ps
+
+    def device_stream(self, chunk_rows: Optional[int] = None, device=None):
+        from ..device import DeviceStream, require_gpu
+        dev = require_gpu(device)
+        if chunk_rows is None:
+            chunk_rows = gemv_chunk_rows(*self.shape)
+        key = (str(dev), int(chunk_rows))
+        ds = self._dev.get(key)
+        if ds is None:
+            ds = DeviceStream(self.panel_stream(int(chunk_rows)), dev)
+            self._dev[key] = ds
+        return ds
+
+    def release_host_streams(self) -> None:
+        """Drop host copies of packed streams (device copies stay)."""
+        self._host.clear()
+
+    def dequant_device(self, device=None):
+        """W_hat as a (K, N) fp32 device tensor in the original channel order."""
+        return self.device_stream(None, device).dequant()
+
+    def to_array(self) -> np.ndarray:
+        """Reconstruct the full float32 matrix (gemm.py:510-538), dequantized on the GPU."""
+        return self.dequant_device().cpu().numpy()
+
+
+# ---------------------------------------------------------------------------------------
+# mtc_gemm
+# ---------------------------------------------------------------------------------------
+def _as_device_tensor(x, device):
+    import torch
+    if isinstance(x, torch.Tensor):
+        return x.to(device) if x.device != device else x
+    arr = np.asarray(x)
+    if arr.dtype not in (np.float32,):
+        arr = arr.astype(np.float32)
+    return torch.from_numpy(np.ascontiguousarray(arr)).to(device)
+
+
+def mtc_gemm(A, B: MTCMatrix, *, compute: str = "auto", out_dtype=None):
+    """Y = A @ W_hat.
+
+    - A MTCMatrix (reference form): returns np.ndarray fp32 C = A_hat @ B_hat.
+    - A dense (M, K) or (K,), numpy or torch: returns the same kind (device
+      tensor for torch input). compute="fp32" runs the fp32 decode kernel
+      (default for M <= 16), compute="bf16" the bf16 MFMA kernel (default above).
+    """
+    if not isinstance(B, MTCMatrix):
+        raise TypeError(f"right operand must be an MTCMatrix, got {type(B).__name__}")
+    import torch
+    from ..device import require_gpu
+    dev = require_gpu()
+    if isinstance(A, MTCMatrix):
+        M, K = A.shape
+        K2, N = B.shape
+        assert K == K2, f"Shape mismatch: {A.shape} vs {B.shape}"
+        assert A.block_size == B.block_size, "Block size mismatch"
+        a_hat = A.dequant_device(dev)
+        return B.device_stream(None, dev).gemv_f32(a_hat).cpu().numpy()
+
+    from_numpy = not isinstance(A, torch.Tensor)
+    X = _as_device_tensor(A, dev)
+    squeeze = X.dim() == 1
+    if squeeze:
+        X = X.unsqueeze(0)
+    if X.dim() != 2:
+        raise ValueError(f"X must be 1-D or 2-D, got shape {tuple(X.shape)}")
+    M, K = X.shape
+    if K != B.shape[0]:
+        raise ValueError(f"Shape mismatch: X {tuple(X.shape)} vs W {B.shape}")
+    if compute == "auto":
+        compute = "fp32" if M <= DECODE_MAX_M else "bf16"
+    if M == 0:
+        Y = torch.zeros((0, B.shape[1]), dtype=out_dtype or torch.float32, device=dev)
+    elif compute == "fp32":
+        Xf = X.float()
+        if Xf.stride(1) != 1:
+            Xf = Xf.contiguous()
+        Y = B.device_stream(None, dev).gemv_f32(Xf)
+        if out_dtype is not None and out_dtype != torch.float32:
+            Y = Y.to(out_dtype)
+    elif compute == "bf16":
+        Xb = X if X.dtype in (torch.float32, torch.bfloat16) else X.float()
+        if Xb.stride(1) != 1:
+            Xb = Xb.contiguous()
+        Y = B.device_stream(GEMM_CHUNK_ROWS, dev).gemm_bf16(Xb, out_dtype=out_dtype)
+    else:
+        raise ValueError(f"compute must be 'auto', 'fp32' or 'bf16', got {compute!r}")
+    if squeeze:
+        Y = Y.squeeze(0)
+    if from_numpy:
+        return Y.float().cpu().numpy()
+    return Y

@@ -1,0 +1,214 @@
+"""GPU parity of the HIP path against the CPU oracle (run on an MI355X).
+
+Bars (north-star): W_hat bit-exact vs the oracle's qt_dequant (-0.0 == +0.0
+never arises: the quadtree W_hat has no negative zeros); Y within relative
+Frobenius 1e-5 of fp64 X @ W_hat for the fp32 path and 2e-3 for the bf16
+MFMA path (fp64 reference built from the same bf16-rounded X).
+"""
+
+import numpy as np
+import pytest
+
+from oracle import mtc_oracle as O
+from tensorpack_amd.core.allocation import rd_allocate, rd_allocate_pair
+from tensorpack_amd.core.permutation import PermutedQuadtreeRD
+from tensorpack_amd.core.quadtree import QuadtreeRD
+from tensorpack_amd.kernels.gemm import MTCMatrix, mtc_gemm
+
+from conftest import outlier_matrix
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-5
+TOL_BF16 = 2e-3
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _oracle_what(alloc, W):
+    """Oracle W_hat (original channel order) of a QT or QT-P allocation of W."""
+    if hasattr(alloc, "inner"):
+        i = alloc.inner
+        return O.permuted_qt_dequant(W, alloc.row_perm, alloc.col_perm, i.sizes, i.leaf, i.modes, i.scales)
+    return O.qt_dequant(W, alloc.sizes, alloc.leaf, alloc.modes, alloc.scales)
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+CASES = [
+    # name, K, N, seed, permuted, budget, sizes
+    ("outlier-qt-2.5", 256, 256, 1, False, 2.5, (32, 16, 8, 4)),
+    ("outlier-qtp-4.25", 256, 384, 2, True, 4.25, (32, 16, 8, 4)),
+    ("outlier-qt-9", 192, 128, 3, False, 9.0, (32, 16, 8, 4)),
+    ("qt-p16-heavy", 128, 96, 4, False, 14.0, (32, 16, 8, 4)),
+    ("qtp-2.2-root16", 320, 160, 5, True, 2.2, (16, 8, 4)),
+]
+
+
+@pytest.fixture(scope="module")
+def allocs():
+    out = {}
+    for name, K, N, seed, perm, budget, sizes in CASES:
+        W = outlier_matrix(seed, K, N)
+        h = np.exp(np.random.RandomState(seed + 100).randn(K))
+        cls = PermutedQuadtreeRD if perm else QuadtreeRD
+        a = cls(W, h, sizes).select(budget)
+        out[name] = (W, a, MTCMatrix.from_quadtree(a, W))
+    return out
+
+
+@pytest.mark.parametrize("name", [c[0] for c in CASES])
+def test_dequant_bit_exact(gpu, allocs, name):
+    W, a, m = allocs[name]
+    _say("dequant", name)
+    got = m.to_array()
+    ref = _oracle_what(a, W)
+    assert np.array_equal(_bits(got), _bits(ref)), name
+    assert not np.signbit(got[got == 0]).any()
+
+
+@pytest.mark.parametrize("chunk_rows", [32, 64, 160, 512])
+def test_dequant_any_chunking(gpu, allocs, chunk_rows):
+    W, a, m = allocs["outlier-qtp-4.25"]
+    _say("dequant chunking", chunk_rows)
+    got = m.device_stream(chunk_rows).dequant().cpu().numpy()
+    assert np.array_equal(_bits(got), _bits(_oracle_what(a, W)))
+
+
+@pytest.mark.parametrize("name", [c[0] for c in CASES])
+@pytest.mark.parametrize("M", [1, 2, 3, 5, 8, 16, 17, 40])
+def test_gemv_f32(gpu, allocs, name, M):
+    import torch
+    W, a, m = allocs[name]
+    _say("gemv", name, M)
+    X = np.random.RandomState(M).randn(M, W.shape[0]).astype(np.float32)
+    Y = mtc_gemm(torch.from_numpy(X).to(gpu), m, compute="fp32").cpu().numpy()
+    ref = O.qt_gemm_f64(X, _oracle_what(a, W))
+    err = O.relative_frobenius_error(ref, Y)
+    assert err <= TOL_F32, (name, M, err)
+
+
+@pytest.mark.parametrize("chunk_rows", [32, 64, 96, 512])
+def test_gemv_split_k_chunkings(gpu, allocs, chunk_rows):
+    import torch
+    W, a, m = allocs["outlier-qt-2.5"]
+    _say("gemv chunking", chunk_rows)
+    X = np.random.RandomState(7).randn(4, W.shape[0]).astype(np.float32)
+    ds = m.device_stream(chunk_rows)
+    Y1 = ds.gemv_f32(torch.from_numpy(X).to(gpu)).cpu().numpy()
+    Y2 = ds.gemv_f32(torch.from_numpy(X).to(gpu)).cpu().numpy()
+    assert np.array_equal(Y1, Y2), "fp32 path must be deterministic (counters must self-reset)"
+    err = O.relative_frobenius_error(O.qt_gemm_f64(X, _oracle_what(a, W)), Y1)
+    assert err <= TOL_F32, err
+
+
+@pytest.mark.parametrize("name", [c[0] for c in CASES])
+@pytest.mark.parametrize("M", [1, 31, 128, 200])
+@pytest.mark.parametrize("xdtype", ["f32", "bf16"])
+def test_gemm_bf16(gpu, allocs, name, M, xdtype):
+    import torch
+    W, a, m = allocs[name]
+    _say("gemm", name, M, xdtype)
+    X = np.random.RandomState(M + 1).randn(M, W.shape[0]).astype(np.float32)
+    Xt = torch.from_numpy(X).to(gpu)
+    if xdtype == "bf16":
+        Xt = Xt.to(torch.bfloat16)
+    Y = mtc_gemm(Xt, m, compute="bf16").float().cpu().numpy()
+    ref = O.qt_gemm_f64(O.bf16_round(X), _oracle_what(a, W))
+    err = O.relative_frobenius_error(ref, Y)
+    assert err <= TOL_BF16, (name, M, err)
+
+
+def test_gemm_bf16_output(gpu, allocs):
+    import torch
+    W, a, m = allocs["outlier-qt-2.5"]
+    X = torch.randn(64, W.shape[0], device=gpu, dtype=torch.bfloat16)
+    Y = mtc_gemm(X, m, compute="bf16", out_dtype=torch.bfloat16)
+    assert Y.dtype == torch.bfloat16 and Y.shape == (64, W.shape[1])
+    ref = O.qt_gemm_f64(X.float().cpu().numpy(), _oracle_what(a, W))
+    assert O.relative_frobenius_error(ref, Y.float().cpu().numpy()) <= TOL_BF16 + 4e-3
+
+
+def test_numpy_in_numpy_out_and_vector(gpu, allocs):
+    W, a, m = allocs["outlier-qtp-4.25"]
+    x = np.random.RandomState(3).randn(W.shape[0]).astype(np.float32)
+    y = mtc_gemm(x, m)
+    assert isinstance(y, np.ndarray) and y.shape == (W.shape[1],)
+    ref = O.qt_gemm_f64(x[None], _oracle_what(a, W))[0]
+    assert O.relative_frobenius_error(ref, y) <= TOL_F32
+
+
+def test_all_p0_and_single_mode_edges(gpu):
+    """All-P0 (budget floor), every element one 4x4 P16 leaf, negative scales."""
+    W = outlier_matrix(9, 64, 64)
+    W[:, :32] = 0.0                       # an all-zero panel -> P0 leaves everywhere in it
+    a = QuadtreeRD(W, None, (32, 16, 8, 4)).select(1.0)
+    m = MTCMatrix.from_quadtree(a, W)
+    ref = O.qt_dequant(W, a.sizes, a.leaf, a.modes, a.scales)
+    assert np.array_equal(_bits(m.to_array()), _bits(ref))
+    X = np.random.RandomState(1).randn(2, 64).astype(np.float32)
+    assert O.relative_frobenius_error(O.qt_gemm_f64(X, ref), mtc_gemm(X, m)) <= TOL_F32
+    # a budget high enough for P16 everywhere
+    b = QuadtreeRD(W, None, (4,)).select(17.5)
+    assert all((b.modes[4][b.leaf[4]] == 16) | (b.modes[4][b.leaf[4]] == 0))
+    mb = MTCMatrix.from_quadtree(b, W)
+    refb = O.qt_dequant(W, b.sizes, b.leaf, b.modes, b.scales)
+    assert np.array_equal(_bits(mb.to_array()), _bits(refb))
+    assert O.relative_frobenius_error(O.qt_gemm_f64(X, refb), mtc_gemm(X, mb)) <= TOL_F32
+
+
+def test_uniform_form_packed_kernel_matches_simulation(gpu):
+    """tests/test_allocation.py:69-86 on the GPU: arena round trip exact, GEMM < 1e-5."""
+    for budget in (2.6, 3.3, 5.2, 6.3, 9.0):
+        rng = np.random.RandomState(5)
+        A = rng.randn(128, 96).astype(np.float32)
+        B = rng.randn(96, 64).astype(np.float32)
+        A[:, :32] *= 1e-4
+        B[32:64] *= 20.0
+        a, b = rd_allocate_pair(A, B, budget)
+        Am = MTCMatrix.from_allocation(A, a.modes, a.scales, 16)
+        Bm = MTCMatrix.from_allocation(B, b.modes, b.scales, 16)
+        np.testing.assert_allclose(Am.to_array(), a.dequant, rtol=0, atol=0)
+        np.testing.assert_allclose(Bm.to_array(), b.dequant, rtol=0, atol=0)
+        C_sim = a.dequant.astype(np.float64) @ b.dequant.astype(np.float64)
+        assert O.relative_frobenius_error(C_sim, mtc_gemm(Am, Bm)) < 1e-5
+        assert Am.total_bytes_allocated * 8 == a.payload_bits
+        assert Bm.total_bytes_allocated * 8 == b.payload_bits
+
+
+def test_uniform_form_dense_x(gpu):
+    rng = np.random.RandomState(8)
+    W = rng.randn(256, 128).astype(np.float32)
+    al = rd_allocate(W, 4.0, None, 32)
+    m = MTCMatrix.from_allocation(W, al.modes, al.scales, 32)
+    X = rng.randn(3, 256).astype(np.float32)
+    assert O.relative_frobenius_error(O.qt_gemm_f64(X, al.dequant), mtc_gemm(X, m)) <= TOL_F32
+
+
+def test_errors_are_clean(gpu, allocs):
+    import ctypes
+    import torch
+    from tensorpack_amd import _abi
+    W, a, m = allocs["outlier-qt-2.5"]
+    with pytest.raises(ValueError):
+        mtc_gemm(torch.zeros(2, W.shape[0] + 1, device=gpu), m)
+    ds = m.device_stream(None)
+    lib = ds.lib
+    X = torch.zeros(1, W.shape[0], device=gpu)
+    Y = torch.zeros(1, W.shape[1], device=gpu)
+    assert lib.mtc_gemv_f32(ctypes.byref(ds.desc), None, W.shape[0], Y.data_ptr(), W.shape[1], 1, None, 0, None) == -1
+    assert lib.mtc_gemv_f32(ctypes.byref(ds.desc), X.data_ptr(), W.shape[0], Y.data_ptr(), W.shape[1], 0, None, 0,
+                            None) == -3
+    bad = _abi.MtcStreamDesc()
+    assert lib.mtc_gemv_f32(ctypes.byref(bad), X.data_ptr(), W.shape[0], Y.data_ptr(), W.shape[1], 1, None, 0,
+                            None) == -7
+    assert b"ABI" in lib.mtc_last_error()
+    g = m.device_stream(64)
+    assert lib.mtc_gemm_bf16(ctypes.byref(ds.desc), X.data_ptr(), 0, W.shape[0], Y.data_ptr(), 0, W.shape[1], 1,
+                             None) in (0, -3)
+    assert lib.mtc_gemm_bf16(ctypes.byref(g.desc), X.data_ptr(), 7, W.shape[0], Y.data_ptr(), 0, W.shape[1], 1,
+                             None) == -4
