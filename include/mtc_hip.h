@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define MTC_ABI_VERSION 1
+#define MTC_ABI_VERSION 3
 
 enum {
   MTC_OK = 0,
@@ -48,26 +48,34 @@ enum { MTC_DTYPE_F32 = 0, MTC_DTYPE_BF16 = 1 };
 
 /*
  * Panel stream. The (permuted) weight Wp is K x N (reduction x output). It is
- * cut into work units u = panel * n_chunks + chunk: panel = 32 output columns,
- * chunk = `chunk_rows` reduction rows. Within a unit, non-P0 leaves are grouped
- * into buckets of equal (leaf size S in {4,8,16,32}, code width P in
- * {2,3,4,5,6,8,16}).
+ * cut into work units u = panel * n_chunks + chunk: panel = 32 output columns
+ * = 8 column groups (cg) of 4 columns, chunk = `chunk_rows` reduction rows
+ * (multiple of 32, at most 4096). Within a unit, lane chunks are grouped by cg
+ * and bucketed by (leaf size S in {4,8,16,32}, code width P in
+ * {2,3,4,5,6,8,16}); a unit's buckets, payload and leaf words are contiguous.
  *
- *  unit_buckets[u] .. unit_buckets[u+1]-1 : bucket indices of unit u
- *  buckets[4*b + 0] : payload offset of the bucket, in dwords (multiple of 4)
- *  buckets[4*b + 1] : index of the bucket's first leaf word
- *  buckets[4*b + 2] : number of 32-code lane chunks
+ *  unit_hdr[32*u + 0..1]   : payload dword range [begin, end) of the unit (begin % 4 == 0)
+ *  unit_hdr[32*u + 2..3]   : leaf-word range [begin, end)
+ *  unit_hdr[32*u + 4..5]   : bucket range [begin, end)
+ *  unit_hdr[32*u + 7]      : dwords a decode block stages on chip: max over the unit's column-group
+ *                            pairs of (pair payload + 4 per pair bucket) + the unit's leaf words
+ *  unit_hdr[32*u + 8..16]  : bucket offset of cg 0..8, relative to the unit's first bucket
+ *  unit_hdr[32*u + 17..25] : payload offset of cg 0..8 in dwords, relative to the unit's payload
+ *  unit_hdr[32*u + 26]     : as word 7 for blocks of four column groups
+ *  buckets[4*b + 0] : payload offset of the bucket in dwords, relative to the unit (multiple of 4)
+ *  buckets[4*b + 1] : first leaf word of the bucket, relative to the unit
+ *  buckets[4*b + 2] : lane chunks in the bucket (bits 0-15) | first chunk within its cg (bits 16-31)
  *  buckets[4*b + 3] : log2(S) | P << 8
- *  leaf_word[l]     : bits 0-7 row offset in the unit / 4, bits 8-10 column
- *                     offset in the panel / 4, bit 11 pad leaf (ignored),
+ *  leaf_word[l]     : bits 0-9 row offset in the unit / 4, bit 13 pad leaf (ignored),
  *                     bits 16-31 bf16 scale
  *  leaf_scale[l]    : fp32 scale (only with MTC_FLAG_FP32_SCALES)
  *
  * A lane chunk is 32 codes in P dwords: code i occupies bits [i*P, i*P+P) of
- * the little-endian bit string (two's complement). Codes of a leaf are in
- * column-major order; a chunk holds 32/S columns of one leaf for S >= 8, and
- * two whole 4x4 leaves (2j, 2j+1) for S = 4 (odd buckets end with a pad leaf
- * whose codes are zero).
+ * the little-endian bit string (two's complement). Every chunk lands in the 4
+ * columns of its cg: for S >= 8 it is 4 columns x 8 rows of one leaf, code i
+ * at column i/8, row i%8, and chunk t of a bucket is leaf t/(S/8), row block
+ * t%(S/8); for S = 4 it is leaves 2t and 2t+1 (16 codes each, column-major; an
+ * odd group ends with a pad leaf). A leaf's word is shared by every cg it spans.
  *
  * Y[:, col_perm[n]] = X[:, row_perm] * Wp[:, n]; NULL perms mean identity.
  */
@@ -80,11 +88,13 @@ typedef struct mtc_stream_desc {
   int32_t n_panels;
   int32_t n_chunks;
   int32_t n_buckets;
+  int32_t max_unit_words;  /* max over units of unit_hdr[32*u + 7] */
+  int32_t max_unit_words4; /* max over units of unit_hdr[32*u + 26] */
   int64_t n_leaves;
   int64_t payload_dwords;
   const uint32_t* payload;
   const uint32_t* buckets;
-  const int32_t* unit_buckets;
+  const int32_t* unit_hdr;
   const uint32_t* leaf_word;
   const float* leaf_scale;
   const int32_t* row_perm;

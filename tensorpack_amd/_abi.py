@@ -2,7 +2,7 @@
 
 import ctypes
 
-ABI_VERSION = 1
+ABI_VERSION = 3
 
 MTC_OK = 0
 MTC_DTYPE_F32 = 0
@@ -28,11 +28,13 @@ class MtcStreamDesc(ctypes.Structure):
         ("n_panels", ctypes.c_int32),
         ("n_chunks", ctypes.c_int32),
         ("n_buckets", ctypes.c_int32),
+        ("max_unit_words", ctypes.c_int32),
+        ("max_unit_words4", ctypes.c_int32),
         ("n_leaves", ctypes.c_int64),
         ("payload_dwords", ctypes.c_int64),
         ("payload", ctypes.c_void_p),
         ("buckets", ctypes.c_void_p),
-        ("unit_buckets", ctypes.c_void_p),
+        ("unit_hdr", ctypes.c_void_p),
         ("leaf_word", ctypes.c_void_p),
         ("leaf_scale", ctypes.c_void_p),
         ("row_perm", ctypes.c_void_p),

@@ -24,7 +24,6 @@ INCLUDE = os.path.join(ROOT, "include")
 HIP_SOURCES = ["mtc_hip.hip"]
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
-    "-ffp-contract=off",
     # packed fp32 VALU ops stay disabled (known to misbehave on this part)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-fvisibility=hidden",

@@ -13,6 +13,8 @@ namespace mtc {
 
 constexpr int kPanel = 32;        // output columns per panel (= widest leaf)
 constexpr int kCodesPerChunk = 32;
+constexpr uint32_t kLeafPad = 1u << 13;   // leaf word flag: padding leaf, contributes nothing
+constexpr int kMaxChunkRows = 4096;
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t hi16) {
   return __uint_as_float(hi16 << 16);
@@ -53,6 +55,24 @@ __device__ __forceinline__ void load_chunk(const uint32_t* __restrict__ src, uin
   }
 }
 
+// P dwords of a chunk staged in LDS (16-byte aligned when P % 4 == 0, 8-byte when P == 2).
+template <int P>
+__device__ __forceinline__ void lds_chunk(const uint32_t* src, uint32_t (&w)[P]) {
+  if constexpr (P % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < P / 4; ++i) {
+      const u32x4_t v = reinterpret_cast<const u32x4_t*>(src)[i];
+      w[4 * i + 0] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+    }
+  } else if constexpr (P == 2) {
+    const u32x2_t v = *reinterpret_cast<const u32x2_t*>(src);
+    w[0] = v.x; w[1] = v.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < P; ++i) w[i] = src[i];
+  }
+}
+
 // Signed code i (0..31) of a chunk.
 template <int P>
 __device__ __forceinline__ int chunk_code(const uint32_t (&w)[P], int i) {
@@ -68,33 +88,23 @@ __device__ __forceinline__ void decode_chunk(const uint32_t (&w)[P], float (&q)[
   for (int i = 0; i < 32; ++i) q[i] = static_cast<float>(chunk_code<P>(w, i));
 }
 
-// Geometry of a lane chunk of leaf size S: G = 32/S column groups of R = S rows.
-// For S >= 8 every group belongs to leaf `t / (S*S/32)`, column
-// (t % (S*S/32)) * G + g. For S = 4 groups 0-3 are leaf 2t, 4-7 leaf 2t+1.
-template <int S>
-struct ChunkGeom {
-  static constexpr int R = S;
-  static constexpr int G = 32 / S;
-  static constexpr int chunks_per_leaf = (S * S) / 32;   // 0 for S = 4
-};
-
-constexpr uint32_t kLeafPad = 1u << 11;   // leaf word flag: padding leaf, contributes nothing
-
 struct LeafInfo {
   int row;    // first row within the unit
-  int col;    // first column within the panel
   bool pad;
   float scale;
 };
 
 __device__ __forceinline__ LeafInfo leaf_info(uint32_t word, const float* __restrict__ fscale, uint32_t leaf) {
   LeafInfo li;
-  li.row = static_cast<int>(word & 0xFFu) * 4;
-  li.col = static_cast<int>((word >> 8) & 0x7u) * 4;
+  li.row = static_cast<int>(word & 0x3FFu) * 4;
   li.pad = (word & kLeafPad) != 0;
   li.scale = fscale ? fscale[leaf] : bf16_bits_to_f32(word >> 16);
   return li;
 }
+
+constexpr int kGroup = 4;             // columns per column group
+constexpr int kGroups = kPanel / kGroup;
+constexpr int kUnitHdr = 32;          // words per unit header
 
 }  // namespace mtc
 

@@ -47,7 +47,7 @@ class DeviceStream:
 
         self.payload = up(ps.payload.view(np.int32), np.int32)
         self.buckets = up(ps.buckets.reshape(-1).view(np.int32), np.int32)
-        self.unit_buckets = up(ps.unit_buckets, np.int32)
+        self.unit_hdr = up(ps.unit_hdr.reshape(-1), np.int32)
         self.leaf_word = up(ps.leaf_word.view(np.int32), np.int32)
         self.leaf_scale = up(ps.leaf_scale, np.float32)
         self.row_perm = up(ps.row_perm, np.int32)
@@ -58,11 +58,13 @@ class DeviceStream:
         d.flags = _abi.MTC_FLAG_FP32_SCALES if ps.leaf_scale is not None else 0
         d.K, d.N, d.chunk_rows = ps.K, ps.N, ps.chunk_rows
         d.n_panels, d.n_chunks = ps.n_panels, ps.n_chunks
-        d.n_buckets = int(ps.unit_buckets[-1])
+        d.n_buckets = ps.n_buckets
+        d.max_unit_words = int(ps.max_unit_words)
+        d.max_unit_words4 = int(ps.max_unit_words4)
         d.n_leaves = int(ps.leaf_word.size)
         d.payload_dwords = int(ps.payload.size)
         ptr = lambda t: None if t is None else t.data_ptr()
-        d.payload, d.buckets, d.unit_buckets = ptr(self.payload), ptr(self.buckets), ptr(self.unit_buckets)
+        d.payload, d.buckets, d.unit_hdr = ptr(self.payload), ptr(self.buckets), ptr(self.unit_hdr)
         d.leaf_word, d.leaf_scale = ptr(self.leaf_word), ptr(self.leaf_scale)
         d.row_perm, d.col_perm = ptr(self.row_perm), ptr(self.col_perm)
         self.desc = d
@@ -73,12 +75,12 @@ class DeviceStream:
         """A second device copy of the same stream (distinct buffers, same contents)."""
         other = object.__new__(DeviceStream)
         other.device, other.host, other.lib = self.device, self.host, self.lib
-        for name in ("payload", "buckets", "unit_buckets", "leaf_word", "leaf_scale", "row_perm", "col_perm"):
+        for name in ("payload", "buckets", "unit_hdr", "leaf_word", "leaf_scale", "row_perm", "col_perm"):
             t = getattr(self, name)
             setattr(other, name, None if t is None else t.clone())
         d = _abi.MtcStreamDesc.from_buffer_copy(self.desc)
         ptr = lambda t: None if t is None else t.data_ptr()
-        d.payload, d.buckets, d.unit_buckets = ptr(other.payload), ptr(other.buckets), ptr(other.unit_buckets)
+        d.payload, d.buckets, d.unit_hdr = ptr(other.payload), ptr(other.buckets), ptr(other.unit_hdr)
         d.leaf_word, d.leaf_scale = ptr(other.leaf_word), ptr(other.leaf_scale)
         d.row_perm, d.col_perm = ptr(other.row_perm), ptr(other.col_perm)
         other.desc = d
@@ -87,7 +89,7 @@ class DeviceStream:
 
     def device_bytes(self) -> int:
         n = 0
-        for name in ("payload", "buckets", "unit_buckets", "leaf_word", "leaf_scale", "row_perm", "col_perm"):
+        for name in ("payload", "buckets", "unit_hdr", "leaf_word", "leaf_scale", "row_perm", "col_perm"):
             t = getattr(self, name)
             if t is not None:
                 n += t.numel() * t.element_size()

@@ -17,6 +17,7 @@ semantics (gemm.py:541-574): C = A_hat @ B_hat in fp32.
 All arithmetic runs in libmtc_hip.so; without a GPU these calls raise.
 """
 
+import os
 from math import ceil
 from typing import Dict, Optional, Tuple
 
@@ -30,16 +31,31 @@ from ..packer import PanelStream, pack_levels, weight_codes
 
 GEMM_CHUNK_ROWS = 64          # K step of the bf16 MFMA kernel
 DECODE_MAX_M = 16             # M at or below this takes the fp32 decode kernel under compute="auto"
-GEMV_TARGET_UNITS = 1024      # work units wanted per decode launch (256 CUs x 4)
+DECODE_X_LDS_BYTES = 64 * 1024   # on-chip budget for the gathered X rows of one decode block
+DECODE_LDS_BYTES = 160 * 1024    # per-block LDS of gfx950
 
 
-def gemv_chunk_rows(K: int, N: int) -> int:
-    """Rows per decode work unit: enough units to fill the chip, 64..512 rows each."""
-    panels = max(N // 32, 1)
-    chunks = max(1, -(-GEMV_TARGET_UNITS // panels))
-    rows = -(-K // chunks)
-    rows = -(-rows // 32) * 32
-    return int(min(max(rows, 64), 512))
+def _decode_mt(M: int) -> int:
+    """Rows of X per decode block (larger M runs several blocks along M)."""
+    return 1 if M <= 1 else 2 if M <= 2 else 4
+
+
+def gemv_chunk_rows(K: int, N: int, M: int = 1) -> int:
+    """Rows per decode work unit: the whole reduction dimension when the
+    gathered X rows (M_tile x rows fp32) fit the on-chip budget, so no block
+    needs a cross-block reduction; otherwise the largest multiple of 32 that fits."""
+    env = os.environ.get("MTC_GEMV_CHUNK_ROWS")
+    if env:
+        return int(env)
+    cap = DECODE_X_LDS_BYTES // (4 * _decode_mt(M)) // 32 * 32
+    rows = -(-K // 32) * 32
+    return int(max(32, min(rows, cap, 4096)))
+
+
+def _decode_lds_need(ps: PanelStream, M: int) -> int:
+    mt = _decode_mt(M)
+    staged = ps.max_unit_words if mt <= 2 else ps.max_unit_words4
+    return 4 * (mt * ps.chunk_rows + 8 * mt * 4 + staged)
 
 
 # ---------------------------------------------------------------------------------------
@@ -237,11 +253,16 @@ class MTCMatrix:
             self._host[chunk_rows] = ps
         return ps
 
-    def device_stream(self, chunk_rows: Optional[int] = None, device=None):
+    def device_stream(self, chunk_rows: Optional[int] = None, device=None, M: int = 1):
+        """Device copy of the stream cut into `chunk_rows`-row units (default: the
+        decode layout for M rows, shrunk until one unit fits on chip)."""
         from ..device import DeviceStream, require_gpu
         dev = require_gpu(device)
         if chunk_rows is None:
-            chunk_rows = gemv_chunk_rows(*self.shape)
+            chunk_rows = gemv_chunk_rows(self.shape[0], self.shape[1], M)
+            while chunk_rows > 32 and _decode_lds_need(self.panel_stream(chunk_rows), M) > DECODE_LDS_BYTES:
+                self._host.pop(chunk_rows, None)
+                chunk_rows = max(32, (chunk_rows // 2) // 32 * 32)
         key = (str(dev), int(chunk_rows))
         ds = self._dev.get(key)
         if ds is None:
@@ -294,7 +315,7 @@ def mtc_gemm(A, B: MTCMatrix, *, compute: str = "auto", out_dtype=None):
         assert K == K2, f"Shape mismatch: {A.shape} vs {B.shape}"
         assert A.block_size == B.block_size, "Block size mismatch"
         a_hat = A.dequant_device(dev)
-        return B.device_stream(None, dev).gemv_f32(a_hat).cpu().numpy()
+        return B.device_stream(None, dev, M).gemv_f32(a_hat).cpu().numpy()
 
     from_numpy = not isinstance(A, torch.Tensor)
     X = _as_device_tensor(A, dev)
@@ -314,7 +335,7 @@ def mtc_gemm(A, B: MTCMatrix, *, compute: str = "auto", out_dtype=None):
         Xf = X.float()
         if Xf.stride(1) != 1:
             Xf = Xf.contiguous()
-        Y = B.device_stream(None, dev).gemv_f32(Xf)
+        Y = B.device_stream(None, dev, M).gemv_f32(Xf)
         if out_dtype is not None and out_dtype != torch.float32:
             Y = Y.to(out_dtype)
     elif compute == "bf16":

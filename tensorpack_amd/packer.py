@@ -1,15 +1,18 @@
 """Packer: quadtree (or uniform-block) allocation -> device "panel stream".
 
 Replaces the reference's arena packer (mtc/kernels/gemm.py:432-488,
-MTCMatrix.from_allocation) for quadtree leaves. The stream layout is defined
-in include/mtc_hip.h; in short:
+MTCMatrix.from_allocation) for quadtree leaves. The byte layout is defined in
+include/mtc_hip.h; in short:
 
-- work unit = (panel of 32 output columns, chunk of `chunk_rows` reduction rows)
-- inside a unit, non-P0 leaves are bucketed by (leaf size S, code width P),
-  buckets ordered S = 32, 16, 8, 4 then P ascending, leaves row-major inside
-- each bucket is a run of 32-code lane chunks, P dwords each, 16-byte aligned
-- one 32-bit word per leaf: row/4, col/4, pad flag, bf16 scale
-- P0 leaves are not stored at all
+- work unit = (panel of 32 output columns, chunk of `chunk_rows` reduction rows);
+  a panel is 8 column groups (cg) of 4 columns
+- a lane chunk is 32 codes that all land in ONE column group: 4 columns x 8
+  rows of a leaf of size 8/16/32, or two 4x4 leaves of one column group
+- inside a unit, chunks are grouped by cg, then bucketed by (leaf size S,
+  code width P), S = 32, 16, 8, 4 then P ascending, leaves by row, then row block
+- each bucket is P dwords per chunk, 16-byte aligned
+- one 32-bit word per leaf (row/4, pad flag, bf16 scale), stored once and shared
+  by every column group the leaf covers; P0 leaves are not stored at all
 
 Codes are computed exactly as the reference quantizer does
 (clip(round_half_even(w / s)), fp32 division; allocation.py:89-94), so the
@@ -24,10 +27,17 @@ import numpy as np
 from .core.allocation import quantize_blocks, to_blocks
 
 PANEL = 32
+GROUP = 4                              # columns per column group
+N_GROUPS = PANEL // GROUP              # 8
 LEAF_SIZES = (32, 16, 8, 4)
 CODE_WIDTHS = (2, 3, 4, 5, 6, 8, 16)
-LEAF_PAD = 1 << 11
+LEAF_PAD = 1 << 13
+ROW_BITS = 10                          # leaf word: row/4 in bits 0-9
+MAX_CHUNK_ROWS = 4 << ROW_BITS         # 4096
+UNIT_HDR_WORDS = 32
 _LOG2 = {32: 5, 16: 4, 8: 3, 4: 2}
+
+CodeSource = Callable[[int, int, np.ndarray, np.ndarray, np.ndarray], np.ndarray]
 
 
 @dataclass
@@ -38,12 +48,14 @@ class PanelStream:
     chunk_rows: int
     payload: np.ndarray                 # uint32
     buckets: np.ndarray                 # uint32 (n_buckets, 4)
-    unit_buckets: np.ndarray            # int32 (n_units + 1,)
+    unit_hdr: np.ndarray                # int32 (n_units, 32)
     leaf_word: np.ndarray               # uint32
     leaf_scale: Optional[np.ndarray]    # float32 or None (bf16 scales in leaf_word)
     row_perm: Optional[np.ndarray] = None   # int32 or None
     col_perm: Optional[np.ndarray] = None   # int32 or None
     n_real_leaves: int = 0
+    max_unit_words: int = 0             # decode block of 2 column groups, max staged dwords
+    max_unit_words4: int = 0            # decode block of 4 column groups
     stats: Dict[str, float] = field(default_factory=dict)
 
     @property
@@ -59,12 +71,16 @@ class PanelStream:
         return self.n_panels * self.n_chunks
 
     @property
+    def n_buckets(self) -> int:
+        return int(self.unit_hdr[-1, 5]) if self.n_units else 0
+
+    @property
     def fp32_scales(self) -> bool:
         return self.leaf_scale is not None
 
     def nbytes(self) -> int:
         """Device bytes of the stream (payload + tables + permutations)."""
-        n = self.payload.nbytes + self.buckets.nbytes + self.unit_buckets.nbytes + self.leaf_word.nbytes
+        n = self.payload.nbytes + 16 * self.n_buckets + self.unit_hdr.nbytes + self.leaf_word.nbytes
         for a in (self.leaf_scale, self.row_perm, self.col_perm):
             if a is not None:
                 n += a.nbytes
@@ -110,9 +126,6 @@ def _bf16_bits(scale: np.ndarray) -> np.ndarray:
     return bits >> 16
 
 
-CodeSource = Callable[[int, int, np.ndarray, np.ndarray, np.ndarray], np.ndarray]
-
-
 def weight_codes(Wp: np.ndarray) -> CodeSource:
     """Codes of leaves (level S, width P, grid rows ii, cols jj, scales sc) quantized from Wp."""
     Wp = np.asarray(Wp, dtype=np.float32)
@@ -126,6 +139,14 @@ def weight_codes(Wp: np.ndarray) -> CodeSource:
     return source
 
 
+def _kind_rank(S: int, P: int) -> int:
+    return LEAF_SIZES.index(S) * len(CODE_WIDTHS) + CODE_WIDTHS.index(P)
+
+
+_KIND_S = np.array([LEAF_SIZES[r // len(CODE_WIDTHS)] for r in range(len(LEAF_SIZES) * len(CODE_WIDTHS))])
+_KIND_P = np.array([CODE_WIDTHS[r % len(CODE_WIDTHS)] for r in range(len(LEAF_SIZES) * len(CODE_WIDTHS))])
+
+
 def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np.ndarray],
                 modes: Dict[int, np.ndarray], scales: Dict[int, np.ndarray], codes_of: CodeSource,
                 chunk_rows: int = 512, scale_format: str = "bf16", row_perm: Optional[np.ndarray] = None,
@@ -136,18 +157,20 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
     listed leaves (see weight_codes).
     """
     K, N = (int(x) for x in shape)
-    if N % PANEL or K % 4:
-        raise ValueError(f"panel stream needs N % {PANEL} == 0 and K % 4 == 0, got {Wp.shape}")
-    if chunk_rows % 32 or not 32 <= chunk_rows <= 1024:
-        raise ValueError(f"chunk_rows={chunk_rows} must be a multiple of 32 in [32, 1024]")
+    if N % PANEL or K % 8:
+        raise ValueError(f"panel stream needs N % {PANEL} == 0 and K % 8 == 0, got {shape}")
+    if chunk_rows % 32 or not 32 <= chunk_rows <= MAX_CHUNK_ROWS:
+        raise ValueError(f"chunk_rows={chunk_rows} must be a multiple of 32 in [32, {MAX_CHUNK_ROWS}]")
     if scale_format not in ("bf16", "fp32"):
         raise ValueError(scale_format)
     n_chunks = -(-K // chunk_rows)
     n_units = (N // PANEL) * n_chunks
 
-    # ---- per (S, P) kind: sorted leaves, lane chunks, leaf words -------------------
-    kinds = []   # (S, P, unit_of_leaf(padded), chunk words (nc, P), leaf words, leaf scales, per-unit leaf counts)
+    # per kind: leaf words (+ unit/kind keys) and chunk records
+    lw_words, lw_scales, lw_unit, lw_kind = [], [], [], []
+    ch_unit, ch_cg, ch_kind, ch_row, ch_leaf, ch_words = [], [], [], [], [], []
     n_real = 0
+    n_lw = 0
     for S in sorted((int(s) for s in sizes), reverse=True):
         if S not in LEAF_SIZES:
             raise ValueError(f"leaf size {S} not supported by the panel stream (sizes {LEAF_SIZES})")
@@ -158,91 +181,159 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
             ii, jj = np.nonzero(lv_leaf & (lv_mode == P))
             if ii.size == 0:
                 continue
+            kr = _kind_rank(S, P)
             k0, n0 = ii * S, jj * S
             unit = (n0 // PANEL) * n_chunks + k0 // chunk_rows
-            order = np.lexsort((n0, k0, unit))
-            ii, jj, k0, n0, unit = ii[order], jj[order], k0[order], n0[order], unit[order]
+            c0 = n0 % PANEL
+            order = np.lexsort((k0, c0, unit))
+            ii, jj, k0, c0, unit = ii[order], jj[order], k0[order], c0[order], unit[order]
             sc = lv_scale[ii, jj]
-            q = codes_of(S, P, ii, jj, sc)                                     # (n, S, S) codes
-            codes = np.asarray(q).astype(np.int32).transpose(0, 2, 1).reshape(len(ii), S * S)   # column-major per leaf
-            rowoff = (k0 % chunk_rows) // 4
-            coloff = (n0 % PANEL) // 4
+            q = np.asarray(codes_of(S, P, ii, jj, sc)).astype(np.int32)          # (n, S, S) row-major
+            n_real += ii.size
+            words = ((k0 % chunk_rows) // 4).astype(np.uint32)
             if scale_format == "bf16":
-                words = (rowoff | (coloff << 8) | (_bf16_bits(sc) << 16)).astype(np.uint32)
-            else:
-                words = (rowoff | (coloff << 8)).astype(np.uint32)
-            n_real += len(ii)
-            counts = np.bincount(unit, minlength=n_units)
+                words = words | (_bf16_bits(sc) << 16).astype(np.uint32)
             if S == 4:
-                # pair leaves per chunk; an odd bucket gets a pad leaf (zero codes, pad flag)
-                odd = np.nonzero(counts & 1)[0]
+                # two leaves of one (unit, column group) per chunk; an odd group gets a pad leaf
+                grp = unit * N_GROUPS + c0 // GROUP
+                edges = np.flatnonzero(np.concatenate([[True], grp[1:] != grp[:-1], [True]]))
+                odd = np.flatnonzero(np.diff(edges) & 1)
                 if odd.size:
-                    ends = np.cumsum(counts)[odd]                  # insert after each odd bucket's last leaf
-                    codes = np.insert(codes, ends, 0, axis=0)
+                    ends = edges[odd + 1]
+                    q = np.insert(q, ends, 0, axis=0)
                     words = np.insert(words, ends, np.uint32(LEAF_PAD))
                     sc = np.insert(sc, ends, np.float32(0))
-                    unit = np.insert(unit, ends, odd)
-                    counts = counts + (counts & 1)
-            chunk_words = pack_codes(codes.reshape(-1, 32), P)
-            kinds.append((S, P, counts, chunk_words, words, sc))
+                    unit = np.insert(unit, ends, unit[ends - 1])
+                    c0 = np.insert(c0, ends, c0[ends - 1])
+                    k0 = np.insert(k0, ends, k0[ends - 1])
+                n = q.shape[0]
+                gidx = n_lw + np.arange(n)
+                ch_unit.append(unit[0::2])
+                ch_cg.append(c0[0::2] // GROUP)
+                ch_kind.append(np.full(n // 2, kr))
+                ch_row.append(k0[0::2])
+                ch_leaf.append(gidx[0::2])
+                ch_words.append(pack_codes(q.transpose(0, 2, 1).reshape(n // 2, 32), P))
+            else:
+                n = q.shape[0]
+                nrb, ncg = S // 8, S // GROUP
+                gidx = n_lw + np.arange(n)
+                # (n, rb, r, cgi, c) -> (n, cgi, rb, c, r): chunk = 4 columns x 8 rows, column-major
+                codes = q.reshape(n, nrb, 8, ncg, GROUP).transpose(0, 3, 1, 4, 2).reshape(n * ncg * nrb, 32)
+                shp = (n, ncg, nrb)
+                ch_unit.append(np.broadcast_to(unit[:, None, None], shp).reshape(-1))
+                ch_cg.append(((c0 // GROUP)[:, None, None] + np.arange(ncg)[None, :, None] + 0 * np.arange(nrb)).reshape(-1))
+                ch_kind.append(np.full(n * ncg * nrb, kr))
+                ch_row.append((k0[:, None, None] + 8 * np.arange(nrb)[None, None, :] + 0 * np.arange(ncg)[None, :, None]).reshape(-1))
+                ch_leaf.append(np.broadcast_to(gidx[:, None, None], shp).reshape(-1))
+                ch_words.append(pack_codes(codes, P))
+            lw_words.append(words)
+            lw_scales.append(sc)
+            lw_unit.append(unit)
+            lw_kind.append(np.full(n, kr))
+            n_lw += n
 
-    # ---- bucket table: units ascending, kinds in the order built above ----------------
-    counts_mat = np.stack([k[2] for k in kinds], axis=1) if kinds else np.zeros((n_units, 0), np.int64)
-    present = counts_mat > 0                                        # (n_units, n_kinds)
-    unit_idx, kind_idx = np.nonzero(present)                        # row-major: unit, then kind
-    n_buckets = unit_idx.size
-    unit_buckets = np.zeros(n_units + 1, dtype=np.int32)
-    np.cumsum(present.sum(axis=1), out=unit_buckets[1:])
-    leaves_per = counts_mat[unit_idx, kind_idx].astype(np.int64)
-    S_of = np.array([k[0] for k in kinds], dtype=np.int64)
-    P_of = np.array([k[1] for k in kinds], dtype=np.int64)
-    Sb, Pb = S_of[kind_idx], P_of[kind_idx]
-    chunks_per = leaves_per * Sb * Sb // 32
-    dwords = chunks_per * Pb
-    aligned = (dwords + 3) & ~3
-    pay_off = np.zeros(n_buckets, dtype=np.int64)
-    if n_buckets:
-        pay_off[1:] = np.cumsum(aligned)[:-1]
-    leaf_off = np.zeros(n_buckets, dtype=np.int64)
-    if n_buckets:
-        leaf_off[1:] = np.cumsum(leaves_per)[:-1]
-    total_dw = int(aligned.sum())
-    total_leaves = int(leaves_per.sum())
-    if total_dw >= 2 ** 32 or total_leaves >= 2 ** 32:
-        raise ValueError("stream too large for 32-bit offsets")
+    # ---- leaf words in (unit, kind, c0, k0) order: each bucket's leaves form one run ----
+    if n_lw:
+        wu = np.concatenate(lw_unit).astype(np.int64)
+        wk = np.concatenate(lw_kind).astype(np.int64)
+        lw_order = np.lexsort((np.arange(n_lw), wk, wu))       # keeps each kind's (c0, k0) order
+        lw_pos = np.empty(n_lw, dtype=np.int64)
+        lw_pos[lw_order] = np.arange(n_lw)
+        leaf_word = np.concatenate(lw_words)[lw_order]
+        leaf_scale = np.concatenate(lw_scales)[lw_order] if scale_format == "fp32" else None
+        leaf_begin = np.searchsorted(wu[lw_order], np.arange(n_units + 1)).astype(np.int64)
+    else:
+        leaf_word = np.zeros(1, np.uint32)
+        leaf_scale = np.zeros(1, np.float32) if scale_format == "fp32" else None
+        lw_pos = np.zeros(0, np.int64)
+        leaf_begin = np.zeros(n_units + 1, np.int64)
 
-    payload = np.zeros(max(total_dw, 4), dtype=np.uint32)
-    leaf_word = np.zeros(max(total_leaves, 1), dtype=np.uint32)
-    leaf_scale = np.zeros(max(total_leaves, 1), dtype=np.float32) if scale_format == "fp32" else None
-    for ki, (S, P, counts, chunk_words, words, sc) in enumerate(kinds):
-        sel = np.nonzero(kind_idx == ki)[0]                         # this kind's buckets, unit order
-        if sel.size == 0:
-            continue
-        nl = leaves_per[sel]
-        nc = chunks_per[sel]
-        # payload: the kind's chunk rows are already in bucket order
-        src_start = np.concatenate([[0], np.cumsum(nc)[:-1]])
-        dst = np.repeat(pay_off[sel] - src_start * P, nc * P) + np.arange(int(nc.sum()) * P)
-        payload[dst] = chunk_words.reshape(-1)
-        lsrc = np.concatenate([[0], np.cumsum(nl)[:-1]])
-        ldst = np.repeat(leaf_off[sel] - lsrc, nl) + np.arange(int(nl.sum()))
-        leaf_word[ldst] = words
-        if leaf_scale is not None:
-            leaf_scale[ldst] = sc
+    # ---- chunks in (unit, cg, kind, row) order -> buckets and payload ----
+    if ch_unit:
+        cu = np.concatenate(ch_unit).astype(np.int64)
+        cc = np.concatenate(ch_cg).astype(np.int64)
+        ck = np.concatenate(ch_kind).astype(np.int64)
+        cr = np.concatenate(ch_row).astype(np.int64)
+        cl = lw_pos[np.concatenate(ch_leaf).astype(np.int64)]
+        cP = np.concatenate([np.full(w.shape[0], w.shape[1]) for w in ch_words]).astype(np.int64)
+        src_off = np.concatenate([[0], np.cumsum(cP)[:-1]])
+        src = np.concatenate([w.reshape(-1) for w in ch_words])
+        corder = np.lexsort((cr, ck, cc, cu))
+        cu, cc, ck, cl, cP, src_off = cu[corder], cc[corder], ck[corder], cl[corder], cP[corder], src_off[corder]
+        n_ch = cu.size
+        bkey = (cu * N_GROUPS + cc) * 64 + ck
+        b_start = np.flatnonzero(np.concatenate([[True], bkey[1:] != bkey[:-1]]))
+        n_buckets = b_start.size
+        b_cnt = np.diff(np.concatenate([b_start, [n_ch]]))
+        b_unit, b_cg, b_kind = cu[b_start], cc[b_start], ck[b_start]
+        b_S, b_P = _KIND_S[b_kind], _KIND_P[b_kind]
+        b_dw = (b_cnt * b_P + 3) & ~3
+        b_pay = np.concatenate([[0], np.cumsum(b_dw)[:-1]])
+        total_dw = int(b_dw.sum())
+        payload = np.zeros(max(total_dw, 4), dtype=np.uint32)
+        b_of = np.repeat(np.arange(n_buckets), b_cnt)
+        dst = b_pay[b_of] + (np.arange(n_ch) - b_start[b_of]) * cP
+        for P in np.unique(cP):
+            sel = np.flatnonzero(cP == P)
+            payload[(dst[sel][:, None] + np.arange(P)).reshape(-1)] = src[(src_off[sel][:, None] + np.arange(P)).reshape(-1)]
+        # first chunk of each bucket within its column group
+        gkey = cu * N_GROUPS + cc
+        g_start = np.flatnonzero(np.concatenate([[True], gkey[1:] != gkey[:-1]]))
+        g_of = np.repeat(np.arange(g_start.size), np.diff(np.concatenate([g_start, [n_ch]])))
+        b_cstart = b_start - g_start[g_of[b_start]]
+        b_leaf = cl[b_start]
+        pay_after = np.concatenate([b_pay, [total_dw]])
+    else:
+        n_buckets, total_dw = 0, 0
+        payload = np.zeros(4, np.uint32)
+        b_unit = b_cg = b_cnt = b_cstart = b_leaf = b_pay = np.zeros(0, np.int64)
+        b_S = b_P = np.zeros(0, np.int64)
+        pay_after = np.zeros(1, np.int64)
+
+    if payload.size >= 2 ** 31 or leaf_word.size >= 2 ** 31:
+        raise ValueError("stream too large for 31-bit offsets")
+    if n_buckets and (b_cnt.max() >= 1 << 16 or b_cstart.max() >= 1 << 16):
+        raise ValueError("a column group holds 65536 or more lane chunks; use a smaller chunk_rows")
+
+    # ---- unit headers ----
+    hdr = np.zeros((n_units, UNIT_HDR_WORDS), dtype=np.int64)
+    ub = np.searchsorted(b_unit, np.arange(n_units + 1))
+    hdr[:, 0], hdr[:, 1] = pay_after[ub[:-1]], pay_after[ub[1:]]
+    hdr[:, 2], hdr[:, 3] = leaf_begin[:-1], leaf_begin[1:]
+    hdr[:, 4], hdr[:, 5] = ub[:-1], ub[1:]
+    hdr[:, 6] = ub[1:] - ub[:-1]
+    gb = np.searchsorted(b_unit * N_GROUPS + b_cg, np.arange(n_units * N_GROUPS + 1))
+    gb = np.concatenate([gb[:-1].reshape(n_units, N_GROUPS), ub[1:, None]], axis=1)      # (n_units, 9)
+    hdr[:, 8:17] = gb - hdr[:, 4:5]
+    hdr[:, 17:26] = pay_after[gb] - hdr[:, 0:1]
+    # dwords one decode block (a pair of column groups) stages on chip: the pair's payload and
+    # bucket entries plus all of the unit's leaf words; hdr[7] is the max over the unit's pairs
+    pair_pay = hdr[:, 17 + 2:26:2] - hdr[:, 17:25:2]
+    pair_bk = hdr[:, 8 + 2:17:2] - hdr[:, 8:16:2]
+    hdr[:, 7] = (pair_pay + 4 * pair_bk).max(axis=1) + (hdr[:, 3] - hdr[:, 2])
+    # the same for blocks of four column groups
+    quad_pay = hdr[:, 17 + 4:26:4] - hdr[:, 17:22:4]
+    quad_bk = hdr[:, 8 + 4:17:4] - hdr[:, 8:13:4]
+    hdr[:, 26] = (quad_pay + 4 * quad_bk).max(axis=1) + (hdr[:, 3] - hdr[:, 2])
+    max_unit_words = int(hdr[:, 7].max()) if n_units else 0
+    max_unit_words4 = int(hdr[:, 26].max()) if n_units else 0
 
     buckets = np.zeros((max(n_buckets, 1), 4), dtype=np.uint32)
     if n_buckets:
-        buckets[:n_buckets, 0] = pay_off
-        buckets[:n_buckets, 1] = leaf_off
-        buckets[:n_buckets, 2] = chunks_per
-        buckets[:n_buckets, 3] = np.array([_LOG2[int(s)] for s in Sb], dtype=np.uint32) | (Pb.astype(np.uint32) << 8)
+        buckets[:n_buckets, 0] = b_pay - hdr[b_unit, 0]
+        buckets[:n_buckets, 1] = b_leaf - hdr[b_unit, 2]
+        buckets[:n_buckets, 2] = b_cnt | (b_cstart << 16)
+        buckets[:n_buckets, 3] = np.array([_LOG2[int(s)] for s in b_S], dtype=np.uint32) | (b_P.astype(np.uint32) << 8)
 
-    stats = {"payload_bytes": float(total_dw * 4), "n_buckets": float(n_buckets), "n_leaves": float(n_real)}
-    return PanelStream(K=K, N=N, chunk_rows=chunk_rows, payload=payload, buckets=buckets, unit_buckets=unit_buckets,
-                       leaf_word=leaf_word, leaf_scale=leaf_scale,
+    stats = {"payload_bytes": float(total_dw * 4), "n_buckets": float(n_buckets), "n_leaves": float(n_real),
+             "max_unit_bytes": float(4 * max_unit_words)}
+    return PanelStream(K=K, N=N, chunk_rows=chunk_rows, payload=payload, buckets=buckets,
+                       unit_hdr=hdr.astype(np.int32), leaf_word=leaf_word, leaf_scale=leaf_scale,
                        row_perm=None if row_perm is None else np.ascontiguousarray(row_perm, dtype=np.int32),
                        col_perm=None if col_perm is None else np.ascontiguousarray(col_perm, dtype=np.int32),
-                       n_real_leaves=n_real, stats=stats)
+                       n_real_leaves=n_real, max_unit_words=max_unit_words,
+                       max_unit_words4=max_unit_words4, stats=stats)
 
 
 def decode_stream(ps: PanelStream) -> np.ndarray:
@@ -252,24 +343,31 @@ def decode_stream(ps: PanelStream) -> np.ndarray:
     """
     K, N = ps.K, ps.N
     Wp = np.zeros((K, N), dtype=np.float32)
-    nb = int(ps.unit_buckets[-1])
-    for b in range(nb):
-        off, l0, nc, key = (int(x) for x in ps.buckets[b])
-        S, P = 1 << (key & 0xFF), key >> 8
-        u = int(np.searchsorted(ps.unit_buckets, b, side="right") - 1)
+    for u in range(ps.n_units):
         panel, chunk = divmod(u, ps.n_chunks)
-        codes = unpack_codes(ps.payload[off: off + nc * P].reshape(nc, P), P).reshape(-1, S * S)
-        nleaf = codes.shape[0]
-        words = ps.leaf_word[l0: l0 + nleaf]
-        for i in range(nleaf):
-            wd = int(words[i])
-            if wd & LEAF_PAD:
-                continue
-            r0 = chunk * ps.chunk_rows + (wd & 0xFF) * 4
-            c0 = panel * PANEL + ((wd >> 8) & 7) * 4
-            s = ps.leaf_scale[l0 + i] if ps.leaf_scale is not None else np.uint32(wd >> 16 << 16).view(np.float32)
-            blk = codes[i].reshape(S, S).T.astype(np.float32) * np.float32(s)
-            Wp[r0: r0 + S, c0: c0 + S] = blk
+        h = [int(x) for x in ps.unit_hdr[u]]
+        for g in range(N_GROUPS):
+            for b in range(h[4] + h[8 + g], h[4] + h[9 + g]):
+                prel, lrel, w2, key = (int(x) for x in ps.buckets[b])
+                nc = w2 & 0xFFFF
+                S, P = 1 << (key & 0xFF), key >> 8
+                off = h[0] + prel
+                codes = unpack_codes(ps.payload[off: off + nc * P].reshape(nc, P), P)
+                l0 = h[2] + lrel
+                for t in range(nc):
+                    if S == 4:
+                        parts = [(l0 + 2 * t, codes[t, :16], 0, 4), (l0 + 2 * t + 1, codes[t, 16:], 0, 4)]
+                    else:
+                        parts = [(l0 + t // (S // 8), codes[t], 8 * (t % (S // 8)), 8)]
+                    for li, cd, rrel, rows in parts:
+                        wd = int(ps.leaf_word[li])
+                        if wd & LEAF_PAD:
+                            continue
+                        r0 = chunk * ps.chunk_rows + (wd & ((1 << ROW_BITS) - 1)) * 4 + rrel
+                        c0 = panel * PANEL + GROUP * g
+                        s = ps.leaf_scale[li] if ps.leaf_scale is not None else \
+                            np.array([wd >> 16 << 16], dtype=np.uint32).view(np.float32)[0]
+                        Wp[r0: r0 + rows, c0: c0 + GROUP] = cd.reshape(GROUP, rows).T.astype(np.float32) * np.float32(s)
     if ps.leaf_scale is None:
         Wp = Wp + np.float32(0.0)      # quadtree W_hat never holds -0.0
     if ps.row_perm is None and ps.col_perm is None:
