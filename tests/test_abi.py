@@ -1,0 +1,132 @@
+"""C-ABI: both libraries load without a GPU, export every function declared in
+include/*.h, the ctypes descriptor mirrors the C struct byte for byte, and
+host-side validation turns bad input into error codes (no GPU call is made)."""
+
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import numpy as np
+import pytest
+
+from tensorpack_amd import _abi, _native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INCLUDE = os.path.join(ROOT, "include")
+
+
+def _declared(header):
+    text = open(os.path.join(INCLUDE, header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(mtc_[a-z_0-9]+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def hip():
+    return _native.hip_lib()
+
+
+def test_every_declared_symbol_is_exported(hip):
+    rd = _native.rd_lib()
+    for header, lib in (("mtc_hip.h", hip), ("mtc_rd.h", rd)):
+        names = _declared(header)
+        assert names, header
+        for n in names:
+            assert hasattr(lib, n), f"{n} declared in {header} but not exported"
+    assert set(_abi.EXPORTED) == set(_declared("mtc_hip.h"))
+    assert hip.mtc_abi_version() == _abi.ABI_VERSION
+    assert rd.mtc_rd_abi_version() == 1
+
+
+def test_descriptor_layout_matches_c():
+    fields = [f[0] for f in _abi.MtcStreamDesc._fields_]
+    src = "#include <stddef.h>\n#include <stdio.h>\n#include \"mtc_hip.h\"\nint main(void){\n"
+    src += 'printf("%zu\\n", sizeof(mtc_stream_desc));\n'
+    for f in fields:
+        src += f'printf("%zu\\n", offsetof(mtc_stream_desc, {f}));\n'
+    src += "return 0;}\n"
+    with tempfile.TemporaryDirectory() as d:
+        c, exe = os.path.join(d, "t.c"), os.path.join(d, "t")
+        open(c, "w").write(src)
+        subprocess.run(["gcc", "-I", INCLUDE, c, "-o", exe], check=True)
+        out = [int(x) for x in subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split()]
+    assert out[0] == ctypes.sizeof(_abi.MtcStreamDesc)
+    assert out[1:] == [getattr(_abi.MtcStreamDesc, f).offset for f in fields]
+
+
+def _desc(**kw):
+    d = _abi.MtcStreamDesc()
+    d.abi_version = _abi.ABI_VERSION
+    d.K, d.N, d.chunk_rows = 256, 64, 128
+    d.n_panels, d.n_chunks = 2, 2
+    d.n_buckets, d.max_unit_words, d.max_unit_words4 = 4, 100, 100
+    d.n_leaves, d.payload_dwords = 4, 64
+    dummy = 0x1000
+    d.payload = d.buckets = d.unit_hdr = d.leaf_word = dummy
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+def test_descriptor_validation(hip):
+    ok = _desc()
+    assert hip.mtc_check_desc(ctypes.byref(ok)) == 0
+    cases = {
+        "abi_version": (99, -7), "N": (60, -2), "K": (0, -2), "chunk_rows": (48, -2),
+        "n_panels": (3, -2), "n_chunks": (1, -2), "unit_hdr": (None, -1), "payload": (None, -1),
+        "max_unit_words4": (50, -2),
+    }
+    for field, (val, code) in cases.items():
+        assert hip.mtc_check_desc(ctypes.byref(_desc(**{field: val}))) == code, field
+        assert hip.mtc_last_error()
+    assert hip.mtc_check_desc(None) == -1
+    # fp32-scale flag and table must agree
+    assert hip.mtc_check_desc(ctypes.byref(_desc(flags=_abi.MTC_FLAG_FP32_SCALES))) == -1
+    assert hip.mtc_check_desc(ctypes.byref(_desc(leaf_scale=0x2000))) == -2
+
+
+def test_entry_points_reject_bad_arguments_before_any_gpu_call(hip):
+    d = _desc()
+    ref = ctypes.byref(d)
+    assert hip.mtc_gemv_f32(ref, None, 256, 0x10, 64, 1, None, 0, None) == -1
+    assert hip.mtc_gemv_f32(ref, 0x10, 256, 0x10, 64, 0, None, 0, None) == -3
+    assert hip.mtc_gemv_f32(ref, 0x10, 100, 0x10, 64, 1, None, 0, None) == -3
+    need = hip.mtc_gemv_workspace_bytes(ref, 1)
+    assert need > 0                                             # two chunks -> split-K workspace
+    assert hip.mtc_gemv_f32(ref, 0x10, 256, 0x10, 64, 1, None, 0, None) == -5
+    assert hip.mtc_gemv_f32(ref, 0x10, 256, 0x10, 64, 1, 0x20, need - 1, None) == -5
+    assert hip.mtc_gemm_bf16(ref, 0x10, 0, 256, 0x10, 0, 64, 4, None) == -3      # chunk_rows != 64
+    g = _desc(chunk_rows=64, n_chunks=4)
+    assert hip.mtc_gemm_bf16(ctypes.byref(g), 0x10, 5, 256, 0x10, 0, 64, 4, None) == -4
+    assert hip.mtc_gemm_bf16(ctypes.byref(g), 0x10, 0, 256, 0x10, 9, 64, 4, None) == -4
+    assert hip.mtc_gemm_bf16(ctypes.byref(g), None, 0, 256, 0x10, 0, 64, 4, None) == -1
+    assert hip.mtc_dequant(ref, None, None) == -1
+
+
+def test_rd_search_rejects_bad_block_size():
+    rd = _native.rd_lib()
+    F, D = _native.c_f32p, _native.c_f64p
+    z = np.zeros(16, np.float32)
+    hd = np.zeros(16, np.float64)
+    out_d = np.zeros(4, np.float64)
+    out_s = np.zeros(4, np.float32)
+    rc = rd.mtc_rd_search(_native.ptr(z, F), _native.ptr(hd, D), _native.ptr(z, F), 1, 3, -2.0, 1.0, 2.0,
+                          _native.ptr(z, F), 1, _native.ptr(z, F), 1, 0, 1, _native.ptr(out_d, D),
+                          _native.ptr(out_s, F))
+    assert rc == -1
+
+
+def test_gpu_path_fails_loudly_without_gpu():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    from tensorpack_amd.core.quadtree import QuadtreeRD
+    from tensorpack_amd.kernels.gemm import MTCMatrix, mtc_gemm
+    W = np.random.RandomState(0).randn(64, 64).astype(np.float32)
+    m = MTCMatrix.from_quadtree(QuadtreeRD(W, None, (32, 16)).select(4.0), W)
+    with pytest.raises(RuntimeError, match="GPU"):
+        mtc_gemm(np.ones((1, 64), np.float32), m)
+    with pytest.raises(RuntimeError, match="GPU"):
+        m.to_array()

@@ -1,0 +1,101 @@
+"""Known answers: the reference's published quadtree results, reproduced exactly.
+
+results/pareto.json of the reference holds, for each synthetic scenario and
+each budget of RD_BUDGETS (mtc/benchmarks/benchmark_pareto.py:33), the total
+bits/element (4 decimals) and the relative output error of MTC-QT and MTC-QT-P.
+The scenario matrices come from seeded np.random.RandomState streams:
+- llm_like: benchmark_pareto.py:141-153 (make_llm_like) + :156-164 (weight only)
+- gaussian / uniform / outliers / multi_scale: benchmark_runner.py:21-51
+  (generate_matrix, N = 512, seeds 42 / 43) + benchmark_pareto.py:126-138.
+Matching both numbers at every budget pins the restated scale search, bf16
+rounding, tree pruning and bisection (a single flipped leaf moves bits or error).
+"""
+
+import json
+import os
+
+import numpy as np
+import pytest
+
+from tensorpack_amd.core.permutation import PermutedQuadtreeRD
+from tensorpack_amd.core.quadtree import QuadtreeRD
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+KAT = json.load(open(os.path.join(HERE, "golden", "pareto_qt_kat.json")))["scenarios"]
+QT, QTP = "MTC-QT quadtree 32-4 (ours)", "MTC-QT-P permuted quadtree (ours)"
+SOLVER = {QT: QuadtreeRD, QTP: PermutedQuadtreeRD}
+
+
+def llm_like(K=1024, N=1024, T=512, seed=0):
+    rng = np.random.RandomState(seed)
+    W = (rng.standard_t(df=4, size=(K, N)) * 0.02).astype(np.float32)
+    W *= np.exp(rng.randn(K, 1) * 0.5).astype(np.float32)
+    chan = np.exp(rng.randn(K) * 0.3)
+    hot = rng.choice(K, size=max(1, K // 100), replace=False)
+    chan[hot] *= 30.0
+    X_cal = (rng.randn(T, K) * chan).astype(np.float32)
+    X_test = (rng.randn(T, K) * chan).astype(np.float32)
+    return W, X_cal, X_test
+
+
+def synthetic(dist, N, seed):
+    rng = np.random.RandomState(seed)
+    if dist == "gaussian":
+        return rng.randn(N, N).astype(np.float32)
+    if dist == "uniform":
+        return rng.uniform(-1.0, 1.0, size=(N, N)).astype(np.float32)
+    if dist == "outliers":
+        base = rng.randn(N, N).astype(np.float32) * 0.05
+        mask = rng.rand(N, N) < 0.02
+        big = rng.uniform(-25.0, 25.0, size=(N, N)).astype(np.float32)
+        base[mask] = big[mask]
+        return base
+    base = rng.randn(N, N).astype(np.float32)
+    for bi in range(N // 16):
+        for bj in range(N // 16):
+            base[bi * 16:(bi + 1) * 16, bj * 16:(bj + 1) * 16] *= 10.0 ** rng.uniform(-3.0, 2.0)
+    return base
+
+
+def rel_err(ref, pred):
+    return float(np.linalg.norm(ref - pred) / np.linalg.norm(ref))
+
+
+def _check(points, got):
+    for p, (bits, err) in zip(points, got):
+        assert round(bits, 4) == p["bits"], (p["label"], bits, p["bits"])
+        # both errors are f32 norms of f32 BLAS products; only BLAS summation order may differ
+        assert err == pytest.approx(p["rel_err"], rel=1e-5), (p["label"], err, p["rel_err"])
+
+
+@pytest.mark.parametrize("family", [QT, QTP])
+def test_llm_like_known_answers(family):
+    W, X_cal, X_test = llm_like()
+    Y = X_test @ W
+    h = (X_cal.astype(np.float64) ** 2).mean(axis=0)
+    solver = SOLVER[family](W, h, (32, 16, 8, 4))
+    pts = KAT["llm_like (weight-only, calibrated)"][family]
+    got = []
+    for p in pts:
+        a = solver.select(float(p["label"][:-1]))
+        got.append((a.bits_per_element, rel_err(Y, X_test @ a.dequant)))
+    _check(pts, got)
+
+
+@pytest.mark.parametrize("dist", ["gaussian", "uniform", "outliers", "multi_scale"])
+@pytest.mark.parametrize("family", [QT, QTP])
+def test_both_operand_known_answers(dist, family):
+    A = synthetic(dist, 512, 42)
+    B = synthetic(dist, 512, 43)
+    C = A @ B
+    hA = (B.astype(np.float64) ** 2).sum(axis=1)
+    hB = (A.astype(np.float64) ** 2).sum(axis=0)
+    sa = SOLVER[family](A.T, hA, (32, 16, 8, 4))
+    sb = SOLVER[family](B, hB, (32, 16, 8, 4))
+    pts = KAT[f"{dist} (A@B, both quantized)"][family]
+    got = []
+    for p in pts:
+        b = float(p["label"][:-1])
+        qa, qb = sa.select(b), sb.select(b)
+        got.append(((qa.bits_per_element + qb.bits_per_element) / 2.0, rel_err(C, qa.dequant.T @ qb.dequant)))
+    _check(pts, got)

@@ -1,0 +1,154 @@
+"""Packer: the panel stream must carry exactly the oracle's W_hat (host decode,
+bit-exact), keep its layout invariants, and the uniform-block arena must keep
+the reference byte layout."""
+
+import numpy as np
+import pytest
+from hypothesis import given, settings, strategies as st
+
+from oracle import mtc_oracle as O
+from tensorpack_amd.core.allocation import rd_allocate_pair
+from tensorpack_amd.core.permutation import PermutedQuadtreeRD
+from tensorpack_amd.core.quadtree import QuadtreeRD
+from tensorpack_amd.kernels.gemm import MTCMatrix, arena_decode, arena_encode
+from tensorpack_amd.packer import (LEAF_PAD, N_GROUPS, decode_stream, pack_codes, unpack_codes)
+
+from conftest import outlier_matrix
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def _oracle(alloc, W):
+    if hasattr(alloc, "inner"):
+        i = alloc.inner
+        return O.permuted_qt_dequant(W, alloc.row_perm, alloc.col_perm, i.sizes, i.leaf, i.modes, i.scales)
+    return O.qt_dequant(W, alloc.sizes, alloc.leaf, alloc.modes, alloc.scales)
+
+
+@pytest.mark.parametrize("P", [2, 3, 4, 5, 6, 8, 16])
+def test_pack_codes_round_trip_and_bit_order(P):
+    lo, hi = -(1 << (P - 1)), (1 << (P - 1)) - 1
+    q = np.random.RandomState(P).randint(lo, hi + 1, size=(9, 32))
+    w = pack_codes(q, P)
+    assert w.shape == (9, P)
+    assert np.array_equal(unpack_codes(w, P), q)
+    one = np.zeros((1, 32), np.int64)
+    one[0, 1] = 1                                     # code 1 starts at bit P
+    assert pack_codes(one, P)[0, (P) // 32] == 1 << (P % 32)
+
+
+CASES = [(QuadtreeRD, 2.2), (QuadtreeRD, 4.25), (QuadtreeRD, 9.0), (QuadtreeRD, 15.0),
+         (PermutedQuadtreeRD, 2.5), (PermutedQuadtreeRD, 4.25)]
+
+
+@pytest.mark.parametrize("cls,budget", CASES)
+@pytest.mark.parametrize("chunk_rows", [32, 96, 256])
+def test_stream_decodes_to_oracle_w_hat(cls, budget, chunk_rows):
+    W = outlier_matrix(int(budget * 10), 256, 160)
+    h = np.exp(np.random.RandomState(9).randn(256))
+    a = cls(W, h, (32, 16, 8, 4)).select(budget)
+    ps = MTCMatrix.from_quadtree(a, W).panel_stream(chunk_rows)
+    assert np.array_equal(_bits(decode_stream(ps)), _bits(_oracle(a, W)))
+
+
+def test_stream_layout_invariants():
+    W = outlier_matrix(11, 256, 128)
+    a = QuadtreeRD(W, None, (32, 16, 8, 4)).select(3.0)
+    ps = MTCMatrix.from_quadtree(a, W).panel_stream(128)
+    h = ps.unit_hdr
+    assert np.all(h[:, 0] % 4 == 0) and np.all(h[:-1, 1] == h[1:, 0])
+    assert np.all(h[:-1, 5] == h[1:, 4]) and np.all(h[:-1, 3] == h[1:, 2])
+    assert np.all(np.diff(h[:, 8:17], axis=1) >= 0) and np.all(h[:, 16] == h[:, 5] - h[:, 4])
+    assert np.all(np.diff(h[:, 17:26], axis=1) >= 0) and np.all(h[:, 25] == h[:, 1] - h[:, 0])
+    nb = ps.n_buckets
+    b = ps.buckets[:nb]
+    assert np.all(b[:, 0] % 4 == 0)
+    S, P = 1 << (b[:, 3] & 0xFF), b[:, 3] >> 8
+    assert set(S.tolist()) <= {4, 8, 16, 32} and set(P.tolist()) <= {2, 3, 4, 5, 6, 8, 16}
+    # chunk counts: every non-P0 weight once (S=4 pad leaves are zero codes)
+    area = sum(int((a.leaf[s] & (a.modes[s] != 0)).sum()) * s * s for s in a.sizes)
+    n_chunks = int((b[:, 2] & 0xFFFF).sum())
+    pads = int(np.sum(ps.leaf_word & LEAF_PAD != 0))
+    assert n_chunks * 32 == area + 16 * pads
+    # per column group the chunk index restarts at 0 and runs contiguously
+    for u in range(ps.n_units):
+        for g in range(N_GROUPS):
+            lo_, hi_ = h[u, 4] + h[u, 8 + g], h[u, 4] + h[u, 9 + g]
+            start = 0
+            for k in range(lo_, hi_):
+                assert ps.buckets[k, 2] >> 16 == start
+                start += ps.buckets[k, 2] & 0xFFFF
+
+
+def test_payload_accounting_matches_allocator_bits():
+    W = outlier_matrix(12, 256, 256)
+    a = QuadtreeRD(W, None, (32, 16, 8, 4)).select(4.0)
+    ps = MTCMatrix.from_quadtree(a, W).panel_stream(256)
+    payload_bits = sum(int((a.leaf[s] & (a.modes[s] == m)).sum()) * s * s * m
+                       for s in a.sizes for m in (2, 3, 4, 5, 6, 8, 16))
+    b = ps.buckets[:ps.n_buckets]
+    n, P = (b[:, 2] & 0xFFFF).astype(np.int64), (b[:, 3] >> 8).astype(np.int64)
+    # chunk words = allocator payload + the zero codes of S=4 pad leaves (16 codes each)
+    pad_bits = 0
+    for k in np.flatnonzero((b[:, 3] & 0xFF) == 2):
+        u = int(np.searchsorted(ps.unit_hdr[:, 5], k, side="right"))
+        l0 = ps.unit_hdr[u, 2] + b[k, 1]
+        pad_bits += 16 * int(P[k]) * int(np.sum(ps.leaf_word[l0: l0 + 2 * n[k]] & LEAF_PAD != 0))
+    assert int((n * P * 32).sum()) == payload_bits + pad_bits
+    # each bucket is then padded to 16 bytes
+    assert ps.stats["payload_bytes"] * 8 == int((((n * P + 3) // 4) * 4 * 32).sum())
+
+
+@settings(max_examples=15, deadline=None)
+@given(seed=st.integers(0, 10 ** 6), budget=st.floats(1.8, 12.0), rows=st.sampled_from([64, 128]),
+       perm=st.booleans(), sizes=st.sampled_from([(32, 16, 8, 4), (16, 8, 4), (8, 4), (4,), (32,)]))
+def test_fuzz_leaf_mixes(seed, budget, rows, perm, sizes):
+    rng = np.random.RandomState(seed)
+    W = (rng.randn(rows, 64) * 10.0 ** rng.uniform(-2, 1, size=(rows, 1))).astype(np.float32)
+    W[rng.rand(rows, 64) < 0.03] = 20.0
+    cls = PermutedQuadtreeRD if perm else QuadtreeRD
+    try:
+        a = cls(W, np.exp(rng.randn(rows)), sizes).select(budget)
+    except ValueError:
+        return                                             # budget below this size set's floor
+    ps = MTCMatrix.from_quadtree(a, W).panel_stream(32 * int(rng.randint(1, 4)))
+    assert np.array_equal(_bits(decode_stream(ps)), _bits(_oracle(a, W)))
+
+
+# ---------------- uniform-block arena (reference layout) ----------------
+@pytest.mark.parametrize("mode", [2, 3, 4, 5, 6, 8, 16])
+def test_arena_codec_matches_oracle(mode):
+    lo, hi = O.QRANGE[mode]
+    q = np.random.RandomState(mode + 50).randint(lo, hi + 1, size=(5, 256))
+    enc = arena_encode(q, mode)
+    assert np.array_equal(enc, O.arena_pack(q, mode))
+    assert np.array_equal(arena_decode(enc, mode, 256), q)
+
+
+def test_uniform_from_allocation_layout_and_accounting():
+    rng = np.random.RandomState(5)
+    A = rng.randn(128, 96).astype(np.float32)
+    B = rng.randn(96, 64).astype(np.float32)
+    A[:, :32] *= 1e-4
+    B[32:64] *= 20.0
+    a, b = rd_allocate_pair(A, B, 3.3)
+    Am = MTCMatrix.from_allocation(A, a.modes, a.scales, 16)
+    assert Am.total_bytes_allocated * 8 == a.payload_bits
+    # the arena holds the reference byte layout: decode it block by block
+    blocks = O.blocks_of(A, 16)
+    for i in range(Am.offsets.shape[0]):
+        for j in range(Am.offsets.shape[1]):
+            m = int(Am.precisions[i, j])
+            if m == 0:
+                continue
+            nb = m * 256 // 8
+            raw = Am.arena.raw_buffer[int(Am.offsets[i, j]): int(Am.offsets[i, j]) + nb][None]
+            q = O.arena_unpack(raw, m, 256).reshape(16, 16)
+            want = O.quantize_blocks(blocks[i, j][None], m, np.array([a.scales[i, j]], np.float32))[0]
+            assert np.array_equal(q, want)
+    # and its panel stream decodes to the allocator's dequant (fp32 scales)
+    ps = Am.panel_stream(64)
+    assert ps.fp32_scales
+    np.testing.assert_array_equal(decode_stream(ps), a.dequant)
