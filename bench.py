@@ -50,7 +50,85 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--graph", type=int, default=1, help="replay the timed calls from a HIP graph")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH_SIZE/WRITE_SIZE passes")
+    ap.add_argument("--pmc-child", help=argparse.SUPPRESS)
     return ap.parse_args()
+
+
+COPY_BYTES = 256 << 20
+
+
+def pmc_child(path):
+    """Body of one counter pass: a plain device copy of known size, then the decode kernel."""
+    import torch
+    from tensorpack_amd.device import DeviceStream
+    from tensorpack_amd.packer import PanelStream
+    ps = PanelStream.load(path)
+    with np.load(path.replace(".npz", "_x.npz")) as z:
+        x = z["x"]
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(4):
+        dst.copy_(src)
+    ds = DeviceStream(ps)
+    copies = [ds] + [ds.clone() for _ in range(7)]
+    X = torch.from_numpy(x).cuda()
+    Y = torch.empty((X.shape[0], ps.N), dtype=torch.float32, device="cuda")
+    for c in copies:
+        c.workspace(X.shape[0])
+    torch.cuda.synchronize()
+    for _ in range(4):
+        for c in copies:
+            c.gemv_f32(X, out=Y)
+    torch.cuda.synchronize()
+    print("pmc child done", flush=True)
+
+
+def traffic_passes(ps, x, kernel="k_gemv"):
+    """HBM bytes per decode launch from two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE).
+
+    Each counter is scaled by what it reads for a device copy of COPY_BYTES in the
+    same pass (bytes moved / counter bytes), so unit or per-instance conventions of
+    the counter cancel. Runs before this process touches the GPU; returns None
+    when rocprofv3 is unavailable or a pass fails."""
+    import shutil
+    import subprocess
+    import tempfile
+    from tensorpack_amd.profiling import dispatch_values
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        log("traffic: rocprofv3 not found")
+        return None
+    tmp = tempfile.mkdtemp(prefix="mtc_pmc_")
+    path = os.path.join(tmp, "stream.npz")
+    ps.save(path)
+    np.savez(os.path.join(tmp, "stream_x.npz"), x=x)
+    res = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        cmd = ["timeout", "-s", "KILL", "120", exe, "--pmc", counter, "-d", tmp, "-o", counter, "--",
+               sys.executable, os.path.abspath(__file__), "--pmc-child", path]
+        log("traffic pass: " + " ".join(cmd[3:]))
+        r = subprocess.run(cmd, capture_output=True, text=True, env=dict(os.environ, TMPDIR="/tmp"))
+        db = os.path.join(tmp, counter + "_results.db")
+        if r.returncode != 0 or not os.path.exists(db):
+            log(f"traffic pass {counter} failed (rc {r.returncode}): {r.stderr[-400:]}")
+            return None
+        kern = dispatch_values(db, counter, kernel)
+        # the four COPY_BYTES device copies are the largest copy dispatches of the pass
+        # (host-to-device staging copies share the kernel name but are small)
+        copy = sorted(dispatch_values(db, counter, "copyBuffer"))[-4:]
+        if not kern or len(copy) < 4 or min(copy) <= 0:
+            log(f"traffic pass {counter}: kernel or copy dispatches missing")
+            return None
+        copy_kib = sum(copy) / len(copy)
+        res[counter] = {"kernel_kib": sum(kern) / len(kern), "copy_kib": copy_kib,
+                        "factor": COPY_BYTES / (copy_kib * 1024.0), "copy_spread": max(copy) / min(copy)}
+    fetch = res["FETCH_SIZE"]["kernel_kib"] * 1024.0 * res["FETCH_SIZE"]["factor"]
+    write = res["WRITE_SIZE"]["kernel_kib"] * 1024.0 * res["WRITE_SIZE"]["factor"]
+    shutil.rmtree(tmp, ignore_errors=True)
+    return {"bytes": fetch + write, "fetch_bytes": fetch, "write_bytes": write,
+            "fetch_factor": res["FETCH_SIZE"]["factor"], "write_factor": res["WRITE_SIZE"]["factor"]}
 
 
 def timed_calls(torch, launch_list, steps, warmup, use_graph):
@@ -102,6 +180,9 @@ def timed_calls(torch, launch_list, steps, warmup, use_graph):
 
 def main():
     args = parse()
+    if args.pmc_child:
+        pmc_child(args.pmc_child)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
@@ -111,8 +192,6 @@ def main():
     from tensorpack_amd.kernels.gemm import MTCMatrix, GEMM_CHUNK_ROWS
     from tensorpack_amd.device import require_gpu
 
-    dev = require_gpu()
-    torch.cuda.set_device(dev)
     res = {}
 
     # ---------------- c2 decode ----------------
@@ -121,6 +200,12 @@ def main():
     alloc = wl.allocate()
     log(f"c2 allocation {time.time() - t0:.1f}s, {alloc.bits_per_element:.4f} b/w")
     m = MTCMatrix.from_quadtree(alloc, wl.W)
+    traffic = None
+    if not args.no_traffic:
+        # counter passes run in child processes before this one initialises the GPU
+        traffic = traffic_passes(m.panel_stream(m.decode_chunk_rows(1)), wl.activations(1))
+    dev = require_gpu()
+    torch.cuda.set_device(dev)
     t0 = time.time()
     ds = m.device_stream()
     log(f"c2 packed in {time.time() - t0:.1f}s: chunk_rows={ds.host.chunk_rows} stream {ds.device_bytes()} B, "
@@ -224,8 +309,9 @@ def main():
                    "stream_bytes": per_copy, "rotating_copies": n_copies,
                    "chunk_rows": ds.host.chunk_rows, "graph_replay": bool(args.graph)},
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": gbs / HBM_PEAK_GBS, "traffic": None, "kernel": "k_gemv<1>",
-                     "stream_GBps": per_copy / (ms * 1e-3) / 1e9},
+                     "frac": gbs / HBM_PEAK_GBS, "traffic": None if traffic is None else traffic["bytes"],
+                     "kernel": "k_gemv<1>", "stream_GBps": per_copy / (ms * 1e-3) / 1e9,
+                     "traffic_detail": traffic},
         "cpu_baseline": cpu,
         "extra": res,
     }

@@ -253,16 +253,22 @@ class MTCMatrix:
             self._host[chunk_rows] = ps
         return ps
 
+    def decode_chunk_rows(self, M: int = 1) -> int:
+        """Rows per unit of the decode layout for M rows: gemv_chunk_rows, halved
+        until the largest unit's on-chip staging fits the LDS budget (host only)."""
+        chunk_rows = gemv_chunk_rows(self.shape[0], self.shape[1], M)
+        while chunk_rows > 32 and _decode_lds_need(self.panel_stream(chunk_rows), M) > DECODE_LDS_BYTES:
+            self._host.pop(chunk_rows, None)
+            chunk_rows = max(32, (chunk_rows // 2) // 32 * 32)
+        return chunk_rows
+
     def device_stream(self, chunk_rows: Optional[int] = None, device=None, M: int = 1):
         """Device copy of the stream cut into `chunk_rows`-row units (default: the
         decode layout for M rows, shrunk until one unit fits on chip)."""
         from ..device import DeviceStream, require_gpu
         dev = require_gpu(device)
         if chunk_rows is None:
-            chunk_rows = gemv_chunk_rows(self.shape[0], self.shape[1], M)
-            while chunk_rows > 32 and _decode_lds_need(self.panel_stream(chunk_rows), M) > DECODE_LDS_BYTES:
-                self._host.pop(chunk_rows, None)
-                chunk_rows = max(32, (chunk_rows // 2) // 32 * 32)
+            chunk_rows = self.decode_chunk_rows(M)
         key = (str(dev), int(chunk_rows))
         ds = self._dev.get(key)
         if ds is None:

@@ -35,6 +35,7 @@ LEAF_PAD = 1 << 13
 ROW_BITS = 10                          # leaf word: row/4 in bits 0-9
 MAX_CHUNK_ROWS = 4 << ROW_BITS         # 4096
 UNIT_HDR_WORDS = 32
+STREAM_FORMAT = 3                      # panel stream layout version (matches the C-ABI version)
 _LOG2 = {32: 5, 16: 4, 8: 3, 4: 2}
 
 CodeSource = Callable[[int, int, np.ndarray, np.ndarray, np.ndarray], np.ndarray]
@@ -85,6 +86,29 @@ class PanelStream:
             if a is not None:
                 n += a.nbytes
         return int(n)
+
+    # ---- on-disk form: one .npz of plain arrays (no pickled objects) ----
+    _ARRAYS = ("payload", "buckets", "unit_hdr", "leaf_word", "leaf_scale", "row_perm", "col_perm")
+
+    def save(self, path) -> None:
+        arrays = {k: getattr(self, k) for k in self._ARRAYS if getattr(self, k) is not None}
+        meta = np.array([STREAM_FORMAT, self.K, self.N, self.chunk_rows, self.n_real_leaves,
+                         self.max_unit_words, self.max_unit_words4], dtype=np.int64)
+        np.savez(path, meta=meta, stats_keys=np.array(sorted(self.stats), dtype=str),
+                 stats_vals=np.array([self.stats[k] for k in sorted(self.stats)], dtype=np.float64), **arrays)
+
+    @classmethod
+    def load(cls, path) -> "PanelStream":
+        with np.load(path, allow_pickle=False) as z:
+            meta = [int(x) for x in z["meta"]]
+            if meta[0] != STREAM_FORMAT:
+                raise ValueError(f"{path}: panel stream format {meta[0]}, this build reads {STREAM_FORMAT}")
+            get = lambda k: np.array(z[k]) if k in z.files else None
+            stats = dict(zip([str(k) for k in z["stats_keys"]], [float(v) for v in z["stats_vals"]]))
+            return cls(K=meta[1], N=meta[2], chunk_rows=meta[3], payload=get("payload"), buckets=get("buckets"),
+                       unit_hdr=get("unit_hdr"), leaf_word=get("leaf_word"), leaf_scale=get("leaf_scale"),
+                       row_perm=get("row_perm"), col_perm=get("col_perm"), n_real_leaves=meta[4],
+                       max_unit_words=meta[5], max_unit_words4=meta[6], stats=stats)
 
 
 def pack_codes(codes: np.ndarray, P: int) -> np.ndarray:
