@@ -189,7 +189,7 @@ def main():
         sys.exit(2)
     import torch
     from tensorpack_amd import workloads
-    from tensorpack_amd.kernels.gemm import MTCMatrix, GEMM_CHUNK_ROWS
+    from tensorpack_amd.kernels.gemm import MTCMatrix
     from tensorpack_amd.device import require_gpu
 
     res = {}
@@ -276,7 +276,7 @@ def main():
         log(f"c4 allocation {time.time() - t0:.1f}s, {a4.bits_per_element:.4f} b/w")
         m4 = MTCMatrix.from_quadtree(a4, wl4.W)
         t0 = time.time()
-        g4 = m4.device_stream(GEMM_CHUNK_ROWS)
+        g4 = m4.device_tiles()
         log(f"c4 packed in {time.time() - t0:.1f}s")
         M4 = 4096
         X4 = torch.from_numpy(wl4.activations(M4)).to(dev).to(torch.bfloat16)

@@ -12,7 +12,8 @@
  * Reference interfaces replaced (Sharexi/TensorPack, Python + numba, no FFI):
  *   mtc_gemv_f32   <- mtc/kernels/gemm.py:124-210 (mtc_gemm_core_kernel) as
  *                     driven by mtc_gemm, gemm.py:541-574, for decode shapes
- *   mtc_gemm_bf16  <- same kernel/entry point, prefill shapes (bf16 MFMA)
+ *   mtc_gemm_bf16  <- same kernel/entry point, prefill shapes (bf16 MFMA), over
+ *                     the tile stream (mtc_tile_desc)
  *   mtc_dequant    <- MTCMatrix.to_array, gemm.py:510-538, and
  *                     qt_dequant / permuted_qt_dequant, mtc/core/quadtree.py:157-171,
  *                     mtc/core/permutation.py:76-79
@@ -28,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MTC_ABI_VERSION 3
+#define MTC_ABI_VERSION 4
 
 enum {
   MTC_OK = 0,
@@ -121,10 +122,53 @@ size_t mtc_gemv_workspace_bytes(const mtc_stream_desc* d, int M);
 int mtc_gemv_f32(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y, int64_t ldy, int M,
                  void* workspace, size_t workspace_bytes, void* hip_stream);
 
-/* bf16 MFMA path (prefill): X is fp32 (rounded to bf16 on load) or bf16; Y is
- * fp32 or bf16; fp32 accumulation. Requires a stream with chunk_rows == 64. */
-int mtc_gemm_bf16(const mtc_stream_desc* d, const void* X, int x_dtype, int64_t ldx, void* Y, int y_dtype,
-                  int64_t ldy, int M, void* hip_stream);
+/*
+ * Tile stream (prefill). Wp (K x N) is cut into steps of 64 reduction rows x
+ * 256 output columns; step = col_tile * n_ksteps + kstep. A step holds 512
+ * cells of 8 rows x 4 columns (column group c = 0..63 of the tile, row block
+ * r = 0..7), each covered by one leaf of size >= 8 or by two 4x4 leaves (top
+ * rows 0-3, bottom rows 4-7), so a cell has a (code width, scale) pair per half.
+ * A cell is stored in the class of its wider half, as offset-binary codes
+ * u = q + 2^(w-1):
+ *   class 0 (P <= 4):  4 dwords; column j in dword j, byte k = u[row k] | u[row k+4] << 4
+ *   class 1 (P <= 8):  8 dwords; column j in dwords 2j (rows 0-3) and 2j+1 (rows 4-7), byte per row
+ *   class 2 (P = 16): 16 dwords; column j in dwords 4j+h: rows 2h (bits 0-15), 2h+1 (bits 16-31)
+ *   class 3 (P0):      no payload (zeros)
+ * cells[step*512 + i] (2 words, or 4 with MTC_FLAG_FP32_SCALES):
+ *   word 0 : payload offset within the step in dwords (bits 0-13) | class << 14 | (c*8 + r) << 16
+ *   word 1 : bf16 scale of the top half | bf16 scale of the bottom half << 16
+ *            (fp32 scales: word 1 top, word 2 bottom, word 3 unused)
+ * Within a step, cells are sorted by class, then position.
+ * step_off[step] : payload offset of the step in dwords (n_steps + 1 entries).
+ * The device stages bf16(q * s) per weight (q * s is exact in fp32).
+ */
+typedef struct mtc_tile_desc {
+  uint32_t abi_version;
+  uint32_t flags;          /* MTC_FLAG_FP32_SCALES: 4-word cells with fp32 scales */
+  int32_t K;
+  int32_t N;
+  int32_t n_ksteps;        /* ceil(K / 64) */
+  int32_t n_col_tiles;     /* ceil(N / 256) */
+  int64_t payload_dwords;
+  const uint32_t* cells;
+  const uint32_t* step_off;
+  const uint32_t* payload;
+  const int32_t* row_perm;
+  const int32_t* col_perm;
+} mtc_tile_desc;
+
+int mtc_check_tile_desc(const mtc_tile_desc* d);
+
+/* Bytes of prefill workspace for M rows of X of dtype x_dtype: M*K*2 when X
+ * must be staged as bf16 first (fp32 X, or a row permutation to gather), else 0. */
+size_t mtc_gemm_workspace_bytes(const mtc_tile_desc* d, int M, int x_dtype);
+
+/* bf16 MFMA path (prefill): Y (M x N, fp32 or bf16, leading dim ldy) =
+ * X (M x K, fp32 or bf16, leading dim ldx) * W_hat with bf16 operands and
+ * fp32 accumulation. bf16 X read in place must have 16-byte aligned rows
+ * (ldx % 8 == 0). Any M >= 1. */
+int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, int64_t ldx, void* Y, int y_dtype,
+                  int64_t ldy, int M, void* workspace, size_t workspace_bytes, void* hip_stream);
 
 #ifdef __cplusplus
 }

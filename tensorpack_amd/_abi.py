@@ -2,7 +2,7 @@
 
 import ctypes
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 MTC_OK = 0
 MTC_DTYPE_F32 = 0
@@ -15,7 +15,8 @@ ERROR_NAMES = {
 }
 
 EXPORTED = ("mtc_abi_version", "mtc_last_error", "mtc_check_desc", "mtc_dequant",
-            "mtc_gemv_workspace_bytes", "mtc_gemv_f32", "mtc_gemm_bf16")
+            "mtc_gemv_workspace_bytes", "mtc_gemv_f32", "mtc_check_tile_desc", "mtc_gemm_workspace_bytes",
+            "mtc_gemm_bf16")
 
 
 class MtcStreamDesc(ctypes.Structure):
@@ -45,6 +46,26 @@ class MtcStreamDesc(ctypes.Structure):
 DescP = ctypes.POINTER(MtcStreamDesc)
 
 
+class MtcTileDesc(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
+        ("K", ctypes.c_int32),
+        ("N", ctypes.c_int32),
+        ("n_ksteps", ctypes.c_int32),
+        ("n_col_tiles", ctypes.c_int32),
+        ("payload_dwords", ctypes.c_int64),
+        ("cells", ctypes.c_void_p),
+        ("step_off", ctypes.c_void_p),
+        ("payload", ctypes.c_void_p),
+        ("row_perm", ctypes.c_void_p),
+        ("col_perm", ctypes.c_void_p),
+    ]
+
+
+TileDescP = ctypes.POINTER(MtcTileDesc)
+
+
 def declare(lib: ctypes.CDLL) -> None:
     vp, i32, i64, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
     lib.mtc_abi_version.restype = i32
@@ -59,8 +80,12 @@ def declare(lib: ctypes.CDLL) -> None:
     lib.mtc_gemv_workspace_bytes.argtypes = [DescP, i32]
     lib.mtc_gemv_f32.restype = i32
     lib.mtc_gemv_f32.argtypes = [DescP, vp, i64, vp, i64, i32, vp, sz, vp]
+    lib.mtc_check_tile_desc.restype = i32
+    lib.mtc_check_tile_desc.argtypes = [TileDescP]
+    lib.mtc_gemm_workspace_bytes.restype = sz
+    lib.mtc_gemm_workspace_bytes.argtypes = [TileDescP, i32, i32]
     lib.mtc_gemm_bf16.restype = i32
-    lib.mtc_gemm_bf16.argtypes = [DescP, vp, i32, i64, vp, i32, i64, i32, vp]
+    lib.mtc_gemm_bf16.argtypes = [TileDescP, vp, i32, i64, vp, i32, i64, i32, vp, sz, vp]
 
 
 class MtcError(RuntimeError):

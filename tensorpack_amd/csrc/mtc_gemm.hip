@@ -1,0 +1,378 @@
+// gfx950 prefill kernel: Y = X * W_hat with W_hat decoded from the tile stream
+// into bf16 LDS tiles and multiplied on v_mfma_f32_32x32x16_bf16 (fp32 accumulate).
+//
+//   k_stage_x   : X -> bf16 Xp = X[:, row_perm] (only for fp32 X or a row permutation)
+//   k_gemm_tile : one 256 x 256 output tile per block, 8 waves (2 x 4) of 128 x 64,
+//                 K in steps of 64; A (bf16 X) and B (decoded weights) double-buffered
+//                 in LDS with an XOR swizzle of 16-byte segments; the next step's X
+//                 rows and cell payload are loaded into registers while the current
+//                 step's MFMAs run, then decoded/stored into the other buffer; one
+//                 barrier per step. Output columns go through col_perm.
+//
+// Reference behaviour: mtc/kernels/gemm.py:124-210 (block loop: skip P0 blocks,
+// unpack, scale, multiply-accumulate) with W_hat as in mtc/core/quadtree.py:157-171.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mtc_hip.h"
+#include "mtc_host.h"
+
+#define MTC_API extern "C" __attribute__((visibility("default")))
+
+using mtc::host::check_launch;
+using mtc::host::fail;
+using mtc::host::ok;
+
+namespace {
+
+constexpr int kTM = 256;                    // output rows per block
+constexpr int kTN = 256;                    // output columns per block (= one column tile)
+constexpr int kTK = 64;                     // reduction rows per step
+constexpr int kCells = 512;                 // cells per step
+constexpr int kThreads = 512;
+constexpr int kTileBytes = kTM * kTK * 2;   // one bf16 operand tile (A and B are the same size)
+constexpr int kLdsBytes = 4 * kTileBytes;   // A and B, two buffers each: 128 KiB
+constexpr int kRowGroup = 8;                // row tiles per launch-order group (L2 reuse of B)
+constexpr int kXcds = 8;
+constexpr int kStageThreads = 256;
+
+static_assert(kTN / 4 * (kTK / 8) == kCells, "one cell per (column group, row block)");
+static_assert(kThreads == kCells, "one cell per thread");
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// Byte offset of 16-byte segment `seg` (0..7) of row `row` in a [rows][64] bf16 tile.
+// The XOR spreads the 8 rows of a 128-byte bank line over all segments, so the
+// MFMA operand reads (32 rows, one segment) and the stores are conflict-free.
+__device__ __forceinline__ uint32_t swz(int row, int seg) {
+  return (uint32_t)(row * 128 + ((seg ^ (row & 7)) << 4));
+}
+
+// Hides a value's known bits so byte extraction compiles to v_cvt_f32_ubyteN.
+__device__ __forceinline__ uint32_t opaque(uint32_t x) {
+  asm("" : "+v"(x));
+  return x;
+}
+
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  bf16x2_t p = {(__bf16)a, (__bf16)b};  // v_cvt_pk_bf16_f32, round to nearest even
+  return __builtin_bit_cast(uint32_t, p);
+}
+
+// Rows 0-3 from the bytes of `top` (scale st, offset term ct), rows 4-7 from `bot`.
+__device__ __forceinline__ u32x4_t dec_bytes(uint32_t top, uint32_t bot, float st, float ct, float sb, float cb) {
+  u32x4_t r;
+  r.x = pk_bf16(__builtin_fmaf((float)(top & 0xFFu), st, ct), __builtin_fmaf((float)((top >> 8) & 0xFFu), st, ct));
+  r.y = pk_bf16(__builtin_fmaf((float)((top >> 16) & 0xFFu), st, ct), __builtin_fmaf((float)(top >> 24), st, ct));
+  r.z = pk_bf16(__builtin_fmaf((float)(bot & 0xFFu), sb, cb), __builtin_fmaf((float)((bot >> 8) & 0xFFu), sb, cb));
+  r.w = pk_bf16(__builtin_fmaf((float)((bot >> 16) & 0xFFu), sb, cb), __builtin_fmaf((float)(bot >> 24), sb, cb));
+  return r;
+}
+
+__device__ __forceinline__ uint32_t dec_shorts(uint32_t v, float s, float c) {
+  return pk_bf16(__builtin_fmaf((float)(v & 0xFFFFu), s, c), __builtin_fmaf((float)(v >> 16), s, c));
+}
+
+// The 4 columns (8 rows each, bf16) of one cell from its payload words.
+// value = (u - offset) * s evaluated as fma(u, s, -offset * s): exact in fp32.
+__device__ __forceinline__ void decode_cell(uint32_t cls, const u32x4_t* pw, float st, float sb, u32x4_t* out) {
+  if (cls == 0) {
+    const float ct = -8.0f * st, cb = -8.0f * sb;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t x = pw[0][j];
+      out[j] = dec_bytes(opaque(x & 0x0F0F0F0Fu), opaque((x >> 4) & 0x0F0F0F0Fu), st, ct, sb, cb);
+    }
+  } else if (cls == 1) {
+    const float ct = -128.0f * st, cb = -128.0f * sb;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out[j] = dec_bytes(pw[j >> 1][(2 * j) & 3], pw[j >> 1][(2 * j + 1) & 3], st, ct, sb, cb);
+  } else if (cls == 2) {
+    const float ct = -32768.0f * st, cb = -32768.0f * sb;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      out[j].x = dec_shorts(pw[j].x, st, ct);
+      out[j].y = dec_shorts(pw[j].y, st, ct);
+      out[j].z = dec_shorts(pw[j].z, sb, cb);
+      out[j].w = dec_shorts(pw[j].w, sb, cb);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out[j] = u32x4_t{0u, 0u, 0u, 0u};
+  }
+}
+
+template <bool kFS, int kYDT>
+__global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, const __bf16* __restrict__ X,
+                                                        int64_t ldx, void* __restrict__ Y, int64_t ldy, int M,
+                                                        int n_row_tiles, int tiles_per_xcd) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  constexpr int CW = kFS ? 4 : 2;
+
+  // Tile order: each XCD takes a contiguous range of tile ids; ids run over groups of
+  // kRowGroup row tiles, row tile fastest, so the blocks in flight on one XCD share
+  // column tiles (B) and row tiles (A) in its L2.
+  const int tile = (int)(blockIdx.x % kXcds) * tiles_per_xcd + (int)(blockIdx.x / kXcds);
+  const int n_ct = d.n_col_tiles;
+  if (tile >= n_row_tiles * n_ct) return;
+  const int per_group = kRowGroup * n_ct;
+  const int grp = tile / per_group, in_grp = tile - grp * per_group;
+  const int first = grp * kRowGroup;
+  const int rows_in = min(n_row_tiles - first, kRowGroup);
+  const int rt = first + in_grp % rows_in, ct = in_grp / rows_in;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+  const int m0 = rt * kTM, n0 = ct * kTN;
+  const int nks = d.n_ksteps;
+  const uint32_t* cells = d.cells + ((size_t)ct * nks * kCells + tid) * CW;
+  const uint32_t* step_off = d.step_off + (size_t)ct * nks;
+
+  // A staging: thread covers 16-byte segment a_seg of rows a_r + 64 i. Rows past M and
+  // segments past K load from the first row / first element and are replaced by zeros.
+  const int a_seg = tid & 7, a_r = tid >> 3;
+  const __bf16* xrow[4];
+  bool xok[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + a_r + 64 * i;
+    xok[i] = m < M;
+    xrow[i] = X + (int64_t)(xok[i] ? m : 0) * ldx;
+  }
+  u32x4_t areg[4];
+  u32x4_t pw[4];
+  auto load_a = [&](int ks) {
+    const int k = ks * kTK + a_seg * 8;
+    const bool kok = k < d.K;                 // K % 8 == 0: a segment is wholly in or out
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(xrow[i] + (kok ? k : 0));
+      areg[i] = (kok && xok[i]) ? v : u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_a = [&](unsigned char* as) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4_t*>(as + swz(a_r + 64 * i, a_seg)) = areg[i];
+  };
+  auto load_payload = [&](uint32_t w0, uint32_t base) {
+    const uint32_t cls = (w0 >> 14) & 3u;
+    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(d.payload + base + (w0 & 0x3FFFu));
+    if (cls == 0) {
+      pw[0] = src[0];
+    } else if (cls == 1) {
+      pw[0] = src[0];
+      pw[1] = src[1];
+    } else if (cls == 2) {
+      pw[0] = src[0];
+      pw[1] = src[1];
+      pw[2] = src[2];
+      pw[3] = src[3];
+    }
+  };
+  auto decode_store = [&](unsigned char* bs, uint32_t w0, uint32_t w1, uint32_t w2) {
+    float st, sb;
+    if (kFS) {
+      st = __uint_as_float(w1);
+      sb = __uint_as_float(w2);
+    } else {
+      st = __uint_as_float(w1 << 16);
+      sb = __uint_as_float(w1 & 0xFFFF0000u);
+    }
+    const uint32_t pos = w0 >> 16;
+    const int col = (int)(pos >> 3) * 4, seg = (int)(pos & 7u);
+    u32x4_t o[4];
+    decode_cell((w0 >> 14) & 3u, pw, st, sb, o);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4_t*>(bs + swz(col + j, seg)) = o[j];
+  };
+
+  f32x16_t acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16_t{};
+
+  // prologue: step 0 into buffer 0, descriptor of step 1 in registers
+  {
+    const uint32_t w0 = cells[0], w1 = cells[1], w2 = kFS ? cells[2] : 0u;
+    load_a(0);
+    load_payload(w0, step_off[0]);
+    store_a(lds);
+    decode_store(lds + 2 * kTileBytes, w0, w1, w2);
+  }
+  uint32_t c0 = 0, c1 = 0, c2 = 0, cbase = 0;
+  if (nks > 1) {
+    const uint32_t* cp = cells + (size_t)kCells * CW;
+    c0 = cp[0];
+    c1 = cp[1];
+    if (kFS) c2 = cp[2];
+    cbase = step_off[1];
+  }
+  __syncthreads();
+
+  for (int ks = 0; ks < nks; ++ks) {
+    const int buf = ks & 1;
+    const bool more = ks + 1 < nks;
+    if (more) {
+      load_a(ks + 1);
+      load_payload(c0, cbase);
+    }
+    uint32_t f0 = 0, f1 = 0, f2 = 0, fbase = 0;
+    if (ks + 2 < nks) {
+      const uint32_t* cp = cells + (size_t)(ks + 2) * kCells * CW;
+      f0 = cp[0];
+      f1 = cp[1];
+      if (kFS) f2 = cp[2];
+      fbase = step_off[ks + 2];
+    }
+
+    const unsigned char* as = lds + buf * kTileBytes;
+    const unsigned char* bs = lds + (2 + buf) * kTileBytes;
+#pragma unroll
+    for (int kk = 0; kk < kTK / 16; ++kk) {
+      const int seg = kk * 2 + (lane >> 5);
+      bf16x8_t a[4], b[2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        a[i] = *reinterpret_cast<const bf16x8_t*>(as + swz(wm * 128 + i * 32 + (lane & 31), seg));
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        b[j] = *reinterpret_cast<const bf16x8_t*>(bs + swz(wn * 64 + j * 32 + (lane & 31), seg));
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+
+    if (more) {
+      store_a(lds + (buf ^ 1) * kTileBytes);
+      decode_store(lds + (2 + (buf ^ 1)) * kTileBytes, c0, c1, c2);
+    }
+    c0 = f0;
+    c1 = f1;
+    c2 = f2;
+    cbase = fbase;
+    __syncthreads();
+  }
+
+  // epilogue: C element e of lane l is row (e/4)*8 + (l/32)*4 + e%4, column l%32
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+    const bool cok = col < d.N;
+    const int ycol = d.col_perm ? d.col_perm[cok ? col : 0] : col;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = m0 + wm * 128 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+        if (cok && row < M) {
+          if (kYDT == MTC_DTYPE_F32)
+            reinterpret_cast<float*>(Y)[(int64_t)row * ldy + ycol] = acc[i][j][e];
+          else
+            reinterpret_cast<__bf16*>(Y)[(int64_t)row * ldy + ycol] = (__bf16)acc[i][j][e];
+        }
+      }
+    }
+  }
+}
+
+// Xp[m, k] = bf16(X[m, row_perm[k]]) (identity without a permutation); 8 outputs per thread.
+__global__ __launch_bounds__(kStageThreads) void k_stage_x(const void* __restrict__ X, int xdt, int64_t ldx,
+                                                           const int32_t* __restrict__ row_perm,
+                                                           __bf16* __restrict__ Xp, int K) {
+  const int64_t m = blockIdx.y;
+  const int k0 = ((int)blockIdx.x * kStageThreads + (int)threadIdx.x) * 8;
+  if (k0 >= K) return;
+  float v[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int src = row_perm ? row_perm[k0 + t] : k0 + t;
+    v[t] = xdt == MTC_DTYPE_F32 ? reinterpret_cast<const float*>(X)[m * ldx + src]
+                                : (float)reinterpret_cast<const __bf16*>(X)[m * ldx + src];
+  }
+  u32x4_t o{pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3]), pk_bf16(v[4], v[5]), pk_bf16(v[6], v[7])};
+  *reinterpret_cast<u32x4_t*>(Xp + m * K + k0) = o;
+}
+
+int check_tile_desc(const mtc_tile_desc* d) {
+  if (!d) return fail(MTC_E_NULL, "tile descriptor is NULL");
+  if (d->abi_version != MTC_ABI_VERSION)
+    return fail(MTC_E_VERSION, "descriptor ABI %u, library ABI %d", d->abi_version, MTC_ABI_VERSION);
+  if (d->K <= 0 || d->N <= 0 || d->N % 32 || d->K % 8)
+    return fail(MTC_E_DESC, "bad shape K=%d N=%d (N must be a multiple of 32, K of 8)", d->K, d->N);
+  if (d->n_ksteps != (d->K + kTK - 1) / kTK || d->n_col_tiles != (d->N + kTN - 1) / kTN)
+    return fail(MTC_E_DESC, "n_ksteps=%d n_col_tiles=%d inconsistent with K=%d N=%d", d->n_ksteps, d->n_col_tiles,
+                d->K, d->N);
+  if (d->flags & ~MTC_FLAG_FP32_SCALES) return fail(MTC_E_DESC, "unknown flags 0x%x", d->flags);
+  if (!d->cells || !d->step_off || !d->payload) return fail(MTC_E_NULL, "tile stream arrays missing");
+  if (d->payload_dwords < 4) return fail(MTC_E_DESC, "payload_dwords=%lld", (long long)d->payload_dwords);
+  return ok();
+}
+
+bool needs_staging(const mtc_tile_desc* d, int x_dtype) { return d->row_perm || x_dtype == MTC_DTYPE_F32; }
+
+template <bool kFS, int kYDT>
+int launch_tile(const mtc_tile_desc* d, const __bf16* X, int64_t ldx, void* Y, int64_t ldy, int M, hipStream_t st) {
+  const void* fn = reinterpret_cast<const void*>(&k_gemm_tile<kFS, kYDT>);
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+  if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+  const int n_row_tiles = (M + kTM - 1) / kTM;
+  const int64_t n_tiles = (int64_t)n_row_tiles * d->n_col_tiles;
+  if (n_tiles > (int64_t)1 << 30) return fail(MTC_E_SHAPE, "M=%d gives too many tiles", M);
+  const int tiles_per_xcd = (int)((n_tiles + kXcds - 1) / kXcds);
+  hipLaunchKernelGGL((k_gemm_tile<kFS, kYDT>), dim3(tiles_per_xcd * kXcds), dim3(kThreads), kLdsBytes, st, *d, X,
+                     ldx, Y, ldy, M, n_row_tiles, tiles_per_xcd);
+  return check_launch("k_gemm_tile");
+}
+
+}  // namespace
+
+MTC_API int mtc_check_tile_desc(const mtc_tile_desc* d) { return check_tile_desc(d); }
+
+MTC_API size_t mtc_gemm_workspace_bytes(const mtc_tile_desc* d, int M, int x_dtype) {
+  if (check_tile_desc(d) || M <= 0) return 0;
+  return needs_staging(d, x_dtype) ? (size_t)M * d->K * 2 : 0;
+}
+
+MTC_API int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, int64_t ldx, void* Y, int y_dtype,
+                          int64_t ldy, int M, void* workspace, size_t workspace_bytes, void* hip_stream) {
+  int rc = check_tile_desc(d);
+  if (rc) return rc;
+  if (!X || !Y) return fail(MTC_E_NULL, "X or Y is NULL");
+  if (x_dtype != MTC_DTYPE_F32 && x_dtype != MTC_DTYPE_BF16) return fail(MTC_E_DTYPE, "x_dtype=%d", x_dtype);
+  if (y_dtype != MTC_DTYPE_F32 && y_dtype != MTC_DTYPE_BF16) return fail(MTC_E_DTYPE, "y_dtype=%d", y_dtype);
+  if (M <= 0) return fail(MTC_E_SHAPE, "M=%d must be positive", M);
+  if (ldx < d->K || ldy < d->N) return fail(MTC_E_SHAPE, "ldx=%lld < K or ldy=%lld < N", (long long)ldx, (long long)ldy);
+  hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);
+  const __bf16* xb = reinterpret_cast<const __bf16*>(X);
+  int64_t ldb = ldx;
+  if (needs_staging(d, x_dtype)) {
+    const size_t need = (size_t)M * d->K * 2;
+    if (!workspace || workspace_bytes < need)
+      return fail(MTC_E_WORKSPACE, "prefill workspace of %zu bytes needed, %zu given", need,
+                  workspace ? workspace_bytes : 0);
+    if (reinterpret_cast<uintptr_t>(workspace) & 15) return fail(MTC_E_WORKSPACE, "workspace not 16-byte aligned");
+    dim3 grid((d->K / 8 + kStageThreads - 1) / kStageThreads, M);
+    hipLaunchKernelGGL(k_stage_x, grid, dim3(kStageThreads), 0, st, X, x_dtype, ldx, d->row_perm,
+                       reinterpret_cast<__bf16*>(workspace), d->K);
+    rc = check_launch("k_stage_x");
+    if (rc) return rc;
+    xb = reinterpret_cast<const __bf16*>(workspace);
+    ldb = d->K;
+  } else if (ldx % 8 || (reinterpret_cast<uintptr_t>(X) & 15)) {
+    return fail(MTC_E_SHAPE, "bf16 X read in place needs 16-byte aligned rows (ldx=%lld)", (long long)ldx);
+  }
+  const bool fs = d->flags & MTC_FLAG_FP32_SCALES;
+  if (fs) {
+    return y_dtype == MTC_DTYPE_F32 ? launch_tile<true, MTC_DTYPE_F32>(d, xb, ldb, Y, ldy, M, st)
+                                    : launch_tile<true, MTC_DTYPE_BF16>(d, xb, ldb, Y, ldy, M, st);
+  }
+  return y_dtype == MTC_DTYPE_F32 ? launch_tile<false, MTC_DTYPE_F32>(d, xb, ldb, Y, ldy, M, st)
+                                  : launch_tile<false, MTC_DTYPE_BF16>(d, xb, ldb, Y, ldy, M, st);
+}

@@ -1,4 +1,5 @@
-// gfx950 kernels and C-ABI for Y = X * W_hat over the panel stream.
+// gfx950 decode kernels and C-ABI for Y = X * W_hat over the panel stream,
+// plus the host error state shared with mtc_gemm.hip.
 //
 //   k_fill_zero  : zero an fp32 buffer (used before dequant; no memset nodes)
 //   k_dequant    : stream -> dense W_hat (bit-exact q*s, +0.0 for P0)
@@ -6,8 +7,7 @@
 //                  the unit's payload is staged in LDS, each wave owns one
 //                  column group and accumulates its 4 columns in registers
 //                  (no atomics), then reduces across lanes once.
-//   k_gemm_bf16  : prefill path, leaves dequantized to bf16 tiles in LDS,
-//                  v_mfma_f32_32x32x16_bf16 with fp32 accumulation
+//   (the prefill path, k_gemm_tile over the tile stream, is in mtc_gemm.hip)
 //
 // Reference behaviour: mtc/kernels/gemm.py:124-210 (block loop: skip P0
 // blocks, unpack codes, scale, fp32 multiply-accumulate) for a dense X and a
@@ -21,37 +21,17 @@
 
 #include "mtc_hip.h"
 #include "mtc_decode.h"
+#include "mtc_host.h"
 
 using namespace mtc;
+using mtc::host::check_launch;
+using mtc::host::fail;
+using mtc::host::ok;
 
-typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
-typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
 
 #define MTC_API extern "C" __attribute__((visibility("default")))
 
 namespace {
-
-thread_local char g_err[512] = "";
-
-int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
-int fail(int code, const char* fmt, ...) {
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(g_err, sizeof(g_err), fmt, ap);
-  va_end(ap);
-  return code;
-}
-
-int ok() {
-  g_err[0] = '\0';
-  return MTC_OK;
-}
-
-int check_launch(const char* what) {
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(MTC_E_LAUNCH, "%s: %s", what, hipGetErrorString(e));
-  return ok();
-}
 
 // Bucket entry fields.
 struct Bucket {
@@ -415,184 +395,6 @@ __global__ __launch_bounds__(64 * kGemvWavesPerGroup * gemv_groups(MT)) void k_g
 }
 
 // ---------------------------------------------------------------------------
-// bf16 MFMA GEMM (prefill)
-// ---------------------------------------------------------------------------
-constexpr int kGBM = 128;              // rows of X per block
-constexpr int kGBN = 128;              // output columns per block (4 panels)
-constexpr int kGBK = 64;               // reduction rows per step (= stream chunk_rows)
-constexpr int kGLds = kGBK + 8;        // bf16 elements per LDS row (padded)
-
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
-}
-
-// R consecutive-k bf16 values q[0..R) * scale written at LDS row position dst.
-template <int R>
-__device__ __forceinline__ void store_bf16_run(uint16_t* dst, const float* q, float scale) {
-  if constexpr (R == 8) {
-    uint4 v;
-    v.x = pack_bf16x2(q[0] * scale, q[1] * scale);
-    v.y = pack_bf16x2(q[2] * scale, q[3] * scale);
-    v.z = pack_bf16x2(q[4] * scale, q[5] * scale);
-    v.w = pack_bf16x2(q[6] * scale, q[7] * scale);
-    *reinterpret_cast<uint4*>(dst) = v;
-  } else {
-    uint2 v;
-    v.x = pack_bf16x2(q[0] * scale, q[1] * scale);
-    v.y = pack_bf16x2(q[2] * scale, q[3] * scale);
-    *reinterpret_cast<uint2*>(dst) = v;
-  }
-}
-
-// One chunk into the bf16 weight tile: bs points at column 0 of the chunk's column group.
-template <int S, int P>
-__device__ __forceinline__ void gemm_chunk(const uint32_t* src, const uint32_t* lw, uint32_t t, const float* fscale,
-                                           uint32_t lg0, uint16_t* bs) {
-  uint32_t w[P];
-  load_chunk<P, false>(src, w);
-  float q[32];
-  decode_chunk<P>(w, q);
-  if constexpr (S == 4) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t leaf = 2 * t + h;
-      const LeafInfo li = leaf_info(lw[leaf], fscale, lg0 + leaf);
-      if (li.pad) continue;
-#pragma unroll
-      for (int c = 0; c < kGroup; ++c) store_bf16_run<4>(bs + c * kGLds + li.row, q + 16 * h + 4 * c, li.scale);
-    }
-  } else {
-    constexpr int NRB = S / 8;
-    const uint32_t leaf = t / NRB;
-    const LeafInfo li = leaf_info(lw[leaf], fscale, lg0 + leaf);
-    const int row = li.row + 8 * (int)(t % NRB);
-#pragma unroll
-    for (int c = 0; c < kGroup; ++c) store_bf16_run<8>(bs + c * kGLds + row, q + 8 * c, li.scale);
-  }
-}
-
-__device__ __forceinline__ uint16_t load_x_bf16(const void* X, int xdt, int64_t idx) {
-  if (xdt == MTC_DTYPE_BF16) return reinterpret_cast<const uint16_t*>(X)[idx];
-  return (uint16_t)f32_to_bf16_bits(reinterpret_cast<const float*>(X)[idx]);
-}
-
-__global__ __launch_bounds__(256) void k_gemm_bf16(const mtc_stream_desc d, const void* __restrict__ X, int xdt, int64_t ldx,
-                                                  void* __restrict__ Y, int ydt, int64_t ldy, int M, int x_vec) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[kGBM * kGLds];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[kGBN * kGLds];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int p0 = blockIdx.x * (kGBN / kPanel);
-  const int m0 = blockIdx.y * kGBM;
-  const int wm = wave >> 1, wn = wave & 1;
-  f32x16_t acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-
-  for (int chunk = 0; chunk < d.n_chunks; ++chunk) {
-    const int kb = chunk * kGBK;
-    const int rows = min(kGBK, d.K - kb);
-    __syncthreads();
-    // zero the weight tile (P0 leaves leave zeros behind)
-    for (int i = tid; i < kGBN * kGLds / 8; i += 256) reinterpret_cast<uint4*>(Bs)[i] = make_uint4(0, 0, 0, 0);
-    // activation tile: 128 rows x 64 k, 8 k per item
-    for (int it = tid; it < kGBM * (kGBK / 8); it += 256) {
-      const int r = it >> 3, k8 = (it & 7) * 8;
-      const int m = m0 + r;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (m < M) {
-        if (x_vec && k8 + 8 <= rows) {
-          v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(X) + (int64_t)m * ldx + kb + k8);
-        } else {
-          uint16_t e[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            e[j] = 0;
-            if (k8 + j < rows) {
-              int k = kb + k8 + j;
-              if (d.row_perm) k = d.row_perm[k];
-              e[j] = load_x_bf16(X, xdt, (int64_t)m * ldx + k);
-            }
-          }
-          v.x = e[0] | ((uint32_t)e[1] << 16);
-          v.y = e[2] | ((uint32_t)e[3] << 16);
-          v.z = e[4] | ((uint32_t)e[5] << 16);
-          v.w = e[6] | ((uint32_t)e[7] << 16);
-        }
-      }
-      *reinterpret_cast<uint4*>(As + r * kGLds + k8) = v;
-    }
-    __syncthreads();
-    // weight tile: 4 panels x 8 column groups; wave w decodes column groups w and w+4 of every panel
-    for (int pi = 0; pi < kGBN / kPanel; ++pi) {
-      const int p = p0 + pi;
-      if (p >= d.n_panels) break;
-      const int u = p * d.n_chunks + chunk;
-      const int32_t* hdr = d.unit_hdr + kUnitHdr * u;
-      for (int g = wave; g < kGroups; g += 4) {
-        uint16_t* bs = Bs + (pi * kPanel + g * kGroup) * kGLds;
-        const uint32_t* bk = d.buckets + 4 * (hdr[4] + hdr[8 + g]);
-        const int nb = hdr[9 + g] - hdr[8 + g];
-        for (int b = 0; b < nb; ++b) {
-          const Bucket e = read_bucket(bk + 4 * b);
-          const uint32_t* src = d.payload + hdr[0] + e.pay;
-          const uint32_t* lw = d.leaf_word + hdr[2] + e.leaf;
-          for (uint32_t t = lane; t < e.n; t += 64) {
-            switch (e.key) {
-#define MTC_CASE(S, P) \
-  case MTC_BUCKET_KEY(S, P): gemm_chunk<S, P>(src + t * P, lw, t, d.leaf_scale, hdr[2] + e.leaf, bs); break;
-              MTC_FOR_EACH_BUCKET(MTC_CASE)
-#undef MTC_CASE
-              default: break;
-            }
-          }
-        }
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int ks = 0; ks < kGBK / 16; ++ks) {
-      bf16x8_t a[2], b[2];
-      const int koff = ks * 16 + (lane >> 5) * 8;
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        a[i] = *reinterpret_cast<const bf16x8_t*>(As + (wm * 64 + i * 32 + (lane & 31)) * kGLds + koff);
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        b[j] = *reinterpret_cast<const bf16x8_t*>(Bs + (wn * 64 + j * 32 + (lane & 31)) * kGLds + koff);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-    }
-  }
-
-  // epilogue: accumulator element e of lane l is row (e/4)*8 + (l/32)*4 + e%4, column l%32
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = p0 * kPanel + wn * 64 + j * 32 + (lane & 31);
-      if (n >= d.N) continue;
-      const int col = d.col_perm ? d.col_perm[n] : n;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int m = m0 + wm * 64 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-        if (m < M) {
-          if (ydt == MTC_DTYPE_BF16)
-            reinterpret_cast<uint16_t*>(Y)[(int64_t)m * ldy + col] = (uint16_t)f32_to_bf16_bits(acc[i][j][e]);
-          else
-            reinterpret_cast<float*>(Y)[(int64_t)m * ldy + col] = acc[i][j][e];
-        }
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
 // host helpers
 // ---------------------------------------------------------------------------
 int check_desc(const mtc_stream_desc* d) {
@@ -620,12 +422,7 @@ int check_desc(const mtc_stream_desc* d) {
 
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-size_t device_lds_limit() {
-  int dev = 0, v = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 64 * 1024;
-  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0) return 64 * 1024;
-  return (size_t)v;
-}
+using mtc::host::device_lds_limit;
 
 int gemv_mt(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : 4; }
 
@@ -674,7 +471,7 @@ int launch_gemv(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y,
 
 MTC_API int mtc_abi_version(void) { return MTC_ABI_VERSION; }
 
-MTC_API const char* mtc_last_error(void) { return g_err; }
+MTC_API const char* mtc_last_error(void) { return mtc::host::last_error(); }
 
 MTC_API int mtc_check_desc(const mtc_stream_desc* d) { return check_desc(d); }
 
@@ -716,20 +513,43 @@ MTC_API int mtc_gemv_f32(const mtc_stream_desc* d, const float* X, int64_t ldx, 
   }
 }
 
-MTC_API int mtc_gemm_bf16(const mtc_stream_desc* d, const void* X, int x_dtype, int64_t ldx, void* Y, int y_dtype,
-                          int64_t ldy, int M, void* hip_stream) {
-  int rc = check_desc(d);
-  if (rc) return rc;
-  if (!X || !Y) return fail(MTC_E_NULL, "X or Y is NULL");
-  if (d->chunk_rows != kGBK) return fail(MTC_E_SHAPE, "bf16 GEMM needs a stream with chunk_rows=%d (got %d)", kGBK, d->chunk_rows);
-  if (x_dtype != MTC_DTYPE_F32 && x_dtype != MTC_DTYPE_BF16) return fail(MTC_E_DTYPE, "x_dtype=%d", x_dtype);
-  if (y_dtype != MTC_DTYPE_F32 && y_dtype != MTC_DTYPE_BF16) return fail(MTC_E_DTYPE, "y_dtype=%d", y_dtype);
-  if (M <= 0) return fail(MTC_E_SHAPE, "M=%d must be positive", M);
-  if (ldx < d->K || ldy < d->N) return fail(MTC_E_SHAPE, "ldx=%lld < K or ldy=%lld < N", (long long)ldx, (long long)ldy);
-  // 16-byte activation loads: bf16, unpermuted, row starts aligned
-  const int x_vec = (x_dtype == MTC_DTYPE_BF16 && !d->row_perm && ldx % 8 == 0 &&
-                     (reinterpret_cast<uintptr_t>(X) & 15) == 0) ? 1 : 0;
-  dim3 grid((d->n_panels * kPanel + kGBN - 1) / kGBN, (M + kGBM - 1) / kGBM);
-  hipLaunchKernelGGL(k_gemm_bf16, grid, dim3(256), 0, as_stream(hip_stream), *d, X, x_dtype, ldx, Y, y_dtype, ldy, M, x_vec);
-  return check_launch("k_gemm_bf16");
+// ---------------------------------------------------------------------------
+// shared host state (declared in mtc_host.h)
+// ---------------------------------------------------------------------------
+namespace mtc {
+namespace host {
+
+namespace {
+thread_local char g_err[512] = "";
 }
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return MTC_OK;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(MTC_E_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+const char* last_error() { return g_err; }
+
+size_t device_lds_limit() {
+  int dev = 0, v = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 64 * 1024;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0) return 64 * 1024;
+  return (size_t)v;
+}
+
+}  // namespace host
+}  // namespace mtc

@@ -12,6 +12,7 @@ import numpy as np
 
 from . import _abi, _native
 from .packer import PanelStream
+from .tilestream import TileStream
 
 
 def _torch():
@@ -142,6 +143,56 @@ class DeviceStream:
         _abi.check(self.lib, "mtc_gemv_f32", rc)
         return out
 
+
+class DeviceTiles:
+    """A TileStream (prefill layout) uploaded to one GPU, plus its ctypes descriptor."""
+
+    def __init__(self, ts: TileStream, device=None):
+        torch = _torch()
+        self.device = require_gpu(device)
+        self.host = ts
+        self.lib = _native.hip_lib()
+
+        def up(a: Optional[np.ndarray]):
+            if a is None:
+                return None
+            return torch.from_numpy(np.ascontiguousarray(a).reshape(-1).view(np.int32)).to(self.device)
+
+        self.cells, self.step_off, self.payload = up(ts.cells), up(ts.step_off), up(ts.payload)
+        self.row_perm, self.col_perm = up(ts.row_perm), up(ts.col_perm)
+        d = _abi.MtcTileDesc()
+        d.abi_version = _abi.ABI_VERSION
+        d.flags = _abi.MTC_FLAG_FP32_SCALES if ts.fp32_scales else 0
+        d.K, d.N, d.n_ksteps, d.n_col_tiles = ts.K, ts.N, ts.n_ksteps, ts.n_col_tiles
+        d.payload_dwords = int(ts.payload.size)
+        ptr = lambda t: None if t is None else t.data_ptr()
+        d.cells, d.step_off, d.payload = ptr(self.cells), ptr(self.step_off), ptr(self.payload)
+        d.row_perm, d.col_perm = ptr(self.row_perm), ptr(self.col_perm)
+        self.desc = d
+        _abi.check(self.lib, "mtc_check_tile_desc", self.lib.mtc_check_tile_desc(ctypes.byref(d)))
+        self._ws = None
+
+    @property
+    def K(self) -> int:
+        return self.host.K
+
+    @property
+    def N(self) -> int:
+        return self.host.N
+
+    def device_bytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (self.cells, self.step_off, self.payload, self.row_perm,
+                                                           self.col_perm) if t is not None)
+
+    def workspace(self, M: int, x_dtype: int):
+        need = int(self.lib.mtc_gemm_workspace_bytes(ctypes.byref(self.desc), int(M), int(x_dtype)))
+        if need == 0:
+            return None, 0
+        if self._ws is None or self._ws.numel() < need:
+            torch = _torch()
+            self._ws = torch.empty(need, dtype=torch.uint8, device=self.device)
+        return self._ws, need
+
     def gemm_bf16(self, X, out=None, out_dtype=None):
         torch = _torch()
         assert X.dim() == 2 and X.stride(1) == 1 and X.dtype in (torch.float32, torch.bfloat16)
@@ -152,7 +203,9 @@ class DeviceStream:
         assert out.dtype in (torch.float32, torch.bfloat16) and out.stride(1) == 1
         xdt = _abi.MTC_DTYPE_BF16 if X.dtype == torch.bfloat16 else _abi.MTC_DTYPE_F32
         ydt = _abi.MTC_DTYPE_BF16 if out.dtype == torch.bfloat16 else _abi.MTC_DTYPE_F32
+        ws, nbytes = self.workspace(M, xdt)
         rc = self.lib.mtc_gemm_bf16(ctypes.byref(self.desc), X.data_ptr(), xdt, X.stride(0), out.data_ptr(), ydt,
-                                    out.stride(0), M, current_stream_handle(self.device))
+                                    out.stride(0), M, None if ws is None else ws.data_ptr(), nbytes,
+                                    current_stream_handle(self.device))
         _abi.check(self.lib, "mtc_gemm_bf16", rc)
         return out

@@ -28,8 +28,8 @@ from ..core.arena import MemoryArena
 from ..core.permutation import PermutedQTAllocation
 from ..core.quadtree import QTAllocation
 from ..packer import PanelStream, pack_levels, weight_codes
+from ..tilestream import TileStream, pack_tiles
 
-GEMM_CHUNK_ROWS = 64          # K step of the bf16 MFMA kernel
 DECODE_MAX_M = 16             # M at or below this takes the fp32 decode kernel under compute="auto"
 DECODE_X_LDS_BYTES = 64 * 1024   # on-chip budget for the gathered X rows of one decode block
 DECODE_LDS_BYTES = 160 * 1024    # per-block LDS of gfx950
@@ -119,7 +119,7 @@ class MTCMatrix:
         self.pointer_tensor = pointer_tensor
         self.allocation = None
         self._levels: Optional[_Levels] = None
-        self._host: Dict[int, PanelStream] = {}
+        self._host: Dict[object, object] = {}
         self._dev: Dict[Tuple[str, int], object] = {}
 
     # ---- constructors ------------------------------------------------------------------
@@ -276,6 +276,27 @@ class MTCMatrix:
             self._dev[key] = ds
         return ds
 
+    def tile_stream(self) -> TileStream:
+        """Host image of the prefill (bf16 MFMA) layout."""
+        ts = self._host.get("tiles")
+        if ts is None:
+            lv = self._levels if self._levels is not None else self._uniform_levels()
+            ts = pack_tiles(lv.shape, lv.sizes, lv.leaf, lv.modes, lv.scales, lv.codes_of, lv.scale_format,
+                            lv.row_perm, lv.col_perm)
+            self._host["tiles"] = ts
+        return ts
+
+    def device_tiles(self, device=None):
+        """Device copy of the prefill layout."""
+        from ..device import DeviceTiles, require_gpu
+        dev = require_gpu(device)
+        key = (str(dev), "tiles")
+        dt = self._dev.get(key)
+        if dt is None:
+            dt = DeviceTiles(self.tile_stream(), dev)
+            self._dev[key] = dt
+        return dt
+
     def release_host_streams(self) -> None:
         """Drop host copies of packed streams (device copies stay)."""
         self._host.clear()
@@ -348,7 +369,7 @@ def mtc_gemm(A, B: MTCMatrix, *, compute: str = "auto", out_dtype=None):
         Xb = X if X.dtype in (torch.float32, torch.bfloat16) else X.float()
         if Xb.stride(1) != 1:
             Xb = Xb.contiguous()
-        Y = B.device_stream(GEMM_CHUNK_ROWS, dev).gemm_bf16(Xb, out_dtype=out_dtype)
+        Y = B.device_tiles(dev).gemm_bf16(Xb, out_dtype=out_dtype)
     else:
         raise ValueError(f"compute must be 'auto', 'fp32' or 'bf16', got {compute!r}")
     if squeeze:

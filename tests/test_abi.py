@@ -97,12 +97,52 @@ def test_entry_points_reject_bad_arguments_before_any_gpu_call(hip):
     assert need > 0                                             # two chunks -> split-K workspace
     assert hip.mtc_gemv_f32(ref, 0x10, 256, 0x10, 64, 1, None, 0, None) == -5
     assert hip.mtc_gemv_f32(ref, 0x10, 256, 0x10, 64, 1, 0x20, need - 1, None) == -5
-    assert hip.mtc_gemm_bf16(ref, 0x10, 0, 256, 0x10, 0, 64, 4, None) == -3      # chunk_rows != 64
-    g = _desc(chunk_rows=64, n_chunks=4)
-    assert hip.mtc_gemm_bf16(ctypes.byref(g), 0x10, 5, 256, 0x10, 0, 64, 4, None) == -4
-    assert hip.mtc_gemm_bf16(ctypes.byref(g), 0x10, 0, 256, 0x10, 9, 64, 4, None) == -4
-    assert hip.mtc_gemm_bf16(ctypes.byref(g), None, 0, 256, 0x10, 0, 64, 4, None) == -1
     assert hip.mtc_dequant(ref, None, None) == -1
+    t = ctypes.byref(_tdesc())
+    assert hip.mtc_gemm_bf16(t, 0x10, 5, 256, 0x10, 0, 300, 4, None, 0, None) == -4
+    assert hip.mtc_gemm_bf16(t, 0x10, 1, 256, 0x10, 9, 300, 4, None, 0, None) == -4
+    assert hip.mtc_gemm_bf16(t, None, 1, 256, 0x10, 0, 300, 4, None, 0, None) == -1
+    assert hip.mtc_gemm_bf16(t, 0x10, 1, 100, 0x10, 0, 300, 4, None, 0, None) == -3
+    assert hip.mtc_gemm_bf16(t, 0x10, 1, 256, 0x10, 0, 300, 0, None, 0, None) == -3
+    assert hip.mtc_gemm_bf16(t, 0x10, 1, 260, 0x10, 0, 300, 4, None, 0, None) == -3      # unaligned bf16 rows
+    need = hip.mtc_gemm_workspace_bytes(t, 4, 0)
+    assert need == 4 * 256 * 2 and hip.mtc_gemm_workspace_bytes(t, 4, 1) == 0
+    assert hip.mtc_gemm_bf16(t, 0x10, 0, 256, 0x10, 0, 300, 4, 0x20, need - 1, None) == -5
+    tp = ctypes.byref(_tdesc(row_perm=0x3000))
+    assert hip.mtc_gemm_workspace_bytes(tp, 4, 1) == 4 * 256 * 2
+
+
+def _tdesc(**kw):
+    d = _abi.MtcTileDesc()
+    d.abi_version = _abi.ABI_VERSION
+    d.K, d.N, d.n_ksteps, d.n_col_tiles = 256, 288, 4, 2
+    d.payload_dwords = 64
+    d.cells = d.step_off = d.payload = 0x1000
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+def test_tile_descriptor_layout_and_validation(hip):
+    fields = [f[0] for f in _abi.MtcTileDesc._fields_]
+    src = "#include <stddef.h>\n#include <stdio.h>\n#include \"mtc_hip.h\"\nint main(void){\n"
+    src += 'printf("%zu\\n", sizeof(mtc_tile_desc));\n'
+    for f in fields:
+        src += f'printf("%zu\\n", offsetof(mtc_tile_desc, {f}));\n'
+    src += "return 0;}\n"
+    with tempfile.TemporaryDirectory() as d:
+        c, exe = os.path.join(d, "t.c"), os.path.join(d, "t")
+        open(c, "w").write(src)
+        subprocess.run(["gcc", "-I", INCLUDE, c, "-o", exe], check=True)
+        out = [int(x) for x in subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split()]
+    assert out[0] == ctypes.sizeof(_abi.MtcTileDesc)
+    assert out[1:] == [getattr(_abi.MtcTileDesc, f).offset for f in fields]
+    assert hip.mtc_check_tile_desc(ctypes.byref(_tdesc())) == 0
+    cases = {"abi_version": (3, -7), "N": (100, -2), "K": (252, -2), "n_ksteps": (3, -2), "n_col_tiles": (1, -2),
+             "flags": (4, -2), "cells": (None, -1), "payload": (None, -1), "step_off": (None, -1)}
+    for field, (val, code) in cases.items():
+        assert hip.mtc_check_tile_desc(ctypes.byref(_tdesc(**{field: val}))) == code, field
+    assert hip.mtc_check_tile_desc(None) == -1
 
 
 def test_rd_search_rejects_bad_block_size():

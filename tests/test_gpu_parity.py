@@ -123,6 +123,61 @@ def test_gemm_bf16(gpu, allocs, name, M, xdtype):
     assert err <= TOL_BF16, (name, M, err)
 
 
+@pytest.mark.parametrize("name", [c[0] for c in CASES])
+def test_gemm_stages_bf16_w_hat_exactly(gpu, allocs, name):
+    """X = I makes the MFMA path return its staged weight tile: it must equal
+    bf16(W_hat) bit for bit (a single product per output, exact in fp32)."""
+    import torch
+    W, a, m = allocs[name]
+    _say("gemm identity", name)
+    K = W.shape[0]
+    I = torch.eye(K, device=gpu, dtype=torch.bfloat16)
+    Y = mtc_gemm(I, m, compute="bf16").cpu().numpy()
+    want = O.bf16_round(_oracle_what(a, W)) + np.float32(0.0)
+    assert np.array_equal(_bits(Y), _bits(want)), name
+    # fp32 X (staged to bf16 on the device) gives the same
+    Y32 = mtc_gemm(I.float(), m, compute="bf16").cpu().numpy()
+    assert np.array_equal(_bits(Y32), _bits(want)), name
+
+
+@pytest.mark.parametrize("M", [255, 257, 600])
+def test_gemm_bf16_row_tiles(gpu, allocs, M):
+    import torch
+    W, a, m = allocs["outlier-qtp-4.25"]
+    _say("gemm row tiles", M)
+    X = np.random.RandomState(M).randn(M, W.shape[0]).astype(np.float32)
+    Y = mtc_gemm(torch.from_numpy(X).to(gpu).to(torch.bfloat16), m, compute="bf16").cpu().numpy()
+    err = O.relative_frobenius_error(O.qt_gemm_f64(O.bf16_round(X), _oracle_what(a, W)), Y)
+    assert err <= TOL_BF16, (M, err)
+
+
+def test_gemm_partial_k_step_and_strided_x(gpu):
+    """K = 96 (a 64-row step and a half step), N = 64, X a strided view."""
+    import torch
+    W = outlier_matrix(21, 96, 64)
+    a = QuadtreeRD(W, None, (32, 16, 8, 4)).select(5.0)
+    m = MTCMatrix.from_quadtree(a, W)
+    big = torch.randn(70, 104, device=gpu, dtype=torch.bfloat16)
+    X = big[:, :96]                                               # ldx = 104
+    Y = mtc_gemm(X, m, compute="bf16").cpu().numpy()
+    ref = O.qt_gemm_f64(X.float().cpu().numpy(), _oracle_what(a, W))
+    assert O.relative_frobenius_error(ref, Y) <= TOL_BF16
+
+
+def test_gemm_uniform_form_fp32_scales(gpu):
+    import torch
+    rng = np.random.RandomState(8)
+    W = rng.randn(256, 128).astype(np.float32)
+    al = rd_allocate(W, 4.0, None, 32)
+    m = MTCMatrix.from_allocation(W, al.modes, al.scales, 32)
+    X = rng.randn(300, 256).astype(np.float32)
+    Y = mtc_gemm(torch.from_numpy(X).to(gpu), m, compute="bf16").cpu().numpy()
+    assert O.relative_frobenius_error(O.qt_gemm_f64(O.bf16_round(X), al.dequant), Y) <= TOL_BF16
+    I = torch.eye(256, device=gpu, dtype=torch.bfloat16)
+    Yi = mtc_gemm(I, m, compute="bf16").cpu().numpy()
+    assert np.array_equal(_bits(Yi), _bits(O.bf16_round(al.dequant) + np.float32(0.0)))
+
+
 def test_gemm_bf16_output(gpu, allocs):
     import torch
     W, a, m = allocs["outlier-qt-2.5"]
@@ -207,8 +262,12 @@ def test_errors_are_clean(gpu, allocs):
     assert lib.mtc_gemv_f32(ctypes.byref(bad), X.data_ptr(), W.shape[0], Y.data_ptr(), W.shape[1], 1, None, 0,
                             None) == -7
     assert b"ABI" in lib.mtc_last_error()
-    g = m.device_stream(64)
-    assert lib.mtc_gemm_bf16(ctypes.byref(ds.desc), X.data_ptr(), 0, W.shape[0], Y.data_ptr(), 0, W.shape[1], 1,
-                             None) in (0, -3)
+    g = m.device_tiles()
     assert lib.mtc_gemm_bf16(ctypes.byref(g.desc), X.data_ptr(), 7, W.shape[0], Y.data_ptr(), 0, W.shape[1], 1,
-                             None) == -4
+                             None, 0, None) == -4
+    # fp32 X needs the bf16 staging workspace
+    assert lib.mtc_gemm_bf16(ctypes.byref(g.desc), X.data_ptr(), 0, W.shape[0], Y.data_ptr(), 0, W.shape[1], 1,
+                             None, 0, None) == -5
+    Xb = torch.zeros(1, W.shape[0] + 1, device=gpu, dtype=torch.bfloat16)
+    assert lib.mtc_gemm_bf16(ctypes.byref(g.desc), Xb.data_ptr(), 1, W.shape[0] + 1, Y.data_ptr(), 0, W.shape[1],
+                             1, None, 0, None) == -3                                  # rows not 16-byte aligned
