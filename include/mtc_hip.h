@@ -139,7 +139,9 @@ int mtc_gemv_f32(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y
  *   word 1 : bf16 scale of the top half | bf16 scale of the bottom half << 16
  *            (fp32 scales: word 1 top, word 2 bottom, word 3 unused)
  * Within a step, cells are sorted by class, then position.
- * step_off[step] : payload offset of the step in dwords (n_steps + 1 entries).
+ * step_off[step] : payload offset of the step in dwords (n_steps + 1 entries); the
+ *   payload array extends at least 8 dwords past step_off[n_steps] (the kernel reads
+ *   32 bytes per cell whatever its class).
  * The device stages bf16(q * s) per weight (q * s is exact in fp32).
  */
 typedef struct mtc_tile_desc {

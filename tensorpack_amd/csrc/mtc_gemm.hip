@@ -2,12 +2,14 @@
 // into bf16 LDS tiles and multiplied on v_mfma_f32_32x32x16_bf16 (fp32 accumulate).
 //
 //   k_stage_x   : X -> bf16 Xp = X[:, row_perm] (only for fp32 X or a row permutation)
-//   k_gemm_tile : one 256 x 256 output tile per block, 8 waves (2 x 4) of 128 x 64,
-//                 K in steps of 64; A (bf16 X) and B (decoded weights) double-buffered
-//                 in LDS with an XOR swizzle of 16-byte segments; the next step's X
-//                 rows and cell payload are loaded into registers while the current
-//                 step's MFMAs run, then decoded/stored into the other buffer; one
-//                 barrier per step. Output columns go through col_perm.
+//   k_gemm_tile : one 256 x 256 output tile per block, K in steps of 64. Warp-specialized:
+//                 8 consumer waves (2 x 4 of 128 x 64 outputs) only read the staged bf16
+//                 tiles and issue MFMAs; 4 producer waves (one per SIMD) stage step k+1
+//                 from registers (X rows and two decoded cells per thread) into the other
+//                 LDS buffer and then load step k+2's X rows and cell payload. A (bf16 X)
+//                 and B (decoded weights) are double-buffered with an XOR swizzle of
+//                 16-byte segments; one barrier per step. Output columns go through
+//                 col_perm.
 //
 // Reference behaviour: mtc/kernels/gemm.py:124-210 (block loop: skip P0 blocks,
 // unpack, scale, multiply-accumulate) with W_hat as in mtc/core/quadtree.py:157-171.
@@ -30,7 +32,11 @@ constexpr int kTM = 256;                    // output rows per block
 constexpr int kTN = 256;                    // output columns per block (= one column tile)
 constexpr int kTK = 64;                     // reduction rows per step
 constexpr int kCells = 512;                 // cells per step
-constexpr int kThreads = 512;
+constexpr int kConsumerWaves = 8;           // 2 x 4 waves of 128 x 64 outputs
+constexpr int kProducerWaves = 4;           // one per SIMD: loads, decode, LDS stores
+constexpr int kThreads = 64 * (kConsumerWaves + kProducerWaves);
+constexpr int kProducers = 64 * kProducerWaves;
+constexpr int kSegsPerProducer = kTM * (kTK / 8) / kProducers;   // 16-byte X segments per producer
 constexpr int kTileBytes = kTM * kTK * 2;   // one bf16 operand tile (A and B are the same size)
 constexpr int kLdsBytes = 4 * kTileBytes;   // A and B, two buffers each: 128 KiB
 constexpr int kRowGroup = 8;                // row tiles per launch-order group (L2 reuse of B)
@@ -38,7 +44,7 @@ constexpr int kXcds = 8;
 constexpr int kStageThreads = 256;
 
 static_assert(kTN / 4 * (kTK / 8) == kCells, "one cell per (column group, row block)");
-static_assert(kThreads == kCells, "one cell per thread");
+static_assert(2 * kProducers == kCells, "two cells per producer thread");
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
@@ -46,10 +52,13 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // Byte offset of 16-byte segment `seg` (0..7) of row `row` in a [rows][64] bf16 tile.
-// The XOR spreads the 8 rows of a 128-byte bank line over all segments, so the
-// MFMA operand reads (32 rows, one segment) and the stores are conflict-free.
+// LDS has 64 banks of 4 bytes: a row's 128 bytes fill one half of the banks (by row
+// parity), and a 16-lane group of a 128-bit access is conflict-free when its 16
+// (row parity, segment) pairs are distinct. The MFMA operand reads take 16 rows at
+// one segment, so the segment is XORed with (row & 7) ^ ((row >> 3) & 1): rows r and
+// r + 8 share parity and get different segments.
 __device__ __forceinline__ uint32_t swz(int row, int seg) {
-  return (uint32_t)(row * 128 + ((seg ^ (row & 7)) << 4));
+  return (uint32_t)(row * 128 + ((seg ^ (row & 7) ^ ((row >> 3) & 1)) << 4));
 }
 
 // Hides a value's known bits so byte extraction compiles to v_cvt_f32_ubyteN.
@@ -126,159 +135,181 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, c
   const int rt = first + in_grp % rows_in, ct = in_grp / rows_in;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 2, wn = wave & 3;
   const int m0 = rt * kTM, n0 = ct * kTN;
   const int nks = d.n_ksteps;
-  const uint32_t* cells = d.cells + ((size_t)ct * nks * kCells + tid) * CW;
-  const uint32_t* step_off = d.step_off + (size_t)ct * nks;
 
-  // A staging: thread covers 16-byte segment a_seg of rows a_r + 64 i. Rows past M and
-  // segments past K load from the first row / first element and are replaced by zeros.
-  const int a_seg = tid & 7, a_r = tid >> 3;
-  const __bf16* xrow[4];
-  bool xok[4];
+  if (wave < kConsumerWaves) {
+    // ---------------- consumers: bf16 MFMA over the staged tiles ----------------
+    const int wm = wave >> 2, wn = wave & 3;
+    f32x16_t acc[4][2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = m0 + a_r + 64 * i;
-    xok[i] = m < M;
-    xrow[i] = X + (int64_t)(xok[i] ? m : 0) * ldx;
-  }
-  u32x4_t areg[4];
-  u32x4_t pw[4];
-  auto load_a = [&](int ks) {
-    const int k = ks * kTK + a_seg * 8;
-    const bool kok = k < d.K;                 // K % 8 == 0: a segment is wholly in or out
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(xrow[i] + (kok ? k : 0));
-      areg[i] = (kok && xok[i]) ? v : u32x4_t{0u, 0u, 0u, 0u};
-    }
-  };
-  auto store_a = [&](unsigned char* as) {
+      for (int j = 0; j < 2; ++j) acc[i][j] = f32x16_t{};
+    __syncthreads();                                       // step 0 staged
+    for (int ks = 0; ks < nks; ++ks) {
+      const unsigned char* as = lds + (ks & 1) * kTileBytes;
+      const unsigned char* bs = lds + (2 + (ks & 1)) * kTileBytes;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4_t*>(as + swz(a_r + 64 * i, a_seg)) = areg[i];
-  };
-  auto load_payload = [&](uint32_t w0, uint32_t base) {
-    const uint32_t cls = (w0 >> 14) & 3u;
-    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(d.payload + base + (w0 & 0x3FFFu));
-    if (cls == 0) {
-      pw[0] = src[0];
-    } else if (cls == 1) {
-      pw[0] = src[0];
-      pw[1] = src[1];
-    } else if (cls == 2) {
-      pw[0] = src[0];
-      pw[1] = src[1];
-      pw[2] = src[2];
-      pw[3] = src[3];
-    }
-  };
-  auto decode_store = [&](unsigned char* bs, uint32_t w0, uint32_t w1, uint32_t w2) {
-    float st, sb;
-    if (kFS) {
-      st = __uint_as_float(w1);
-      sb = __uint_as_float(w2);
-    } else {
-      st = __uint_as_float(w1 << 16);
-      sb = __uint_as_float(w1 & 0xFFFF0000u);
-    }
-    const uint32_t pos = w0 >> 16;
-    const int col = (int)(pos >> 3) * 4, seg = (int)(pos & 7u);
-    u32x4_t o[4];
-    decode_cell((w0 >> 14) & 3u, pw, st, sb, o);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4_t*>(bs + swz(col + j, seg)) = o[j];
-  };
-
-  f32x16_t acc[4][2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16_t{};
-
-  // prologue: step 0 into buffer 0, descriptor of step 1 in registers
-  {
-    const uint32_t w0 = cells[0], w1 = cells[1], w2 = kFS ? cells[2] : 0u;
-    load_a(0);
-    load_payload(w0, step_off[0]);
-    store_a(lds);
-    decode_store(lds + 2 * kTileBytes, w0, w1, w2);
-  }
-  uint32_t c0 = 0, c1 = 0, c2 = 0, cbase = 0;
-  if (nks > 1) {
-    const uint32_t* cp = cells + (size_t)kCells * CW;
-    c0 = cp[0];
-    c1 = cp[1];
-    if (kFS) c2 = cp[2];
-    cbase = step_off[1];
-  }
-  __syncthreads();
-
-  for (int ks = 0; ks < nks; ++ks) {
-    const int buf = ks & 1;
-    const bool more = ks + 1 < nks;
-    if (more) {
-      load_a(ks + 1);
-      load_payload(c0, cbase);
-    }
-    uint32_t f0 = 0, f1 = 0, f2 = 0, fbase = 0;
-    if (ks + 2 < nks) {
-      const uint32_t* cp = cells + (size_t)(ks + 2) * kCells * CW;
-      f0 = cp[0];
-      f1 = cp[1];
-      if (kFS) f2 = cp[2];
-      fbase = step_off[ks + 2];
-    }
-
-    const unsigned char* as = lds + buf * kTileBytes;
-    const unsigned char* bs = lds + (2 + buf) * kTileBytes;
-#pragma unroll
-    for (int kk = 0; kk < kTK / 16; ++kk) {
-      const int seg = kk * 2 + (lane >> 5);
-      bf16x8_t a[4], b[2];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        a[i] = *reinterpret_cast<const bf16x8_t*>(as + swz(wm * 128 + i * 32 + (lane & 31), seg));
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        b[j] = *reinterpret_cast<const bf16x8_t*>(bs + swz(wn * 64 + j * 32 + (lane & 31), seg));
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int kk = 0; kk < kTK / 16; ++kk) {
+        const int seg = kk * 2 + (lane >> 5);
+        bf16x8_t a[4], b[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+          b[j] = *reinterpret_cast<const bf16x8_t*>(bs + swz(wn * 64 + j * 32 + (lane & 31), seg));
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          a[i] = *reinterpret_cast<const bf16x8_t*>(as + swz(wm * 128 + i * 32 + (lane & 31), seg));
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+      }
+      __syncthreads();                                     // buffer ks free, step ks+1 staged
     }
 
-    if (more) {
-      store_a(lds + (buf ^ 1) * kTileBytes);
-      decode_store(lds + (2 + (buf ^ 1)) * kTileBytes, c0, c1, c2);
-    }
-    c0 = f0;
-    c1 = f1;
-    c2 = f2;
-    cbase = fbase;
-    __syncthreads();
-  }
-
-  // epilogue: C element e of lane l is row (e/4)*8 + (l/32)*4 + e%4, column l%32
+    // epilogue: C element e of lane l is row (e/4)*8 + (l/32)*4 + e%4, column l%32
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int col = n0 + wn * 64 + j * 32 + (lane & 31);
-    const bool cok = col < d.N;
-    const int ycol = d.col_perm ? d.col_perm[cok ? col : 0] : col;
+    for (int j = 0; j < 2; ++j) {
+      const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+      const bool cok = col < d.N;
+      const int ycol = d.col_perm ? d.col_perm[cok ? col : 0] : col;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < 4; ++i) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int row = m0 + wm * 128 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-        if (cok && row < M) {
-          if (kYDT == MTC_DTYPE_F32)
-            reinterpret_cast<float*>(Y)[(int64_t)row * ldy + ycol] = acc[i][j][e];
-          else
-            reinterpret_cast<__bf16*>(Y)[(int64_t)row * ldy + ycol] = (__bf16)acc[i][j][e];
+        for (int e = 0; e < 16; ++e) {
+          const int row = m0 + wm * 128 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+          if (cok && row < M) {
+            if (kYDT == MTC_DTYPE_F32)
+              reinterpret_cast<float*>(Y)[(int64_t)row * ldy + ycol] = acc[i][j][e];
+            else
+              reinterpret_cast<__bf16*>(Y)[(int64_t)row * ldy + ycol] = (__bf16)acc[i][j][e];
+          }
         }
       }
     }
+    return;
+  }
+
+  // ---------------- producers: load X and cells, decode, stage the next step ----------------
+  const int p = tid - 64 * kConsumerWaves;                 // 0 .. kProducers-1
+  const uint32_t* cells = d.cells + ((size_t)ct * nks * kCells + p) * CW;
+  const uint32_t* step_off = d.step_off + (size_t)ct * nks;
+  const bool full_m = m0 + kTM <= M;
+
+  // X: 16-byte segment a_seg of rows a_r + 32 i. Rows past M and segments past K load
+  // from row 0 / element 0 and are replaced by zeros.
+  const int a_seg = p & 7, a_r = p >> 3;
+  u32x4_t areg[kSegsPerProducer];
+  auto load_a = [&](int ks) {
+    const int k = ks * kTK + a_seg * 8;
+    if (full_m && (ks + 1) * kTK <= d.K) {
+#pragma unroll
+      for (int i = 0; i < kSegsPerProducer; ++i)
+        areg[i] = *reinterpret_cast<const u32x4_t*>(X + (int64_t)(m0 + a_r + 32 * i) * ldx + k);
+    } else {
+      const bool kok = k < d.K;                            // K % 8 == 0: a segment is wholly in or out
+#pragma unroll
+      for (int i = 0; i < kSegsPerProducer; ++i) {
+        const int m = m0 + a_r + 32 * i;
+        const bool ok = kok && m < M;
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(X + (int64_t)(ok ? m : 0) * ldx + (ok ? k : 0));
+        areg[i] = ok ? v : u32x4_t{0u, 0u, 0u, 0u};
+      }
+    }
+  };
+
+  // cells p and p + kProducers of a step: descriptor words of the step being staged
+  // (c0, c1) and of the step after it (n0w, n1w); payload words of the staged step.
+  uint32_t c0[CW], c1[CW], n0w[CW], n1w[CW];
+  uint32_t cur_base = 0, nxt_base = 0;
+  u32x4_t q0[4], q1[4];
+  auto load_desc = [&](int ks, uint32_t (&w0)[CW], uint32_t (&w1)[CW], uint32_t& base) {
+    const uint32_t* cp = cells + (size_t)ks * kCells * CW;
+#pragma unroll
+    for (int t = 0; t < CW; ++t) {
+      w0[t] = cp[t];
+      w1[t] = cp[(size_t)kProducers * CW + t];
+    }
+    base = step_off[ks];
+  };
+  auto load_cell = [&](const uint32_t (&w)[CW], u32x4_t (&q)[4]) {
+    const uint32_t cls = (w[0] >> 14) & 3u;
+    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(d.payload + cur_base + (w[0] & 0x3FFFu));
+    if (cls == 0) {
+      q[0] = src[0];
+    } else if (cls == 1) {
+      q[0] = src[0];
+      q[1] = src[1];
+    } else if (cls == 2) {
+      q[0] = src[0];
+      q[1] = src[1];
+      q[2] = src[2];
+      q[3] = src[3];
+    }
+  };
+  auto load_payload = [&]() {
+    load_cell(c0, q0);
+    load_cell(c1, q1);
+  };
+  auto stage_cell = [&](unsigned char* bs, const uint32_t (&w)[CW], const u32x4_t (&q)[4]) {
+    float st, sb;
+    if (kFS) {
+      st = __uint_as_float(w[1]);
+      sb = __uint_as_float(w[2]);
+    } else {
+      st = __uint_as_float(w[1] << 16);
+      sb = __uint_as_float(w[1] & 0xFFFF0000u);
+    }
+    const uint32_t pos = w[0] >> 16;
+    const int col = (int)(pos >> 3) * 4, seg = (int)(pos & 7u);
+    u32x4_t o[4];
+    decode_cell((w[0] >> 14) & 3u, q, st, sb, o);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4_t*>(bs + swz(col + j, seg)) = o[j];
+  };
+  auto fill = [&](int buf) {
+    unsigned char* as = lds + buf * kTileBytes;
+    unsigned char* bs = lds + (2 + buf) * kTileBytes;
+#pragma unroll
+    for (int i = 0; i < kSegsPerProducer; ++i) *reinterpret_cast<u32x4_t*>(as + swz(a_r + 32 * i, a_seg)) = areg[i];
+    stage_cell(bs, c0, q0);
+    stage_cell(bs, c1, q1);
+  };
+  auto advance = [&]() {
+#pragma unroll
+    for (int t = 0; t < CW; ++t) {
+      c0[t] = n0w[t];
+      c1[t] = n1w[t];
+    }
+    cur_base = nxt_base;
+  };
+
+  // prologue: stage step 0, hold step 1 in registers, descriptor of step 2
+  load_desc(0, c0, c1, cur_base);
+  if (nks > 1) load_desc(1, n0w, n1w, nxt_base);
+  load_a(0);
+  load_payload();
+  fill(0);
+  if (nks > 1) {
+    advance();
+    load_a(1);
+    load_payload();
+    if (nks > 2) load_desc(2, n0w, n1w, nxt_base);
+  }
+  __syncthreads();
+  for (int ks = 0; ks < nks; ++ks) {
+    if (ks + 1 < nks) {
+      fill((ks + 1) & 1);                                  // step ks+1 from registers
+      if (ks + 2 < nks) {
+        advance();
+        load_a(ks + 2);
+        load_payload();
+        if (ks + 3 < nks) load_desc(ks + 3, n0w, n1w, nxt_base);
+      }
+    }
+    __syncthreads();
   }
 }
 

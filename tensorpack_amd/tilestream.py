@@ -41,6 +41,7 @@ CLS_W4, CLS_W8, CLS_W16, CLS_Z = 0, 1, 2, 3
 CLS_DWORDS = np.array([4, 8, 16, 0], dtype=np.int64)
 CLS_OFFSET = (8, 128, 32768)
 TILE_FORMAT = 1
+PAYLOAD_PAD = 8                     # dwords after the last step (see pack_tiles)
 _WIDTHS = (2, 3, 4, 5, 6, 8, 16)
 
 
@@ -155,7 +156,8 @@ def pack_tiles(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np.
     step_off = np.concatenate([[0], np.cumsum(step_tot)]).astype(np.int64)
     if step_off[-1] >= 2 ** 32:
         raise ValueError("tile stream payload too large for 32-bit step offsets")
-    payload = np.zeros(max(int(step_off[-1]), 4), dtype=np.uint32)
+    # 8 dwords of tail padding: the device reads 32 bytes per cell whatever its class
+    payload = np.zeros(int(step_off[-1]) + PAYLOAD_PAD, dtype=np.uint32)
 
     # codes of each cell: (n, 4 columns, 8 rows)
     if Q.shape != (R * 8, G * 4):
