@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MTC_ABI_VERSION 4
+#define MTC_ABI_VERSION 5
 
 enum {
   MTC_OK = 0,
@@ -63,6 +63,8 @@ enum { MTC_DTYPE_F32 = 0, MTC_DTYPE_BF16 = 1 };
  *  unit_hdr[32*u + 8..16]  : bucket offset of cg 0..8, relative to the unit's first bucket
  *  unit_hdr[32*u + 17..25] : payload offset of cg 0..8 in dwords, relative to the unit's payload
  *  unit_hdr[32*u + 26]     : as word 7 for blocks of four column groups
+ *  unit_hdr[32*u + 27..28] : first step record and record count of column groups 0-3
+ *  unit_hdr[32*u + 29..30] : the same for column groups 4-7
  *  buckets[4*b + 0] : payload offset of the bucket in dwords, relative to the unit (multiple of 4)
  *  buckets[4*b + 1] : first leaf word of the bucket, relative to the unit
  *  buckets[4*b + 2] : lane chunks in the bucket (bits 0-15) | first chunk within its cg (bits 16-31)
@@ -70,6 +72,17 @@ enum { MTC_DTYPE_F32 = 0, MTC_DTYPE_BF16 = 1 };
  *  leaf_word[l]     : bits 0-9 row offset in the unit / 4, bit 13 pad leaf (ignored),
  *                     bits 16-31 bf16 scale
  *  leaf_scale[l]    : fp32 scale (only with MTC_FLAG_FP32_SCALES)
+ *  steps[16*r + ..] : decode step record: one per (unit, block of 4 column groups, bucket
+ *                     kind, 16-chunk step j), ordered by unit, block, kind, j:
+ *                     word 0 = kind key (bits 0-15) | j << 16; words 1-4 = payload offset
+ *                     (unit-relative dwords) of the kind's bucket in each of the 4 column
+ *                     groups; words 5-8 = its first leaf word (unit-relative); words 9-12 =
+ *                     chunks of that bucket in this step, min(max(n - 16j, 0), 16) (0: the
+ *                     group has no bucket of the kind; its offsets then name another
+ *                     existing bucket); words 13-15 = 0
+ *
+ * The payload array extends at least 4 dwords past the last bucket (the kernels read
+ * chunks with 16-byte loads that may run up to 3 dwords past a chunk's end).
  *
  * A lane chunk is 32 codes in P dwords: code i occupies bits [i*P, i*P+P) of
  * the little-endian bit string (two's complement). Every chunk lands in the 4
@@ -100,6 +113,8 @@ typedef struct mtc_stream_desc {
   const float* leaf_scale;
   const int32_t* row_perm;
   const int32_t* col_perm;
+  const uint32_t* steps;   /* n_steps step records of 16 words */
+  int64_t n_steps;
 } mtc_stream_desc;
 
 int mtc_abi_version(void);

@@ -2,7 +2,7 @@
 
 import ctypes
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 MTC_OK = 0
 MTC_DTYPE_F32 = 0
@@ -40,6 +40,8 @@ class MtcStreamDesc(ctypes.Structure):
         ("leaf_scale", ctypes.c_void_p),
         ("row_perm", ctypes.c_void_p),
         ("col_perm", ctypes.c_void_p),
+        ("steps", ctypes.c_void_p),
+        ("n_steps", ctypes.c_int64),
     ]
 
 

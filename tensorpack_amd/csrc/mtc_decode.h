@@ -102,6 +102,15 @@ __device__ __forceinline__ LeafInfo leaf_info(uint32_t word, const float* __rest
   return li;
 }
 
+// Leaf fields with the fp32 scale (if any) already loaded.
+__device__ __forceinline__ LeafInfo leaf_info_v(uint32_t word, bool fp32_scales, float fscale) {
+  LeafInfo li;
+  li.row = static_cast<int>(word & 0x3FFu) * 4;
+  li.pad = (word & kLeafPad) != 0;
+  li.scale = fp32_scales ? fscale : bf16_bits_to_f32(word >> 16);
+  return li;
+}
+
 constexpr int kGroup = 4;             // columns per column group
 constexpr int kGroups = kPanel / kGroup;
 constexpr int kUnitHdr = 32;          // words per unit header

@@ -134,7 +134,8 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, c
   const int rows_in = min(n_row_tiles - first, kRowGroup);
   const int rt = first + in_grp % rows_in, ct = in_grp / rows_in;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: keeps per-wave control scalar
   const int m0 = rt * kTM, n0 = ct * kTN;
   const int nks = d.n_ksteps;
 

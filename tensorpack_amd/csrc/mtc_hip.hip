@@ -131,33 +131,79 @@ __global__ __launch_bounds__(512) void k_dequant(const mtc_stream_desc d, float*
 // ---------------------------------------------------------------------------
 // fp32 decode GEMV
 //
-// Block = (unit, G adjacent column groups), two waves per column group. The
-// block copies its column groups' payload and bucket entries and the unit's
-// leaf words into LDS with every load of a round in flight at once, and
-// gathers X rows (row_perm) into LDS alongside. A column group's work is a
-// list of 64-chunk steps, each inside ONE bucket (a bucket of n chunks gives
-// ceil(n/64) steps), so the bucket kind of a step is wave-uniform and
-// dispatches on a scalar register; the group's two waves split the steps.
-// Lanes accumulate their 4 columns in registers (no atomics). Blocks of one
-// unit are mapped to the same XCD so its leaf words stay in one L2.
+// Block = (unit, G adjacent column groups), V waves per column group. Only X
+// (gathered through row_perm) is staged in LDS. A column group's work is a list
+// of 64-chunk steps, each inside ONE bucket (a bucket of n chunks gives
+// ceil(n/64) steps), split into V contiguous ranges, one per wave; the bucket
+// entry of a step is read with scalar loads, so its kind dispatches on a scalar
+// register. Each lane streams its chunk's P payload dwords and its leaf word(s)
+// straight from memory into registers, one step ahead of the step it decodes,
+// and accumulates its column group's 4 columns (times MT rows) in registers;
+// lanes and waves are combined once at the end (no atomics). Blocks of one unit
+// are mapped to the same XCD so the unit's leaf words stay in one L2.
 // ---------------------------------------------------------------------------
+constexpr int kMaxP = 16;
+typedef uint32_t u32x16_t __attribute__((ext_vector_type(16)));   // a step's payload words (one SSA value)
+
+typedef const __attribute__((address_space(4))) uint32_t* cu32p;
+typedef const __attribute__((address_space(4))) int32_t* ci32p;
+
+// Loads of one step into a lane's registers: its chunk's payload dwords (w[0..P)), its
+// leaf word(s) and, for fp32-scale streams, the leaf scale(s). Every step issues the same
+// kStepLoads vector loads into the same registers whatever its kind: four 16-byte payload
+// loads at offsets 0, 4, 8, 12 dwords, where the loads a P-dword chunk does not need read
+// one wave-uniform stand-in address instead (the words they fill are read only by wider
+// kinds). The compiler's waits before decoding a step then stay partial.
+// Chunks are dword aligned; a 16-byte load past a chunk reads the next chunk or the
+// stream's tail padding. Lanes past the bucket's end re-read its last chunk and are
+// masked when accumulating.
+constexpr int kStepLoads = 8;
+typedef uint32_t u32x4u_t __attribute__((ext_vector_type(4), aligned(4)));
+
+__device__ __forceinline__ u32x4_t ldu4(const uint32_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4u_t*>(p));
+}
+
+__device__ __forceinline__ void gemv_load(const uint32_t* __restrict__ pay, const uint32_t* __restrict__ lwp,
+                                          const float* __restrict__ fsp, const uint32_t* __restrict__ dummy,
+                                          bool fp32_scales, uint32_t key, uint32_t t, u32x16_t& w, uint32_t& lw0,
+                                          uint32_t& lw1, float& fs0, float& fs1) {
+  const uint32_t P = key >> 8, ls = key & 0xFFu;
+  const uint32_t* src = pay + t * P;
+  // loads a kind does not need read one wave-uniform address (a single cache line)
+  const u32x4_t a = ldu4(src);
+  const u32x4_t b = ldu4(P > 4 ? src + 4 : dummy);
+  const u32x4_t c = ldu4(P > 8 ? src + 8 : dummy);
+  const u32x4_t e = ldu4(P > 8 ? src + 12 : dummy);
+  w = __builtin_shufflevector(__builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7),
+                              __builtin_shufflevector(c, e, 0, 1, 2, 3, 4, 5, 6, 7), 0, 1, 2, 3, 4, 5, 6, 7, 8, 9,
+                              10, 11, 12, 13, 14, 15);
+  // leaf words and scales: always two loads each
+  const uint32_t l0 = ls == 2 ? 2 * t : t >> (ls - 3);
+  lw0 = lwp[l0];
+  lw1 = ls == 2 ? lwp[l0 + 1] : dummy[0];
+  fs0 = fp32_scales ? fsp[l0] : __uint_as_float(dummy[1]);
+  fs1 = fp32_scales && ls == 2 ? fsp[l0 + 1] : __uint_as_float(dummy[2]);
+}
+
 __device__ __forceinline__ float dot4(const float4 x, const float* q) {
   return x.x * q[0] + x.y * q[1] + x.z * q[2] + x.w * q[3];
 }
 
-// One lane chunk from LDS into the lane's 4-column accumulators.
+// One lane chunk (payload in registers) into the lane's 4-column accumulators.
 template <int S, int P, int MT>
-__device__ __forceinline__ void gemv_chunk(const uint32_t* src, const uint32_t* lw, uint32_t t, const float* fscale,
-                                           uint32_t lg0, const float* xs, int kc, float (&acc)[MT][kGroup]) {
+__device__ __forceinline__ void gemv_chunk(const u32x16_t rw, uint32_t lw0, uint32_t lw1, float fs0, float fs1,
+                                           bool fp32_scales, uint32_t t, const float* xs, int kc,
+                                           float (&acc)[MT][kGroup]) {
   uint32_t w[P];
-  lds_chunk<P>(src, w);
+#pragma unroll
+  for (int i = 0; i < P; ++i) w[i] = rw[i];
   float q[32];
   decode_chunk<P>(w, q);
   if constexpr (S == 4) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const uint32_t leaf = 2 * t + h;
-      const LeafInfo li = leaf_info(lw[leaf], fscale, lg0 + leaf);
+      const LeafInfo li = leaf_info_v(h ? lw1 : lw0, fp32_scales, h ? fs1 : fs0);
       if (li.pad) continue;
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
@@ -168,8 +214,7 @@ __device__ __forceinline__ void gemv_chunk(const uint32_t* src, const uint32_t* 
     }
   } else {
     constexpr int NRB = S / 8;
-    const uint32_t leaf = t / NRB;
-    const LeafInfo li = leaf_info(lw[leaf], fscale, lg0 + leaf);
+    const LeafInfo li = leaf_info_v(lw0, fp32_scales, fs0);
     const int row = li.row + 8 * (int)(t % NRB);
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -181,35 +226,40 @@ __device__ __forceinline__ void gemv_chunk(const uint32_t* src, const uint32_t* 
   }
 }
 
-constexpr int kGemvWavesPerGroup = 2;
-constexpr int kStageU4 = 8;     // uint4 payload loads in flight per thread per staging round
-constexpr int kStageW = 8;      // leaf-word loads per thread per round
+constexpr int kStepGroups = 4;              // column groups one decode step covers
+constexpr int kStepLanes = 16;              // lanes per column group in a step
+constexpr int kStepWords = 16;              // words per step record
+// waves per block: 16 for M tiles of 1-2 rows, 8 for 4 rows (more accumulators per lane)
+__host__ __device__ constexpr int gemv_waves(int MT) { return MT <= 2 ? 16 : 8; }
+constexpr int kGemvBlocksPerUnit = kGroups / kStepGroups;
 constexpr int kXcds = 8;
 
-__device__ __forceinline__ float wave_sum(float v) {
+// Sum over the 16 lanes of a lane's column-group slot.
+__device__ __forceinline__ float slot_sum(float v) {
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  for (int off = kStepLanes / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
   return v;
 }
 
-// M-tile rows -> column groups per block (more X rows on chip, fewer blocks per CU)
-__host__ __device__ constexpr int gemv_groups(int MT) { return MT <= 2 ? 2 : 4; }
+__device__ __forceinline__ uint32_t pick4(uint32_t a, uint32_t b, uint32_t c, uint32_t e, int g) {
+  return g == 0 ? a : g == 1 ? b : g == 2 ? c : e;
+}
 
 template <int MT>
-__global__ __launch_bounds__(64 * kGemvWavesPerGroup * gemv_groups(MT)) void k_gemv(
-    const mtc_stream_desc d, const float* __restrict__ X, int64_t ldx, float* __restrict__ Y, int64_t ldy, int M,
-    float* __restrict__ part, uint32_t* __restrict__ counters) {
+__global__ __launch_bounds__(64 * gemv_waves(MT)) void k_gemv(const mtc_stream_desc d, const float* __restrict__ X,
+                                                          int64_t ldx, float* __restrict__ Y, int64_t ldy, int M,
+                                                          float* __restrict__ part, uint32_t* __restrict__ counters) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
-  constexpr int G = gemv_groups(MT), V = kGemvWavesPerGroup, W = G * V, T = 64 * W;
-  constexpr int BPU = kGroups / G;                    // blocks per unit
+  constexpr int W = gemv_waves(MT), T = 64 * W, BPU = kGemvBlocksPerUnit;
   const int kc = d.chunk_rows;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: keeps per-wave control scalar
   const int n_units = d.n_panels * d.n_chunks;
-  // block -> (unit, column-group block) with all blocks of a unit on one XCD
+  // block -> (unit, block of 4 column groups) with both blocks of a unit on one XCD
   const int xcd = blockIdx.x % kXcds, slot = blockIdx.x / kXcds;
   const int u = (slot / BPU) * kXcds + xcd;
   if (u >= n_units) return;                           // padding block of the XCD mapping
-  const int cg_lo = (slot % BPU) * G;
+  const int cb = slot % BPU;
   const int mt = blockIdx.y;
   const int panel = u / d.n_chunks, chunk = u - panel * d.n_chunks;
   const int m0 = mt * MT;
@@ -217,52 +267,62 @@ __global__ __launch_bounds__(64 * kGemvWavesPerGroup * gemv_groups(MT)) void k_g
   const int rows = min(kc, d.K - kb);
 
   float* xs = smem;                                   // [MT][kc]
-  float* red = xs + MT * kc;                          // [waves][MT][4]
-  uint32_t* s_pay = reinterpret_cast<uint32_t*>(red + W * MT * kGroup);   // 16-byte aligned
+  float* red = xs + MT * kc;                          // [waves][4 slots][MT][4]
 
-  const int32_t* hdr = d.unit_hdr + kUnitHdr * u;
-  const int pay_lo = hdr[17 + cg_lo], npay = hdr[17 + cg_lo + G] - pay_lo;
-  const int lf0 = hdr[2], nlf = hdr[3] - hdr[2];
-  const int bk_lo = hdr[8 + cg_lo], nbk = hdr[8 + cg_lo + G] - bk_lo;
-  uint32_t* s_lw = s_pay + npay;
-  uint32_t* s_bk = s_lw + nlf;
+  const ci32p hdr = (ci32p)(d.unit_hdr + kUnitHdr * u);
+  const uint32_t* pay_u = d.payload + hdr[0];
+  const uint32_t* lw_u = d.leaf_word + hdr[2];
+  // fp32 scales of the unit's leaves (a stand-in address that is never used otherwise)
+  const bool fscales = d.leaf_scale != nullptr;
+  const float* fs_u = fscales ? d.leaf_scale + hdr[2] : reinterpret_cast<const float*>(lw_u);
 
-  // ---- stage: every global load of a round (branch-free, clamped index) goes
-  // out before any LDS store; X indices and bucket entries ride along ----
+  // ---- this wave's step records: [s_beg, s_end) of the block's list ----
+  const int nrec = hdr[28 + 2 * cb];
+  const cu32p rec = (cu32p)(d.steps + (size_t)hdr[27 + 2 * cb] * kStepWords);
+  const int per = (nrec + W - 1) / W;
+  const int s_beg = min(wave * per, nrec), s_end = min(s_beg + per, nrec);
+  const int g = lane / kStepLanes, li = lane % kStepLanes;   // column-group slot, lane in slot
+
+  // A step's per-lane view: chunk t of this slot's bucket, active if li < valid chunks.
+  // Inactive lanes load chunk 0 of the bucket (every referenced bucket has one).
+  struct Regs {
+    u32x16_t w;
+    uint32_t lw0, lw1;
+    float fs0, fs1;
+    uint32_t t, key;
+    bool on;
+  };
+  auto fetch = [&](int st, Regs& r) __attribute__((always_inline)) {
+    const cu32p e = rec + st * kStepWords;
+    const uint32_t w0 = e[0];
+    const uint32_t pay = pick4(e[1], e[2], e[3], e[4], g);
+    const uint32_t leaf = pick4(e[5], e[6], e[7], e[8], g);
+    const uint32_t nv = pick4(e[9], e[10], e[11], e[12], g);
+    r.key = w0 & 0xFFFFu;
+    r.on = (uint32_t)li < nv;
+    r.t = r.on ? kStepLanes * (w0 >> 16) + li : 0u;
+    gemv_load(pay_u + pay, lw_u + leaf, fs_u + leaf, pay_u, fscales, r.key, r.t, r.w, r.lw0, r.lw1, r.fs0, r.fs1);
+  };
+
+  // A wave has about ceil(records / 16) steps (3 for full-K units); the loads of its
+  // first kAhead steps all go out before X is staged, so their latency is paid once.
+  // All kAhead fetches are issued unconditionally (clamped to the wave's last step) so
+  // the compiler's waits before each decode are partial.
+  Regs r0{}, r1{}, r2{};
+  if (s_beg < s_end) {
+    fetch(s_beg, r0);
+    fetch(min(s_beg + 1, s_end - 1), r1);
+    fetch(min(s_beg + 2, s_end - 1), r2);
+  }
+
+  // ---- X rows of the unit into LDS while the first step's loads are in flight ----
   {
-    const u32x4_t* gpay = reinterpret_cast<const u32x4_t*>(d.payload + hdr[0] + pay_lo);
-    const uint32_t* glw = d.leaf_word + lf0;
-    const int npay4 = npay >> 2;
     constexpr int XR = kMaxChunkRows / T;
     int kk[XR];
 #pragma unroll
     for (int i = 0; i < XR; ++i) {
-      const int k = kb + min(i * T + tid, rows - 1);
-      kk[i] = d.row_perm ? d.row_perm[k] : k;
-    }
-    for (int i = tid; i < 4 * nbk; i += T) s_bk[i] = d.buckets[4 * (hdr[4] + bk_lo) + i];
-    const int rounds = max((npay4 + T * kStageU4 - 1) / (T * kStageU4), (nlf + T * kStageW - 1) / (T * kStageW));
-    for (int r = 0; r < rounds; ++r) {
-      u32x4_t pv[kStageU4];
-      uint32_t lv[kStageW];
-      if (npay4 > 0) {
-#pragma unroll
-        for (int i = 0; i < kStageU4; ++i) pv[i] = __builtin_nontemporal_load(gpay + min((r * kStageU4 + i) * T + tid, npay4 - 1));
-      }
-      if (nlf > 0) {
-#pragma unroll
-        for (int i = 0; i < kStageW; ++i) lv[i] = glw[min((r * kStageW + i) * T + tid, nlf - 1)];
-      }
-#pragma unroll
-      for (int i = 0; i < kStageU4; ++i) {
-        const int idx = (r * kStageU4 + i) * T + tid;
-        if (idx < npay4) reinterpret_cast<u32x4_t*>(s_pay)[idx] = pv[i];
-      }
-#pragma unroll
-      for (int i = 0; i < kStageW; ++i) {
-        const int idx = (r * kStageW + i) * T + tid;
-        if (idx < nlf) s_lw[idx] = lv[i];
-      }
+      const int r = kb + min(i * T + tid, rows - 1);
+      kk[i] = d.row_perm ? d.row_perm[r] : r;
     }
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -279,76 +339,57 @@ __global__ __launch_bounds__(64 * kGemvWavesPerGroup * gemv_groups(MT)) void k_g
   }
   __syncthreads();
 
-  // ---- decode: the column group's steps, split between its V waves ----
+  // ---- decode: the prefetched steps, then any further steps one at a time ----
   float acc[MT][kGroup];
 #pragma unroll
   for (int m = 0; m < MT; ++m)
 #pragma unroll
     for (int c = 0; c < kGroup; ++c) acc[m][c] = 0.0f;
-  {
-    const int gl = wave / V, sub = wave % V;
-    const int b0 = hdr[8 + cg_lo + gl] - bk_lo, b1 = hdr[8 + cg_lo + gl + 1] - bk_lo;
-    int nsteps = 0;
-    for (int b = b0; b < b1; ++b) nsteps += (int)(((s_bk[4 * b + 2] & 0xFFFFu) + 63) >> 6);
-    const int per = (nsteps + V - 1) / V;
-    const int s_beg = sub * per, s_end = min(s_beg + per, nsteps);
-    // advance to the bucket holding step s_beg (uniform)
-    int b = b0, bsteps = 0, s = 0;
-    if (s_beg < s_end) {
-      while (true) {
-        bsteps = (int)(((s_bk[4 * b + 2] & 0xFFFFu) + 63) >> 6);
-        if (s + bsteps > s_beg) break;
-        s += bsteps;
-        ++b;
-      }
-    }
-    int k = s_beg - s;                                // step within bucket b
-    for (int st = s_beg; st < s_end; ++st) {
-      const Bucket e = read_bucket(s_bk + 4 * b);
-      const uint32_t t = (uint32_t)(64 * k + lane);
-      if (t < e.n) {
-        const uint32_t* src = s_pay + (e.pay - pay_lo);
-        const uint32_t* lw = s_lw + e.leaf;
-        const uint32_t lg0 = lf0 + e.leaf;
-        // e.key is the same for every lane (one bucket per step): scalar dispatch
-        switch (__builtin_amdgcn_readfirstlane(e.key)) {
+  auto compute = [&](const Regs& cur) __attribute__((always_inline)) {
+    if (cur.on) {
+      switch (__builtin_amdgcn_readfirstlane(cur.key)) {
 #define MTC_CASE(S, P) \
-  case MTC_BUCKET_KEY(S, P): gemv_chunk<S, P, MT>(src + t * P, lw, t, d.leaf_scale, lg0, xs, kc, acc); break;
-          MTC_FOR_EACH_BUCKET(MTC_CASE)
+  case MTC_BUCKET_KEY(S, P): \
+    gemv_chunk<S, P, MT>(cur.w, cur.lw0, cur.lw1, cur.fs0, cur.fs1, fscales, cur.t, xs, kc, acc); \
+    break;
+        MTC_FOR_EACH_BUCKET(MTC_CASE)
 #undef MTC_CASE
-          default: break;
-        }
-      }
-      if (++k == bsteps && st + 1 < s_end) {
-        ++b;
-        k = 0;
-        bsteps = (int)(((s_bk[4 * b + 2] & 0xFFFFu) + 63) >> 6);
+        default: break;
       }
     }
+  };
+  const int ns = s_end - s_beg;
+  if (ns > 0) compute(r0);
+  if (ns > 1) compute(r1);
+  if (ns > 2) compute(r2);
+  for (int st = s_beg + 3; st < s_end; ++st) {
+    fetch(st, r0);
+    compute(r0);
   }
+
+  // ---- reduce: the 16 lanes of each slot, then the block's waves ----
 #pragma unroll
   for (int m = 0; m < MT; ++m)
 #pragma unroll
-    for (int c = 0; c < kGroup; ++c) acc[m][c] = wave_sum(acc[m][c]);
-  if (lane == 0) {
+    for (int c = 0; c < kGroup; ++c) acc[m][c] = slot_sum(acc[m][c]);
+  if (li == 0) {
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
-      for (int c = 0; c < kGroup; ++c) red[(wave * MT + m) * kGroup + c] = acc[m][c];
+      for (int c = 0; c < kGroup; ++c) red[((wave * kStepGroups + g) * MT + m) * kGroup + c] = acc[m][c];
   }
   __syncthreads();
 
-  // ---- combine the waves of each column group; write Y or this block's partial ----
-  constexpr int nout = MT * G * kGroup;
+  constexpr int nout = MT * kStepGroups * kGroup;
   if (d.n_chunks == 1) {
     for (int i = tid; i < nout; i += T) {
-      const int m = i / (G * kGroup), gc = i - m * (G * kGroup);
-      const int gl = gc / kGroup, c = gc - gl * kGroup;
+      const int m = i / (kStepGroups * kGroup), gc = i - m * (kStepGroups * kGroup);
+      const int g2 = gc / kGroup, c = gc - g2 * kGroup;
       float v = 0.0f;
 #pragma unroll
-      for (int s2 = 0; s2 < V; ++s2) v += red[((gl * V + s2) * MT + m) * kGroup + c];
+      for (int w2 = 0; w2 < W; ++w2) v += red[((w2 * kStepGroups + g2) * MT + m) * kGroup + c];
       if (m0 + m < M) {
-        int col = panel * kPanel + (cg_lo + gl) * kGroup + c;
+        int col = panel * kPanel + (cb * kStepGroups + g2) * kGroup + c;
         if (d.col_perm) col = d.col_perm[col];
         Y[(int64_t)(m0 + m) * ldy + col] = v;
       }
@@ -360,12 +401,13 @@ __global__ __launch_bounds__(64 * kGemvWavesPerGroup * gemv_groups(MT)) void k_g
   constexpr int n_part = MT * kPanel;
   float* mine = part + ((size_t)mt * n_units + u) * n_part;
   for (int i = tid; i < nout; i += T) {
-    const int m = i / (G * kGroup), gc = i - m * (G * kGroup);
-    const int gl = gc / kGroup, c = gc - gl * kGroup;
+    const int m = i / (kStepGroups * kGroup), gc = i - m * (kStepGroups * kGroup);
+    const int g2 = gc / kGroup, c = gc - g2 * kGroup;
     float v = 0.0f;
 #pragma unroll
-    for (int s2 = 0; s2 < V; ++s2) v += red[((gl * V + s2) * MT + m) * kGroup + c];
-    __hip_atomic_store(mine + m * kPanel + (cg_lo + gl) * kGroup + c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int w2 = 0; w2 < W; ++w2) v += red[((w2 * kStepGroups + g2) * MT + m) * kGroup + c];
+    __hip_atomic_store(mine + m * kPanel + (cb * kStepGroups + g2) * kGroup + c, v, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
   }
   __threadfence();
   __syncthreads();
@@ -417,6 +459,8 @@ int check_desc(const mtc_stream_desc* d) {
     return fail(MTC_E_NULL, "fp32-scale stream without leaf_scale");
   if (!(d->flags & MTC_FLAG_FP32_SCALES) && d->leaf_scale)
     return fail(MTC_E_DESC, "leaf_scale given but MTC_FLAG_FP32_SCALES not set");
+  if (d->n_steps < 0 || (d->n_buckets > 0 && (!d->steps || d->n_steps == 0)))
+    return fail(MTC_E_NULL, "decode step records missing (n_steps=%lld)", (long long)d->n_steps);
   return ok();
 }
 
@@ -436,9 +480,7 @@ size_t gemv_ws_layout(const mtc_stream_desc* d, int M, size_t* counters_bytes) {
 }
 
 size_t gemv_lds_bytes(const mtc_stream_desc* d, int MT) {
-  const int waves = kGemvWavesPerGroup * gemv_groups(MT);
-  const int staged = gemv_groups(MT) == 2 ? d->max_unit_words : d->max_unit_words4;
-  return ((size_t)MT * d->chunk_rows + (size_t)waves * MT * kGroup + (size_t)staged) * 4;
+  return ((size_t)MT * d->chunk_rows + (size_t)gemv_waves(MT) * kStepGroups * MT * kGroup) * 4;
 }
 
 template <int MT>
@@ -451,18 +493,17 @@ int launch_gemv(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y,
   const size_t shmem = gemv_lds_bytes(d, MT);
   const size_t limit = device_lds_limit();
   if (shmem > limit)
-    return fail(MTC_E_SHAPE, "fp32 path: %d rows x chunk_rows=%d with %d staged words needs %zu B of LDS (limit %zu); "
-                "use a stream with smaller chunk_rows", MT, d->chunk_rows, d->max_unit_words, shmem, limit);
+    return fail(MTC_E_SHAPE, "fp32 path: %d rows x chunk_rows=%d needs %zu B of LDS (limit %zu); "
+                "use a stream with smaller chunk_rows", MT, d->chunk_rows, shmem, limit);
   if (shmem > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv<MT>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
     if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
   }
-  constexpr int G = gemv_groups(MT);
   const int n_units = d->n_panels * d->n_chunks;
   const int units_padded = (n_units + kXcds - 1) / kXcds * kXcds;
-  dim3 grid(units_padded * (kGroups / G), (M + MT - 1) / MT);
-  hipLaunchKernelGGL(k_gemv<MT>, grid, dim3(64 * kGemvWavesPerGroup * G), shmem, st, *d, X, ldx, Y, ldy, M, part,
+  dim3 grid(units_padded * kGemvBlocksPerUnit, (M + MT - 1) / MT);
+  hipLaunchKernelGGL(k_gemv<MT>, grid, dim3(64 * gemv_waves(MT)), shmem, st, *d, X, ldx, Y, ldy, M, part,
                      counters);
   return check_launch("k_gemv");
 }

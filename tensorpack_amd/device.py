@@ -32,6 +32,9 @@ def current_stream_handle(device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+_DEV_ARRAYS = ("payload", "buckets", "unit_hdr", "leaf_word", "leaf_scale", "row_perm", "col_perm", "steps")
+
+
 class DeviceStream:
     """A PanelStream uploaded to one GPU, plus its ctypes descriptor."""
 
@@ -53,6 +56,7 @@ class DeviceStream:
         self.leaf_scale = up(ps.leaf_scale, np.float32)
         self.row_perm = up(ps.row_perm, np.int32)
         self.col_perm = up(ps.col_perm, np.int32)
+        self.steps = up(None if ps.steps is None else ps.steps.reshape(-1).view(np.int32), np.int32)
 
         d = _abi.MtcStreamDesc()
         d.abi_version = _abi.ABI_VERSION
@@ -68,6 +72,8 @@ class DeviceStream:
         d.payload, d.buckets, d.unit_hdr = ptr(self.payload), ptr(self.buckets), ptr(self.unit_hdr)
         d.leaf_word, d.leaf_scale = ptr(self.leaf_word), ptr(self.leaf_scale)
         d.row_perm, d.col_perm = ptr(self.row_perm), ptr(self.col_perm)
+        d.steps = ptr(self.steps)
+        d.n_steps = 0 if ps.steps is None else int(ps.steps.shape[0])
         self.desc = d
         _abi.check(self.lib, "mtc_check_desc", self.lib.mtc_check_desc(ctypes.byref(d)))
         self._ws: Dict[int, "object"] = {}
@@ -76,7 +82,7 @@ class DeviceStream:
         """A second device copy of the same stream (distinct buffers, same contents)."""
         other = object.__new__(DeviceStream)
         other.device, other.host, other.lib = self.device, self.host, self.lib
-        for name in ("payload", "buckets", "unit_hdr", "leaf_word", "leaf_scale", "row_perm", "col_perm"):
+        for name in _DEV_ARRAYS:
             t = getattr(self, name)
             setattr(other, name, None if t is None else t.clone())
         d = _abi.MtcStreamDesc.from_buffer_copy(self.desc)
@@ -84,13 +90,14 @@ class DeviceStream:
         d.payload, d.buckets, d.unit_hdr = ptr(other.payload), ptr(other.buckets), ptr(other.unit_hdr)
         d.leaf_word, d.leaf_scale = ptr(other.leaf_word), ptr(other.leaf_scale)
         d.row_perm, d.col_perm = ptr(other.row_perm), ptr(other.col_perm)
+        d.steps = ptr(other.steps)
         other.desc = d
         other._ws = {}
         return other
 
     def device_bytes(self) -> int:
         n = 0
-        for name in ("payload", "buckets", "unit_hdr", "leaf_word", "leaf_scale", "row_perm", "col_perm"):
+        for name in _DEV_ARRAYS:
             t = getattr(self, name)
             if t is not None:
                 n += t.numel() * t.element_size()

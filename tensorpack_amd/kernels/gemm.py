@@ -53,9 +53,11 @@ def gemv_chunk_rows(K: int, N: int, M: int = 1) -> int:
 
 
 def _decode_lds_need(ps: PanelStream, M: int) -> int:
+    """LDS bytes of one decode block: the gathered X rows plus the per-wave partial sums
+    (mirrors gemv_lds_bytes in csrc/mtc_hip.hip; the payload streams through registers)."""
     mt = _decode_mt(M)
-    staged = ps.max_unit_words if mt <= 2 else ps.max_unit_words4
-    return 4 * (mt * ps.chunk_rows + 8 * mt * 4 + staged)
+    waves = 16 if mt <= 2 else 8
+    return 4 * (mt * ps.chunk_rows + waves * 4 * mt * 4)
 
 
 # ---------------------------------------------------------------------------------------

@@ -35,7 +35,11 @@ LEAF_PAD = 1 << 13
 ROW_BITS = 10                          # leaf word: row/4 in bits 0-9
 MAX_CHUNK_ROWS = 4 << ROW_BITS         # 4096
 UNIT_HDR_WORDS = 32
-STREAM_FORMAT = 3                      # panel stream layout version (matches the C-ABI version)
+STREAM_FORMAT = 5                      # panel stream layout version (matches the C-ABI version)
+PAYLOAD_PAD = 4                        # dwords after the last bucket
+STEP_GROUPS = 4                        # column groups one decode step covers
+STEP_LANES = 16                        # lanes (chunks) per column group in a step
+STEP_WORDS = 16                        # words per step record
 _LOG2 = {32: 5, 16: 4, 8: 3, 4: 2}
 
 CodeSource = Callable[[int, int, np.ndarray, np.ndarray, np.ndarray], np.ndarray]
@@ -52,6 +56,7 @@ class PanelStream:
     unit_hdr: np.ndarray                # int32 (n_units, 32)
     leaf_word: np.ndarray               # uint32
     leaf_scale: Optional[np.ndarray]    # float32 or None (bf16 scales in leaf_word)
+    steps: Optional[np.ndarray] = None  # uint32 (n_records, 16): decode step records
     row_perm: Optional[np.ndarray] = None   # int32 or None
     col_perm: Optional[np.ndarray] = None   # int32 or None
     n_real_leaves: int = 0
@@ -82,13 +87,13 @@ class PanelStream:
     def nbytes(self) -> int:
         """Device bytes of the stream (payload + tables + permutations)."""
         n = self.payload.nbytes + 16 * self.n_buckets + self.unit_hdr.nbytes + self.leaf_word.nbytes
-        for a in (self.leaf_scale, self.row_perm, self.col_perm):
+        for a in (self.leaf_scale, self.row_perm, self.col_perm, self.steps):
             if a is not None:
                 n += a.nbytes
         return int(n)
 
     # ---- on-disk form: one .npz of plain arrays (no pickled objects) ----
-    _ARRAYS = ("payload", "buckets", "unit_hdr", "leaf_word", "leaf_scale", "row_perm", "col_perm")
+    _ARRAYS = ("payload", "buckets", "unit_hdr", "leaf_word", "leaf_scale", "row_perm", "col_perm", "steps")
 
     def save(self, path) -> None:
         arrays = {k: getattr(self, k) for k in self._ARRAYS if getattr(self, k) is not None}
@@ -107,7 +112,7 @@ class PanelStream:
             stats = dict(zip([str(k) for k in z["stats_keys"]], [float(v) for v in z["stats_vals"]]))
             return cls(K=meta[1], N=meta[2], chunk_rows=meta[3], payload=get("payload"), buckets=get("buckets"),
                        unit_hdr=get("unit_hdr"), leaf_word=get("leaf_word"), leaf_scale=get("leaf_scale"),
-                       row_perm=get("row_perm"), col_perm=get("col_perm"), n_real_leaves=meta[4],
+                       steps=get("steps"), row_perm=get("row_perm"), col_perm=get("col_perm"), n_real_leaves=meta[4],
                        max_unit_words=meta[5], max_unit_words4=meta[6], stats=stats)
 
 
@@ -295,7 +300,7 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
         b_dw = (b_cnt * b_P + 3) & ~3
         b_pay = np.concatenate([[0], np.cumsum(b_dw)[:-1]])
         total_dw = int(b_dw.sum())
-        payload = np.zeros(max(total_dw, 4), dtype=np.uint32)
+        payload = np.zeros(total_dw + PAYLOAD_PAD, dtype=np.uint32)   # tail padding: 16-byte loads may run past a chunk
         b_of = np.repeat(np.arange(n_buckets), b_cnt)
         dst = b_pay[b_of] + (np.arange(n_ch) - b_start[b_of]) * cP
         for P in np.unique(cP):
@@ -310,7 +315,7 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
         pay_after = np.concatenate([b_pay, [total_dw]])
     else:
         n_buckets, total_dw = 0, 0
-        payload = np.zeros(4, np.uint32)
+        payload = np.zeros(PAYLOAD_PAD, np.uint32)
         b_unit = b_cg = b_cnt = b_cstart = b_leaf = b_pay = np.zeros(0, np.int64)
         b_S = b_P = np.zeros(0, np.int64)
         pay_after = np.zeros(1, np.int64)
@@ -343,6 +348,42 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
     max_unit_words = int(hdr[:, 7].max()) if n_units else 0
     max_unit_words4 = int(hdr[:, 26].max()) if n_units else 0
 
+    # ---- decode step records: one per (unit, block of 4 column groups, kind, 16-chunk step) ----
+    steps = np.zeros((0, STEP_WORDS), dtype=np.uint32)
+    blk_begin = np.zeros(n_units * 2 + 1, dtype=np.int64)
+    if n_buckets:
+        blk = b_cg // STEP_GROUPS
+        slot = b_cg % STEP_GROUPS
+        order = np.lexsort((slot, b_kind, blk, b_unit))
+        gk = (b_unit[order] * 2 + blk[order]) * 64 + b_kind[order]
+        gstart = np.flatnonzero(np.concatenate([[True], gk[1:] != gk[:-1]]))
+        n_grp = gstart.size
+        gid = np.repeat(np.arange(n_grp), np.diff(np.concatenate([gstart, [n_buckets]])))
+        g_steps = np.maximum.reduceat(-(-b_cnt[order] // STEP_LANES), gstart)
+        gb = np.full((n_grp, STEP_GROUPS), -1, dtype=np.int64)
+        gb[gid, slot[order]] = order
+        first = order[gstart]
+        miss = gb < 0
+        gb[miss] = np.broadcast_to(first[:, None], gb.shape)[miss]          # safe offsets, no valid chunks
+        g_n = np.where(miss, 0, b_cnt[gb])
+        rec_g = np.repeat(np.arange(n_grp), g_steps)
+        j = np.arange(rec_g.size) - np.repeat(np.concatenate([[0], np.cumsum(g_steps)[:-1]]), g_steps)
+        bb = gb[rec_g]
+        u_of = b_unit[bb[:, 0]]
+        steps = np.zeros((rec_g.size, STEP_WORDS), dtype=np.int64)
+        b_key = np.array([_LOG2[int(v)] for v in b_S], dtype=np.int64) | (b_P.astype(np.int64) << 8)
+        steps[:, 0] = b_key[bb[:, 0]] | (j << 16)
+        steps[:, 1:5] = b_pay[bb] - hdr[u_of, 0][:, None]
+        steps[:, 5:9] = b_leaf[bb] - hdr[u_of, 2][:, None]
+        steps[:, 9:13] = np.clip(g_n[rec_g] - STEP_LANES * j[:, None], 0, STEP_LANES)
+        steps = steps.astype(np.uint32)
+        rec_blk = b_unit[first][rec_g] * 2 + blk[first][rec_g]
+        blk_begin = np.searchsorted(rec_blk, np.arange(n_units * 2 + 1)).astype(np.int64)
+    hdr[:, 27] = blk_begin[0:-1:2]
+    hdr[:, 28] = blk_begin[1::2] - blk_begin[0:-1:2]
+    hdr[:, 29] = blk_begin[1::2]
+    hdr[:, 30] = blk_begin[2::2] - blk_begin[1::2]
+
     buckets = np.zeros((max(n_buckets, 1), 4), dtype=np.uint32)
     if n_buckets:
         buckets[:n_buckets, 0] = b_pay - hdr[b_unit, 0]
@@ -353,7 +394,7 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
     stats = {"payload_bytes": float(total_dw * 4), "n_buckets": float(n_buckets), "n_leaves": float(n_real),
              "max_unit_bytes": float(4 * max_unit_words)}
     return PanelStream(K=K, N=N, chunk_rows=chunk_rows, payload=payload, buckets=buckets,
-                       unit_hdr=hdr.astype(np.int32), leaf_word=leaf_word, leaf_scale=leaf_scale,
+                       unit_hdr=hdr.astype(np.int32), leaf_word=leaf_word, leaf_scale=leaf_scale, steps=steps,
                        row_perm=None if row_perm is None else np.ascontiguousarray(row_perm, dtype=np.int32),
                        col_perm=None if col_perm is None else np.ascontiguousarray(col_perm, dtype=np.int32),
                        n_real_leaves=n_real, max_unit_words=max_unit_words,

@@ -64,7 +64,8 @@ def _desc(**kw):
     d.n_buckets, d.max_unit_words, d.max_unit_words4 = 4, 100, 100
     d.n_leaves, d.payload_dwords = 4, 64
     dummy = 0x1000
-    d.payload = d.buckets = d.unit_hdr = d.leaf_word = dummy
+    d.payload = d.buckets = d.unit_hdr = d.leaf_word = d.steps = dummy
+    d.n_steps = 8
     for k, v in kw.items():
         setattr(d, k, v)
     return d
@@ -76,7 +77,7 @@ def test_descriptor_validation(hip):
     cases = {
         "abi_version": (99, -7), "N": (60, -2), "K": (0, -2), "chunk_rows": (48, -2),
         "n_panels": (3, -2), "n_chunks": (1, -2), "unit_hdr": (None, -1), "payload": (None, -1),
-        "max_unit_words4": (50, -2),
+        "max_unit_words4": (50, -2), "steps": (None, -1), "n_steps": (0, -1),
     }
     for field, (val, code) in cases.items():
         assert hip.mtc_check_desc(ctypes.byref(_desc(**{field: val}))) == code, field
@@ -138,7 +139,7 @@ def test_tile_descriptor_layout_and_validation(hip):
     assert out[0] == ctypes.sizeof(_abi.MtcTileDesc)
     assert out[1:] == [getattr(_abi.MtcTileDesc, f).offset for f in fields]
     assert hip.mtc_check_tile_desc(ctypes.byref(_tdesc())) == 0
-    cases = {"abi_version": (3, -7), "N": (100, -2), "K": (252, -2), "n_ksteps": (3, -2), "n_col_tiles": (1, -2),
+    cases = {"abi_version": (4, -7), "N": (100, -2), "K": (252, -2), "n_ksteps": (3, -2), "n_col_tiles": (1, -2),
              "flags": (4, -2), "cells": (None, -1), "payload": (None, -1), "step_off": (None, -1)}
     for field, (val, code) in cases.items():
         assert hip.mtc_check_tile_desc(ctypes.byref(_tdesc(**{field: val}))) == code, field
