@@ -401,44 +401,69 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
                        max_unit_words4=max_unit_words4, stats=stats)
 
 
-def decode_stream(ps: PanelStream) -> np.ndarray:
-    """Host decoder of a panel stream back to W_hat (original channel order).
+def _place_chunks(ps: PanelStream, Wp: np.ndarray, u: int, g: int, S: int, P: int, off: int, l0: int,
+                  ts: np.ndarray) -> None:
+    """Dequantize chunks `ts` of the bucket whose payload starts at dword `off` and whose
+    first leaf word is `l0` (both absolute) into Wp (permuted channel order)."""
+    panel, chunk = divmod(u, ps.n_chunks)
+    for t in (int(x) for x in ts):
+        cd_all = unpack_codes(ps.payload[off + t * P: off + (t + 1) * P].reshape(1, P), P)[0]
+        if S == 4:
+            parts = [(l0 + 2 * t, cd_all[:16], 0, 4), (l0 + 2 * t + 1, cd_all[16:], 0, 4)]
+        else:
+            parts = [(l0 + t // (S // 8), cd_all, 8 * (t % (S // 8)), 8)]
+        for li, cd, rrel, rows in parts:
+            wd = int(ps.leaf_word[li])
+            if wd & LEAF_PAD:
+                continue
+            r0 = chunk * ps.chunk_rows + (wd & ((1 << ROW_BITS) - 1)) * 4 + rrel
+            c0 = panel * PANEL + GROUP * g
+            s = ps.leaf_scale[li] if ps.leaf_scale is not None else \
+                np.array([wd >> 16 << 16], dtype=np.uint32).view(np.float32)[0]
+            Wp[r0: r0 + rows, c0: c0 + GROUP] = cd.reshape(GROUP, rows).T.astype(np.float32) * np.float32(s)
 
-    A debugging aid mirroring the device dequant kernel; the GPU path never calls it.
-    """
-    K, N = ps.K, ps.N
-    Wp = np.zeros((K, N), dtype=np.float32)
-    for u in range(ps.n_units):
-        panel, chunk = divmod(u, ps.n_chunks)
-        h = [int(x) for x in ps.unit_hdr[u]]
-        for g in range(N_GROUPS):
-            for b in range(h[4] + h[8 + g], h[4] + h[9 + g]):
-                prel, lrel, w2, key = (int(x) for x in ps.buckets[b])
-                nc = w2 & 0xFFFF
-                S, P = 1 << (key & 0xFF), key >> 8
-                off = h[0] + prel
-                codes = unpack_codes(ps.payload[off: off + nc * P].reshape(nc, P), P)
-                l0 = h[2] + lrel
-                for t in range(nc):
-                    if S == 4:
-                        parts = [(l0 + 2 * t, codes[t, :16], 0, 4), (l0 + 2 * t + 1, codes[t, 16:], 0, 4)]
-                    else:
-                        parts = [(l0 + t // (S // 8), codes[t], 8 * (t % (S // 8)), 8)]
-                    for li, cd, rrel, rows in parts:
-                        wd = int(ps.leaf_word[li])
-                        if wd & LEAF_PAD:
-                            continue
-                        r0 = chunk * ps.chunk_rows + (wd & ((1 << ROW_BITS) - 1)) * 4 + rrel
-                        c0 = panel * PANEL + GROUP * g
-                        s = ps.leaf_scale[li] if ps.leaf_scale is not None else \
-                            np.array([wd >> 16 << 16], dtype=np.uint32).view(np.float32)[0]
-                        Wp[r0: r0 + rows, c0: c0 + GROUP] = cd.reshape(GROUP, rows).T.astype(np.float32) * np.float32(s)
+
+def _to_original_order(ps: PanelStream, Wp: np.ndarray) -> np.ndarray:
     if ps.leaf_scale is None:
         Wp = Wp + np.float32(0.0)      # quadtree W_hat never holds -0.0
     if ps.row_perm is None and ps.col_perm is None:
         return Wp
-    pr = np.arange(K) if ps.row_perm is None else ps.row_perm
-    pc = np.arange(N) if ps.col_perm is None else ps.col_perm
+    pr = np.arange(ps.K) if ps.row_perm is None else ps.row_perm
+    pc = np.arange(ps.N) if ps.col_perm is None else ps.col_perm
     out = np.empty_like(Wp)
     out[np.ix_(pr, pc)] = Wp
     return out
+
+
+def decode_stream(ps: PanelStream) -> np.ndarray:
+    """Host decoder of a panel stream back to W_hat (original channel order), walking
+    the bucket table. A debugging aid; the GPU path never calls it."""
+    Wp = np.zeros((ps.K, ps.N), dtype=np.float32)
+    for u in range(ps.n_units):
+        h = [int(x) for x in ps.unit_hdr[u]]
+        for g in range(N_GROUPS):
+            for b in range(h[4] + h[8 + g], h[4] + h[9 + g]):
+                prel, lrel, w2, key = (int(x) for x in ps.buckets[b])
+                _place_chunks(ps, Wp, u, g, 1 << (key & 0xFF), key >> 8, h[0] + prel, h[2] + lrel,
+                              np.arange(w2 & 0xFFFF))
+    return _to_original_order(ps, Wp)
+
+
+def decode_steps(ps: PanelStream) -> np.ndarray:
+    """Host decoder that walks the step records the way the decode kernel does: for
+    each unit and block of 4 column groups, records [hdr[27 + 2b], +hdr[28 + 2b]);
+    lane li of slot g takes chunk 16 * j + li of that slot's bucket when li is below
+    the slot's valid-chunk count. A debugging aid; the GPU path never calls it."""
+    Wp = np.zeros((ps.K, ps.N), dtype=np.float32)
+    for u in range(ps.n_units):
+        h = [int(x) for x in ps.unit_hdr[u]]
+        for blk in range(N_GROUPS // STEP_GROUPS):
+            beg, cnt = h[27 + 2 * blk], h[28 + 2 * blk]
+            for e in ps.steps[beg: beg + cnt]:
+                e = [int(x) for x in e]
+                key, j = e[0] & 0xFFFF, e[0] >> 16
+                for g in range(STEP_GROUPS):
+                    nv = e[9 + g]
+                    _place_chunks(ps, Wp, u, blk * STEP_GROUPS + g, 1 << (key & 0xFF), key >> 8,
+                                  h[0] + e[1 + g], h[2] + e[5 + g], STEP_LANES * j + np.arange(nv))
+    return _to_original_order(ps, Wp)

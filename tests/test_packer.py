@@ -11,7 +11,8 @@ from tensorpack_amd.core.allocation import rd_allocate_pair
 from tensorpack_amd.core.permutation import PermutedQuadtreeRD
 from tensorpack_amd.core.quadtree import QuadtreeRD
 from tensorpack_amd.kernels.gemm import MTCMatrix, arena_decode, arena_encode
-from tensorpack_amd.packer import (LEAF_PAD, N_GROUPS, decode_stream, pack_codes, unpack_codes)
+from tensorpack_amd.packer import (LEAF_PAD, N_GROUPS, STEP_GROUPS, STEP_LANES, decode_stream, decode_steps,
+                                   pack_codes, unpack_codes)
 
 from conftest import outlier_matrix
 
@@ -152,3 +153,58 @@ def test_uniform_from_allocation_layout_and_accounting():
     ps = Am.panel_stream(64)
     assert ps.fp32_scales
     np.testing.assert_array_equal(decode_stream(ps), a.dequant)
+
+
+# ---------------- decode step records ----------------
+
+@pytest.mark.parametrize("cls,budget", [(QuadtreeRD, 2.2), (QuadtreeRD, 9.0), (PermutedQuadtreeRD, 4.25)])
+@pytest.mark.parametrize("chunk_rows", [32, 256])
+def test_step_records_decode_to_oracle_w_hat(cls, budget, chunk_rows):
+    W = outlier_matrix(int(budget * 10) + 1, 256, 160)
+    a = cls(W, np.exp(np.random.RandomState(4).randn(256)), (32, 16, 8, 4)).select(budget)
+    ps = MTCMatrix.from_quadtree(a, W).panel_stream(chunk_rows)
+    assert np.array_equal(_bits(decode_steps(ps)), _bits(_oracle(a, W)))
+
+
+def test_step_records_cover_every_chunk_once():
+    W = outlier_matrix(21, 512, 256)
+    a = QuadtreeRD(W, None, (32, 16, 8, 4)).select(3.5)
+    ps = MTCMatrix.from_quadtree(a, W).panel_stream(256)
+    h, st = ps.unit_hdr.astype(np.int64), ps.steps.astype(np.int64)
+    # the two blocks of each unit own consecutive, disjoint record ranges covering the table
+    assert np.all(h[:, 29] == h[:, 27] + h[:, 28])
+    assert np.all(h[1:, 27] == h[:-1, 29] + h[:-1, 30]) and h[0, 27] == 0
+    assert h[-1, 29] + h[-1, 30] == st.shape[0]
+    nv = st[:, 9:13]
+    assert nv.min() >= 0 and nv.max() <= STEP_LANES and np.all(nv.max(axis=1) > 0)
+    assert np.all(st[:, 13:] == 0)
+    seen = {}
+    for u in range(ps.n_units):
+        for blk in range(2):
+            recs = st[h[u, 27 + 2 * blk]: h[u, 27 + 2 * blk] + h[u, 28 + 2 * blk]]
+            for e in recs:
+                key, j = int(e[0] & 0xFFFF), int(e[0] >> 16)
+                for g in range(STEP_GROUPS):
+                    cg = blk * STEP_GROUPS + g
+                    # the slot's offsets name one of this column group's buckets of the same kind
+                    b = [k for k in range(h[u, 4] + h[u, 8 + cg], h[u, 4] + h[u, 9 + cg])
+                         if ps.buckets[k, 0] == e[1 + g] and ps.buckets[k, 1] == e[5 + g]]
+                    if e[9 + g] == 0:
+                        continue
+                    assert len(b) == 1 and int(ps.buckets[b[0], 3]) == key
+                    for t in range(STEP_LANES * j, STEP_LANES * j + int(e[9 + g])):
+                        assert (b[0], t) not in seen
+                        seen[(b[0], t)] = 1
+    expect = {(k, t) for k in range(ps.n_buckets) for t in range(int(ps.buckets[k, 2] & 0xFFFF))}
+    assert set(seen) == expect
+
+
+def test_step_records_survive_save_load(tmp_path):
+    W = outlier_matrix(22, 128, 64)
+    a = QuadtreeRD(W, None, (32, 16, 8, 4)).select(4.0)
+    ps = MTCMatrix.from_quadtree(a, W).panel_stream(64)
+    f = tmp_path / "s.npz"
+    ps.save(str(f))
+    back = type(ps).load(str(f))
+    assert np.array_equal(back.steps, ps.steps) and np.array_equal(back.unit_hdr, ps.unit_hdr)
+    assert np.array_equal(_bits(decode_steps(back)), _bits(decode_stream(ps)))
