@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MTC_ABI_VERSION 5
+#define MTC_ABI_VERSION 6
 
 enum {
   MTC_OK = 0,
@@ -85,13 +85,15 @@ enum { MTC_DTYPE_F32 = 0, MTC_DTYPE_BF16 = 1 };
  * chunks with 16-byte loads that may run up to 3 dwords past a chunk's end).
  *
  * A lane chunk is 32 codes in P dwords: code i occupies bits [i*P, i*P+P) of
- * the little-endian bit string (two's complement). Every chunk lands in the 4
+ * the little-endian bit string, stored offset-binary (u = q + 2^(P-1), so the
+ * signed code q = u - 2^(P-1)). Every chunk lands in the 4
  * columns of its cg: for S >= 8 it is 4 columns x 8 rows of one leaf, code i
  * at column i/8, row i%8, and chunk t of a bucket is leaf t/(S/8), row block
  * t%(S/8); for S = 4 it is leaves 2t and 2t+1 (16 codes each, column-major; an
  * odd group ends with a pad leaf). A leaf's word is shared by every cg it spans.
  *
  * Y[:, col_perm[n]] = X[:, row_perm] * Wp[:, n]; NULL perms mean identity.
+ * payload and row_perm must be 16-byte aligned.
  */
 typedef struct mtc_stream_desc {
   uint32_t abi_version;

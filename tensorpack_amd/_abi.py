@@ -2,7 +2,7 @@
 
 import ctypes
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 MTC_OK = 0
 MTC_DTYPE_F32 = 0

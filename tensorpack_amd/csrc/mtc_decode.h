@@ -1,9 +1,11 @@
 // Device-side decoding of the panel stream (layout documented in include/mtc_hip.h).
 //
-// A lane chunk is 32 two's-complement codes of P bits packed LSB-first into P
-// dwords. After full unrolling every bit position is a compile-time constant,
-// so each code costs one v_bfe_i32 (or v_alignbit + v_bfe_i32 when it
-// straddles a dword) and one v_cvt_f32_i32.
+// A lane chunk is 32 offset-binary codes u = q + 2^(P-1) of P bits packed
+// LSB-first into P dwords. After full unrolling every bit position is a
+// compile-time constant: byte-aligned fields (P = 2, 4 after one mask per 4 or 8
+// codes, P = 8 directly) convert with v_cvt_f32_ubyteN, other widths with one
+// v_bfe_u32 (or v_alignbit + v_and when a code straddles a dword) and one
+// v_cvt_f32_u32.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -73,19 +75,67 @@ __device__ __forceinline__ void lds_chunk(const uint32_t* src, uint32_t (&w)[P])
   }
 }
 
-// Signed code i (0..31) of a chunk.
-template <int P>
-__device__ __forceinline__ int chunk_code(const uint32_t (&w)[P], int i) {
-  const int b = i * P, j = b >> 5, o = b & 31;
-  if (o + P <= 32) return static_cast<int>(w[j] << (32 - o - P)) >> (32 - P);
-  const uint32_t v = __builtin_amdgcn_alignbit(w[(j + 1) < P ? (j + 1) : j], w[j], o);
-  return static_cast<int>(v << (32 - P)) >> (32 - P);
+// Hides a value's known bits so byte extraction compiles to v_cvt_f32_ubyteN.
+__device__ __forceinline__ uint32_t opaque(uint32_t x) {
+  asm("" : "+v"(x));
+  return x;
 }
 
+__device__ __forceinline__ float ubyte(uint32_t x, int k) { return (float)((x >> (8 * k)) & 0xFFu); }
+
+// Offset-binary code i (0..31) of a chunk.
+template <int P>
+__device__ __forceinline__ uint32_t chunk_ucode(const uint32_t (&w)[P], int i) {
+  const int b = i * P, j = b >> 5, o = b & 31;
+  if (o + P <= 32) return (w[j] >> o) & ((1u << P) - 1u);
+  return __builtin_amdgcn_alignbit(w[(j + 1) < P ? (j + 1) : j], w[j], o) & ((1u << P) - 1u);
+}
+
+// The 32 offset-binary codes of a chunk as floats (exact), in code order.
+template <int P>
+__device__ __forceinline__ void decode_chunk_u(const uint32_t (&w)[P], float (&u)[32]) {
+  if constexpr (P == 8) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) u[4 * j + k] = ubyte(w[j], k);
+  } else if constexpr (P == 4) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t lo = opaque(w[j] & 0x0F0F0F0Fu), hi = opaque((w[j] >> 4) & 0x0F0F0F0Fu);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        u[8 * j + 2 * k] = ubyte(lo, k);
+        u[8 * j + 2 * k + 1] = ubyte(hi, k);
+      }
+    }
+  } else if constexpr (P == 2) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint32_t f = opaque((w[j] >> (2 * s)) & 0x03030303u);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) u[16 * j + 4 * k + s] = ubyte(f, k);
+      }
+  } else if constexpr (P == 16) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      u[2 * j] = (float)(w[j] & 0xFFFFu);
+      u[2 * j + 1] = (float)(w[j] >> 16);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) u[i] = (float)chunk_ucode<P>(w, i);
+  }
+}
+
+// Signed codes q = u - 2^(P-1) as floats (exact).
 template <int P>
 __device__ __forceinline__ void decode_chunk(const uint32_t (&w)[P], float (&q)[32]) {
+  decode_chunk_u<P>(w, q);
 #pragma unroll
-  for (int i = 0; i < 32; ++i) q[i] = static_cast<float>(chunk_code<P>(w, i));
+  for (int i = 0; i < 32; ++i) q[i] -= (float)(1 << (P - 1));
 }
 
 struct LeafInfo {
@@ -123,6 +173,9 @@ constexpr int kUnitHdr = 32;          // words per unit header
   F(16, 2) F(16, 3) F(16, 4) F(16, 5) F(16, 6) F(16, 8) F(16, 16) \
   F(8, 2) F(8, 3) F(8, 4) F(8, 5) F(8, 6) F(8, 8) F(8, 16) \
   F(4, 2) F(4, 3) F(4, 4) F(4, 5) F(4, 6) F(4, 8) F(4, 16)
+
+// Expands F(S, P) for every code width at one leaf size.
+#define MTC_FOR_EACH_WIDTH(S, F) F(S, 2) F(S, 3) F(S, 4) F(S, 5) F(S, 6) F(S, 8) F(S, 16)
 
 #define MTC_LOG2_SIZE(S) ((S) == 32 ? 5 : (S) == 16 ? 4 : (S) == 8 ? 3 : 2)
 #define MTC_BUCKET_KEY(S, P) (MTC_LOG2_SIZE(S) | ((P) << 8))

@@ -3,10 +3,10 @@
 //
 //   k_fill_zero  : zero an fp32 buffer (used before dequant; no memset nodes)
 //   k_dequant    : stream -> dense W_hat (bit-exact q*s, +0.0 for P0)
-//   k_gemv<MT>   : fp32 decode path. One block per (unit, column-group range);
-//                  the unit's payload is staged in LDS, each wave owns one
-//                  column group and accumulates its 4 columns in registers
-//                  (no atomics), then reduces across lanes once.
+//   k_gemv<MT,FS>: fp32 decode path for M tiles of MT rows (FS: fp32 leaf
+//                  scales). One block per (unit, 4 column groups); waves walk
+//                  the block's step records, streaming payload into registers,
+//                  and accumulate 4 columns per lane; one reduction at the end.
 //   (the prefill path, k_gemm_tile over the tile stream, is in mtc_gemm.hip)
 //
 // Reference behaviour: mtc/kernels/gemm.py:124-210 (block loop: skip P0
@@ -131,21 +131,21 @@ __global__ __launch_bounds__(512) void k_dequant(const mtc_stream_desc d, float*
 // ---------------------------------------------------------------------------
 // fp32 decode GEMV
 //
-// Block = (unit, G adjacent column groups), V waves per column group. Only X
-// (gathered through row_perm) is staged in LDS. A column group's work is a list
-// of 64-chunk steps, each inside ONE bucket (a bucket of n chunks gives
-// ceil(n/64) steps), split into V contiguous ranges, one per wave; the bucket
-// entry of a step is read with scalar loads, so its kind dispatches on a scalar
-// register. Each lane streams its chunk's P payload dwords and its leaf word(s)
-// straight from memory into registers, one step ahead of the step it decodes,
-// and accumulates its column group's 4 columns (times MT rows) in registers;
-// lanes and waves are combined once at the end (no atomics). Blocks of one unit
-// are mapped to the same XCD so the unit's leaf words stay in one L2.
+// Block = (unit, block of 4 column groups), W waves. The block's work is its list of
+// step records; wave w executes records w, w + W, w + 2W, ... (round robin, so the
+// waves of each SIMD get near-equal counts). In a step, lane 16g + i decodes chunk
+// 16j + i of column-group slot g's bucket of the step's kind: one kind per step, so
+// the decode is a scalar (readfirstlane) switch into fully unrolled code. Each lane
+// streams its chunk's payload dwords and leaf word(s) straight from memory into
+// registers, the first three steps' loads before anything else, and accumulates its
+// column group's 4 columns (times MT rows) in registers. X (gathered through
+// row_perm) and its 4- and 8-row sums are staged in LDS. Lanes and waves are
+// combined once at the end (no atomics unless K is split over units). Blocks of one
+// unit are mapped to the same XCD so the unit's leaf words stay in one L2.
 // ---------------------------------------------------------------------------
 constexpr int kMaxP = 16;
 typedef uint32_t u32x16_t __attribute__((ext_vector_type(16)));   // a step's payload words (one SSA value)
 
-typedef const __attribute__((address_space(4))) uint32_t* cu32p;
 typedef const __attribute__((address_space(4))) int32_t* ci32p;
 
 // Loads of one step into a lane's registers: its chunk's payload dwords (w[0..P)), its
@@ -164,42 +164,76 @@ __device__ __forceinline__ u32x4_t ldu4(const uint32_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4u_t*>(p));
 }
 
-__device__ __forceinline__ void gemv_load(const uint32_t* __restrict__ pay, const uint32_t* __restrict__ lwp,
-                                          const float* __restrict__ fsp, const uint32_t* __restrict__ dummy,
-                                          bool fp32_scales, uint32_t key, uint32_t t, u32x16_t& w, uint32_t& lw0,
-                                          uint32_t& lw1, float& fs0, float& fs1) {
+// Loads at a 32-bit dword offset from a wave-uniform base: the offset is formed as a
+// 32-bit byte count so the load can use the scalar-base + vector-offset form.
+__device__ __forceinline__ u32x4_t ldu4_at(const uint32_t* base, uint32_t dw) {
+  return __builtin_nontemporal_load(
+      reinterpret_cast<const u32x4u_t*>(reinterpret_cast<const char*>(base) + (dw << 2)));
+}
+template <typename T>
+__device__ __forceinline__ T ld_at(const T* base, uint32_t i) {
+  return *reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + (i << 2));
+}
+
+template <bool FS>
+__device__ __forceinline__ void gemv_load(const uint32_t* __restrict__ pay_u, const uint32_t* __restrict__ lw_u,
+                                          const float* __restrict__ fs_u, uint32_t key, uint32_t pay, uint32_t leaf,
+                                          uint32_t t, u32x16_t& w, uint32_t& lw0, uint32_t& lw1, float& fs0,
+                                          float& fs1) {
   const uint32_t P = key >> 8, ls = key & 0xFFu;
-  const uint32_t* src = pay + t * P;
-  // loads a kind does not need read one wave-uniform address (a single cache line)
-  const u32x4_t a = ldu4(src);
-  const u32x4_t b = ldu4(P > 4 ? src + 4 : dummy);
-  const u32x4_t c = ldu4(P > 8 ? src + 8 : dummy);
-  const u32x4_t e = ldu4(P > 8 ? src + 12 : dummy);
+  const uint32_t off = pay + t * P;                  // dwords from the unit's payload
+  // loads a kind does not need read the unit's first 4 payload dwords (one line per wave)
+  const u32x4_t a = ldu4_at(pay_u, off);
+  const u32x4_t b = ldu4_at(pay_u, P > 4 ? off + 4 : 0u);
+  const u32x4_t c = ldu4_at(pay_u, P > 8 ? off + 8 : 0u);
+  const u32x4_t e = ldu4_at(pay_u, P > 8 ? off + 12 : 0u);
   w = __builtin_shufflevector(__builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7),
                               __builtin_shufflevector(c, e, 0, 1, 2, 3, 4, 5, 6, 7), 0, 1, 2, 3, 4, 5, 6, 7, 8, 9,
                               10, 11, 12, 13, 14, 15);
-  // leaf words and scales: always two loads each
-  const uint32_t l0 = ls == 2 ? 2 * t : t >> (ls - 3);
-  lw0 = lwp[l0];
-  lw1 = ls == 2 ? lwp[l0 + 1] : dummy[0];
-  fs0 = fp32_scales ? fsp[l0] : __uint_as_float(dummy[1]);
-  fs1 = fp32_scales && ls == 2 ? fsp[l0 + 1] : __uint_as_float(dummy[2]);
+  // leaf words (and fp32 scales): always two loads each; the second reads the unit's
+  // first leaf when the chunk has one leaf
+  const uint32_t l0 = leaf + (ls == 2 ? 2 * t : t >> (ls - 3));
+  const uint32_t l1 = ls == 2 ? l0 + 1 : 0u;
+  lw0 = ld_at(lw_u, l0);
+  lw1 = ld_at(lw_u, l1);
+  if constexpr (FS) {
+    fs0 = ld_at(fs_u, l0);
+    fs1 = ld_at(fs_u, l1);
+  } else {
+    fs0 = fs1 = 0.0f;
+  }
 }
 
-__device__ __forceinline__ float dot4(const float4 x, const float* q) {
-  return x.x * q[0] + x.y * q[1] + x.z * q[2] + x.w * q[3];
-}
+// X rows of a unit as staged in LDS: xs[m][r] = X[m0 + m, row_perm[kb + r]], plus the
+// sums of each 4-row and 8-row block (xs4[m][r / 4], xs8[m][r / 8]) that turn a chunk's
+// offset-binary dot product into the signed one: sum_r x_r q_r = sum_r x_r u_r - 2^(P-1) sum_r x_r.
+// Blocks of 4 M rows keep no 4-row sums (they add them from the x values instead), so
+// that two blocks of a 4096-row unit fit one CU's LDS.
+__host__ __device__ constexpr bool gemv_sum4(int MT) { return MT <= 2; }
 
-// One lane chunk (payload in registers) into the lane's 4-column accumulators.
+struct XStage {
+  const float* xs;
+  const float* xs4;
+  const float* xs8;
+  int kc;
+};
+
+// One lane chunk (payload in registers) into the lane's 4-column accumulators:
+// acc[m][c] += s * (sum_r x[m][r] * u[r][c] - off * sum_r x[m][r]) per leaf.
+// S = 4: two 4x4 leaves. S = 8 stands for every leaf size of 8 or more: chunk t is row
+// block t & rb_mask of its leaf (rb_mask = S / 8 - 1, wave-uniform), so the three sizes
+// share one code path.
 template <int S, int P, int MT>
 __device__ __forceinline__ void gemv_chunk(const u32x16_t rw, uint32_t lw0, uint32_t lw1, float fs0, float fs1,
-                                           bool fp32_scales, uint32_t t, const float* xs, int kc,
+                                           bool fp32_scales, uint32_t t, uint32_t rb_mask, const XStage& xt,
                                            float (&acc)[MT][kGroup]) {
+  static_assert(S == 4 || S == 8, "leaf sizes 16 and 32 take the S = 8 path");
+  constexpr float off = (float)(1 << (P - 1));
   uint32_t w[P];
 #pragma unroll
   for (int i = 0; i < P; ++i) w[i] = rw[i];
-  float q[32];
-  decode_chunk<P>(w, q);
+  float u[32];
+  decode_chunk_u<P>(w, u);
   if constexpr (S == 4) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -207,21 +241,46 @@ __device__ __forceinline__ void gemv_chunk(const u32x16_t rw, uint32_t lw0, uint
       if (li.pad) continue;
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
-        const float4 x = *reinterpret_cast<const float4*>(xs + m * kc + li.row);
+        const float4 x = *reinterpret_cast<const float4*>(xt.xs + m * xt.kc + li.row);
+        float x4;
+        if constexpr (gemv_sum4(MT)) {
+          x4 = xt.xs4[m * (xt.kc / 4) + (li.row >> 2)];
+        } else {
+          x4 = (x.x + x.y) + (x.z + x.w);
+        }
+        const float init = -off * x4;
 #pragma unroll
-        for (int c = 0; c < kGroup; ++c) acc[m][c] += li.scale * dot4(x, q + 16 * h + 4 * c);
+        for (int c = 0; c < kGroup; ++c) {
+          const float* q = u + 16 * h + 4 * c;
+          float dsum = __builtin_fmaf(x.x, q[0], init);
+          dsum = __builtin_fmaf(x.y, q[1], dsum);
+          dsum = __builtin_fmaf(x.z, q[2], dsum);
+          dsum = __builtin_fmaf(x.w, q[3], dsum);
+          acc[m][c] = __builtin_fmaf(li.scale, dsum, acc[m][c]);
+        }
       }
     }
   } else {
-    constexpr int NRB = S / 8;
     const LeafInfo li = leaf_info_v(lw0, fp32_scales, fs0);
-    const int row = li.row + 8 * (int)(t % NRB);
+    const int row = li.row + 8 * (int)(t & rb_mask);
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-      const float4 x0 = *reinterpret_cast<const float4*>(xs + m * kc + row);
-      const float4 x1 = *reinterpret_cast<const float4*>(xs + m * kc + row + 4);
+      const float4 x0 = *reinterpret_cast<const float4*>(xt.xs + m * xt.kc + row);
+      const float4 x1 = *reinterpret_cast<const float4*>(xt.xs + m * xt.kc + row + 4);
+      const float init = -off * xt.xs8[m * (xt.kc / 8) + (row >> 3)];
 #pragma unroll
-      for (int c = 0; c < kGroup; ++c) acc[m][c] += li.scale * (dot4(x0, q + 8 * c) + dot4(x1, q + 8 * c + 4));
+      for (int c = 0; c < kGroup; ++c) {
+        const float* q = u + 8 * c;
+        float dsum = __builtin_fmaf(x0.x, q[0], init);
+        dsum = __builtin_fmaf(x0.y, q[1], dsum);
+        dsum = __builtin_fmaf(x0.z, q[2], dsum);
+        dsum = __builtin_fmaf(x0.w, q[3], dsum);
+        dsum = __builtin_fmaf(x1.x, q[4], dsum);
+        dsum = __builtin_fmaf(x1.y, q[5], dsum);
+        dsum = __builtin_fmaf(x1.z, q[6], dsum);
+        dsum = __builtin_fmaf(x1.w, q[7], dsum);
+        acc[m][c] = __builtin_fmaf(li.scale, dsum, acc[m][c]);
+      }
     }
   }
 }
@@ -241,12 +300,11 @@ __device__ __forceinline__ float slot_sum(float v) {
   return v;
 }
 
-__device__ __forceinline__ uint32_t pick4(uint32_t a, uint32_t b, uint32_t c, uint32_t e, int g) {
-  return g == 0 ? a : g == 1 ? b : g == 2 ? c : e;
-}
 
-template <int MT>
-__global__ __launch_bounds__(64 * gemv_waves(MT)) void k_gemv(const mtc_stream_desc d, const float* __restrict__ X,
+// At least 4 waves per SIMD: a 16-wave block fills a CU's 4 SIMDs; two 8-wave blocks
+// (M tiles of 4 rows) share one only if each wave keeps to 128 VGPRs.
+template <int MT, bool FS>
+__global__ __launch_bounds__(64 * gemv_waves(MT), 4) void k_gemv(const mtc_stream_desc d, const float* __restrict__ X,
                                                           int64_t ldx, float* __restrict__ Y, int64_t ldy, int M,
                                                           float* __restrict__ part, uint32_t* __restrict__ counters) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
@@ -267,22 +325,42 @@ __global__ __launch_bounds__(64 * gemv_waves(MT)) void k_gemv(const mtc_stream_d
   const int rows = min(kc, d.K - kb);
 
   float* xs = smem;                                   // [MT][kc]
-  float* red = xs + MT * kc;                          // [waves][4 slots][MT][4]
+  float* xs4 = xs + MT * kc;                          // [MT][kc / 4] (MT <= 2 only)
+  float* xs8 = xs4 + (gemv_sum4(MT) ? MT * (kc / 4) : 0);   // [MT][kc / 8]
+  float* red = xs8 + MT * (kc / 8);                   // [waves][4 slots][MT][4]
 
   const ci32p hdr = (ci32p)(d.unit_hdr + kUnitHdr * u);
   const uint32_t* pay_u = d.payload + hdr[0];
   const uint32_t* lw_u = d.leaf_word + hdr[2];
-  // fp32 scales of the unit's leaves (a stand-in address that is never used otherwise)
-  const bool fscales = d.leaf_scale != nullptr;
-  const float* fs_u = fscales ? d.leaf_scale + hdr[2] : reinterpret_cast<const float*>(lw_u);
+  // fp32 scales of the unit's leaves (FS: the stream carries them instead of bf16 scales)
+  const float* fs_u = FS ? d.leaf_scale + hdr[2] : nullptr;
 
-  // ---- this wave's step records: [s_beg, s_end) of the block's list ----
+  // ---- X row indices first: they depend on nothing, so their latency overlaps the
+  //      header -> record -> payload chain below ----
+  constexpr int XG = kMaxChunkRows / (4 * T);        // 4-row groups per thread (kc <= kMaxChunkRows)
+  const bool perm = d.row_perm != nullptr;
+  int4 kk[XG];
+#pragma unroll
+  for (int i = 0; i < XG; ++i) {
+    const int r = 4 * (i * T + tid);                  // first of 4 rows, unit-relative
+    if (perm && r < rows) {
+      kk[i] = *reinterpret_cast<const int4*>(d.row_perm + kb + r);   // kb, r multiples of 4
+    } else {
+      kk[i] = make_int4(kb + r, kb + r + 1, kb + r + 2, kb + r + 3);
+    }
+  }
+
+  // ---- this wave's step records: records wave, wave + W, wave + 2W, ... of the block's list ----
   const int nrec = hdr[28 + 2 * cb];
-  const cu32p rec = (cu32p)(d.steps + (size_t)hdr[27 + 2 * cb] * kStepWords);
-  const int per = (nrec + W - 1) / W;
-  const int s_beg = min(wave * per, nrec), s_end = min(s_beg + per, nrec);
+  const uint32_t* rec = d.steps + (size_t)hdr[27 + 2 * cb] * kStepWords;
+  const int ns = wave < nrec ? (nrec - wave + W - 1) / W : 0;   // steps of this wave
   const int g = lane / kStepLanes, li = lane % kStepLanes;   // column-group slot, lane in slot
 
+  // A lane's slot of a record: [payload offset, first leaf, valid chunks, kind | j << 16]
+  // (16 bytes; the 16 lanes of a slot read the same words).
+  auto slot_of = [&](int k) __attribute__((always_inline)) {
+    return *reinterpret_cast<const u32x4_t*>(rec + (wave + k * W) * kStepWords + 4 * g);
+  };
   // A step's per-lane view: chunk t of this slot's bucket, active if li < valid chunks.
   // Inactive lanes load chunk 0 of the bucket (every referenced bucket has one).
   struct Regs {
@@ -292,52 +370,57 @@ __global__ __launch_bounds__(64 * gemv_waves(MT)) void k_gemv(const mtc_stream_d
     uint32_t t, key;
     bool on;
   };
-  auto fetch = [&](int st, Regs& r) __attribute__((always_inline)) {
-    const cu32p e = rec + st * kStepWords;
-    const uint32_t w0 = e[0];
-    const uint32_t pay = pick4(e[1], e[2], e[3], e[4], g);
-    const uint32_t leaf = pick4(e[5], e[6], e[7], e[8], g);
-    const uint32_t nv = pick4(e[9], e[10], e[11], e[12], g);
-    r.key = w0 & 0xFFFFu;
-    r.on = (uint32_t)li < nv;
-    r.t = r.on ? kStepLanes * (w0 >> 16) + li : 0u;
-    gemv_load(pay_u + pay, lw_u + leaf, fs_u + leaf, pay_u, fscales, r.key, r.t, r.w, r.lw0, r.lw1, r.fs0, r.fs1);
+  auto fetch = [&](const u32x4_t f, Regs& r) __attribute__((always_inline)) {
+    r.key = __builtin_amdgcn_readfirstlane(f.w & 0xFFFFu);   // one kind per record
+    r.on = (uint32_t)li < f.z;
+    r.t = r.on ? kStepLanes * (f.w >> 16) + li : 0u;
+    gemv_load<FS>(pay_u, lw_u, fs_u, r.key, f.x, f.y, r.t, r.w, r.lw0, r.lw1, r.fs0, r.fs1);
   };
 
-  // A wave has about ceil(records / 16) steps (3 for full-K units); the loads of its
-  // first kAhead steps all go out before X is staged, so their latency is paid once.
-  // All kAhead fetches are issued unconditionally (clamped to the wave's last step) so
-  // the compiler's waits before each decode are partial.
-  Regs r0{}, r1{}, r2{};
-  if (s_beg < s_end) {
-    fetch(s_beg, r0);
-    fetch(min(s_beg + 1, s_end - 1), r1);
-    fetch(min(s_beg + 2, s_end - 1), r2);
+  // A wave has about ceil(records / W) steps (3 for full-K units of a 4096-row matrix);
+  // the records of its first three steps are read together, then their payload loads
+  // all go out before X is staged, so the latency of each level is paid once. All three
+  // fetches are issued unconditionally (clamped to the wave's last step) so the
+  // compiler's waits before each decode are partial.
+  Regs r0, r1, r2;                                   // read only for steps the wave has
+  if (ns > 0) {
+    const u32x4_t f0 = slot_of(0), f1 = slot_of(min(1, ns - 1)), f2 = slot_of(min(2, ns - 1));
+    fetch(f0, r0);
+    fetch(f1, r1);
+    fetch(f2, r2);
   }
 
-  // ---- X rows of the unit into LDS while the first step's loads are in flight ----
-  {
-    constexpr int XR = kMaxChunkRows / T;
-    int kk[XR];
+  // ---- X rows of the unit (gathered) and their 4- and 8-row sums into LDS ----
 #pragma unroll
-    for (int i = 0; i < XR; ++i) {
-      const int r = kb + min(i * T + tid, rows - 1);
-      kk[i] = d.row_perm ? d.row_perm[r] : r;
+  for (int m = 0; m < MT; ++m) {
+    const float* xrow = X + (int64_t)min(m0 + m, M - 1) * ldx;
+    const bool mv = m0 + m < M;
+    float4 xv[XG];
+#pragma unroll
+    for (int i = 0; i < XG; ++i) {
+      const int r = 4 * (i * T + tid);
+      if (r < rows && mv) {
+        xv[i] = make_float4(xrow[kk[i].x], xrow[kk[i].y], xrow[kk[i].z], xrow[kk[i].w]);
+      } else {
+        xv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
     }
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const float* xrow = X + (int64_t)min(m0 + m, M - 1) * ldx;
-      float xv[XR];
-#pragma unroll
-      for (int i = 0; i < XR; ++i) xv[i] = (i * T < kc) ? xrow[kk[i]] : 0.0f;
-#pragma unroll
-      for (int i = 0; i < XR; ++i) {
-        const int rr = i * T + tid;
-        if (rr < kc) xs[m * kc + rr] = (rr < rows && m0 + m < M) ? xv[i] : 0.0f;
+    for (int i = 0; i < XG; ++i) {
+      const int r = 4 * (i * T + tid);
+      if (i * 4 * T < kc) {                           // wave-uniform: the loop covers kc rows
+        const float s4 = (xv[i].x + xv[i].y) + (xv[i].z + xv[i].w);
+        const float s8 = s4 + __shfl_xor(s4, 1, 64);  // rows r & ~7 .. +7: this lane and its pair
+        if (r < kc) {
+          *reinterpret_cast<float4*>(xs + m * kc + r) = xv[i];
+          if constexpr (gemv_sum4(MT)) xs4[m * (kc / 4) + (r >> 2)] = s4;
+          if ((r & 7) == 0) xs8[m * (kc / 8) + (r >> 3)] = s8;
+        }
       }
     }
   }
   __syncthreads();
+  const XStage xt{xs, xs4, xs8, kc};
 
   // ---- decode: the prefetched steps, then any further steps one at a time ----
   float acc[MT][kGroup];
@@ -347,23 +430,26 @@ __global__ __launch_bounds__(64 * gemv_waves(MT)) void k_gemv(const mtc_stream_d
     for (int c = 0; c < kGroup; ++c) acc[m][c] = 0.0f;
   auto compute = [&](const Regs& cur) __attribute__((always_inline)) {
     if (cur.on) {
-      switch (__builtin_amdgcn_readfirstlane(cur.key)) {
+      const uint32_t key = cur.key;
+      const uint32_t ls = key & 0xFFu;
+      const uint32_t rb_mask = ls > 3 ? (1u << (ls - 3)) - 1u : 0u;
+      switch (ls == 2 ? key : (key & ~0xFFu) | 3u) {   // sizes 8, 16, 32 share a case
 #define MTC_CASE(S, P) \
   case MTC_BUCKET_KEY(S, P): \
-    gemv_chunk<S, P, MT>(cur.w, cur.lw0, cur.lw1, cur.fs0, cur.fs1, fscales, cur.t, xs, kc, acc); \
+    gemv_chunk<S, P, MT>(cur.w, cur.lw0, cur.lw1, cur.fs0, cur.fs1, FS, cur.t, rb_mask, xt, acc); \
     break;
-        MTC_FOR_EACH_BUCKET(MTC_CASE)
+        MTC_FOR_EACH_WIDTH(8, MTC_CASE)
+        MTC_FOR_EACH_WIDTH(4, MTC_CASE)
 #undef MTC_CASE
         default: break;
       }
     }
   };
-  const int ns = s_end - s_beg;
   if (ns > 0) compute(r0);
   if (ns > 1) compute(r1);
   if (ns > 2) compute(r2);
-  for (int st = s_beg + 3; st < s_end; ++st) {
-    fetch(st, r0);
+  for (int k = 3; k < ns; ++k) {
+    fetch(slot_of(k), r0);
     compute(r0);
   }
 
@@ -461,6 +547,8 @@ int check_desc(const mtc_stream_desc* d) {
     return fail(MTC_E_DESC, "leaf_scale given but MTC_FLAG_FP32_SCALES not set");
   if (d->n_steps < 0 || (d->n_buckets > 0 && (!d->steps || d->n_steps == 0)))
     return fail(MTC_E_NULL, "decode step records missing (n_steps=%lld)", (long long)d->n_steps);
+  if ((reinterpret_cast<uintptr_t>(d->payload) | reinterpret_cast<uintptr_t>(d->row_perm)) % 16)
+    return fail(MTC_E_DESC, "payload and row_perm must be 16-byte aligned");
   return ok();
 }
 
@@ -479,8 +567,11 @@ size_t gemv_ws_layout(const mtc_stream_desc* d, int M, size_t* counters_bytes) {
   return cb + n_mt * (size_t)d->n_panels * d->n_chunks * mt * kPanel * sizeof(float);
 }
 
+// LDS of a decode block: X rows, their 4- and 8-row sums, and the cross-wave reduction.
 size_t gemv_lds_bytes(const mtc_stream_desc* d, int MT) {
-  return ((size_t)MT * d->chunk_rows + (size_t)gemv_waves(MT) * kStepGroups * MT * kGroup) * 4;
+  const size_t kc = (size_t)d->chunk_rows;
+  return ((size_t)MT * (kc + (gemv_sum4(MT) ? kc / 4 : 0) + kc / 8) +
+          (size_t)gemv_waves(MT) * kStepGroups * MT * kGroup) * 4;
 }
 
 template <int MT>
@@ -495,16 +586,22 @@ int launch_gemv(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y,
   if (shmem > limit)
     return fail(MTC_E_SHAPE, "fp32 path: %d rows x chunk_rows=%d needs %zu B of LDS (limit %zu); "
                 "use a stream with smaller chunk_rows", MT, d->chunk_rows, shmem, limit);
+  const bool fs = d->leaf_scale != nullptr;
+  const void* kern = fs ? reinterpret_cast<const void*>(&k_gemv<MT, true>) : reinterpret_cast<const void*>(&k_gemv<MT, false>);
   if (shmem > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv<MT>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
+    hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
     if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
   }
   const int n_units = d->n_panels * d->n_chunks;
   const int units_padded = (n_units + kXcds - 1) / kXcds * kXcds;
   dim3 grid(units_padded * kGemvBlocksPerUnit, (M + MT - 1) / MT);
-  hipLaunchKernelGGL(k_gemv<MT>, grid, dim3(64 * gemv_waves(MT)), shmem, st, *d, X, ldx, Y, ldy, M, part,
-                     counters);
+  if (fs) {
+    hipLaunchKernelGGL((k_gemv<MT, true>), grid, dim3(64 * gemv_waves(MT)), shmem, st, *d, X, ldx, Y, ldy, M, part,
+                       counters);
+  } else {
+    hipLaunchKernelGGL((k_gemv<MT, false>), grid, dim3(64 * gemv_waves(MT)), shmem, st, *d, X, ldx, Y, ldy, M, part,
+                       counters);
+  }
   return check_launch("k_gemv");
 }
 

@@ -53,11 +53,13 @@ def gemv_chunk_rows(K: int, N: int, M: int = 1) -> int:
 
 
 def _decode_lds_need(ps: PanelStream, M: int) -> int:
-    """LDS bytes of one decode block: the gathered X rows plus the per-wave partial sums
-    (mirrors gemv_lds_bytes in csrc/mtc_hip.hip; the payload streams through registers)."""
+    """LDS bytes of one decode block: the gathered X rows, their 8-row (and, for M tiles
+    of 1-2 rows, 4-row) sums, and the per-wave partial sums (mirrors gemv_lds_bytes in
+    csrc/mtc_hip.hip; the payload streams through registers)."""
     mt = _decode_mt(M)
     waves = 16 if mt <= 2 else 8
-    return 4 * (mt * ps.chunk_rows + waves * 4 * mt * 4)
+    kc = ps.chunk_rows
+    return 4 * (mt * (kc + (kc // 4 if mt <= 2 else 0) + kc // 8) + waves * 4 * mt * 4)
 
 
 # ---------------------------------------------------------------------------------------

@@ -35,7 +35,7 @@ LEAF_PAD = 1 << 13
 ROW_BITS = 10                          # leaf word: row/4 in bits 0-9
 MAX_CHUNK_ROWS = 4 << ROW_BITS         # 4096
 UNIT_HDR_WORDS = 32
-STREAM_FORMAT = 5                      # panel stream layout version (matches the C-ABI version)
+STREAM_FORMAT = 6                      # panel stream layout version (matches the C-ABI version)
 PAYLOAD_PAD = 4                        # dwords after the last bucket
 STEP_GROUPS = 4                        # column groups one decode step covers
 STEP_LANES = 16                        # lanes (chunks) per column group in a step
@@ -117,9 +117,12 @@ class PanelStream:
 
 
 def pack_codes(codes: np.ndarray, P: int) -> np.ndarray:
-    """(n, 32) signed codes -> (n, P) uint32; code i at bits [i*P, i*P+P) of the chunk."""
+    """(n, 32) signed codes q -> (n, P) uint32 of offset-binary codes u = q + 2^(P-1);
+    code i at bits [i*P, i*P+P) of the chunk."""
     n = codes.shape[0]
-    u = (codes.astype(np.int64) & ((1 << P) - 1)).astype(np.uint64)
+    u = (codes.astype(np.int64) + (1 << (P - 1))).astype(np.uint64)
+    if np.any(u >> np.uint64(P)):
+        raise ValueError(f"codes outside the signed {P}-bit range")
     out = np.zeros((n, P), dtype=np.uint64)
     for i in range(32):
         bit = i * P
@@ -143,8 +146,7 @@ def unpack_codes(words: np.ndarray, P: int) -> np.ndarray:
         if sh + P > 32:
             v |= w[:, j + 1] << np.uint64(32 - sh)
         v &= mask
-        out[:, i] = v.astype(np.int64)
-    out[out >= (1 << (P - 1))] -= 1 << P
+        out[:, i] = v.astype(np.int64) - (1 << (P - 1))
     return out.astype(np.int32)
 
 
@@ -370,13 +372,13 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
         j = np.arange(rec_g.size) - np.repeat(np.concatenate([[0], np.cumsum(g_steps)[:-1]]), g_steps)
         bb = gb[rec_g]
         u_of = b_unit[bb[:, 0]]
-        steps = np.zeros((rec_g.size, STEP_WORDS), dtype=np.int64)
+        steps = np.zeros((rec_g.size, STEP_GROUPS, 4), dtype=np.int64)      # slot g = words 4g .. 4g+3
         b_key = np.array([_LOG2[int(v)] for v in b_S], dtype=np.int64) | (b_P.astype(np.int64) << 8)
-        steps[:, 0] = b_key[bb[:, 0]] | (j << 16)
-        steps[:, 1:5] = b_pay[bb] - hdr[u_of, 0][:, None]
-        steps[:, 5:9] = b_leaf[bb] - hdr[u_of, 2][:, None]
-        steps[:, 9:13] = np.clip(g_n[rec_g] - STEP_LANES * j[:, None], 0, STEP_LANES)
-        steps = steps.astype(np.uint32)
+        steps[:, :, 0] = b_pay[bb] - hdr[u_of, 0][:, None]
+        steps[:, :, 1] = b_leaf[bb] - hdr[u_of, 2][:, None]
+        steps[:, :, 2] = np.clip(g_n[rec_g] - STEP_LANES * j[:, None], 0, STEP_LANES)
+        steps[:, :, 3] = (b_key[bb[:, 0]] | (j << 16))[:, None]
+        steps = steps.reshape(rec_g.size, STEP_WORDS).astype(np.uint32)
         rec_blk = b_unit[first][rec_g] * 2 + blk[first][rec_g]
         blk_begin = np.searchsorted(rec_blk, np.arange(n_units * 2 + 1)).astype(np.int64)
     hdr[:, 27] = blk_begin[0:-1:2]
@@ -452,18 +454,18 @@ def decode_stream(ps: PanelStream) -> np.ndarray:
 def decode_steps(ps: PanelStream) -> np.ndarray:
     """Host decoder that walks the step records the way the decode kernel does: for
     each unit and block of 4 column groups, records [hdr[27 + 2b], +hdr[28 + 2b]);
-    lane li of slot g takes chunk 16 * j + li of that slot's bucket when li is below
-    the slot's valid-chunk count. A debugging aid; the GPU path never calls it."""
+    slot g of a record is words 4g .. 4g+3 (payload offset, first leaf, valid chunks,
+    kind | j << 16), and lane li of the slot takes chunk 16 * j + li of that bucket
+    when li is below the valid-chunk count. A debugging aid; the GPU path never calls it."""
     Wp = np.zeros((ps.K, ps.N), dtype=np.float32)
     for u in range(ps.n_units):
         h = [int(x) for x in ps.unit_hdr[u]]
         for blk in range(N_GROUPS // STEP_GROUPS):
             beg, cnt = h[27 + 2 * blk], h[28 + 2 * blk]
             for e in ps.steps[beg: beg + cnt]:
-                e = [int(x) for x in e]
-                key, j = e[0] & 0xFFFF, e[0] >> 16
                 for g in range(STEP_GROUPS):
-                    nv = e[9 + g]
+                    pay, leaf, nv, kj = (int(x) for x in e[4 * g: 4 * g + 4])
+                    key, j = kj & 0xFFFF, kj >> 16
                     _place_chunks(ps, Wp, u, blk * STEP_GROUPS + g, 1 << (key & 0xFF), key >> 8,
-                                  h[0] + e[1 + g], h[2] + e[5 + g], STEP_LANES * j + np.arange(nv))
+                                  h[0] + pay, h[2] + leaf, STEP_LANES * j + np.arange(nv))
     return _to_original_order(ps, Wp)

@@ -35,9 +35,14 @@ def test_pack_codes_round_trip_and_bit_order(P):
     w = pack_codes(q, P)
     assert w.shape == (9, P)
     assert np.array_equal(unpack_codes(w, P), q)
-    one = np.zeros((1, 32), np.int64)
-    one[0, 1] = 1                                     # code 1 starts at bit P
-    assert pack_codes(one, P)[0, (P) // 32] == 1 << (P % 32)
+    # offset-binary: q = -2^(P-1) packs to all-zero bits; u = 1 for code 1 starts at bit P
+    one = np.full((1, 32), lo, np.int64)
+    one[0, 1] = lo + 1
+    w1 = pack_codes(one, P)
+    assert w1[0, P // 32] == 1 << (P % 32) and int(w1.astype(np.int64).sum()) == 1 << (P % 32)
+    assert np.all(pack_codes(np.zeros((1, 32), np.int64), P)[0] != 0)
+    with pytest.raises(ValueError):
+        pack_codes(np.full((1, 32), hi + 1), P)
 
 
 CASES = [(QuadtreeRD, 2.2), (QuadtreeRD, 4.25), (QuadtreeRD, 9.0), (QuadtreeRD, 15.0),
@@ -175,24 +180,25 @@ def test_step_records_cover_every_chunk_once():
     assert np.all(h[:, 29] == h[:, 27] + h[:, 28])
     assert np.all(h[1:, 27] == h[:-1, 29] + h[:-1, 30]) and h[0, 27] == 0
     assert h[-1, 29] + h[-1, 30] == st.shape[0]
-    nv = st[:, 9:13]
+    sl = st.reshape(-1, STEP_GROUPS, 4)
+    nv = sl[:, :, 2]
     assert nv.min() >= 0 and nv.max() <= STEP_LANES and np.all(nv.max(axis=1) > 0)
-    assert np.all(st[:, 13:] == 0)
+    assert np.all(sl[:, :, 3] == sl[:, :1, 3])            # one kind and step index per record
     seen = {}
     for u in range(ps.n_units):
         for blk in range(2):
-            recs = st[h[u, 27 + 2 * blk]: h[u, 27 + 2 * blk] + h[u, 28 + 2 * blk]]
+            recs = sl[h[u, 27 + 2 * blk]: h[u, 27 + 2 * blk] + h[u, 28 + 2 * blk]]
             for e in recs:
-                key, j = int(e[0] & 0xFFFF), int(e[0] >> 16)
+                key, j = int(e[0, 3] & 0xFFFF), int(e[0, 3] >> 16)
                 for g in range(STEP_GROUPS):
                     cg = blk * STEP_GROUPS + g
                     # the slot's offsets name one of this column group's buckets of the same kind
                     b = [k for k in range(h[u, 4] + h[u, 8 + cg], h[u, 4] + h[u, 9 + cg])
-                         if ps.buckets[k, 0] == e[1 + g] and ps.buckets[k, 1] == e[5 + g]]
-                    if e[9 + g] == 0:
+                         if ps.buckets[k, 0] == e[g, 0] and ps.buckets[k, 1] == e[g, 1]]
+                    if e[g, 2] == 0:
                         continue
                     assert len(b) == 1 and int(ps.buckets[b[0], 3]) == key
-                    for t in range(STEP_LANES * j, STEP_LANES * j + int(e[9 + g])):
+                    for t in range(STEP_LANES * j, STEP_LANES * j + int(e[g, 2])):
                         assert (b[0], t) not in seen
                         seen[(b[0], t)] = 1
     expect = {(k, t) for k in range(ps.n_buckets) for t in range(int(ps.buckets[k, 2] & 0xFFFF))}
