@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MTC_ABI_VERSION 6
+#define MTC_ABI_VERSION 7
 
 enum {
   MTC_OK = 0,
@@ -63,8 +63,9 @@ enum { MTC_DTYPE_F32 = 0, MTC_DTYPE_BF16 = 1 };
  *  unit_hdr[32*u + 8..16]  : bucket offset of cg 0..8, relative to the unit's first bucket
  *  unit_hdr[32*u + 17..25] : payload offset of cg 0..8 in dwords, relative to the unit's payload
  *  unit_hdr[32*u + 26]     : as word 7 for blocks of four column groups
- *  unit_hdr[32*u + 27..28] : first step record and record count of column groups 0-3
- *  unit_hdr[32*u + 29..30] : the same for column groups 4-7
+ *  unit_hdr[32*u + 27..28] : overflow start (a record index) and record count of decode block 0
+ *                            (column groups 0-3)
+ *  unit_hdr[32*u + 29..30] : the same for decode block 1 (column groups 4-7)
  *  buckets[4*b + 0] : payload offset of the bucket in dwords, relative to the unit (multiple of 4)
  *  buckets[4*b + 1] : first leaf word of the bucket, relative to the unit
  *  buckets[4*b + 2] : lane chunks in the bucket (bits 0-15) | first chunk within its cg (bits 16-31)
@@ -72,17 +73,21 @@ enum { MTC_DTYPE_F32 = 0, MTC_DTYPE_BF16 = 1 };
  *  leaf_word[l]     : bits 0-9 row offset in the unit / 4, bit 13 pad leaf (ignored),
  *                     bits 16-31 bf16 scale
  *  leaf_scale[l]    : fp32 scale (only with MTC_FLAG_FP32_SCALES)
- *  steps[16*r + ..] : decode step record: one per (unit, block of 4 column groups, bucket
- *                     kind, 16-chunk step j), ordered by unit, block, kind, j:
- *                     word 0 = kind key (bits 0-15) | j << 16; words 1-4 = payload offset
- *                     (unit-relative dwords) of the kind's bucket in each of the 4 column
- *                     groups; words 5-8 = its first leaf word (unit-relative); words 9-12 =
- *                     chunks of that bucket in this step, min(max(n - 16j, 0), 16) (0: the
- *                     group has no bucket of the kind; its offsets then name another
- *                     existing bucket); words 13-15 = 0
+ *  steps[16*r + ..] : decode step records. Decode block B = 2*u + b (unit u, block b of 4
+ *                     column groups) owns count = unit_hdr[32*u + 28 + 2b] records, ordered by
+ *                     bucket kind, then 16-chunk step j. Its record i < F = fixed_steps is
+ *                     steps record B*F + i; record i >= F is record overflow_start + i - F.
+ *                     Record n_blocks*F (n_blocks = 2 * n_units) and unused fixed places are
+ *                     null records (no valid chunks). A record is 4 slots, one per column
+ *                     group of the block; slot g = words 4g..4g+3: absolute payload offset
+ *                     (dwords) of the kind's bucket in that column group, its absolute first
+ *                     leaf-word index, the bucket's chunks in this step, min(max(n - 16j, 0),
+ *                     16) (0: no bucket of the kind; the offsets then name another existing
+ *                     bucket, or payload dword 0 and leaf word 0), and kind key | j << 16.
  *
  * The payload array extends at least 4 dwords past the last bucket (the kernels read
- * chunks with 16-byte loads that may run up to 3 dwords past a chunk's end).
+ * chunks with 16-byte loads that may run up to 3 dwords past a chunk's end); leaf_word
+ * holds at least one word.
  *
  * A lane chunk is 32 codes in P dwords: code i occupies bits [i*P, i*P+P) of
  * the little-endian bit string, stored offset-binary (u = q + 2^(P-1), so the
@@ -106,6 +111,8 @@ typedef struct mtc_stream_desc {
   int32_t n_buckets;
   int32_t max_unit_words;  /* max over units of unit_hdr[32*u + 7] */
   int32_t max_unit_words4; /* max over units of unit_hdr[32*u + 26] */
+  int32_t fixed_steps;     /* step records per decode block at fixed positions: 0, 16, 32 or 48 */
+  int32_t reserved;        /* 0 */
   int64_t n_leaves;
   int64_t payload_dwords;
   const uint32_t* payload;

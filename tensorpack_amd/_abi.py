@@ -2,7 +2,7 @@
 
 import ctypes
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 MTC_OK = 0
 MTC_DTYPE_F32 = 0
@@ -31,6 +31,8 @@ class MtcStreamDesc(ctypes.Structure):
         ("n_buckets", ctypes.c_int32),
         ("max_unit_words", ctypes.c_int32),
         ("max_unit_words4", ctypes.c_int32),
+        ("fixed_steps", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
         ("n_leaves", ctypes.c_int64),
         ("payload_dwords", ctypes.c_int64),
         ("payload", ctypes.c_void_p),

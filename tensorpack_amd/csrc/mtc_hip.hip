@@ -164,44 +164,85 @@ __device__ __forceinline__ u32x4_t ldu4(const uint32_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4u_t*>(p));
 }
 
-// Loads at a 32-bit dword offset from a wave-uniform base: the offset is formed as a
-// 32-bit byte count so the load can use the scalar-base + vector-offset form.
-__device__ __forceinline__ u32x4_t ldu4_at(const uint32_t* base, uint32_t dw) {
-  return __builtin_nontemporal_load(
-      reinterpret_cast<const u32x4u_t*>(reinterpret_cast<const char*>(base) + (dw << 2)));
-}
-template <typename T>
-__device__ __forceinline__ T ld_at(const T* base, uint32_t i) {
-  return *reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + (i << 2));
+typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
+
+// Workgroup barrier that orders LDS only: waits for this wave's LDS accesses, not for its
+// global loads, which may stay in flight across it (__syncthreads() waits for both).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Buffer resources: a wave-uniform base and byte size in scalar registers, so every load
+// is one instruction with a 32-bit per-lane byte offset, and an offset past the end
+// reads zeros instead of faulting.
+constexpr int kBufferFormat = 0x00020000;            // dword 3 of a raw gfx9 buffer resource
+constexpr int kNT = 2;                               // load cache policy: nontemporal
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                           (int)min(bytes, (int64_t)0x7FFFFFFF), kBufferFormat);
+}
+
+// A step's loads into a lane's registers. Every kind issues the same number of load
+// instructions (2 payload, 2 leaf-word and, with fp32 scales, 2 scale loads), so the
+// compiler's in-order wait counts stay exact across steps of different kinds; each load
+// reads only what the kind needs (the vector memory pipeline's cost grows with lanes x
+// bytes even when lanes share an address), and a load a kind does not need reads past
+// the buffer's end, which returns zeros without a memory access. Payload dwords 8-15 of
+// a P = 16 chunk are loaded when the chunk is decoded (gemv_load_p16_tail).
+constexpr uint32_t kOutOfRange = 0xFFFFFF00u;        // byte offset past any buffer's end
+
 template <bool FS>
-__device__ __forceinline__ void gemv_load(const uint32_t* __restrict__ pay_u, const uint32_t* __restrict__ lw_u,
-                                          const float* __restrict__ fs_u, uint32_t key, uint32_t pay, uint32_t leaf,
-                                          uint32_t t, u32x16_t& w, uint32_t& lw0, uint32_t& lw1, float& fs0,
-                                          float& fs1) {
+__device__ __forceinline__ void gemv_load(__amdgpu_buffer_rsrc_t pay_r, __amdgpu_buffer_rsrc_t lw_r,
+                                          __amdgpu_buffer_rsrc_t fs_r, uint32_t key, uint32_t pay, uint32_t leaf,
+                                          uint32_t t, u32x16_t& w, uint32_t& ob, uint32_t& lw0, uint32_t& lw1,
+                                          float& fs0, float& fs1) {
   const uint32_t P = key >> 8, ls = key & 0xFFu;
-  const uint32_t off = pay + t * P;                  // dwords from the unit's payload
-  // loads a kind does not need read the unit's first 4 payload dwords (one line per wave)
-  const u32x4_t a = ldu4_at(pay_u, off);
-  const u32x4_t b = ldu4_at(pay_u, P > 4 ? off + 4 : 0u);
-  const u32x4_t c = ldu4_at(pay_u, P > 8 ? off + 8 : 0u);
-  const u32x4_t e = ldu4_at(pay_u, P > 8 ? off + 12 : 0u);
-  w = __builtin_shufflevector(__builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7),
-                              __builtin_shufflevector(c, e, 0, 1, 2, 3, 4, 5, 6, 7), 0, 1, 2, 3, 4, 5, 6, 7, 8, 9,
-                              10, 11, 12, 13, 14, 15);
-  // leaf words (and fp32 scales): always two loads each; the second reads the unit's
-  // first leaf when the chunk has one leaf
+  ob = (pay + t * P) << 2;                           // payload byte offset of the chunk
+  if (P <= 4) {
+    if (P == 2) {
+      const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(pay_r, ob, 0, kNT);
+      w[0] = v.x; w[1] = v.y;
+    } else if (P == 3) {
+      const u32x3_t v = __builtin_amdgcn_raw_buffer_load_b96(pay_r, ob, 0, kNT);
+      w[0] = v.x; w[1] = v.y; w[2] = v.z;
+    } else {
+      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(pay_r, ob, 0, kNT);
+      w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    }
+    w[15] = __builtin_amdgcn_raw_buffer_load_b32(pay_r, kOutOfRange, 0, 0);   // count keeper
+  } else {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(pay_r, ob, 0, kNT);
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    if (P == 5) {
+      w[4] = __builtin_amdgcn_raw_buffer_load_b32(pay_r, ob + 16, 0, kNT);
+    } else if (P == 6) {
+      const u32x2_t e = __builtin_amdgcn_raw_buffer_load_b64(pay_r, ob + 16, 0, kNT);
+      w[4] = e.x; w[5] = e.y;
+    } else {
+      const u32x4_t e = __builtin_amdgcn_raw_buffer_load_b128(pay_r, ob + 16, 0, kNT);
+      w[4] = e.x; w[5] = e.y; w[6] = e.z; w[7] = e.w;
+    }
+  }
   const uint32_t l0 = leaf + (ls == 2 ? 2 * t : t >> (ls - 3));
-  const uint32_t l1 = ls == 2 ? l0 + 1 : 0u;
-  lw0 = ld_at(lw_u, l0);
-  lw1 = ld_at(lw_u, l1);
+  const uint32_t b1 = ls == 2 ? (l0 + 1) << 2 : kOutOfRange;   // second 4x4 leaf, if any
+  lw0 = __builtin_amdgcn_raw_buffer_load_b32(lw_r, l0 << 2, 0, 0);
+  lw1 = __builtin_amdgcn_raw_buffer_load_b32(lw_r, b1, 0, 0);
   if constexpr (FS) {
-    fs0 = ld_at(fs_u, l0);
-    fs1 = ld_at(fs_u, l1);
+    fs0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(fs_r, l0 << 2, 0, 0));
+    fs1 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(fs_r, b1, 0, 0));
   } else {
     fs0 = fs1 = 0.0f;
   }
+}
+
+__device__ __forceinline__ u32x16_t gemv_load_p16_tail(__amdgpu_buffer_rsrc_t pay_r, u32x16_t w, uint32_t ob) {
+  const u32x4_t f = __builtin_amdgcn_raw_buffer_load_b128(pay_r, ob + 32, 0, kNT);
+  const u32x4_t h = __builtin_amdgcn_raw_buffer_load_b128(pay_r, ob + 48, 0, kNT);
+  w[8] = f.x; w[9] = f.y; w[10] = f.z; w[11] = f.w;
+  w[12] = h.x; w[13] = h.y; w[14] = h.z; w[15] = h.w;
+  return w;
 }
 
 // X rows of a unit as staged in LDS: xs[m][r] = X[m0 + m, row_perm[kb + r]], plus the
@@ -210,6 +251,13 @@ __device__ __forceinline__ void gemv_load(const uint32_t* __restrict__ pay_u, co
 // Blocks of 4 M rows keep no 4-row sums (they add them from the x values instead), so
 // that two blocks of a 4096-row unit fit one CU's LDS.
 __host__ __device__ constexpr bool gemv_sum4(int MT) { return MT <= 2; }
+
+// Whole X rows are staged and gathered in LDS when there is a row permutation, the M tile
+// has 1-2 rows and K <= 4096 (at most 32 KB per block).
+__host__ __device__ constexpr int gemv_lds_gather_rows(int MT) { return MT <= 2 ? MT : 1; }
+__host__ __device__ constexpr bool gemv_lds_gather(int MT, bool perm, int K) {
+  return perm && MT <= 2 && K <= kMaxChunkRows;
+}
 
 struct XStage {
   const float* xs;
@@ -291,6 +339,7 @@ constexpr int kStepWords = 16;              // words per step record
 // waves per block: 16 for M tiles of 1-2 rows, 8 for 4 rows (more accumulators per lane)
 __host__ __device__ constexpr int gemv_waves(int MT) { return MT <= 2 ? 16 : 8; }
 constexpr int kGemvBlocksPerUnit = kGroups / kStepGroups;
+constexpr int kMaxFixedSteps = 48;          // step records per block at block-computable positions
 constexpr int kXcds = 8;
 
 // Sum over the 16 lanes of a lane's column-group slot.
@@ -303,7 +352,7 @@ __device__ __forceinline__ float slot_sum(float v) {
 
 // At least 4 waves per SIMD: a 16-wave block fills a CU's 4 SIMDs; two 8-wave blocks
 // (M tiles of 4 rows) share one only if each wave keeps to 128 VGPRs.
-template <int MT, bool FS>
+template <int MT, bool FS, bool LG>
 __global__ __launch_bounds__(64 * gemv_waves(MT), 4) void k_gemv(const mtc_stream_desc d, const float* __restrict__ X,
                                                           int64_t ldx, float* __restrict__ Y, int64_t ldy, int M,
                                                           float* __restrict__ part, uint32_t* __restrict__ counters) {
@@ -328,17 +377,20 @@ __global__ __launch_bounds__(64 * gemv_waves(MT), 4) void k_gemv(const mtc_strea
   float* xs4 = xs + MT * kc;                          // [MT][kc / 4] (MT <= 2 only)
   float* xs8 = xs4 + (gemv_sum4(MT) ? MT * (kc / 4) : 0);   // [MT][kc / 8]
   float* red = xs8 + MT * (kc / 8);                   // [waves][4 slots][MT][4]
+  float* xraw = red + W * kStepGroups * MT * kGroup;  // [MT][K] whole X rows (LDS gather only)
 
   const ci32p hdr = (ci32p)(d.unit_hdr + kUnitHdr * u);
-  const uint32_t* pay_u = d.payload + hdr[0];
-  const uint32_t* lw_u = d.leaf_word + hdr[2];
-  // fp32 scales of the unit's leaves (FS: the stream carries them instead of bf16 scales)
-  const float* fs_u = FS ? d.leaf_scale + hdr[2] : nullptr;
 
-  // ---- X row indices first: they depend on nothing, so their latency overlaps the
-  //      header -> record -> payload chain below ----
+  // ---- X first: its loads depend on nothing, so their latency overlaps the record ->
+  //      payload chain below. With a row permutation and X rows that fit on chip (M tiles
+  //      of 1-2 rows, K <= 4096), the rows are read whole and gathered in LDS, so X is one
+  //      load level away and the decode can start before the last payload arrives;
+  //      otherwise the permuted row indices are read here and X is gathered from memory
+  //      after the payload loads are out. ----
   constexpr int XG = kMaxChunkRows / (4 * T);        // 4-row groups per thread (kc <= kMaxChunkRows)
+  constexpr int XR = kMaxChunkRows / T;              // whole-row X values per thread and M row
   const bool perm = d.row_perm != nullptr;
+  constexpr bool lds_gather = LG;                    // host: gemv_lds_gather(MT, perm, K)
   int4 kk[XG];
 #pragma unroll
   for (int i = 0; i < XG; ++i) {
@@ -349,23 +401,42 @@ __global__ __launch_bounds__(64 * gemv_waves(MT), 4) void k_gemv(const mtc_strea
       kk[i] = make_int4(kb + r, kb + r + 1, kb + r + 2, kb + r + 3);
     }
   }
+  float xr[gemv_lds_gather_rows(MT)][XR];
+  if constexpr (lds_gather) {
+#pragma unroll
+    for (int m = 0; m < gemv_lds_gather_rows(MT); ++m) {
+      const float* xrow = X + (int64_t)min(m0 + m, M - 1) * ldx;
+#pragma unroll
+      for (int i = 0; i < XR; ++i) {
+        const int k = i * T + tid;
+        xr[m][i] = (k < d.K && m0 + m < M) ? xrow[k] : 0.0f;
+      }
+    }
+  }
 
-  // ---- this wave's step records: records wave, wave + W, wave + 2W, ... of the block's list ----
-  const int nrec = hdr[28 + 2 * cb];
-  const uint32_t* rec = d.steps + (size_t)hdr[27 + 2 * cb] * kStepWords;
-  const int ns = wave < nrec ? (nrec - wave + W - 1) / W : 0;   // steps of this wave
+  // ---- this wave's step records: records wave, wave + W, wave + 2W, ... of the block's list.
+  //      A block's first F records sit at block-computable places, so the first three steps'
+  //      records are read without waiting for the unit header. ----
+  const int F = d.fixed_steps;
+  const int blk = u * BPU + cb;
+  const uint32_t null_rec = (uint32_t)(d.n_panels * d.n_chunks * BPU) * (uint32_t)F;
   const int g = lane / kStepLanes, li = lane % kStepLanes;   // column-group slot, lane in slot
 
   // A lane's slot of a record: [payload offset, first leaf, valid chunks, kind | j << 16]
   // (16 bytes; the 16 lanes of a slot read the same words).
-  auto slot_of = [&](int k) __attribute__((always_inline)) {
-    return *reinterpret_cast<const u32x4_t*>(rec + (wave + k * W) * kStepWords + 4 * g);
+  const __amdgpu_buffer_rsrc_t rec_r = buffer_of(d.steps, d.n_steps * kStepWords * 4);
+  const __amdgpu_buffer_rsrc_t pay_r = buffer_of(d.payload, d.payload_dwords * 4);
+  const __amdgpu_buffer_rsrc_t lw_r = buffer_of(d.leaf_word, d.n_leaves * 4);
+  const __amdgpu_buffer_rsrc_t fs_r =
+      buffer_of(FS ? static_cast<const void*>(d.leaf_scale) : static_cast<const void*>(d.leaf_word), d.n_leaves * 4);
+  auto slot_of = [&](uint32_t r) __attribute__((always_inline)) {
+    return __builtin_amdgcn_raw_buffer_load_b128(rec_r, (r * kStepWords + 4 * g) * 4, 0, 0);
   };
   // A step's per-lane view: chunk t of this slot's bucket, active if li < valid chunks.
   // Inactive lanes load chunk 0 of the bucket (every referenced bucket has one).
   struct Regs {
     u32x16_t w;
-    uint32_t lw0, lw1;
+    uint32_t ob, lw0, lw1;
     float fs0, fs1;
     uint32_t t, key;
     bool on;
@@ -374,35 +445,65 @@ __global__ __launch_bounds__(64 * gemv_waves(MT), 4) void k_gemv(const mtc_strea
     r.key = __builtin_amdgcn_readfirstlane(f.w & 0xFFFFu);   // one kind per record
     r.on = (uint32_t)li < f.z;
     r.t = r.on ? kStepLanes * (f.w >> 16) + li : 0u;
-    gemv_load<FS>(pay_u, lw_u, fs_u, r.key, f.x, f.y, r.t, r.w, r.lw0, r.lw1, r.fs0, r.fs1);
+    gemv_load<FS>(pay_r, lw_r, fs_r, r.key, f.x, f.y, r.t, r.w, r.ob, r.lw0, r.lw1, r.fs0, r.fs1);
   };
 
-  // A wave has about ceil(records / W) steps (3 for full-K units of a 4096-row matrix);
-  // the records of its first three steps are read together, then their payload loads
-  // all go out before X is staged, so the latency of each level is paid once. All three
-  // fetches are issued unconditionally (clamped to the wave's last step) so the
-  // compiler's waits before each decode are partial.
-  Regs r0, r1, r2;                                   // read only for steps the wave has
-  if (ns > 0) {
-    const u32x4_t f0 = slot_of(0), f1 = slot_of(min(1, ns - 1)), f2 = slot_of(min(2, ns - 1));
+  // The first three steps: block record wave + k*W is a fixed record (or the null record:
+  // a block with records past F has F = 48 >= 3W, so those indices are all fixed). Their
+  // records are read together with X; all of them are waited for here, before any payload
+  // load, so that no later wait (the compiler counts loads in issue order, and the payload
+  // load count varies with the kind) has to include payload that is still in flight.
+  Regs r0, r1, r2;
+  {
+    auto fixed = [&](int k) __attribute__((always_inline)) {
+      const int i = wave + k * W;
+      return slot_of(i < F ? (uint32_t)(blk * F + i) : null_rec);
+    };
+    const u32x4_t f0 = fixed(0), f1 = fixed(1), f2 = fixed(2);
+    asm volatile("" ::"v"(f0.x), "v"(f1.x), "v"(f2.x));
+#pragma unroll
+    for (int i = 0; i < XG; ++i) asm volatile("" ::"v"(kk[i].x));
+    if constexpr (lds_gather) {
+#pragma unroll
+      for (int m = 0; m < gemv_lds_gather_rows(MT); ++m)
+#pragma unroll
+        for (int i = 0; i < XR; ++i) asm volatile("" ::"v"(xr[m][i]));
+    }
     fetch(f0, r0);
     fetch(f1, r1);
     fetch(f2, r2);
   }
 
   // ---- X rows of the unit (gathered) and their 4- and 8-row sums into LDS ----
+  if constexpr (lds_gather) {
+#pragma unroll
+    for (int m = 0; m < gemv_lds_gather_rows(MT); ++m)
+#pragma unroll
+      for (int i = 0; i < XR; ++i) {
+        const int k = i * T + tid;
+        if (k < d.K) xraw[m * d.K + k] = xr[m][i];
+      }
+    lds_barrier();
+  }
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
     const float* xrow = X + (int64_t)min(m0 + m, M - 1) * ldx;
     const bool mv = m0 + m < M;
     float4 xv[XG];
+    if constexpr (lds_gather) {
+      const float* xl = xraw + m * d.K;
 #pragma unroll
-    for (int i = 0; i < XG; ++i) {
-      const int r = 4 * (i * T + tid);
-      if (r < rows && mv) {
-        xv[i] = make_float4(xrow[kk[i].x], xrow[kk[i].y], xrow[kk[i].z], xrow[kk[i].w]);
-      } else {
+      for (int i = 0; i < XG; ++i) {
+        const int r = 4 * (i * T + tid);
         xv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (r < rows && mv) xv[i] = make_float4(xl[kk[i].x], xl[kk[i].y], xl[kk[i].z], xl[kk[i].w]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < XG; ++i) {
+        const int r = 4 * (i * T + tid);
+        xv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (r < rows && mv) xv[i] = make_float4(xrow[kk[i].x], xrow[kk[i].y], xrow[kk[i].z], xrow[kk[i].w]);
       }
     }
 #pragma unroll
@@ -419,7 +520,7 @@ __global__ __launch_bounds__(64 * gemv_waves(MT), 4) void k_gemv(const mtc_strea
       }
     }
   }
-  __syncthreads();
+  lds_barrier();                                      // payload loads stay in flight
   const XStage xt{xs, xs4, xs8, kc};
 
   // ---- decode: the prefetched steps, then any further steps one at a time ----
@@ -436,7 +537,8 @@ __global__ __launch_bounds__(64 * gemv_waves(MT), 4) void k_gemv(const mtc_strea
       switch (ls == 2 ? key : (key & ~0xFFu) | 3u) {   // sizes 8, 16, 32 share a case
 #define MTC_CASE(S, P) \
   case MTC_BUCKET_KEY(S, P): \
-    gemv_chunk<S, P, MT>(cur.w, cur.lw0, cur.lw1, cur.fs0, cur.fs1, FS, cur.t, rb_mask, xt, acc); \
+    gemv_chunk<S, P, MT>(P == 16 ? gemv_load_p16_tail(pay_r, cur.w, cur.ob) : cur.w, cur.lw0, cur.lw1, cur.fs0, \
+                         cur.fs1, FS, cur.t, rb_mask, xt, acc); \
     break;
         MTC_FOR_EACH_WIDTH(8, MTC_CASE)
         MTC_FOR_EACH_WIDTH(4, MTC_CASE)
@@ -445,11 +547,13 @@ __global__ __launch_bounds__(64 * gemv_waves(MT), 4) void k_gemv(const mtc_strea
       }
     }
   };
-  if (ns > 0) compute(r0);
-  if (ns > 1) compute(r1);
-  if (ns > 2) compute(r2);
-  for (int k = 3; k < ns; ++k) {
-    fetch(slot_of(k), r0);
+  compute(r0);                                        // null records have no active lanes
+  compute(r1);
+  compute(r2);
+  const int nrec = hdr[28 + 2 * cb];
+  const uint32_t ovf = (uint32_t)hdr[27 + 2 * cb];
+  for (int i = wave + 3 * W; i < nrec; i += W) {
+    fetch(slot_of(i < F ? (uint32_t)(blk * F + i) : ovf + (uint32_t)(i - F)), r0);
     compute(r0);
   }
 
@@ -547,6 +651,13 @@ int check_desc(const mtc_stream_desc* d) {
     return fail(MTC_E_DESC, "leaf_scale given but MTC_FLAG_FP32_SCALES not set");
   if (d->n_steps < 0 || (d->n_buckets > 0 && (!d->steps || d->n_steps == 0)))
     return fail(MTC_E_NULL, "decode step records missing (n_steps=%lld)", (long long)d->n_steps);
+  if (d->fixed_steps < 0 || d->fixed_steps > kMaxFixedSteps || d->fixed_steps % kStepLanes || d->reserved)
+    return fail(MTC_E_DESC, "fixed_steps=%d must be 0, 16, 32 or 48 (reserved=%d must be 0)", d->fixed_steps,
+                d->reserved);
+  if (d->n_buckets > 0 &&
+      d->n_steps < (int64_t)d->n_panels * d->n_chunks * kGemvBlocksPerUnit * d->fixed_steps + 1)
+    return fail(MTC_E_DESC, "n_steps=%lld is less than the fixed record area plus the null record",
+                (long long)d->n_steps);
   if ((reinterpret_cast<uintptr_t>(d->payload) | reinterpret_cast<uintptr_t>(d->row_perm)) % 16)
     return fail(MTC_E_DESC, "payload and row_perm must be 16-byte aligned");
   return ok();
@@ -567,11 +678,13 @@ size_t gemv_ws_layout(const mtc_stream_desc* d, int M, size_t* counters_bytes) {
   return cb + n_mt * (size_t)d->n_panels * d->n_chunks * mt * kPanel * sizeof(float);
 }
 
-// LDS of a decode block: X rows, their 4- and 8-row sums, and the cross-wave reduction.
+// LDS of a decode block: X rows, their 4- and 8-row sums, the cross-wave reduction and,
+// for the LDS gather, whole X rows.
 size_t gemv_lds_bytes(const mtc_stream_desc* d, int MT) {
   const size_t kc = (size_t)d->chunk_rows;
+  const size_t raw = gemv_lds_gather(MT, d->row_perm != nullptr, d->K) ? (size_t)MT * d->K : 0;
   return ((size_t)MT * (kc + (gemv_sum4(MT) ? kc / 4 : 0) + kc / 8) +
-          (size_t)gemv_waves(MT) * kStepGroups * MT * kGroup) * 4;
+          (size_t)gemv_waves(MT) * kStepGroups * MT * kGroup + raw) * 4;
 }
 
 template <int MT>
@@ -587,7 +700,11 @@ int launch_gemv(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y,
     return fail(MTC_E_SHAPE, "fp32 path: %d rows x chunk_rows=%d needs %zu B of LDS (limit %zu); "
                 "use a stream with smaller chunk_rows", MT, d->chunk_rows, shmem, limit);
   const bool fs = d->leaf_scale != nullptr;
-  const void* kern = fs ? reinterpret_cast<const void*>(&k_gemv<MT, true>) : reinterpret_cast<const void*>(&k_gemv<MT, false>);
+  const bool lg = gemv_lds_gather(MT, d->row_perm != nullptr, d->K);
+  const void* kern = fs ? (lg ? reinterpret_cast<const void*>(&k_gemv<MT, true, (MT <= 2)>)
+                              : reinterpret_cast<const void*>(&k_gemv<MT, true, false>))
+                        : (lg ? reinterpret_cast<const void*>(&k_gemv<MT, false, (MT <= 2)>)
+                              : reinterpret_cast<const void*>(&k_gemv<MT, false, false>));
   if (shmem > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
     if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
@@ -595,13 +712,10 @@ int launch_gemv(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y,
   const int n_units = d->n_panels * d->n_chunks;
   const int units_padded = (n_units + kXcds - 1) / kXcds * kXcds;
   dim3 grid(units_padded * kGemvBlocksPerUnit, (M + MT - 1) / MT);
-  if (fs) {
-    hipLaunchKernelGGL((k_gemv<MT, true>), grid, dim3(64 * gemv_waves(MT)), shmem, st, *d, X, ldx, Y, ldy, M, part,
-                       counters);
-  } else {
-    hipLaunchKernelGGL((k_gemv<MT, false>), grid, dim3(64 * gemv_waves(MT)), shmem, st, *d, X, ldx, Y, ldy, M, part,
-                       counters);
-  }
+  const dim3 block(64 * gemv_waves(MT));
+  void* args[] = {const_cast<mtc_stream_desc*>(d), &X, &ldx, &Y, &ldy, &M, &part, &counters};
+  const hipError_t e = hipLaunchKernel(kern, grid, block, args, shmem, st);
+  if (e != hipSuccess) return fail(MTC_E_LAUNCH, "k_gemv launch: %s", hipGetErrorString(e));
   return check_launch("k_gemv");
 }
 

@@ -66,6 +66,7 @@ class DeviceStream:
         d.n_buckets = ps.n_buckets
         d.max_unit_words = int(ps.max_unit_words)
         d.max_unit_words4 = int(ps.max_unit_words4)
+        d.fixed_steps = int(ps.fixed_steps)
         d.n_leaves = int(ps.leaf_word.size)
         d.payload_dwords = int(ps.payload.size)
         ptr = lambda t: None if t is None else t.data_ptr()

@@ -54,12 +54,14 @@ def gemv_chunk_rows(K: int, N: int, M: int = 1) -> int:
 
 def _decode_lds_need(ps: PanelStream, M: int) -> int:
     """LDS bytes of one decode block: the gathered X rows, their 8-row (and, for M tiles
-    of 1-2 rows, 4-row) sums, and the per-wave partial sums (mirrors gemv_lds_bytes in
-    csrc/mtc_hip.hip; the payload streams through registers)."""
+    of 1-2 rows, 4-row) sums, the per-wave partial sums and, when X is gathered on chip,
+    whole X rows (mirrors gemv_lds_bytes in csrc/mtc_hip.hip; the payload streams through
+    registers)."""
     mt = _decode_mt(M)
     waves = 16 if mt <= 2 else 8
     kc = ps.chunk_rows
-    return 4 * (mt * (kc + (kc // 4 if mt <= 2 else 0) + kc // 8) + waves * 4 * mt * 4)
+    raw = mt * ps.K if (ps.row_perm is not None and mt <= 2 and ps.K <= 4096) else 0   # LDS gather of X
+    return 4 * (mt * (kc + (kc // 4 if mt <= 2 else 0) + kc // 8) + waves * 4 * mt * 4 + raw)
 
 
 # ---------------------------------------------------------------------------------------

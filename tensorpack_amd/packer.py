@@ -35,11 +35,14 @@ LEAF_PAD = 1 << 13
 ROW_BITS = 10                          # leaf word: row/4 in bits 0-9
 MAX_CHUNK_ROWS = 4 << ROW_BITS         # 4096
 UNIT_HDR_WORDS = 32
-STREAM_FORMAT = 6                      # panel stream layout version (matches the C-ABI version)
+STREAM_FORMAT = 7                      # panel stream layout version (matches the C-ABI version)
 PAYLOAD_PAD = 4                        # dwords after the last bucket
 STEP_GROUPS = 4                        # column groups one decode step covers
 STEP_LANES = 16                        # lanes (chunks) per column group in a step
 STEP_WORDS = 16                        # words per step record
+MAX_FIXED_STEPS = 48                   # records per block stored at block-computable positions
+BLOCKS_PER_UNIT = 2                    # decode blocks (of STEP_GROUPS column groups) per unit
+_NULL_KEY = 3 | (2 << 8)               # kind of a record with no chunks (any valid kind)
 _LOG2 = {32: 5, 16: 4, 8: 3, 4: 2}
 
 CodeSource = Callable[[int, int, np.ndarray, np.ndarray, np.ndarray], np.ndarray]
@@ -57,6 +60,7 @@ class PanelStream:
     leaf_word: np.ndarray               # uint32
     leaf_scale: Optional[np.ndarray]    # float32 or None (bf16 scales in leaf_word)
     steps: Optional[np.ndarray] = None  # uint32 (n_records, 16): decode step records
+    fixed_steps: int = 0                # records per decode block at fixed positions (0, 16, 32, 48)
     row_perm: Optional[np.ndarray] = None   # int32 or None
     col_perm: Optional[np.ndarray] = None   # int32 or None
     n_real_leaves: int = 0
@@ -98,7 +102,7 @@ class PanelStream:
     def save(self, path) -> None:
         arrays = {k: getattr(self, k) for k in self._ARRAYS if getattr(self, k) is not None}
         meta = np.array([STREAM_FORMAT, self.K, self.N, self.chunk_rows, self.n_real_leaves,
-                         self.max_unit_words, self.max_unit_words4], dtype=np.int64)
+                         self.max_unit_words, self.max_unit_words4, self.fixed_steps], dtype=np.int64)
         np.savez(path, meta=meta, stats_keys=np.array(sorted(self.stats), dtype=str),
                  stats_vals=np.array([self.stats[k] for k in sorted(self.stats)], dtype=np.float64), **arrays)
 
@@ -113,7 +117,7 @@ class PanelStream:
             return cls(K=meta[1], N=meta[2], chunk_rows=meta[3], payload=get("payload"), buckets=get("buckets"),
                        unit_hdr=get("unit_hdr"), leaf_word=get("leaf_word"), leaf_scale=get("leaf_scale"),
                        steps=get("steps"), row_perm=get("row_perm"), col_perm=get("col_perm"), n_real_leaves=meta[4],
-                       max_unit_words=meta[5], max_unit_words4=meta[6], stats=stats)
+                       max_unit_words=meta[5], max_unit_words4=meta[6], fixed_steps=meta[7], stats=stats)
 
 
 def pack_codes(codes: np.ndarray, P: int) -> np.ndarray:
@@ -351,8 +355,16 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
     max_unit_words4 = int(hdr[:, 26].max()) if n_units else 0
 
     # ---- decode step records: one per (unit, block of 4 column groups, kind, 16-chunk step) ----
-    steps = np.zeros((0, STEP_WORDS), dtype=np.uint32)
-    blk_begin = np.zeros(n_units * 2 + 1, dtype=np.int64)
+    # A block's records, in (kind, step) order, are split into its first F ("fixed") records,
+    # stored at records [b*F, b*F + F) of the table (b = unit * 2 + block; unused places hold
+    # null records), and the rest ("overflow"), stored after the fixed area and one null
+    # record at index n_blocks * F. Offsets are absolute: payload dwords and leaf-word index.
+    n_blocks = n_units * BLOCKS_PER_UNIT
+    null_rec = np.zeros((STEP_GROUPS, 4), dtype=np.int64)
+    null_rec[:, 3] = _NULL_KEY
+    null_rec = null_rec.reshape(STEP_WORDS)
+    recs = np.zeros((0, STEP_WORDS), dtype=np.int64)
+    blk_begin = np.zeros(n_blocks + 1, dtype=np.int64)
     if n_buckets:
         blk = b_cg // STEP_GROUPS
         slot = b_cg % STEP_GROUPS
@@ -371,20 +383,29 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
         rec_g = np.repeat(np.arange(n_grp), g_steps)
         j = np.arange(rec_g.size) - np.repeat(np.concatenate([[0], np.cumsum(g_steps)[:-1]]), g_steps)
         bb = gb[rec_g]
-        u_of = b_unit[bb[:, 0]]
-        steps = np.zeros((rec_g.size, STEP_GROUPS, 4), dtype=np.int64)      # slot g = words 4g .. 4g+3
+        recs = np.zeros((rec_g.size, STEP_GROUPS, 4), dtype=np.int64)      # slot g = words 4g .. 4g+3
         b_key = np.array([_LOG2[int(v)] for v in b_S], dtype=np.int64) | (b_P.astype(np.int64) << 8)
-        steps[:, :, 0] = b_pay[bb] - hdr[u_of, 0][:, None]
-        steps[:, :, 1] = b_leaf[bb] - hdr[u_of, 2][:, None]
-        steps[:, :, 2] = np.clip(g_n[rec_g] - STEP_LANES * j[:, None], 0, STEP_LANES)
-        steps[:, :, 3] = (b_key[bb[:, 0]] | (j << 16))[:, None]
-        steps = steps.reshape(rec_g.size, STEP_WORDS).astype(np.uint32)
+        recs[:, :, 0] = b_pay[bb]
+        recs[:, :, 1] = b_leaf[bb]
+        recs[:, :, 2] = np.clip(g_n[rec_g] - STEP_LANES * j[:, None], 0, STEP_LANES)
+        recs[:, :, 3] = (b_key[bb[:, 0]] | (j << 16))[:, None]
+        recs = recs.reshape(rec_g.size, STEP_WORDS)
         rec_blk = b_unit[first][rec_g] * 2 + blk[first][rec_g]
-        blk_begin = np.searchsorted(rec_blk, np.arange(n_units * 2 + 1)).astype(np.int64)
-    hdr[:, 27] = blk_begin[0:-1:2]
-    hdr[:, 28] = blk_begin[1::2] - blk_begin[0:-1:2]
-    hdr[:, 29] = blk_begin[1::2]
-    hdr[:, 30] = blk_begin[2::2] - blk_begin[1::2]
+        blk_begin = np.searchsorted(rec_blk, np.arange(n_blocks + 1)).astype(np.int64)
+    blk_n = np.diff(blk_begin)
+    F = int(min(MAX_FIXED_STEPS, STEP_LANES * -(-int(blk_n.max(initial=0)) // STEP_LANES)))
+    fixed = np.broadcast_to(null_rec, (n_blocks, F, STEP_WORDS)).copy()
+    pos = np.arange(recs.shape[0]) - np.repeat(blk_begin[:-1], blk_n)      # index within the block
+    rb = np.repeat(np.arange(n_blocks), blk_n)
+    inf = pos < F
+    fixed[rb[inf], pos[inf]] = recs[inf]
+    ovf_n = np.maximum(blk_n - F, 0)
+    ovf_begin = n_blocks * F + 1 + np.concatenate([[0], np.cumsum(ovf_n)[:-1]])
+    steps = np.concatenate([fixed.reshape(-1, STEP_WORDS), null_rec[None], recs[~inf]]).astype(np.uint32)
+    hdr[:, 27] = ovf_begin[0::2]
+    hdr[:, 28] = blk_n[0::2]
+    hdr[:, 29] = ovf_begin[1::2]
+    hdr[:, 30] = blk_n[1::2]
 
     buckets = np.zeros((max(n_buckets, 1), 4), dtype=np.uint32)
     if n_buckets:
@@ -397,6 +418,7 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
              "max_unit_bytes": float(4 * max_unit_words)}
     return PanelStream(K=K, N=N, chunk_rows=chunk_rows, payload=payload, buckets=buckets,
                        unit_hdr=hdr.astype(np.int32), leaf_word=leaf_word, leaf_scale=leaf_scale, steps=steps,
+                       fixed_steps=F,
                        row_perm=None if row_perm is None else np.ascontiguousarray(row_perm, dtype=np.int32),
                        col_perm=None if col_perm is None else np.ascontiguousarray(col_perm, dtype=np.int32),
                        n_real_leaves=n_real, max_unit_words=max_unit_words,
@@ -451,21 +473,31 @@ def decode_stream(ps: PanelStream) -> np.ndarray:
     return _to_original_order(ps, Wp)
 
 
+def step_record_index(ps: PanelStream, u: int, blk: int, r: int) -> int:
+    """Table index of record r of decode block (unit u, column-group block blk): the first
+    `fixed_steps` records of a block sit at block-computable positions, the rest follow
+    the fixed area at the block's overflow start (unit header word 27 + 2 * blk)."""
+    F = ps.fixed_steps
+    if r < F:
+        return (u * BLOCKS_PER_UNIT + blk) * F + r
+    return int(ps.unit_hdr[u, 27 + 2 * blk]) + r - F
+
+
 def decode_steps(ps: PanelStream) -> np.ndarray:
-    """Host decoder that walks the step records the way the decode kernel does: for
-    each unit and block of 4 column groups, records [hdr[27 + 2b], +hdr[28 + 2b]);
-    slot g of a record is words 4g .. 4g+3 (payload offset, first leaf, valid chunks,
-    kind | j << 16), and lane li of the slot takes chunk 16 * j + li of that bucket
-    when li is below the valid-chunk count. A debugging aid; the GPU path never calls it."""
+    """Host decoder that walks the step records the way the decode kernel does: block
+    (unit u, column-group block b) has unit_hdr[u, 28 + 2b] records, located by
+    step_record_index; slot g of a record is words 4g .. 4g+3 (absolute payload offset,
+    absolute first leaf, valid chunks, kind | j << 16), and lane li of the slot takes
+    chunk 16 * j + li of that bucket when li is below the valid-chunk count. A debugging
+    aid; the GPU path never calls it."""
     Wp = np.zeros((ps.K, ps.N), dtype=np.float32)
     for u in range(ps.n_units):
-        h = [int(x) for x in ps.unit_hdr[u]]
-        for blk in range(N_GROUPS // STEP_GROUPS):
-            beg, cnt = h[27 + 2 * blk], h[28 + 2 * blk]
-            for e in ps.steps[beg: beg + cnt]:
+        for blk in range(BLOCKS_PER_UNIT):
+            for r in range(int(ps.unit_hdr[u, 28 + 2 * blk])):
+                e = ps.steps[step_record_index(ps, u, blk, r)]
                 for g in range(STEP_GROUPS):
                     pay, leaf, nv, kj = (int(x) for x in e[4 * g: 4 * g + 4])
                     key, j = kj & 0xFFFF, kj >> 16
                     _place_chunks(ps, Wp, u, blk * STEP_GROUPS + g, 1 << (key & 0xFF), key >> 8,
-                                  h[0] + pay, h[2] + leaf, STEP_LANES * j + np.arange(nv))
+                                  pay, leaf, STEP_LANES * j + np.arange(nv))
     return _to_original_order(ps, Wp)

@@ -38,3 +38,18 @@ def outlier_matrix(seed=0, n=128, m=None):
     mask = rng.rand(n, m) < 0.01
     W[mask] = rng.uniform(-25, 25, size=mask.sum())
     return W
+
+
+def kind_mix_stream(K=4096, N=32, seed=24):
+    """Panel stream of 4x4 leaves whose code width changes with the column group (random
+    codes, power-of-two scales, 30 % P0): the 4 column groups of a decode block step
+    through different kinds, so a block has more step records than the fixed area holds."""
+    from tensorpack_amd.packer import pack_levels
+    rng = np.random.RandomState(seed)
+    widths = np.array([2, 3, 4, 5, 6, 8, 16, 2])
+    modes4 = np.broadcast_to(np.resize(widths, N // 4)[None, :], (K // 4, N // 4)).copy()
+    modes4[rng.rand(K // 4, N // 4) < 0.3] = 0
+    leaf4 = np.ones((K // 4, N // 4), bool)
+    scales4 = (2.0 ** rng.randint(-8, 0, size=(K // 4, N // 4))).astype(np.float32)
+    codes = lambda S, P, ii, jj, sc: rng.randint(-(1 << (P - 1)), 1 << (P - 1), size=(ii.size, S, S))
+    return pack_levels((K, N), (4,), {4: leaf4}, {4: modes4}, {4: scales4}, codes, chunk_rows=K)

@@ -78,6 +78,7 @@ def test_descriptor_validation(hip):
         "abi_version": (99, -7), "N": (60, -2), "K": (0, -2), "chunk_rows": (48, -2),
         "n_panels": (3, -2), "n_chunks": (1, -2), "unit_hdr": (None, -1), "payload": (None, -1),
         "max_unit_words4": (50, -2), "steps": (None, -1), "n_steps": (0, -1),
+        "fixed_steps": (20, -2), "reserved": (1, -2),
     }
     for field, (val, code) in cases.items():
         assert hip.mtc_check_desc(ctypes.byref(_desc(**{field: val}))) == code, field
@@ -86,6 +87,9 @@ def test_descriptor_validation(hip):
     # fp32-scale flag and table must agree
     assert hip.mtc_check_desc(ctypes.byref(_desc(flags=_abi.MTC_FLAG_FP32_SCALES))) == -1
     assert hip.mtc_check_desc(ctypes.byref(_desc(leaf_scale=0x2000))) == -2
+    # the fixed record area of the 8 decode blocks plus the null record must be present
+    assert hip.mtc_check_desc(ctypes.byref(_desc(fixed_steps=16, n_steps=129))) == 0
+    assert hip.mtc_check_desc(ctypes.byref(_desc(fixed_steps=16, n_steps=128))) == -2
 
 
 def test_entry_points_reject_bad_arguments_before_any_gpu_call(hip):

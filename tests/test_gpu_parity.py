@@ -15,7 +15,7 @@ from tensorpack_amd.core.permutation import PermutedQuadtreeRD
 from tensorpack_amd.core.quadtree import QuadtreeRD
 from tensorpack_amd.kernels.gemm import MTCMatrix, mtc_gemm
 
-from conftest import outlier_matrix
+from conftest import kind_mix_stream, outlier_matrix
 
 pytestmark = pytest.mark.gpu
 
@@ -103,6 +103,21 @@ def test_gemv_split_k_chunkings(gpu, allocs, chunk_rows):
     Y2 = ds.gemv_f32(torch.from_numpy(X).to(gpu)).cpu().numpy()
     assert np.array_equal(Y1, Y2), "fp32 path must be deterministic (counters must self-reset)"
     err = O.relative_frobenius_error(O.qt_gemm_f64(X, _oracle_what(a, W)), Y1)
+    assert err <= TOL_F32, err
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 7])
+def test_gemv_step_records_past_the_fixed_area(gpu, M):
+    # blocks with more step records than the fixed area (overflow list read via the header)
+    import torch
+    from tensorpack_amd.device import DeviceStream
+    from tensorpack_amd.packer import MAX_FIXED_STEPS, decode_stream
+    ps = kind_mix_stream()
+    assert max(ps.unit_hdr[:, 28].max(), ps.unit_hdr[:, 30].max()) > MAX_FIXED_STEPS
+    _say("gemv overflow records", M)
+    X = np.random.RandomState(M + 40).randn(M, ps.K).astype(np.float32)
+    Y = DeviceStream(ps, gpu).gemv_f32(torch.from_numpy(X).to(gpu)).cpu().numpy()
+    err = O.relative_frobenius_error(O.qt_gemm_f64(X, decode_stream(ps)), Y)
     assert err <= TOL_F32, err
 
 

@@ -11,10 +11,11 @@ from tensorpack_amd.core.allocation import rd_allocate_pair
 from tensorpack_amd.core.permutation import PermutedQuadtreeRD
 from tensorpack_amd.core.quadtree import QuadtreeRD
 from tensorpack_amd.kernels.gemm import MTCMatrix, arena_decode, arena_encode
-from tensorpack_amd.packer import (LEAF_PAD, N_GROUPS, STEP_GROUPS, STEP_LANES, decode_stream, decode_steps,
-                                   pack_codes, unpack_codes)
+from tensorpack_amd.packer import (BLOCKS_PER_UNIT, LEAF_PAD, MAX_FIXED_STEPS, N_GROUPS, STEP_GROUPS, STEP_LANES,
+                                   decode_stream, decode_steps, pack_codes, pack_levels, step_record_index,
+                                   unpack_codes)
 
-from conftest import outlier_matrix
+from conftest import kind_mix_stream, outlier_matrix
 
 
 def _bits(a):
@@ -176,33 +177,50 @@ def test_step_records_cover_every_chunk_once():
     a = QuadtreeRD(W, None, (32, 16, 8, 4)).select(3.5)
     ps = MTCMatrix.from_quadtree(a, W).panel_stream(256)
     h, st = ps.unit_hdr.astype(np.int64), ps.steps.astype(np.int64)
-    # the two blocks of each unit own consecutive, disjoint record ranges covering the table
-    assert np.all(h[:, 29] == h[:, 27] + h[:, 28])
-    assert np.all(h[1:, 27] == h[:-1, 29] + h[:-1, 30]) and h[0, 27] == 0
-    assert h[-1, 29] + h[-1, 30] == st.shape[0]
+    F, nb = ps.fixed_steps, ps.n_units * BLOCKS_PER_UNIT
+    n = np.concatenate([h[:, 28:29], h[:, 30:31]], axis=1).reshape(-1)          # records per block
+    assert F % STEP_LANES == 0 and F <= MAX_FIXED_STEPS and F >= min(n.max(), MAX_FIXED_STEPS)
+    # table = fixed area, one null record, then the blocks' overflow records in block order
+    assert st.shape[0] == nb * F + 1 + int(np.maximum(n - F, 0).sum())
     sl = st.reshape(-1, STEP_GROUPS, 4)
+    assert np.all(sl[nb * F, :, 2] == 0)
     nv = sl[:, :, 2]
-    assert nv.min() >= 0 and nv.max() <= STEP_LANES and np.all(nv.max(axis=1) > 0)
+    assert nv.min() >= 0 and nv.max() <= STEP_LANES
     assert np.all(sl[:, :, 3] == sl[:, :1, 3])            # one kind and step index per record
+    used = np.zeros(st.shape[0], bool)
     seen = {}
     for u in range(ps.n_units):
-        for blk in range(2):
-            recs = sl[h[u, 27 + 2 * blk]: h[u, 27 + 2 * blk] + h[u, 28 + 2 * blk]]
-            for e in recs:
+        for blk in range(BLOCKS_PER_UNIT):
+            for r in range(int(h[u, 28 + 2 * blk])):
+                i = step_record_index(ps, u, blk, r)
+                assert not used[i]
+                used[i] = True
+                e = sl[i]
+                assert e[:, 2].max() > 0
                 key, j = int(e[0, 3] & 0xFFFF), int(e[0, 3] >> 16)
                 for g in range(STEP_GROUPS):
                     cg = blk * STEP_GROUPS + g
-                    # the slot's offsets name one of this column group's buckets of the same kind
+                    # the slot's (absolute) offsets name one of this column group's buckets of the kind
                     b = [k for k in range(h[u, 4] + h[u, 8 + cg], h[u, 4] + h[u, 9 + cg])
-                         if ps.buckets[k, 0] == e[g, 0] and ps.buckets[k, 1] == e[g, 1]]
+                         if h[u, 0] + ps.buckets[k, 0] == e[g, 0] and h[u, 2] + ps.buckets[k, 1] == e[g, 1]]
                     if e[g, 2] == 0:
                         continue
                     assert len(b) == 1 and int(ps.buckets[b[0], 3]) == key
                     for t in range(STEP_LANES * j, STEP_LANES * j + int(e[g, 2])):
                         assert (b[0], t) not in seen
                         seen[(b[0], t)] = 1
+    # every record the blocks do not own is a null record
+    assert np.all(sl[~used][:, :, 2] == 0)
     expect = {(k, t) for k in range(ps.n_buckets) for t in range(int(ps.buckets[k, 2] & 0xFFFF))}
     assert set(seen) == expect
+
+
+def test_step_records_overflow_past_the_fixed_area():
+    ps = kind_mix_stream()
+    n = np.concatenate([ps.unit_hdr[:, 28], ps.unit_hdr[:, 30]])
+    assert n.max() > MAX_FIXED_STEPS and ps.fixed_steps == MAX_FIXED_STEPS
+    assert ps.steps.shape[0] > ps.n_units * BLOCKS_PER_UNIT * MAX_FIXED_STEPS + 1
+    assert np.array_equal(_bits(decode_steps(ps)), _bits(decode_stream(ps)))
 
 
 def test_step_records_survive_save_load(tmp_path):
