@@ -342,10 +342,19 @@ constexpr int kGemvBlocksPerUnit = kGroups / kStepGroups;
 constexpr int kMaxFixedSteps = 48;          // step records per block at block-computable positions
 constexpr int kXcds = 8;
 
-// Sum over the 16 lanes of a lane's column-group slot.
+// Sum over the 16 lanes of a column-group slot (one DPP row): row shifts by 1, 2, 4 and 8
+// build an inclusive prefix sum, so the row's last lane ends with the total.
+constexpr int kSlotSumLane = kStepLanes - 1;
+template <int kRowShr>
+__device__ __forceinline__ float row_shr(float v) {   // DPP row_shr; lanes shifted in read 0
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x110 + kRowShr, 0xF,
+                                                                0xF, true));
+}
 __device__ __forceinline__ float slot_sum(float v) {
-#pragma unroll
-  for (int off = kStepLanes / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  v += row_shr<1>(v);
+  v += row_shr<2>(v);
+  v += row_shr<4>(v);
+  v += row_shr<8>(v);
   return v;
 }
 
@@ -562,7 +571,7 @@ __global__ __launch_bounds__(64 * gemv_waves(MT), 4) void k_gemv(const mtc_strea
   for (int m = 0; m < MT; ++m)
 #pragma unroll
     for (int c = 0; c < kGroup; ++c) acc[m][c] = slot_sum(acc[m][c]);
-  if (li == 0) {
+  if (li == kSlotSumLane) {
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
