@@ -3,13 +3,13 @@
 //
 //   k_stage_x   : X -> bf16 Xp = X[:, row_perm] (only for fp32 X or a row permutation)
 //   k_gemm_tile : one 256 x 256 output tile per block, K in steps of 64. Warp-specialized:
-//                 8 consumer waves (2 x 4 of 128 x 64 outputs) only read the staged bf16
-//                 tiles and issue MFMAs; 4 producer waves (one per SIMD) stage step k+1
-//                 from registers (X rows and two decoded cells per thread) into the other
-//                 LDS buffer and then load step k+2's X rows and cell payload. A (bf16 X)
-//                 and B (decoded weights) are double-buffered with an XOR swizzle of
-//                 16-byte segments; one barrier per step. Output columns go through
-//                 col_perm.
+//                 8 consumer waves (2 x 4 of 128 x 64 outputs) copy X tiles straight
+//                 into LDS (buffer loads with the LDS destination, two steps ahead into
+//                 three A buffers) and issue the MFMAs; 4 producer waves (one per SIMD)
+//                 decode step k+1's weight cells from registers into the other of two B
+//                 buffers and load step k+2's cell payload. Tiles use an XOR swizzle of
+//                 16-byte segments; one LDS-only barrier per step (global loads stay in
+//                 flight across it). Output columns go through col_perm.
 //
 // Reference behaviour: mtc/kernels/gemm.py:124-210 (block loop: skip P0 blocks,
 // unpack, scale, multiply-accumulate) with W_hat as in mtc/core/quadtree.py:157-171.
@@ -36,9 +36,12 @@ constexpr int kConsumerWaves = 8;           // 2 x 4 waves of 128 x 64 outputs
 constexpr int kProducerWaves = 4;           // one per SIMD: loads, decode, LDS stores
 constexpr int kThreads = 64 * (kConsumerWaves + kProducerWaves);
 constexpr int kProducers = 64 * kProducerWaves;
-constexpr int kSegsPerProducer = kTM * (kTK / 8) / kProducers;   // 16-byte X segments per producer
 constexpr int kTileBytes = kTM * kTK * 2;   // one bf16 operand tile (A and B are the same size)
-constexpr int kLdsBytes = 4 * kTileBytes;   // A and B, two buffers each: 128 KiB
+constexpr int kABufs = 3;                   // A (X) buffers: copied two steps ahead
+constexpr int kBBufs = 2;                   // B (decoded weight) buffers
+constexpr int kLdsBytes = (kABufs + kBBufs) * kTileBytes;   // 160 KiB, all of a CU's LDS
+constexpr int kDmaPerWave = kTM / 8 / kConsumerWaves;       // 1 KiB (8-row) A copies per consumer wave
+constexpr uint32_t kOutOfRange = 0xFFFFFF00u;               // byte offset past any buffer's end
 constexpr int kRowGroup = 8;                // row tiles per launch-order group (L2 reuse of B)
 constexpr int kXcds = 8;
 constexpr int kStageThreads = 256;
@@ -65,6 +68,31 @@ __device__ __forceinline__ uint32_t swz(int row, int seg) {
 __device__ __forceinline__ uint32_t opaque(uint32_t x) {
   asm("" : "+v"(x));
   return x;
+}
+
+// A raw buffer resource (base, byte size) for the DMA copies below.
+__device__ __forceinline__ u32x4_t buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  return u32x4_t{(uint32_t)b, (uint32_t)(b >> 32) & 0xFFFFu, bytes, 0x00020000u};
+}
+
+// Global -> LDS copy of 16 bytes per lane: lane l's bytes land at LDS address lds + 16 l;
+// a lane whose offset is past the buffer's end writes zeros. Inline assembly, so the
+// compiler neither counts it among its own loads nor makes LDS reads wait for it: the
+// consumer waves, which issue no other vector memory loads in their loop, wait for
+// these copies with their own counted s_waitcnt.
+__device__ __forceinline__ void dma16(u32x4_t rsrc, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voff), "s"(rsrc), "s"(lds)
+               : "memory");
+}
+
+// Workgroup barrier that orders LDS only: waits for this wave's LDS accesses, not for its
+// global loads, so the producers' prefetch stays in flight across it (__syncthreads()
+// would wait for those loads too and expose their latency every step).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 __device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
@@ -140,17 +168,53 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, c
   const int nks = d.n_ksteps;
 
   if (wave < kConsumerWaves) {
-    // ---------------- consumers: bf16 MFMA over the staged tiles ----------------
+    // ---------------- consumers: copy X tiles into LDS, bf16 MFMA over the staged tiles ----------------
+    // A copies: step s's 256 x 64 bf16 X tile is 32 copies of 8 rows; this wave does
+    // copies kDmaPerWave * wave + i. Lane l of a copy fills physical 16-byte slot l of the
+    // 8 rows, so it reads the logical segment that swz() maps there. Rows past M and
+    // segments past K read zeros (out-of-range offsets).
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds;
+    const u32x4_t x_r = buffer_rsrc(X + (int64_t)m0 * ldx, (uint32_t)(kTM * ldx * 2));
+    uint32_t a_off[kDmaPerWave];
+    int a_k[kDmaPerWave];                                  // first K element of the lane's segment
+#pragma unroll
+    for (int i = 0; i < kDmaPerWave; ++i) {
+      const int row = 8 * (kDmaPerWave * wave + i) + (lane >> 3);
+      const int lseg = (lane & 7) ^ (row & 7) ^ ((row >> 3) & 1);
+      a_k[i] = lseg * 8;
+      a_off[i] = m0 + row < M ? (uint32_t)(row * ldx + lseg * 8) * 2 : kOutOfRange;
+    }
+    auto copy_a = [&](int s) __attribute__((always_inline)) {
+      const uint32_t buf = lds0 + (uint32_t)(s % kABufs) * kTileBytes;
+      const uint32_t kb = (uint32_t)(s * kTK) * 2;
+#pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i) {
+        // K % 8 == 0, so a segment is wholly inside or outside K
+        const bool in = a_off[i] != kOutOfRange && s * kTK + a_k[i] < d.K;
+        dma16(x_r, in ? a_off[i] + kb : kOutOfRange,
+              __builtin_amdgcn_readfirstlane(buf + (uint32_t)(kDmaPerWave * wave + i) * 1024u));
+      }
+    };
+
     const int wm = wave >> 2, wn = wave & 3;
     f32x16_t acc[4][2];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[i][j] = f32x16_t{};
-    __syncthreads();                                       // step 0 staged
+    copy_a(0);
+    if (nks > 1) {
+      copy_a(1);
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerWave) : "memory");   // step 0's copies done
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    lds_barrier();                                         // step 0 staged
     for (int ks = 0; ks < nks; ++ks) {
-      const unsigned char* as = lds + (ks & 1) * kTileBytes;
-      const unsigned char* bs = lds + (2 + (ks & 1)) * kTileBytes;
+      const bool ahead = ks + 2 < nks;
+      if (ahead) copy_a(ks + 2);                           // into the buffer step ks-1 used
+      const unsigned char* as = lds + (ks % kABufs) * kTileBytes;
+      const unsigned char* bs = lds + (kABufs + (ks & 1)) * kTileBytes;
 #pragma unroll
       for (int kk = 0; kk < kTK / 16; ++kk) {
         const int seg = kk * 2 + (lane >> 5);
@@ -167,7 +231,13 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, c
           for (int j = 0; j < 2; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
       }
-      __syncthreads();                                     // buffer ks free, step ks+1 staged
+      // step ks+1's copies (issued a step ago) must have landed before the barrier
+      if (ahead) {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerWave) : "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      lds_barrier();                                       // buffers of step ks free, step ks+1 staged
     }
 
     // epilogue: C element e of lane l is row (e/4)*8 + (l/32)*4 + e%4, column l%32
@@ -197,34 +267,10 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, c
   const int p = tid - 64 * kConsumerWaves;                 // 0 .. kProducers-1
   const uint32_t* cells = d.cells + ((size_t)ct * nks * kCells + p) * CW;
   const uint32_t* step_off = d.step_off + (size_t)ct * nks;
-  const bool full_m = m0 + kTM <= M;
-
-  // X: 16-byte segment a_seg of rows a_r + 32 i. Rows past M and segments past K load
-  // from row 0 / element 0 and are replaced by zeros.
-  const int a_seg = p & 7, a_r = p >> 3;
-  u32x4_t areg[kSegsPerProducer];
-  auto load_a = [&](int ks) {
-    const int k = ks * kTK + a_seg * 8;
-    if (full_m && (ks + 1) * kTK <= d.K) {
-#pragma unroll
-      for (int i = 0; i < kSegsPerProducer; ++i)
-        areg[i] = *reinterpret_cast<const u32x4_t*>(X + (int64_t)(m0 + a_r + 32 * i) * ldx + k);
-    } else {
-      const bool kok = k < d.K;                            // K % 8 == 0: a segment is wholly in or out
-#pragma unroll
-      for (int i = 0; i < kSegsPerProducer; ++i) {
-        const int m = m0 + a_r + 32 * i;
-        const bool ok = kok && m < M;
-        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(X + (int64_t)(ok ? m : 0) * ldx + (ok ? k : 0));
-        areg[i] = ok ? v : u32x4_t{0u, 0u, 0u, 0u};
-      }
-    }
-  };
-
-  // cells p and p + kProducers of a step: descriptor words of the step being staged
-  // (c0, c1) and of the step after it (n0w, n1w); payload words of the staged step.
-  uint32_t c0[CW], c1[CW], n0w[CW], n1w[CW];
-  uint32_t cur_base = 0, nxt_base = 0;
+  // cells p and p + kProducers of a step: descriptor words (two sets that swap roles
+  // every step, so no register copies wait on loads in flight) and payload words.
+  uint32_t sa0[CW], sa1[CW], sb0[CW], sb1[CW];
+  uint32_t base_a = 0, base_b = 0;
   u32x4_t q0[4], q1[4];
   auto load_desc = [&](int ks, uint32_t (&w0)[CW], uint32_t (&w1)[CW], uint32_t& base) {
     const uint32_t* cp = cells + (size_t)ks * kCells * CW;
@@ -235,9 +281,9 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, c
     }
     base = step_off[ks];
   };
-  auto load_cell = [&](const uint32_t (&w)[CW], u32x4_t (&q)[4]) {
+  auto load_cell = [&](const uint32_t (&w)[CW], uint32_t base, u32x4_t (&q)[4]) {
     const uint32_t cls = (w[0] >> 14) & 3u;
-    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(d.payload + cur_base + (w[0] & 0x3FFFu));
+    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(d.payload + base + (w[0] & 0x3FFFu));
     if (cls == 0) {
       q[0] = src[0];
     } else if (cls == 1) {
@@ -250,13 +296,13 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, c
       q[3] = src[3];
     }
   };
-  auto load_payload = [&]() {
-    load_cell(c0, q0);
-    load_cell(c1, q1);
+  auto load_payload = [&](const uint32_t (&w0)[CW], const uint32_t (&w1)[CW], uint32_t base) {
+    load_cell(w0, base, q0);
+    load_cell(w1, base, q1);
   };
   auto stage_cell = [&](unsigned char* bs, const uint32_t (&w)[CW], const u32x4_t (&q)[4]) {
     float st, sb;
-    if (kFS) {
+    if constexpr (kFS) {
       st = __uint_as_float(w[1]);
       sb = __uint_as_float(w[2]);
     } else {
@@ -270,47 +316,40 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, c
 #pragma unroll
     for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4_t*>(bs + swz(col + j, seg)) = o[j];
   };
-  auto fill = [&](int buf) {
-    unsigned char* as = lds + buf * kTileBytes;
-    unsigned char* bs = lds + (2 + buf) * kTileBytes;
-#pragma unroll
-    for (int i = 0; i < kSegsPerProducer; ++i) *reinterpret_cast<u32x4_t*>(as + swz(a_r + 32 * i, a_seg)) = areg[i];
-    stage_cell(bs, c0, q0);
-    stage_cell(bs, c1, q1);
+  auto fill = [&](int buf, const uint32_t (&w0)[CW], const uint32_t (&w1)[CW]) {
+    unsigned char* bs = lds + (kABufs + buf) * kTileBytes;
+    stage_cell(bs, w0, q0);
+    stage_cell(bs, w1, q1);
   };
-  auto advance = [&]() {
-#pragma unroll
-    for (int t = 0; t < CW; ++t) {
-      c0[t] = n0w[t];
-      c1[t] = n1w[t];
-    }
-    cur_base = nxt_base;
-  };
-
-  // prologue: stage step 0, hold step 1 in registers, descriptor of step 2
-  load_desc(0, c0, c1, cur_base);
-  if (nks > 1) load_desc(1, n0w, n1w, nxt_base);
-  load_a(0);
-  load_payload();
-  fill(0);
-  if (nks > 1) {
-    advance();
-    load_a(1);
-    load_payload();
-    if (nks > 2) load_desc(2, n0w, n1w, nxt_base);
-  }
-  __syncthreads();
-  for (int ks = 0; ks < nks; ++ks) {
+  // One step while the consumers multiply step ks: stage step ks+1's B tile (descriptors
+  // `cur`, payload already in registers), then load step ks+2's payload (its descriptors
+  // `nxt` were loaded a step earlier) and step ks+3's descriptors into `cur`.
+  auto step = [&](int ks, uint32_t (&c0)[CW], uint32_t (&c1)[CW], uint32_t& cbase, const uint32_t (&n0)[CW],
+                  const uint32_t (&n1)[CW], uint32_t nbase) __attribute__((always_inline)) {
     if (ks + 1 < nks) {
-      fill((ks + 1) & 1);                                  // step ks+1 from registers
+      fill((ks + 1) & 1, c0, c1);
       if (ks + 2 < nks) {
-        advance();
-        load_a(ks + 2);
-        load_payload();
-        if (ks + 3 < nks) load_desc(ks + 3, n0w, n1w, nxt_base);
+        load_payload(n0, n1, nbase);
+        if (ks + 3 < nks) load_desc(ks + 3, c0, c1, cbase);
       }
     }
-    __syncthreads();
+    lds_barrier();
+  };
+
+  // prologue: stage step 0's B tile; hold step 1's payload in registers with its
+  // descriptors in set a, and step 2's descriptors in set b
+  load_desc(0, sb0, sb1, base_b);
+  if (nks > 1) load_desc(1, sa0, sa1, base_a);
+  load_payload(sb0, sb1, base_b);
+  fill(0, sb0, sb1);
+  if (nks > 1) {
+    load_payload(sa0, sa1, base_a);
+    if (nks > 2) load_desc(2, sb0, sb1, base_b);
+  }
+  lds_barrier();
+  for (int ks = 0; ks < nks; ks += 2) {
+    step(ks, sa0, sa1, base_a, sb0, sb1, base_b);
+    if (ks + 1 < nks) step(ks + 1, sb0, sb1, base_b, sa0, sa1, base_a);
   }
 }
 
@@ -351,6 +390,11 @@ bool needs_staging(const mtc_tile_desc* d, int x_dtype) { return d->row_perm || 
 
 template <bool kFS, int kYDT>
 int launch_tile(const mtc_tile_desc* d, const __bf16* X, int64_t ldx, void* Y, int64_t ldy, int M, hipStream_t st) {
+  if ((size_t)kLdsBytes > mtc::host::device_lds_limit())
+    return fail(MTC_E_SHAPE, "prefill kernel needs %d B of LDS per block, device has %zu", kLdsBytes,
+                mtc::host::device_lds_limit());
+  if (ldx >= ((int64_t)1 << 31) / (2 * kTM))
+    return fail(MTC_E_SHAPE, "ldx=%lld too large for the X tile copies", (long long)ldx);
   const void* fn = reinterpret_cast<const void*>(&k_gemm_tile<kFS, kYDT>);
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
   if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
