@@ -17,6 +17,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "mtc_hip.h"
 #include "mtc_host.h"
 
@@ -146,7 +148,8 @@ __device__ __forceinline__ void decode_cell(uint32_t cls, const u32x4_t* pw, flo
 template <bool kFS, int kYDT>
 __global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, const __bf16* __restrict__ X,
                                                         int64_t ldx, void* __restrict__ Y, int64_t ldy, int M,
-                                                        int n_row_tiles, int tiles_per_xcd) {
+                                                        int n_row_tiles, int tiles_per_xcd, int steps_per_split,
+                                                        float* __restrict__ part) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   constexpr int CW = kFS ? 4 : 2;
 
@@ -165,7 +168,10 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, c
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: keeps per-wave control scalar
   const int m0 = rt * kTM, n0 = ct * kTN;
-  const int nks = d.n_ksteps;
+  // split K: this block runs steps kb0 .. kb0 + nks - 1 (blockIdx.y) and, with `part`,
+  // writes its partial tile to part[blockIdx.y] instead of Y
+  const int kb0 = (int)blockIdx.y * steps_per_split;
+  const int nks = min(steps_per_split, d.n_ksteps - kb0);
 
   if (wave < kConsumerWaves) {
     // ---------------- consumers: copy X tiles into LDS, bf16 MFMA over the staged tiles ----------------
@@ -186,11 +192,11 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, c
     }
     auto copy_a = [&](int s) __attribute__((always_inline)) {
       const uint32_t buf = lds0 + (uint32_t)(s % kABufs) * kTileBytes;
-      const uint32_t kb = (uint32_t)(s * kTK) * 2;
+      const uint32_t kb = (uint32_t)((kb0 + s) * kTK) * 2;
 #pragma unroll
       for (int i = 0; i < kDmaPerWave; ++i) {
         // K % 8 == 0, so a segment is wholly inside or outside K
-        const bool in = a_off[i] != kOutOfRange && s * kTK + a_k[i] < d.K;
+        const bool in = a_off[i] != kOutOfRange && (kb0 + s) * kTK + a_k[i] < d.K;
         dma16(x_r, in ? a_off[i] + kb : kOutOfRange,
               __builtin_amdgcn_readfirstlane(buf + (uint32_t)(kDmaPerWave * wave + i) * 1024u));
       }
@@ -240,20 +246,24 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, c
       lds_barrier();                                       // buffers of step ks free, step ks+1 staged
     }
 
-    // epilogue: C element e of lane l is row (e/4)*8 + (l/32)*4 + e%4, column l%32
+    // epilogue: C element e of lane l is row (e/4)*8 + (l/32)*4 + e%4, column l%32.
+    // Split K writes a plain fp32 partial tile to part[blockIdx.y] (no column permutation).
+    float* const yf = part ? part + (size_t)blockIdx.y * M * d.N : reinterpret_cast<float*>(Y);
+    const int64_t ld = part ? (int64_t)d.N : ldy;
+    const bool fp32_out = part || kYDT == MTC_DTYPE_F32;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int col = n0 + wn * 64 + j * 32 + (lane & 31);
       const bool cok = col < d.N;
-      const int ycol = d.col_perm ? d.col_perm[cok ? col : 0] : col;
+      const int ycol = (d.col_perm && !part) ? d.col_perm[cok ? col : 0] : col;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int row = m0 + wm * 128 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
           if (cok && row < M) {
-            if (kYDT == MTC_DTYPE_F32)
-              reinterpret_cast<float*>(Y)[(int64_t)row * ldy + ycol] = acc[i][j][e];
+            if (fp32_out)
+              yf[(int64_t)row * ld + ycol] = acc[i][j][e];
             else
               reinterpret_cast<__bf16*>(Y)[(int64_t)row * ldy + ycol] = (__bf16)acc[i][j][e];
           }
@@ -265,8 +275,8 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, c
 
   // ---------------- producers: load X and cells, decode, stage the next step ----------------
   const int p = tid - 64 * kConsumerWaves;                 // 0 .. kProducers-1
-  const uint32_t* cells = d.cells + ((size_t)ct * nks * kCells + p) * CW;
-  const uint32_t* step_off = d.step_off + (size_t)ct * nks;
+  const uint32_t* cells = d.cells + (((size_t)ct * d.n_ksteps + kb0) * kCells + p) * CW;
+  const uint32_t* step_off = d.step_off + (size_t)ct * d.n_ksteps + kb0;
   // cells p and p + kProducers of a step: descriptor words (two sets that swap roles
   // every step, so no register copies wait on loads in flight) and payload words.
   uint32_t sa0[CW], sa1[CW], sb0[CW], sb1[CW];
@@ -371,6 +381,23 @@ __global__ __launch_bounds__(kStageThreads) void k_stage_x(const void* __restric
   *reinterpret_cast<u32x4_t*>(Xp + m * K + k0) = o;
 }
 
+// Y[m, col_perm[n]] = sum over splits of part[z][m][n] (fixed order: deterministic).
+template <int kYDT>
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ part, int splits, int M, int N,
+                                                       const int32_t* __restrict__ col_perm, void* __restrict__ Y,
+                                                       int64_t ldy) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)M * N) return;
+  const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
+  float v = 0.0f;
+  for (int z = 0; z < splits; ++z) v += part[(size_t)z * M * N + i];
+  const int col = col_perm ? col_perm[n] : n;
+  if (kYDT == MTC_DTYPE_F32)
+    reinterpret_cast<float*>(Y)[(int64_t)m * ldy + col] = v;
+  else
+    reinterpret_cast<__bf16*>(Y)[(int64_t)m * ldy + col] = (__bf16)v;
+}
+
 int check_tile_desc(const mtc_tile_desc* d) {
   if (!d) return fail(MTC_E_NULL, "tile descriptor is NULL");
   if (d->abi_version != MTC_ABI_VERSION)
@@ -388,13 +415,38 @@ int check_tile_desc(const mtc_tile_desc* d) {
 
 bool needs_staging(const mtc_tile_desc* d, int x_dtype) { return d->row_perm || x_dtype == MTC_DTYPE_F32; }
 
+constexpr int kFillCUs = 256;             // blocks that fill the chip (one 256 x 256 tile block per CU)
+constexpr int kMinStepsPerSplit = 4;
+
+// K splits for M rows: enough blocks to fill the chip when the output has few tiles,
+// at least kMinStepsPerSplit K-steps per split. Returns the steps per split.
+int split_steps(const mtc_tile_desc* d, int M, int* splits) {
+  const int64_t n_tiles = (int64_t)((M + kTM - 1) / kTM) * d->n_col_tiles;
+  int want = n_tiles >= kFillCUs ? 1 : (int)((kFillCUs + n_tiles - 1) / n_tiles);
+  want = std::max(1, std::min(want, d->n_ksteps / kMinStepsPerSplit));
+  const int per = (d->n_ksteps + want - 1) / want;
+  *splits = (d->n_ksteps + per - 1) / per;
+  return per;
+}
+
+size_t staging_bytes(const mtc_tile_desc* d, int M, int x_dtype) {
+  return needs_staging(d, x_dtype) ? ((size_t)M * d->K * 2 + 255) / 256 * 256 : 0;
+}
+
+size_t partial_bytes(const mtc_tile_desc* d, int M) {
+  int splits = 1;
+  split_steps(d, M, &splits);
+  return splits > 1 ? (size_t)splits * M * d->N * 4 : 0;
+}
+
 template <bool kFS, int kYDT>
-int launch_tile(const mtc_tile_desc* d, const __bf16* X, int64_t ldx, void* Y, int64_t ldy, int M, hipStream_t st) {
+int launch_tile(const mtc_tile_desc* d, const __bf16* X, int64_t ldx, void* Y, int64_t ldy, int M, float* part,
+                hipStream_t st) {
   if ((size_t)kLdsBytes > mtc::host::device_lds_limit())
     return fail(MTC_E_SHAPE, "prefill kernel needs %d B of LDS per block, device has %zu", kLdsBytes,
                 mtc::host::device_lds_limit());
   if (ldx >= ((int64_t)1 << 31) / (2 * kTM))
-    return fail(MTC_E_SHAPE, "ldx=%lld too large for the X tile copies", (long long)ldx);
+    return fail(MTC_E_SHAPE, "ldx=%lld too large for 32-bit X tile offsets", (long long)ldx);
   const void* fn = reinterpret_cast<const void*>(&k_gemm_tile<kFS, kYDT>);
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
   if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
@@ -402,9 +454,16 @@ int launch_tile(const mtc_tile_desc* d, const __bf16* X, int64_t ldx, void* Y, i
   const int64_t n_tiles = (int64_t)n_row_tiles * d->n_col_tiles;
   if (n_tiles > (int64_t)1 << 30) return fail(MTC_E_SHAPE, "M=%d gives too many tiles", M);
   const int tiles_per_xcd = (int)((n_tiles + kXcds - 1) / kXcds);
-  hipLaunchKernelGGL((k_gemm_tile<kFS, kYDT>), dim3(tiles_per_xcd * kXcds), dim3(kThreads), kLdsBytes, st, *d, X,
-                     ldx, Y, ldy, M, n_row_tiles, tiles_per_xcd);
-  return check_launch("k_gemm_tile");
+  int splits = 1;
+  const int per = split_steps(d, M, &splits);
+  hipLaunchKernelGGL((k_gemm_tile<kFS, kYDT>), dim3(tiles_per_xcd * kXcds, splits), dim3(kThreads), kLdsBytes, st,
+                     *d, X, ldx, Y, ldy, M, n_row_tiles, tiles_per_xcd, per, splits > 1 ? part : nullptr);
+  int rc = check_launch("k_gemm_tile");
+  if (rc || splits == 1) return rc;
+  const int64_t n = (int64_t)M * d->N;
+  hipLaunchKernelGGL(k_splitk_reduce<kYDT>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, part, splits, M,
+                     d->N, d->col_perm, Y, ldy);
+  return check_launch("k_splitk_reduce");
 }
 
 }  // namespace
@@ -413,7 +472,7 @@ MTC_API int mtc_check_tile_desc(const mtc_tile_desc* d) { return check_tile_desc
 
 MTC_API size_t mtc_gemm_workspace_bytes(const mtc_tile_desc* d, int M, int x_dtype) {
   if (check_tile_desc(d) || M <= 0) return 0;
-  return needs_staging(d, x_dtype) ? (size_t)M * d->K * 2 : 0;
+  return staging_bytes(d, M, x_dtype) + partial_bytes(d, M);
 }
 
 MTC_API int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, int64_t ldx, void* Y, int y_dtype,
@@ -428,12 +487,13 @@ MTC_API int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, in
   hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);
   const __bf16* xb = reinterpret_cast<const __bf16*>(X);
   int64_t ldb = ldx;
-  if (needs_staging(d, x_dtype)) {
-    const size_t need = (size_t)M * d->K * 2;
-    if (!workspace || workspace_bytes < need)
-      return fail(MTC_E_WORKSPACE, "prefill workspace of %zu bytes needed, %zu given", need,
-                  workspace ? workspace_bytes : 0);
-    if (reinterpret_cast<uintptr_t>(workspace) & 15) return fail(MTC_E_WORKSPACE, "workspace not 16-byte aligned");
+  const size_t stage = staging_bytes(d, M, x_dtype), need = stage + partial_bytes(d, M);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(MTC_E_WORKSPACE, "prefill workspace of %zu bytes needed, %zu given", need, workspace ? workspace_bytes : 0);
+  if (need && (reinterpret_cast<uintptr_t>(workspace) & 255))
+    return fail(MTC_E_WORKSPACE, "workspace not 256-byte aligned");
+  float* part = need > stage ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + stage) : nullptr;
+  if (stage) {
     dim3 grid((d->K / 8 + kStageThreads - 1) / kStageThreads, M);
     hipLaunchKernelGGL(k_stage_x, grid, dim3(kStageThreads), 0, st, X, x_dtype, ldx, d->row_perm,
                        reinterpret_cast<__bf16*>(workspace), d->K);
@@ -446,9 +506,9 @@ MTC_API int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, in
   }
   const bool fs = d->flags & MTC_FLAG_FP32_SCALES;
   if (fs) {
-    return y_dtype == MTC_DTYPE_F32 ? launch_tile<true, MTC_DTYPE_F32>(d, xb, ldb, Y, ldy, M, st)
-                                    : launch_tile<true, MTC_DTYPE_BF16>(d, xb, ldb, Y, ldy, M, st);
+    return y_dtype == MTC_DTYPE_F32 ? launch_tile<true, MTC_DTYPE_F32>(d, xb, ldb, Y, ldy, M, part, st)
+                                    : launch_tile<true, MTC_DTYPE_BF16>(d, xb, ldb, Y, ldy, M, part, st);
   }
-  return y_dtype == MTC_DTYPE_F32 ? launch_tile<false, MTC_DTYPE_F32>(d, xb, ldb, Y, ldy, M, st)
-                                  : launch_tile<false, MTC_DTYPE_BF16>(d, xb, ldb, Y, ldy, M, st);
+  return y_dtype == MTC_DTYPE_F32 ? launch_tile<false, MTC_DTYPE_F32>(d, xb, ldb, Y, ldy, M, part, st)
+                                  : launch_tile<false, MTC_DTYPE_BF16>(d, xb, ldb, Y, ldy, M, part, st);
 }

@@ -6,6 +6,8 @@ Frobenius 1e-5 of fp64 X @ W_hat for the fp32 path and 2e-3 for the bf16
 MFMA path (fp64 reference built from the same bf16-rounded X).
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -104,6 +106,31 @@ def test_gemv_split_k_chunkings(gpu, allocs, chunk_rows):
     assert np.array_equal(Y1, Y2), "fp32 path must be deterministic (counters must self-reset)"
     err = O.relative_frobenius_error(O.qt_gemm_f64(X, _oracle_what(a, W)), Y1)
     assert err <= TOL_F32, err
+
+
+@pytest.mark.parametrize("M,permuted,ydt", [(100, False, "f32"), (300, True, "f32"), (37, True, "bf16")])
+def test_gemm_split_k(gpu, M, permuted, ydt):
+    # few output tiles and 32 K-steps: the K steps are split over blocks and the fp32
+    # partial tiles summed (and column-permuted) by the reduce kernel
+    import torch
+    K, N = 2048, 256
+    W = outlier_matrix(31, K, N)
+    cls = PermutedQuadtreeRD if permuted else QuadtreeRD
+    a = cls(W, np.exp(np.random.RandomState(32).randn(K)), (32, 16, 8, 4)).select(4.5)
+    m = MTCMatrix.from_quadtree(a, W)
+    g = m.device_tiles(gpu)
+    need = g.lib.mtc_gemm_workspace_bytes(ctypes.byref(g.desc), M, 1)
+    assert need >= 4 * M * N * 2, need                     # at least two fp32 partial tiles
+    _say("gemm split-K", M, permuted, ydt)
+    X = np.random.RandomState(M).randn(M, K).astype(np.float32)
+    Xb = torch.from_numpy(X).to(gpu).to(torch.bfloat16)
+    out_dtype = torch.float32 if ydt == "f32" else torch.bfloat16
+    Y1 = g.gemm_bf16(Xb, out_dtype=out_dtype).float().cpu().numpy()
+    Y2 = g.gemm_bf16(Xb, out_dtype=out_dtype).float().cpu().numpy()
+    assert np.array_equal(Y1, Y2), "split-K reduction must be deterministic"
+    ref = O.qt_gemm_f64(Xb.float().cpu().numpy(), _oracle_what(a, W))
+    err = O.relative_frobenius_error(ref, Y1)
+    assert err <= TOL_BF16, err
 
 
 @pytest.mark.parametrize("M", [1, 2, 4, 7])
