@@ -596,7 +596,11 @@ __global__ __launch_bounds__(64 * gemv_waves(MT), 4) void k_gemv(const mtc_strea
     return;
   }
 
-  // split-K over chunks: deterministic last-block reduction per (M tile, panel)
+  // split-K over chunks: deterministic last-block reduction per (M tile, panel).
+  // Partials and the counter use relaxed device-scope atomics, which the hardware performs
+  // past the XCD-private L2s; ordering comes from waiting for the partial stores to complete
+  // before the counter add. (Acquire/release fences at device scope would write back and
+  // invalidate the whole L2 of the XCD instead, costing tens of microseconds per call.)
   constexpr int n_part = MT * kPanel;
   float* mine = part + ((size_t)mt * n_units + u) * n_part;
   for (int i = tid; i < nout; i += T) {
@@ -608,17 +612,16 @@ __global__ __launch_bounds__(64 * gemv_waves(MT), 4) void k_gemv(const mtc_strea
     __hip_atomic_store(mine + m * kPanel + (cb * kStepGroups + g2) * kGroup + c, v, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   }
-  __threadfence();
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores are complete
   __syncthreads();
   __shared__ int last;
   if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(&counters[mt * d.n_panels + panel], 1u, __ATOMIC_ACQ_REL,
+    const uint32_t prev = __hip_atomic_fetch_add(&counters[mt * d.n_panels + panel], 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
     last = (prev == (uint32_t)(d.n_chunks * BPU - 1));
   }
   __syncthreads();
   if (!last) return;
-  __threadfence();
   const float* pp = part + ((size_t)mt * n_units + (size_t)panel * d.n_chunks) * n_part;
   for (int i = tid; i < n_part; i += T) {
     float v = 0.0f;
