@@ -404,6 +404,21 @@ def main():
         del c16
         log(f"c2 M=16: {ms16 * 1e3:.2f} us/call, {res['c2_m16']['TFLOPs']:.2f} TFLOP/s")
 
+    # ---------------- achievable HBM bandwidth: a plain 1 GiB device copy ----------------
+    src = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    copy_gbs = 2 * src.numel() * 4 * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9     # read + write bytes
+    del src, dst
+    log(f"device copy: {copy_gbs:.0f} GB/s (read + write)")
+
     # ---------------- CPU baseline (bounded sample) ----------------
     cpu = None
     if not args.no_cpu_baseline:
@@ -469,6 +484,7 @@ def main():
                    "chunk_rows": ds.host.chunk_rows, "graph_replay": bool(args.graph)},
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": gbs / HBM_PEAK_GBS, "traffic": None if traffic is None else traffic["bytes"],
+                     "copy_GBps": copy_gbs, "frac_of_copy": gbs / copy_gbs,
                      "kernel": "k_gemv<1>", "stream_GBps": per_copy / (ms * 1e-3) / 1e9,
                      "traffic_detail": traffic},
         "cpu_baseline": cpu,
