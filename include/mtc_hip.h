@@ -12,6 +12,9 @@
  * Reference interfaces replaced (Sharexi/TensorPack, Python + numba, no FFI):
  *   mtc_gemv_f32   <- mtc/kernels/gemm.py:124-210 (mtc_gemm_core_kernel) as
  *                     driven by mtc_gemm, gemm.py:541-574, for decode shapes
+ *   mtc_gemv_f32_group <- several LinearMTCAdaptive.forward calls on one input,
+ *                     mtc/nn/layers.py:150-151 (X @ W per layer), e.g. the q/k/v or
+ *                     gate/up projections of a decoder layer, in one launch
  *   mtc_gemm_bf16  <- same kernel/entry point, prefill shapes (bf16 MFMA), over
  *                     the tile stream (mtc_tile_desc)
  *   mtc_dequant    <- MTCMatrix.to_array, gemm.py:510-538, and
@@ -145,6 +148,15 @@ size_t mtc_gemv_workspace_bytes(const mtc_stream_desc* d, int M);
  * Any M >= 1; tuned for decode (M <= 16). Deterministic. */
 int mtc_gemv_f32(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y, int64_t ldy, int M,
                  void* workspace, size_t workspace_bytes, void* hip_stream);
+
+/* fp32 path for n (1..MTC_MAX_GROUP) matrices that read the same X, in one launch:
+ * Y[i] (M x N_i, leading dim ldy[i]) = X (M x K, leading dim ldx) * W_hat_i.
+ * Every stream must have a single row chunk (n_chunks == 1, so no workspace), the
+ * same K, and the same scale format and row-permutation presence. Each Y[i] equals,
+ * bit for bit, what mtc_gemv_f32 writes for matrix i alone. */
+#define MTC_MAX_GROUP 4
+int mtc_gemv_f32_group(const mtc_stream_desc* const* descs, int n, const float* X, int64_t ldx,
+                       float* const* Y, const int64_t* ldy, int M, void* hip_stream);
 
 /*
  * Tile stream (prefill). Wp (K x N) is cut into steps of 64 reduction rows x

@@ -15,7 +15,7 @@ ERROR_NAMES = {
 }
 
 EXPORTED = ("mtc_abi_version", "mtc_last_error", "mtc_check_desc", "mtc_dequant",
-            "mtc_gemv_workspace_bytes", "mtc_gemv_f32", "mtc_check_tile_desc", "mtc_gemm_workspace_bytes",
+            "mtc_gemv_workspace_bytes", "mtc_gemv_f32", "mtc_gemv_f32_group", "mtc_check_tile_desc", "mtc_gemm_workspace_bytes",
             "mtc_gemm_bf16")
 
 
@@ -70,6 +70,9 @@ class MtcTileDesc(ctypes.Structure):
 TileDescP = ctypes.POINTER(MtcTileDesc)
 
 
+MAX_GROUP = 4                        # MTC_MAX_GROUP: matrices per mtc_gemv_f32_group launch
+
+
 def declare(lib: ctypes.CDLL) -> None:
     vp, i32, i64, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
     lib.mtc_abi_version.restype = i32
@@ -84,6 +87,9 @@ def declare(lib: ctypes.CDLL) -> None:
     lib.mtc_gemv_workspace_bytes.argtypes = [DescP, i32]
     lib.mtc_gemv_f32.restype = i32
     lib.mtc_gemv_f32.argtypes = [DescP, vp, i64, vp, i64, i32, vp, sz, vp]
+    lib.mtc_gemv_f32_group.restype = i32
+    lib.mtc_gemv_f32_group.argtypes = [ctypes.POINTER(DescP), i32, vp, i64, ctypes.POINTER(vp),
+                                       ctypes.POINTER(i64), i32, vp]
     lib.mtc_check_tile_desc.restype = i32
     lib.mtc_check_tile_desc.argtypes = [TileDescP]
     lib.mtc_gemm_workspace_bytes.restype = sz

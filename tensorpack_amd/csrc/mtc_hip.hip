@@ -19,6 +19,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+
 #include "mtc_hip.h"
 #include "mtc_decode.h"
 #include "mtc_host.h"
@@ -359,12 +361,11 @@ __device__ __forceinline__ float slot_sum(float v) {
 }
 
 
-// At least 4 waves per SIMD: a 16-wave block fills a CU's 4 SIMDs; two 8-wave blocks
-// (M tiles of 4 rows) share one only if each wave keeps to 128 VGPRs.
+// One decode block of matrix `d`: block id `bid` along the grid's x (the y index is the M tile).
 template <int MT, bool FS, bool LG>
-__global__ __launch_bounds__(64 * gemv_waves(MT), 4) void k_gemv(const mtc_stream_desc d, const float* __restrict__ X,
-                                                          int64_t ldx, float* __restrict__ Y, int64_t ldy, int M,
-                                                          float* __restrict__ part, uint32_t* __restrict__ counters) {
+__device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int bid, const float* __restrict__ X,
+                                           int64_t ldx, float* __restrict__ Y, int64_t ldy, int M,
+                                           float* __restrict__ part, uint32_t* __restrict__ counters) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   constexpr int W = gemv_waves(MT), T = 64 * W, BPU = kGemvBlocksPerUnit;
   const int kc = d.chunk_rows;
@@ -372,7 +373,7 @@ __global__ __launch_bounds__(64 * gemv_waves(MT), 4) void k_gemv(const mtc_strea
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: keeps per-wave control scalar
   const int n_units = d.n_panels * d.n_chunks;
   // block -> (unit, block of 4 column groups) with both blocks of a unit on one XCD
-  const int xcd = blockIdx.x % kXcds, slot = blockIdx.x / kXcds;
+  const int xcd = bid % kXcds, slot = bid / kXcds;
   const int u = (slot / BPU) * kXcds + xcd;
   if (u >= n_units) return;                           // padding block of the XCD mapping
   const int cb = slot % BPU;
@@ -638,6 +639,35 @@ __global__ __launch_bounds__(64 * gemv_waves(MT), 4) void k_gemv(const mtc_strea
     __hip_atomic_store(&counters[mt * d.n_panels + panel], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// At least 4 waves per SIMD: a 16-wave block fills a CU's 4 SIMDs; two 8-wave blocks
+// (M tiles of 4 rows) share one only if each wave keeps to 128 VGPRs.
+template <int MT, bool FS, bool LG>
+__global__ __launch_bounds__(64 * gemv_waves(MT), 4) void k_gemv(const mtc_stream_desc d, const float* __restrict__ X,
+                                                          int64_t ldx, float* __restrict__ Y, int64_t ldy, int M,
+                                                          float* __restrict__ part, uint32_t* __restrict__ counters) {
+  gemv_block<MT, FS, LG>(d, blockIdx.x, X, ldx, Y, ldy, M, part, counters);
+}
+
+// Up to kMaxGroup single-chunk matrices that read the same X, in one launch: matrix i owns
+// grid blocks [start[i], start[i + 1]) (each range a whole number of XCD rounds, so a block's
+// XCD is the same as in a launch of its own).
+constexpr int kMaxGroup = MTC_MAX_GROUP;
+struct GemvGroup {
+  mtc_stream_desc d[kMaxGroup];
+  float* Y[kMaxGroup];
+  int64_t ldy[kMaxGroup];
+  int start[kMaxGroup + 1];
+};
+
+template <int MT, bool FS, bool LG>
+__global__ __launch_bounds__(64 * gemv_waves(MT), 4) void k_gemv_group(const GemvGroup g, const float* __restrict__ X,
+                                                                int64_t ldx, int M) {
+  int i = 0;
+#pragma unroll
+  for (int k = 1; k < kMaxGroup; ++k) i += (int)blockIdx.x >= g.start[k];
+  gemv_block<MT, FS, LG>(g.d[i], (int)blockIdx.x - g.start[i], X, ldx, g.Y[i], g.ldy[i], M, nullptr, nullptr);
+}
+
 // ---------------------------------------------------------------------------
 // host helpers
 // ---------------------------------------------------------------------------
@@ -731,6 +761,32 @@ int launch_gemv(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y,
   return check_launch("k_gemv");
 }
 
+template <int MT>
+int launch_gemv_group(const GemvGroup& g, int n, const float* X, int64_t ldx, int M, hipStream_t st) {
+  size_t shmem = 0;
+  for (int i = 0; i < n; ++i) shmem = std::max(shmem, gemv_lds_bytes(&g.d[i], MT));
+  const size_t limit = device_lds_limit();
+  if (shmem > limit)
+    return fail(MTC_E_SHAPE, "fp32 group: %d rows need %zu B of LDS (limit %zu)", MT, shmem, limit);
+  const mtc_stream_desc* d = &g.d[0];
+  const bool fs = d->leaf_scale != nullptr;
+  const bool lg = gemv_lds_gather(MT, d->row_perm != nullptr, d->K);
+  const void* kern = fs ? (lg ? reinterpret_cast<const void*>(&k_gemv_group<MT, true, (MT <= 2)>)
+                              : reinterpret_cast<const void*>(&k_gemv_group<MT, true, false>))
+                        : (lg ? reinterpret_cast<const void*>(&k_gemv_group<MT, false, (MT <= 2)>)
+                              : reinterpret_cast<const void*>(&k_gemv_group<MT, false, false>));
+  if (shmem > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
+    if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+  }
+  dim3 grid(g.start[n], (M + MT - 1) / MT);
+  const dim3 block(64 * gemv_waves(MT));
+  void* args[] = {const_cast<GemvGroup*>(&g), &X, &ldx, &M};
+  const hipError_t e = hipLaunchKernel(kern, grid, block, args, shmem, st);
+  if (e != hipSuccess) return fail(MTC_E_LAUNCH, "k_gemv_group launch: %s", hipGetErrorString(e));
+  return check_launch("k_gemv_group");
+}
+
 }  // namespace
 
 MTC_API int mtc_abi_version(void) { return MTC_ABI_VERSION; }
@@ -774,6 +830,45 @@ MTC_API int mtc_gemv_f32(const mtc_stream_desc* d, const float* X, int64_t ldx, 
     case 1: return launch_gemv<1>(d, X, ldx, Y, ldy, M, workspace, st);
     case 2: return launch_gemv<2>(d, X, ldx, Y, ldy, M, workspace, st);
     default: return launch_gemv<4>(d, X, ldx, Y, ldy, M, workspace, st);
+  }
+}
+
+MTC_API int mtc_gemv_f32_group(const mtc_stream_desc* const* descs, int n, const float* X, int64_t ldx,
+                               float* const* Y, const int64_t* ldy, int M, void* hip_stream) {
+  if (!descs || !Y || !ldy) return fail(MTC_E_NULL, "descs, Y or ldy is NULL");
+  if (n < 1 || n > kMaxGroup) return fail(MTC_E_SHAPE, "group of %d matrices (1..%d)", n, kMaxGroup);
+  if (!X) return fail(MTC_E_NULL, "X is NULL");
+  if (M <= 0) return fail(MTC_E_SHAPE, "M=%d must be positive", M);
+  GemvGroup g;
+  memset(&g, 0, sizeof(g));
+  int blocks = 0;
+  for (int i = 0; i < n; ++i) {
+    const mtc_stream_desc* d = descs[i];
+    int rc = check_desc(d);
+    if (rc) return rc;
+    if (!Y[i]) return fail(MTC_E_NULL, "Y[%d] is NULL", i);
+    if (d->n_chunks != 1)
+      return fail(MTC_E_SHAPE, "group member %d has %d row chunks; groups take single-chunk streams", i, d->n_chunks);
+    if (d->K != descs[0]->K) return fail(MTC_E_SHAPE, "group member %d has K=%d, member 0 K=%d", i, d->K, descs[0]->K);
+    if ((d->leaf_scale != nullptr) != (descs[0]->leaf_scale != nullptr) ||
+        (d->row_perm != nullptr) != (descs[0]->row_perm != nullptr))
+      return fail(MTC_E_SHAPE, "group member %d differs from member 0 in scale format or row permutation", i);
+    if (ldx < d->K || ldy[i] < d->N)
+      return fail(MTC_E_SHAPE, "ldx=%lld < K or ldy[%d]=%lld < N", (long long)ldx, i, (long long)ldy[i]);
+    g.d[i] = *d;
+    g.Y[i] = Y[i];
+    g.ldy[i] = ldy[i];
+    g.start[i] = blocks;
+    const int units_padded = (d->n_panels + kXcds - 1) / kXcds * kXcds;
+    blocks += units_padded * kGemvBlocksPerUnit;
+  }
+  for (int i = n; i <= kMaxGroup; ++i) g.start[i] = blocks;
+  if ((M - 1) > (INT64_MAX / ldx)) return fail(MTC_E_SHAPE, "M * ldx overflows");
+  hipStream_t st = as_stream(hip_stream);
+  switch (gemv_mt(M)) {
+    case 1: return launch_gemv_group<1>(g, n, X, ldx, M, st);
+    case 2: return launch_gemv_group<2>(g, n, X, ldx, M, st);
+    default: return launch_gemv_group<4>(g, n, X, ldx, M, st);
   }
 }
 

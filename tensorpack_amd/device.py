@@ -152,6 +152,32 @@ class DeviceStream:
         return out
 
 
+def gemv_f32_group(streams, X, outs=None):
+    """Y_i = X @ W_hat_i for 1..MAX_GROUP single-chunk streams that share X, in one launch
+    (mtc_gemv_f32_group). Each Y_i is bit-identical to streams[i].gemv_f32(X)."""
+    torch = _torch()
+    streams = list(streams)
+    n = len(streams)
+    if not 1 <= n <= _abi.MAX_GROUP:
+        raise ValueError(f"a group holds 1..{_abi.MAX_GROUP} matrices, got {n}")
+    dev = streams[0].device
+    if any(s.device != dev for s in streams):
+        raise ValueError("group members live on different devices")
+    assert X.dim() == 2 and X.dtype == torch.float32 and X.stride(1) == 1, "X must be (M, K) fp32 row-major"
+    M = X.shape[0]
+    if outs is None:
+        outs = [torch.empty((M, s.N), dtype=torch.float32, device=dev) for s in streams]
+    for o, s in zip(outs, streams):
+        assert o.dtype == torch.float32 and o.stride(1) == 1 and tuple(o.shape) == (M, s.N)
+    descs = (_abi.DescP * n)(*[ctypes.pointer(s.desc) for s in streams])
+    ys = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+    lds = (ctypes.c_int64 * n)(*[o.stride(0) for o in outs])
+    lib = streams[0].lib
+    rc = lib.mtc_gemv_f32_group(descs, n, X.data_ptr(), X.stride(0), ys, lds, M, current_stream_handle(dev))
+    _abi.check(lib, "mtc_gemv_f32_group", rc)
+    return outs
+
+
 class DeviceTiles:
     """A TileStream (prefill layout) uploaded to one GPU, plus its ctypes descriptor."""
 

@@ -383,3 +383,64 @@ def mtc_gemm(A, B: MTCMatrix, *, compute: str = "auto", out_dtype=None):
     if from_numpy:
         return Y.float().cpu().numpy()
     return Y
+
+
+def mtc_gemm_group(A, Bs, *, compute: str = "auto"):
+    """[A @ W_hat_i for W_i in Bs] for weights that share the input A (the q/k/v or gate/up
+    projections of a decoder layer; in the reference each is its own
+    LinearMTCAdaptive.forward call, mtc/nn/layers.py:150-151).
+
+    At decode sizes (fp32 path) matrices whose decode streams have a single row chunk run
+    MAX_GROUP at a time in one launch (mtc_gemv_f32_group); each result is bit-identical to
+    mtc_gemm(A, W_i). Other members, and the bf16 path, launch one matrix at a time.
+    Returns a list in the order of Bs, each of the kind mtc_gemm returns.
+    """
+    import torch
+    from .. import _abi
+    from ..device import gemv_f32_group, require_gpu
+    Bs = list(Bs)
+    if not Bs:
+        return []
+    for B in Bs:
+        if not isinstance(B, MTCMatrix):
+            raise TypeError(f"weights must be MTCMatrix, got {type(B).__name__}")
+    dev = require_gpu()
+    from_numpy = not isinstance(A, torch.Tensor)
+    X = _as_device_tensor(A, dev)
+    squeeze = X.dim() == 1
+    if squeeze:
+        X = X.unsqueeze(0)
+    if X.dim() != 2:
+        raise ValueError(f"X must be 1-D or 2-D, got shape {tuple(X.shape)}")
+    M, K = X.shape
+    for B in Bs:
+        if B.shape[0] != K:
+            raise ValueError(f"Shape mismatch: X {tuple(X.shape)} vs W {B.shape}")
+    if compute == "auto":
+        compute = "fp32" if M <= DECODE_MAX_M else "bf16"
+    outs = [None] * len(Bs)
+    if compute == "fp32" and M > 0:
+        Xf = X.float()
+        if Xf.stride(1) != 1:
+            Xf = Xf.contiguous()
+        streams = [B.device_stream(None, dev, M) for B in Bs]
+        # members that can share a launch: one row chunk, same scale format and permutation presence
+        groups: Dict[Tuple[bool, bool], list] = {}
+        for i, s in enumerate(streams):
+            if s.host.n_chunks == 1:
+                key = (s.host.leaf_scale is not None, s.host.row_perm is not None)
+                groups.setdefault(key, []).append(i)
+        for idx in groups.values():
+            for j in range(0, len(idx), _abi.MAX_GROUP):
+                part = idx[j:j + _abi.MAX_GROUP]
+                for i, y in zip(part, gemv_f32_group([streams[i] for i in part], Xf)):
+                    outs[i] = y
+        for i, s in enumerate(streams):
+            if outs[i] is None:
+                outs[i] = s.gemv_f32(Xf)
+        if squeeze:
+            outs = [y.squeeze(0) for y in outs]
+        if from_numpy:
+            return [y.cpu().numpy() for y in outs]
+        return outs
+    return [mtc_gemm(A, B, compute=compute) for B in Bs]

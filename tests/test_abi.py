@@ -117,6 +117,32 @@ def test_entry_points_reject_bad_arguments_before_any_gpu_call(hip):
     assert hip.mtc_gemm_workspace_bytes(tp, 4, 1) == 4 * 256 * 2
 
 
+def test_group_entry_rejects_bad_arguments_before_any_gpu_call(hip):
+    one = _desc(chunk_rows=256, n_chunks=1)                     # single-chunk streams group
+    two = _desc()                                               # two row chunks: not groupable
+    D = _abi.DescP
+    descs = lambda *ds: (D * len(ds))(*[ctypes.pointer(x) for x in ds])
+    ys = lambda n: (ctypes.c_void_p * n)(*([0x10] * n))
+    lds = lambda n, v=64: (ctypes.c_int64 * n)(*([v] * n))
+    f = hip.mtc_gemv_f32_group
+    assert f(None, 1, 0x10, 256, ys(1), lds(1), 1, None) == -1
+    assert f(descs(one), 0, 0x10, 256, ys(1), lds(1), 1, None) == -3
+    assert f(descs(*[one] * 5), 5, 0x10, 256, ys(5), lds(5), 1, None) == -3      # more than MTC_MAX_GROUP
+    assert _abi.MAX_GROUP == 4
+    assert f(descs(one), 1, None, 256, ys(1), lds(1), 1, None) == -1
+    assert f(descs(one), 1, 0x10, 256, ys(1), lds(1), 0, None) == -3
+    assert f(descs(one, two), 2, 0x10, 256, ys(2), lds(2), 1, None) == -3        # split-K member
+    assert b"row chunks" in hip.mtc_last_error()
+    other_k = _desc(K=512, chunk_rows=512, n_chunks=1)
+    assert f(descs(one, other_k), 2, 0x10, 512, ys(2), lds(2), 1, None) == -3     # different K
+    assert f(descs(one, _desc(chunk_rows=256, n_chunks=1, row_perm=0x2000)), 2, 0x10, 256, ys(2), lds(2), 1,
+             None) == -3                                                          # permutation presence
+    assert f(descs(one), 1, 0x10, 100, ys(1), lds(1), 1, None) == -3             # ldx < K
+    assert f(descs(one), 1, 0x10, 256, ys(1), lds(1, 10), 1, None) == -3         # ldy < N
+    assert f(descs(one), 1, 0x10, 256, (ctypes.c_void_p * 1)(None), lds(1), 1, None) == -1
+    assert f(descs(_desc(chunk_rows=256, n_chunks=1, abi_version=3)), 1, 0x10, 256, ys(1), lds(1), 1, None) == -7
+
+
 def _tdesc(**kw):
     d = _abi.MtcTileDesc()
     d.abi_version = _abi.ABI_VERSION
