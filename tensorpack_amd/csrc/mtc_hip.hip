@@ -338,8 +338,13 @@ __device__ __forceinline__ void gemv_chunk(const u32x16_t rw, uint32_t lw0, uint
 constexpr int kStepGroups = 4;              // column groups one decode step covers
 constexpr int kStepLanes = 16;              // lanes per column group in a step
 constexpr int kStepWords = 16;              // words per step record
-// waves per block: 16 for M tiles of 1-2 rows, 8 for 4 rows (more accumulators per lane)
+// waves per block: 16 for M tiles of 1-2 rows, 8 for 4 rows (more accumulators per lane).
+// Streams with at most kFewSteps records per block (small K) use 8-wave blocks for 1-2 rows
+// too: the 16-wave block would leave most waves without a record, and two 8-wave blocks
+// share a CU.
 __host__ __device__ constexpr int gemv_waves(int MT) { return MT <= 2 ? 16 : 8; }
+constexpr int kFewSteps = 16;
+inline int gemv_waves_for(int MT, int fixed_steps) { return (MT <= 2 && fixed_steps <= kFewSteps) ? 8 : gemv_waves(MT); }
 constexpr int kGemvBlocksPerUnit = kGroups / kStepGroups;
 constexpr int kMaxFixedSteps = 48;          // step records per block at block-computable positions
 constexpr int kXcds = 8;
@@ -361,13 +366,14 @@ __device__ __forceinline__ float slot_sum(float v) {
 }
 
 
-// One decode block of matrix `d`: block id `bid` along the grid's x (the y index is the M tile).
-template <int MT, bool FS, bool LG>
+// One decode block of matrix `d`: block id `bid` along the grid's x (the y index is the M tile),
+// NW waves.
+template <int MT, bool FS, bool LG, int NW>
 __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int bid, const float* __restrict__ X,
                                            int64_t ldx, float* __restrict__ Y, int64_t ldy, int M,
                                            float* __restrict__ part, uint32_t* __restrict__ counters) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
-  constexpr int W = gemv_waves(MT), T = 64 * W, BPU = kGemvBlocksPerUnit;
+  constexpr int W = NW, T = 64 * W, BPU = kGemvBlocksPerUnit;
   const int kc = d.chunk_rows;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: keeps per-wave control scalar
@@ -459,7 +465,8 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
   };
 
   // The first three steps: block record wave + k*W is a fixed record (or the null record:
-  // a block with records past F has F = 48 >= 3W, so those indices are all fixed). Their
+  // a block with records past F has F = 48 >= 3W, so those indices are all fixed; 8-wave
+  // blocks of 1-2 rows run only streams with F <= 16, whose blocks have no records past F). Their
   // records are read together with X; all of them are waited for here, before any payload
   // load, so that no later wait (the compiler counts loads in issue order, and the payload
   // load count varies with the kind) has to include payload that is still in flight.
@@ -641,11 +648,11 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
 
 // At least 4 waves per SIMD: a 16-wave block fills a CU's 4 SIMDs; two 8-wave blocks
 // (M tiles of 4 rows) share one only if each wave keeps to 128 VGPRs.
-template <int MT, bool FS, bool LG>
-__global__ __launch_bounds__(64 * gemv_waves(MT), 4) void k_gemv(const mtc_stream_desc d, const float* __restrict__ X,
-                                                          int64_t ldx, float* __restrict__ Y, int64_t ldy, int M,
-                                                          float* __restrict__ part, uint32_t* __restrict__ counters) {
-  gemv_block<MT, FS, LG>(d, blockIdx.x, X, ldx, Y, ldy, M, part, counters);
+template <int MT, bool FS, bool LG, int NW>
+__global__ __launch_bounds__(64 * NW, 4) void k_gemv(const mtc_stream_desc d, const float* __restrict__ X,
+                                                  int64_t ldx, float* __restrict__ Y, int64_t ldy, int M,
+                                                  float* __restrict__ part, uint32_t* __restrict__ counters) {
+  gemv_block<MT, FS, LG, NW>(d, blockIdx.x, X, ldx, Y, ldy, M, part, counters);
 }
 
 // Up to kMaxGroup single-chunk matrices that read the same X, in one launch: matrix i owns
@@ -659,13 +666,29 @@ struct GemvGroup {
   int start[kMaxGroup + 1];
 };
 
-template <int MT, bool FS, bool LG>
-__global__ __launch_bounds__(64 * gemv_waves(MT), 4) void k_gemv_group(const GemvGroup g, const float* __restrict__ X,
-                                                                int64_t ldx, int M) {
+template <int MT, bool FS, bool LG, int NW>
+__global__ __launch_bounds__(64 * NW, 4) void k_gemv_group(const GemvGroup g, const float* __restrict__ X,
+                                                        int64_t ldx, int M) {
   int i = 0;
 #pragma unroll
   for (int k = 1; k < kMaxGroup; ++k) i += (int)blockIdx.x >= g.start[k];
-  gemv_block<MT, FS, LG>(g.d[i], (int)blockIdx.x - g.start[i], X, ldx, g.Y[i], g.ldy[i], M, nullptr, nullptr);
+  gemv_block<MT, FS, LG, NW>(g.d[i], (int)blockIdx.x - g.start[i], X, ldx, g.Y[i], g.ldy[i], M, nullptr, nullptr);
+}
+
+// The kernel instantiation for (M tile, scale format, LDS gather, waves).
+template <int MT, bool Group>
+const void* gemv_kernel(bool fs, bool lg, int nw) {
+  constexpr bool LG = MT <= 2;                        // the LDS gather exists for 1-2 row tiles only
+  constexpr int NW1 = gemv_waves(MT), NW2 = 8;
+#define MTC_GEMV_K(FS_, LG_, NW_) \
+  (Group ? reinterpret_cast<const void*>(&k_gemv_group<MT, FS_, LG_, NW_>) \
+         : reinterpret_cast<const void*>(&k_gemv<MT, FS_, LG_, NW_>))
+  if (nw == NW1)
+    return fs ? (lg ? MTC_GEMV_K(true, LG, NW1) : MTC_GEMV_K(true, false, NW1))
+              : (lg ? MTC_GEMV_K(false, LG, NW1) : MTC_GEMV_K(false, false, NW1));
+  return fs ? (lg ? MTC_GEMV_K(true, LG, NW2) : MTC_GEMV_K(true, false, NW2))
+            : (lg ? MTC_GEMV_K(false, LG, NW2) : MTC_GEMV_K(false, false, NW2));
+#undef MTC_GEMV_K
 }
 
 // ---------------------------------------------------------------------------
@@ -743,10 +766,8 @@ int launch_gemv(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y,
                 "use a stream with smaller chunk_rows", MT, d->chunk_rows, shmem, limit);
   const bool fs = d->leaf_scale != nullptr;
   const bool lg = gemv_lds_gather(MT, d->row_perm != nullptr, d->K);
-  const void* kern = fs ? (lg ? reinterpret_cast<const void*>(&k_gemv<MT, true, (MT <= 2)>)
-                              : reinterpret_cast<const void*>(&k_gemv<MT, true, false>))
-                        : (lg ? reinterpret_cast<const void*>(&k_gemv<MT, false, (MT <= 2)>)
-                              : reinterpret_cast<const void*>(&k_gemv<MT, false, false>));
+  const int nw = gemv_waves_for(MT, d->fixed_steps);
+  const void* kern = gemv_kernel<MT, false>(fs, lg, nw);
   if (shmem > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
     if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
@@ -754,7 +775,7 @@ int launch_gemv(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y,
   const int n_units = d->n_panels * d->n_chunks;
   const int units_padded = (n_units + kXcds - 1) / kXcds * kXcds;
   dim3 grid(units_padded * kGemvBlocksPerUnit, (M + MT - 1) / MT);
-  const dim3 block(64 * gemv_waves(MT));
+  const dim3 block(64 * nw);
   void* args[] = {const_cast<mtc_stream_desc*>(d), &X, &ldx, &Y, &ldy, &M, &part, &counters};
   const hipError_t e = hipLaunchKernel(kern, grid, block, args, shmem, st);
   if (e != hipSuccess) return fail(MTC_E_LAUNCH, "k_gemv launch: %s", hipGetErrorString(e));
@@ -771,16 +792,16 @@ int launch_gemv_group(const GemvGroup& g, int n, const float* X, int64_t ldx, in
   const mtc_stream_desc* d = &g.d[0];
   const bool fs = d->leaf_scale != nullptr;
   const bool lg = gemv_lds_gather(MT, d->row_perm != nullptr, d->K);
-  const void* kern = fs ? (lg ? reinterpret_cast<const void*>(&k_gemv_group<MT, true, (MT <= 2)>)
-                              : reinterpret_cast<const void*>(&k_gemv_group<MT, true, false>))
-                        : (lg ? reinterpret_cast<const void*>(&k_gemv_group<MT, false, (MT <= 2)>)
-                              : reinterpret_cast<const void*>(&k_gemv_group<MT, false, false>));
+  int max_fixed = 0;
+  for (int i = 0; i < n; ++i) max_fixed = std::max(max_fixed, g.d[i].fixed_steps);
+  const int nw = gemv_waves_for(MT, max_fixed);
+  const void* kern = gemv_kernel<MT, true>(fs, lg, nw);
   if (shmem > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
     if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
   }
   dim3 grid(g.start[n], (M + MT - 1) / MT);
-  const dim3 block(64 * gemv_waves(MT));
+  const dim3 block(64 * nw);
   void* args[] = {const_cast<GemvGroup*>(&g), &X, &ldx, &M};
   const hipError_t e = hipLaunchKernel(kern, grid, block, args, shmem, st);
   if (e != hipSuccess) return fail(MTC_E_LAUNCH, "k_gemv_group launch: %s", hipGetErrorString(e));

@@ -40,16 +40,29 @@ def _decode_mt(M: int) -> int:
     return 1 if M <= 1 else 2 if M <= 2 else 4
 
 
+DECODE_FILL_BLOCKS = 256      # decode blocks that fill the chip (one 16-wave block per CU)
+DECODE_MIN_SPLIT_ROWS = 512   # no row chunk below this when splitting only to fill the chip
+
+
 def gemv_chunk_rows(K: int, N: int, M: int = 1) -> int:
-    """Rows per decode work unit: the whole reduction dimension when the
-    gathered X rows (M_tile x rows fp32) fit the on-chip budget, so no block
-    needs a cross-block reduction; otherwise the largest multiple of 32 that fits."""
+    """Rows per decode work unit. The whole reduction dimension when the gathered X rows
+    (M_tile x rows fp32) fit the on-chip budget, so no block needs a cross-block reduction;
+    otherwise the fewest chunks that fit, of equal size (a 4864-row matrix splits 2432 +
+    2432, not 4096 + 768). A matrix that needs a split anyway and has too few column panels
+    to fill the chip (two blocks per unit) is cut into more chunks of at least
+    DECODE_MIN_SPLIT_ROWS rows."""
     env = os.environ.get("MTC_GEMV_CHUNK_ROWS")
     if env:
         return int(env)
-    cap = DECODE_X_LDS_BYTES // (4 * _decode_mt(M)) // 32 * 32
+    cap = min(DECODE_X_LDS_BYTES // (4 * _decode_mt(M)) // 32 * 32, 4096)
     rows = -(-K // 32) * 32
-    return int(max(32, min(rows, cap, 4096)))
+    n = -(-rows // cap)
+    if n > 1:
+        panels = max(1, N // 32)
+        fill = -(-DECODE_FILL_BLOCKS // (2 * panels))
+        n = max(n, min(fill, rows // DECODE_MIN_SPLIT_ROWS))
+    chunk = -(-(-(-rows // n)) // 32) * 32
+    return int(max(32, min(chunk, cap)))
 
 
 def _decode_lds_need(ps: PanelStream, M: int) -> int:
