@@ -44,7 +44,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=2400)
     ap.add_argument("--warmup", type=int, default=240)
     ap.add_argument("--rotate-gib", type=float, default=1.0)
-    ap.add_argument("--prefill-steps", type=int, default=10)
+    ap.add_argument("--prefill-steps", type=int, default=60)
+    ap.add_argument("--prefill-warmup", type=int, default=20)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-m16", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -483,7 +484,7 @@ def main():
         Y4 = torch.empty((M4, wl4.W.shape[1]), dtype=torch.float32, device=dev)
         g4.gemm_bf16(X4, out=Y4)
         torch.cuda.synchronize()
-        s4, ms4 = timed_calls(torch, [lambda: g4.gemm_bf16(X4, out=Y4)], args.prefill_steps, 2, False)
+        s4, ms4 = timed_calls(torch, [lambda: g4.gemm_bf16(X4, out=Y4)], args.prefill_steps, args.prefill_warmup, False)
         flop4 = 2.0 * M4 * wl4.W.shape[0] * wl4.W.shape[1]
         tf = flop4 / (ms4 * 1e-3) / 1e12
         res["c4_prefill"] = {"M": M4, "ms_per_call": ms4, "TFLOPs": tf, "frac_bf16_peak": tf / BF16_PEAK_TFLOPS,
