@@ -45,7 +45,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=240)
     ap.add_argument("--rotate-gib", type=float, default=1.0)
     ap.add_argument("--prefill-steps", type=int, default=60)
-    ap.add_argument("--prefill-warmup", type=int, default=20)
+    ap.add_argument("--prefill-warmup", type=int, default=100)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-m16", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
