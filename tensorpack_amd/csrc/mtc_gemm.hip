@@ -72,6 +72,15 @@ __device__ __forceinline__ uint32_t opaque(uint32_t x) {
   return x;
 }
 
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// A buffer resource (base, byte size) for compiler-visible loads: an offset past the end
+// reads zeros without touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                           (int)(bytes < 0x7FFFFFFF ? bytes : 0x7FFFFFFF), 0x00020000);
+}
+
 // A raw buffer resource (base, byte size) for the DMA copies below.
 __device__ __forceinline__ u32x4_t buffer_rsrc(const void* base, uint32_t bytes) {
   const uint64_t b = (uint64_t)(uintptr_t)base;
@@ -275,36 +284,45 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, c
 
   // ---------------- producers: load X and cells, decode, stage the next step ----------------
   const int p = tid - 64 * kConsumerWaves;                 // 0 .. kProducers-1
-  const uint32_t* cells = d.cells + (((size_t)ct * d.n_ksteps + kb0) * kCells + p) * CW;
   const uint32_t* step_off = d.step_off + (size_t)ct * d.n_ksteps + kb0;
   // cells p and p + kProducers of a step: descriptor words (two sets that swap roles
   // every step, so no register copies wait on loads in flight) and payload words.
+  // Every load goes through a buffer resource and every cell issues the same loads
+  // (one descriptor load, four 16-byte payload loads; those its class does not need
+  // read past the buffer's end and return zeros): with no per-lane branches around
+  // loads, the compiler's waits count exactly, so a step waits only for the loads
+  // issued a step earlier, never for the ones it has just issued.
+  const __amdgpu_buffer_rsrc_t cell_r = buffer_of(d.cells + ((size_t)ct * d.n_ksteps + kb0) * kCells * CW,
+                                                  (int64_t)nks * kCells * CW * 4);
+  const __amdgpu_buffer_rsrc_t pay_r = buffer_of(d.payload, d.payload_dwords * 4);
   uint32_t sa0[CW], sa1[CW], sb0[CW], sb1[CW];
   uint32_t base_a = 0, base_b = 0;
   u32x4_t q0[4], q1[4];
-  auto load_desc = [&](int ks, uint32_t (&w0)[CW], uint32_t (&w1)[CW], uint32_t& base) {
-    const uint32_t* cp = cells + (size_t)ks * kCells * CW;
-#pragma unroll
-    for (int t = 0; t < CW; ++t) {
-      w0[t] = cp[t];
-      w1[t] = cp[(size_t)kProducers * CW + t];
+  auto load_words = [&](uint32_t off, uint32_t (&w)[CW]) __attribute__((always_inline)) {
+    if constexpr (CW == 2) {
+      const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(cell_r, off, 0, 0);
+      w[0] = v.x;
+      w[1] = v.y;
+    } else {
+      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(cell_r, off, 0, 0);
+      w[0] = v.x;
+      w[1] = v.y;
+      w[2] = v.z;
+      w[3] = v.w;
     }
+  };
+  auto load_desc = [&](int ks, uint32_t (&w0)[CW], uint32_t (&w1)[CW], uint32_t& base) {
+    load_words((uint32_t)((ks * kCells + p) * CW) * 4u, w0);
+    load_words((uint32_t)((ks * kCells + p + kProducers) * CW) * 4u, w1);
     base = step_off[ks];
   };
   auto load_cell = [&](const uint32_t (&w)[CW], uint32_t base, u32x4_t (&q)[4]) {
     const uint32_t cls = (w[0] >> 14) & 3u;
-    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(d.payload + base + (w[0] & 0x3FFFu));
-    if (cls == 0) {
-      q[0] = src[0];
-    } else if (cls == 1) {
-      q[0] = src[0];
-      q[1] = src[1];
-    } else if (cls == 2) {
-      q[0] = src[0];
-      q[1] = src[1];
-      q[2] = src[2];
-      q[3] = src[3];
-    }
+    const uint32_t o = (base + (w[0] & 0x3FFFu)) * 4u;
+    const uint32_t n = cls == 0 ? 1u : cls == 1 ? 2u : cls == 2 ? 4u : 0u;
+#pragma unroll
+    for (uint32_t t = 0; t < 4; ++t)
+      q[t] = __builtin_amdgcn_raw_buffer_load_b128(pay_r, t < n ? o + 16u * t : kOutOfRange, 0, 0);
   };
   auto load_payload = [&](const uint32_t (&w0)[CW], const uint32_t (&w1)[CW], uint32_t base) {
     load_cell(w0, base, q0);
