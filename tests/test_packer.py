@@ -232,3 +232,25 @@ def test_step_records_survive_save_load(tmp_path):
     back = type(ps).load(str(f))
     assert np.array_equal(back.steps, ps.steps) and np.array_equal(back.unit_hdr, ps.unit_hdr)
     assert np.array_equal(_bits(decode_steps(back)), _bits(decode_stream(ps)))
+
+
+@pytest.mark.parametrize("K,N,M", [(4096, 4096, 1), (4096, 4096, 16), (8192, 8192, 1), (4864, 896, 1),
+                                   (4864, 896, 16), (896, 896, 1), (896, 4864, 1), (896, 128, 1), (10000, 64, 1),
+                                   (100, 64, 1)])
+def test_decode_row_chunks_are_even_and_fill_the_chip(K, N, M):
+    from tensorpack_amd.kernels.gemm import DECODE_FILL_BLOCKS, DECODE_MIN_SPLIT_ROWS, DECODE_X_LDS_BYTES, \
+        _decode_mt, gemv_chunk_rows
+    c = gemv_chunk_rows(K, N, M)
+    rows = -(-K // 32) * 32
+    cap = min(DECODE_X_LDS_BYTES // (4 * _decode_mt(M)) // 32 * 32, 4096)
+    n = -(-rows // c)
+    assert c % 32 == 0 and 32 <= c <= cap
+    if rows <= cap:
+        assert n == 1                                   # no split when the X rows fit on chip
+    else:
+        need = -(-rows // cap)
+        assert n >= need
+        assert rows - (n - 1) * c > 0 and (n - 1) * c < rows      # every chunk holds rows
+        assert c - (rows - (n - 1) * c) < 32 * n        # chunks are equal up to 32-row rounding
+        if n > need:                                    # a split beyond the minimum only to fill the chip
+            assert 2 * (N // 32) * (n - 1) < DECODE_FILL_BLOCKS and c >= DECODE_MIN_SPLIT_ROWS - 32
