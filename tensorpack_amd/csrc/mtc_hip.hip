@@ -3,10 +3,12 @@
 //
 //   k_fill_zero  : zero an fp32 buffer (used before dequant; no memset nodes)
 //   k_dequant    : stream -> dense W_hat (bit-exact q*s, +0.0 for P0)
-//   k_gemv<MT,FS>: fp32 decode path for M tiles of MT rows (FS: fp32 leaf
-//                  scales). One block per (unit, 4 column groups); waves walk
-//                  the block's step records, streaming payload into registers,
-//                  and accumulate 4 columns per lane; one reduction at the end.
+//   k_gemv<MT,FS,LG,NW>: fp32 decode path for M tiles of MT rows (FS: fp32 leaf
+//                  scales, LG: X rows gathered in LDS, NW waves). One block per
+//                  (unit, 4 column groups); waves walk the block's step records,
+//                  streaming payload into registers, and accumulate 4 columns per
+//                  lane; one reduction at the end.
+//   k_gemv_group : the same blocks for up to 4 matrices that share X, one launch
 //   (the prefill path, k_gemm_tile over the tile stream, is in mtc_gemm.hip)
 //
 // Reference behaviour: mtc/kernels/gemm.py:124-210 (block loop: skip P0
@@ -133,7 +135,8 @@ __global__ __launch_bounds__(512) void k_dequant(const mtc_stream_desc d, float*
 // ---------------------------------------------------------------------------
 // fp32 decode GEMV
 //
-// Block = (unit, block of 4 column groups), W waves. The block's work is its list of
+// Block = (unit, block of 4 column groups), W waves (16, or 8 for 4-row M tiles and for
+// streams whose blocks hold at most 16 records). The block's work is its list of
 // step records; wave w executes records w, w + W, w + 2W, ... (round robin, so the
 // waves of each SIMD get near-equal counts). In a step, lane 16g + i decodes chunk
 // 16j + i of column-group slot g's bucket of the step's kind: one kind per step, so

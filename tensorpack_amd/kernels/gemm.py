@@ -50,7 +50,8 @@ def gemv_chunk_rows(K: int, N: int, M: int = 1) -> int:
     otherwise the fewest chunks that fit, of equal size (a 4864-row matrix splits 2432 +
     2432, not 4096 + 768). A matrix that needs a split anyway and has too few column panels
     to fill the chip (two blocks per unit) is cut into more chunks of at least
-    DECODE_MIN_SPLIT_ROWS rows."""
+    DECODE_MIN_SPLIT_ROWS rows. The environment variable MTC_GEMV_CHUNK_ROWS, when set,
+    overrides the choice (a multiple of 32; for layout experiments)."""
     env = os.environ.get("MTC_GEMV_CHUNK_ROWS")
     if env:
         return int(env)
