@@ -468,6 +468,21 @@ def main():
                          f"reference block loop (gemm.py:124-210)",
                "gpu_vs_cpu_rel_frobenius": O.relative_frobenius_error(y_cpu, y_gpu)}
         log(f"cpu baseline {cpu['value']:.3f} GB/s on {cores} threads; gpu-vs-cpu rel {cpu['gpu_vs_cpu_rel_frobenius']:.2e}")
+        # the reference's own inference path: X @ the cached dequantized weight (LinearMTCAdaptive.forward,
+        # mtc/nn/layers.py:150-151), numpy BLAS over a dense fp32 W_hat
+        w_hat = np.ascontiguousarray(alloc.dequant, dtype=np.float32)
+        x @ w_hat
+        n_np, t0 = 0, time.time()
+        while time.time() - t0 < 2.0 or n_np < 3:
+            x @ w_hat
+            n_np += 1
+        el_np = time.time() - t0
+        cpu["numpy_dequant_matmul"] = {"ms_per_call": 1e3 * el_np / n_np,
+                                       "packed_GBps": packed * n_np / el_np / 1e9,
+                                       "dense_fp32_GBps": w_hat.nbytes * n_np / el_np / 1e9,
+                                       "sample": f"{n_np} calls of x (1 x 4096) @ W_hat (4096 x 4096 fp32) in {el_np:.1f}s"}
+        log(f"cpu numpy X @ W_hat: {1e3 * el_np / n_np:.2f} ms/call")
+        del w_hat
 
     # ---------------- c4 prefill ----------------
     if not args.no_prefill:
