@@ -15,6 +15,7 @@
  *   mtc_gemv_f32_group <- several LinearMTCAdaptive.forward calls on one input,
  *                     mtc/nn/layers.py:150-151 (X @ W per layer), e.g. the q/k/v or
  *                     gate/up projections of a decoder layer, in one launch
+ *   mtc_gemm_bf16_group <- the same layer calls at prefill shapes
  *   mtc_gemm_bf16  <- same kernel/entry point, prefill shapes (bf16 MFMA), over
  *                     the tile stream (mtc_tile_desc)
  *   mtc_dequant    <- MTCMatrix.to_array, gemm.py:510-538, and
@@ -210,6 +211,17 @@ size_t mtc_gemm_workspace_bytes(const mtc_tile_desc* d, int M, int x_dtype);
  * (ldx % 8 == 0). Any M >= 1. */
 int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, int64_t ldx, void* Y, int y_dtype,
                   int64_t ldy, int M, void* workspace, size_t workspace_bytes, void* hip_stream);
+
+/* Prefill for n (1..MTC_MAX_GROUP) matrices that read the same X, one launch per kernel
+ * (X staging, tile GEMM, split-K reduction) instead of one per matrix:
+ * Y[i] (M x N_i, leading dim ldy[i]) = X * W_hat_i. Every tile stream must have the same
+ * K and scale format. The workspace (mtc_gemm_group_workspace_bytes, 256-byte aligned, no
+ * initialisation) holds, per member, its staged X and its split-K partials. Each Y[i]
+ * equals, bit for bit, what mtc_gemm_bf16 writes for matrix i alone. */
+size_t mtc_gemm_group_workspace_bytes(const mtc_tile_desc* const* descs, int n, int M, int x_dtype);
+int mtc_gemm_bf16_group(const mtc_tile_desc* const* descs, int n, const void* X, int x_dtype, int64_t ldx,
+                        void* const* Y, int y_dtype, const int64_t* ldy, int M, void* workspace,
+                        size_t workspace_bytes, void* hip_stream);
 
 #ifdef __cplusplus
 }

@@ -16,7 +16,7 @@ ERROR_NAMES = {
 
 EXPORTED = ("mtc_abi_version", "mtc_last_error", "mtc_check_desc", "mtc_dequant",
             "mtc_gemv_workspace_bytes", "mtc_gemv_f32", "mtc_gemv_f32_group", "mtc_check_tile_desc", "mtc_gemm_workspace_bytes",
-            "mtc_gemm_bf16")
+            "mtc_gemm_bf16", "mtc_gemm_group_workspace_bytes", "mtc_gemm_bf16_group")
 
 
 class MtcStreamDesc(ctypes.Structure):
@@ -96,6 +96,11 @@ def declare(lib: ctypes.CDLL) -> None:
     lib.mtc_gemm_workspace_bytes.argtypes = [TileDescP, i32, i32]
     lib.mtc_gemm_bf16.restype = i32
     lib.mtc_gemm_bf16.argtypes = [TileDescP, vp, i32, i64, vp, i32, i64, i32, vp, sz, vp]
+    lib.mtc_gemm_group_workspace_bytes.restype = sz
+    lib.mtc_gemm_group_workspace_bytes.argtypes = [ctypes.POINTER(TileDescP), i32, i32, i32]
+    lib.mtc_gemm_bf16_group.restype = i32
+    lib.mtc_gemm_bf16_group.argtypes = [ctypes.POINTER(TileDescP), i32, vp, i32, i64, ctypes.POINTER(vp), i32,
+                                        ctypes.POINTER(i64), i32, vp, sz, vp]
 
 
 class MtcError(RuntimeError):

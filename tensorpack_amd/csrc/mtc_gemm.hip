@@ -16,6 +16,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <string.h>
 
 #include <algorithm>
 
@@ -154,18 +155,20 @@ __device__ __forceinline__ void decode_cell(uint32_t cls, const u32x4_t* pw, flo
   }
 }
 
+// One output tile block of matrix `d`: tile-order index bx, K split by (the grid's x and y
+// for a launch of its own).
 template <bool kFS, int kYDT>
-__global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, const __bf16* __restrict__ X,
-                                                        int64_t ldx, void* __restrict__ Y, int64_t ldy, int M,
-                                                        int n_row_tiles, int tiles_per_xcd, int steps_per_split,
-                                                        float* __restrict__ part) {
+__device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const int bx, const int by,
+                                                const __bf16* __restrict__ X, int64_t ldx, void* __restrict__ Y,
+                                                int64_t ldy, int M, int n_row_tiles, int tiles_per_xcd,
+                                                int steps_per_split, float* __restrict__ part) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   constexpr int CW = kFS ? 4 : 2;
 
   // Tile order: each XCD takes a contiguous range of tile ids; ids run over groups of
   // kRowGroup row tiles, row tile fastest, so the blocks in flight on one XCD share
   // column tiles (B) and row tiles (A) in its L2.
-  const int tile = (int)(blockIdx.x % kXcds) * tiles_per_xcd + (int)(blockIdx.x / kXcds);
+  const int tile = (bx % kXcds) * tiles_per_xcd + bx / kXcds;
   const int n_ct = d.n_col_tiles;
   if (tile >= n_row_tiles * n_ct) return;
   const int per_group = kRowGroup * n_ct;
@@ -177,9 +180,9 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, c
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: keeps per-wave control scalar
   const int m0 = rt * kTM, n0 = ct * kTN;
-  // split K: this block runs steps kb0 .. kb0 + nks - 1 (blockIdx.y) and, with `part`,
-  // writes its partial tile to part[blockIdx.y] instead of Y
-  const int kb0 = (int)blockIdx.y * steps_per_split;
+  // split K: this block runs steps kb0 .. kb0 + nks - 1 (split by) and, with `part`,
+  // writes its partial tile to part[by] instead of Y
+  const int kb0 = by * steps_per_split;
   const int nks = min(steps_per_split, d.n_ksteps - kb0);
 
   if (wave < kConsumerWaves) {
@@ -256,8 +259,8 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, c
     }
 
     // epilogue: C element e of lane l is row (e/4)*8 + (l/32)*4 + e%4, column l%32.
-    // Split K writes a plain fp32 partial tile to part[blockIdx.y] (no column permutation).
-    float* const yf = part ? part + (size_t)blockIdx.y * M * d.N : reinterpret_cast<float*>(Y);
+    // Split K writes a plain fp32 partial tile to part[by] (no column permutation).
+    float* const yf = part ? part + (size_t)by * M * d.N : reinterpret_cast<float*>(Y);
     const int64_t ld = part ? (int64_t)d.N : ldy;
     const bool fp32_out = part || kYDT == MTC_DTYPE_F32;
 #pragma unroll
@@ -381,10 +384,45 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, c
   }
 }
 
+template <bool kFS, int kYDT>
+__global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, const __bf16* __restrict__ X,
+                                                        int64_t ldx, void* __restrict__ Y, int64_t ldy, int M,
+                                                        int n_row_tiles, int tiles_per_xcd, int steps_per_split,
+                                                        float* __restrict__ part) {
+  gemm_tile_block<kFS, kYDT>(d, (int)blockIdx.x, (int)blockIdx.y, X, ldx, Y, ldy, M, n_row_tiles, tiles_per_xcd,
+                             steps_per_split, part);
+}
+
+// Up to kMaxGroup matrices that read the same X, in one launch of each kernel: member i owns
+// tile blocks [start[i], start[i + 1]) (whole XCD rounds, so each block runs on the XCD it
+// would in a launch of its own) and K splits 0 .. splits[i] - 1 along the grid's y.
+constexpr int kMaxGroup = MTC_MAX_GROUP;
+struct GemmGroup {
+  mtc_tile_desc d[kMaxGroup];
+  const __bf16* X[kMaxGroup];
+  int64_t ldx[kMaxGroup];
+  void* Y[kMaxGroup];
+  int64_t ldy[kMaxGroup];
+  float* part[kMaxGroup];
+  int tiles_per_xcd[kMaxGroup];
+  int steps_per_split[kMaxGroup];
+  int splits[kMaxGroup];
+  int start[kMaxGroup + 1];
+};
+
+template <bool kFS, int kYDT>
+__global__ __launch_bounds__(kThreads) void k_gemm_tile_group(const GemmGroup g, int M, int n_row_tiles) {
+  int i = 0;
+#pragma unroll
+  for (int k = 1; k < kMaxGroup; ++k) i += (int)blockIdx.x >= g.start[k];
+  if ((int)blockIdx.y >= g.splits[i]) return;               // this member has fewer K splits
+  gemm_tile_block<kFS, kYDT>(g.d[i], (int)blockIdx.x - g.start[i], (int)blockIdx.y, g.X[i], g.ldx[i], g.Y[i], g.ldy[i],
+                             M, n_row_tiles, g.tiles_per_xcd[i], g.steps_per_split[i], g.part[i]);
+}
+
 // Xp[m, k] = bf16(X[m, row_perm[k]]) (identity without a permutation); 8 outputs per thread.
-__global__ __launch_bounds__(kStageThreads) void k_stage_x(const void* __restrict__ X, int xdt, int64_t ldx,
-                                                           const int32_t* __restrict__ row_perm,
-                                                           __bf16* __restrict__ Xp, int K) {
+__device__ __forceinline__ void stage_x_row(const void* __restrict__ X, int xdt, int64_t ldx,
+                                            const int32_t* __restrict__ row_perm, __bf16* __restrict__ Xp, int K) {
   const int64_t m = blockIdx.y;
   const int k0 = ((int)blockIdx.x * kStageThreads + (int)threadIdx.x) * 8;
   if (k0 >= K) return;
@@ -399,12 +437,28 @@ __global__ __launch_bounds__(kStageThreads) void k_stage_x(const void* __restric
   *reinterpret_cast<u32x4_t*>(Xp + m * K + k0) = o;
 }
 
+__global__ __launch_bounds__(kStageThreads) void k_stage_x(const void* __restrict__ X, int xdt, int64_t ldx,
+                                                           const int32_t* __restrict__ row_perm,
+                                                           __bf16* __restrict__ Xp, int K) {
+  stage_x_row(X, xdt, ldx, row_perm, Xp, K);
+}
+
+// Staging for the members of a group that need it (grid z = entry).
+struct StageGroup {
+  const int32_t* row_perm[kMaxGroup];
+  __bf16* Xp[kMaxGroup];
+};
+
+__global__ __launch_bounds__(kStageThreads) void k_stage_x_group(const StageGroup g, const void* __restrict__ X,
+                                                                 int xdt, int64_t ldx, int K) {
+  stage_x_row(X, xdt, ldx, g.row_perm[blockIdx.z], g.Xp[blockIdx.z], K);
+}
+
 // Y[m, col_perm[n]] = sum over splits of part[z][m][n] (fixed order: deterministic).
 template <int kYDT>
-__global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ part, int splits, int M, int N,
-                                                       const int32_t* __restrict__ col_perm, void* __restrict__ Y,
-                                                       int64_t ldy) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void splitk_reduce_at(const int64_t i, const float* __restrict__ part, int splits, int M,
+                                                 int N, const int32_t* __restrict__ col_perm, void* __restrict__ Y,
+                                                 int64_t ldy) {
   if (i >= (int64_t)M * N) return;
   const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
   float v = 0.0f;
@@ -414,6 +468,30 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
     reinterpret_cast<float*>(Y)[(int64_t)m * ldy + col] = v;
   else
     reinterpret_cast<__bf16*>(Y)[(int64_t)m * ldy + col] = (__bf16)v;
+}
+
+template <int kYDT>
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ part, int splits, int M, int N,
+                                                       const int32_t* __restrict__ col_perm, void* __restrict__ Y,
+                                                       int64_t ldy) {
+  splitk_reduce_at<kYDT>((int64_t)blockIdx.x * blockDim.x + threadIdx.x, part, splits, M, N, col_perm, Y, ldy);
+}
+
+// The split-K members of a group (grid y = entry).
+struct ReduceGroup {
+  const float* part[kMaxGroup];
+  int splits[kMaxGroup];
+  int N[kMaxGroup];
+  const int32_t* col_perm[kMaxGroup];
+  void* Y[kMaxGroup];
+  int64_t ldy[kMaxGroup];
+};
+
+template <int kYDT>
+__global__ __launch_bounds__(256) void k_splitk_reduce_group(const ReduceGroup g, int M) {
+  const int e = blockIdx.y;
+  splitk_reduce_at<kYDT>((int64_t)blockIdx.x * blockDim.x + threadIdx.x, g.part[e], g.splits[e], M, g.N[e],
+                         g.col_perm[e], g.Y[e], g.ldy[e]);
 }
 
 int check_tile_desc(const mtc_tile_desc* d) {
@@ -484,6 +562,36 @@ int launch_tile(const mtc_tile_desc* d, const __bf16* X, int64_t ldx, void* Y, i
   return check_launch("k_splitk_reduce");
 }
 
+// Workspace of a group: per member, its staged X (if any) then its split-K partials, each
+// on a 256-byte boundary.
+size_t round256(size_t b) { return (b + 255) / 256 * 256; }
+size_t group_ws_bytes(const mtc_tile_desc* const* descs, int n, int M, int x_dtype) {
+  size_t b = 0;
+  for (int i = 0; i < n; ++i) b += round256(staging_bytes(descs[i], M, x_dtype)) + round256(partial_bytes(descs[i], M));
+  return b;
+}
+
+template <bool kFS, int kYDT>
+int launch_tile_group(GemmGroup& g, int n, int M, const ReduceGroup& rg, int n_red, hipStream_t st) {
+  if ((size_t)kLdsBytes > mtc::host::device_lds_limit())
+    return fail(MTC_E_SHAPE, "prefill kernel needs %d B of LDS per block, device has %zu", kLdsBytes,
+                mtc::host::device_lds_limit());
+  const void* fn = reinterpret_cast<const void*>(&k_gemm_tile_group<kFS, kYDT>);
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+  if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+  const int n_row_tiles = (M + kTM - 1) / kTM;
+  int max_splits = 1;
+  for (int i = 0; i < n; ++i) max_splits = std::max(max_splits, g.splits[i]);
+  hipLaunchKernelGGL((k_gemm_tile_group<kFS, kYDT>), dim3(g.start[n], max_splits), dim3(kThreads), kLdsBytes, st, g, M,
+                     n_row_tiles);
+  int rc = check_launch("k_gemm_tile_group");
+  if (rc || n_red == 0) return rc;
+  int64_t max_n = 0;
+  for (int i = 0; i < n_red; ++i) max_n = std::max(max_n, (int64_t)M * rg.N[i]);
+  hipLaunchKernelGGL(k_splitk_reduce_group<kYDT>, dim3((unsigned)((max_n + 255) / 256), n_red), dim3(256), 0, st, rg, M);
+  return check_launch("k_splitk_reduce_group");
+}
+
 }  // namespace
 
 MTC_API int mtc_check_tile_desc(const mtc_tile_desc* d) { return check_tile_desc(d); }
@@ -529,4 +637,102 @@ MTC_API int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, in
   }
   return y_dtype == MTC_DTYPE_F32 ? launch_tile<false, MTC_DTYPE_F32>(d, xb, ldb, Y, ldy, M, part, st)
                                   : launch_tile<false, MTC_DTYPE_BF16>(d, xb, ldb, Y, ldy, M, part, st);
+}
+
+MTC_API size_t mtc_gemm_group_workspace_bytes(const mtc_tile_desc* const* descs, int n, int M, int x_dtype) {
+  if (!descs || n < 1 || n > kMaxGroup || M <= 0) return 0;
+  for (int i = 0; i < n; ++i)
+    if (check_tile_desc(descs[i])) return 0;
+  return group_ws_bytes(descs, n, M, x_dtype);
+}
+
+MTC_API int mtc_gemm_bf16_group(const mtc_tile_desc* const* descs, int n, const void* X, int x_dtype, int64_t ldx,
+                                void* const* Y, int y_dtype, const int64_t* ldy, int M, void* workspace,
+                                size_t workspace_bytes, void* hip_stream) {
+  if (!descs || !Y || !ldy) return fail(MTC_E_NULL, "descs, Y or ldy is NULL");
+  if (n < 1 || n > kMaxGroup) return fail(MTC_E_SHAPE, "group of %d matrices (1..%d)", n, kMaxGroup);
+  if (!X) return fail(MTC_E_NULL, "X is NULL");
+  if (x_dtype != MTC_DTYPE_F32 && x_dtype != MTC_DTYPE_BF16) return fail(MTC_E_DTYPE, "x_dtype=%d", x_dtype);
+  if (y_dtype != MTC_DTYPE_F32 && y_dtype != MTC_DTYPE_BF16) return fail(MTC_E_DTYPE, "y_dtype=%d", y_dtype);
+  if (M <= 0) return fail(MTC_E_SHAPE, "M=%d must be positive", M);
+  for (int i = 0; i < n; ++i) {
+    const mtc_tile_desc* d = descs[i];
+    int rc = check_tile_desc(d);
+    if (rc) return rc;
+    if (!Y[i]) return fail(MTC_E_NULL, "Y[%d] is NULL", i);
+    if (d->K != descs[0]->K) return fail(MTC_E_SHAPE, "group member %d has K=%d, member 0 K=%d", i, d->K, descs[0]->K);
+    if ((d->flags & MTC_FLAG_FP32_SCALES) != (descs[0]->flags & MTC_FLAG_FP32_SCALES))
+      return fail(MTC_E_SHAPE, "group member %d differs from member 0 in scale format", i);
+    if (ldx < d->K || ldy[i] < d->N)
+      return fail(MTC_E_SHAPE, "ldx=%lld < K or ldy[%d]=%lld < N", (long long)ldx, i, (long long)ldy[i]);
+    if (!needs_staging(d, x_dtype) && (ldx % 8 || (reinterpret_cast<uintptr_t>(X) & 15)))
+      return fail(MTC_E_SHAPE, "bf16 X read in place needs 16-byte aligned rows (ldx=%lld)", (long long)ldx);
+  }
+  const size_t need = group_ws_bytes(descs, n, M, x_dtype);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(MTC_E_WORKSPACE, "prefill workspace of %zu bytes needed, %zu given", need, workspace ? workspace_bytes : 0);
+  if (need && (reinterpret_cast<uintptr_t>(workspace) & 255))
+    return fail(MTC_E_WORKSPACE, "workspace not 256-byte aligned");
+  if (M > (1 << 30)) return fail(MTC_E_SHAPE, "M=%d too large", M);
+  hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);
+  GemmGroup g;
+  StageGroup sg;
+  ReduceGroup rg;
+  memset(&g, 0, sizeof(g));
+  memset(&sg, 0, sizeof(sg));
+  memset(&rg, 0, sizeof(rg));
+  int n_stage = 0, n_red = 0, blocks = 0;
+  char* ws = reinterpret_cast<char*>(workspace);
+  const int n_row_tiles = (M + kTM - 1) / kTM;
+  for (int i = 0; i < n; ++i) {
+    const mtc_tile_desc* d = descs[i];
+    g.d[i] = *d;
+    g.Y[i] = Y[i];
+    g.ldy[i] = ldy[i];
+    const size_t stage = round256(staging_bytes(d, M, x_dtype)), pb = round256(partial_bytes(d, M));
+    if (stage) {
+      sg.row_perm[n_stage] = d->row_perm;
+      sg.Xp[n_stage] = reinterpret_cast<__bf16*>(ws);
+      ++n_stage;
+      g.X[i] = reinterpret_cast<const __bf16*>(ws);
+      g.ldx[i] = d->K;
+    } else {
+      g.X[i] = reinterpret_cast<const __bf16*>(X);
+      g.ldx[i] = ldx;
+    }
+    if (g.ldx[i] >= ((int64_t)1 << 31) / (2 * kTM))
+      return fail(MTC_E_SHAPE, "ldx=%lld too large for 32-bit X tile offsets", (long long)g.ldx[i]);
+    int splits = 1;
+    g.steps_per_split[i] = split_steps(d, M, &splits);
+    g.splits[i] = splits;
+    g.part[i] = splits > 1 ? reinterpret_cast<float*>(ws + stage) : nullptr;
+    if (splits > 1) {
+      rg.part[n_red] = g.part[i];
+      rg.splits[n_red] = splits;
+      rg.N[n_red] = d->N;
+      rg.col_perm[n_red] = d->col_perm;
+      rg.Y[n_red] = Y[i];
+      rg.ldy[n_red] = ldy[i];
+      ++n_red;
+    }
+    ws += stage + pb;
+    const int64_t n_tiles = (int64_t)n_row_tiles * d->n_col_tiles;
+    g.tiles_per_xcd[i] = (int)((n_tiles + kXcds - 1) / kXcds);
+    g.start[i] = blocks;
+    blocks += g.tiles_per_xcd[i] * kXcds;
+  }
+  for (int i = n; i <= kMaxGroup; ++i) g.start[i] = blocks;
+  if (n_stage) {
+    dim3 grid((descs[0]->K / 8 + kStageThreads - 1) / kStageThreads, M, n_stage);
+    hipLaunchKernelGGL(k_stage_x_group, grid, dim3(kStageThreads), 0, st, sg, X, x_dtype, ldx, descs[0]->K);
+    int rc = check_launch("k_stage_x_group");
+    if (rc) return rc;
+  }
+  const bool fs = descs[0]->flags & MTC_FLAG_FP32_SCALES;
+  if (fs) {
+    return y_dtype == MTC_DTYPE_F32 ? launch_tile_group<true, MTC_DTYPE_F32>(g, n, M, rg, n_red, st)
+                                    : launch_tile_group<true, MTC_DTYPE_BF16>(g, n, M, rg, n_red, st);
+  }
+  return y_dtype == MTC_DTYPE_F32 ? launch_tile_group<false, MTC_DTYPE_F32>(g, n, M, rg, n_red, st)
+                                  : launch_tile_group<false, MTC_DTYPE_BF16>(g, n, M, rg, n_red, st);
 }

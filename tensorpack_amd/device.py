@@ -243,3 +243,44 @@ class DeviceTiles:
                                     current_stream_handle(self.device))
         _abi.check(self.lib, "mtc_gemm_bf16", rc)
         return out
+
+
+_GROUP_WS: dict = {}
+
+
+def gemm_bf16_group(tiles, X, outs=None, out_dtype=None):
+    """Y_i = X @ W_hat_i for 1..MAX_GROUP tile streams that share X (same K), one launch per
+    kernel (mtc_gemm_bf16_group). Each Y_i is bit-identical to tiles[i].gemm_bf16(X). The
+    workspace is cached per device; calls on one device are ordered by its stream."""
+    torch = _torch()
+    tiles = list(tiles)
+    n = len(tiles)
+    if not 1 <= n <= _abi.MAX_GROUP:
+        raise ValueError(f"a group holds 1..{_abi.MAX_GROUP} matrices, got {n}")
+    dev = tiles[0].device
+    if any(t.device != dev for t in tiles):
+        raise ValueError("group members live on different devices")
+    assert X.dim() == 2 and X.stride(1) == 1 and X.dtype in (torch.float32, torch.bfloat16)
+    M = X.shape[0]
+    out_dtype = out_dtype or torch.float32
+    if outs is None:
+        outs = [torch.empty((M, t.N), dtype=out_dtype, device=dev) for t in tiles]
+    for o, t in zip(outs, tiles):
+        assert o.dtype in (torch.float32, torch.bfloat16) and o.stride(1) == 1 and tuple(o.shape) == (M, t.N)
+    if len({o.dtype for o in outs}) != 1:
+        raise ValueError("group outputs must share one dtype")
+    xdt = _abi.MTC_DTYPE_BF16 if X.dtype == torch.bfloat16 else _abi.MTC_DTYPE_F32
+    ydt = _abi.MTC_DTYPE_BF16 if outs[0].dtype == torch.bfloat16 else _abi.MTC_DTYPE_F32
+    lib = tiles[0].lib
+    descs = (_abi.TileDescP * n)(*[ctypes.pointer(t.desc) for t in tiles])
+    need = int(lib.mtc_gemm_group_workspace_bytes(descs, n, M, xdt))
+    ws = _GROUP_WS.get(str(dev))
+    if need and (ws is None or ws.numel() < need):
+        ws = torch.empty(need, dtype=torch.uint8, device=dev)
+        _GROUP_WS[str(dev)] = ws
+    ys = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+    lds = (ctypes.c_int64 * n)(*[o.stride(0) for o in outs])
+    rc = lib.mtc_gemm_bf16_group(descs, n, X.data_ptr(), xdt, X.stride(0), ys, ydt, lds, M,
+                                 ws.data_ptr() if need else None, need, current_stream_handle(dev))
+    _abi.check(lib, "mtc_gemm_bf16_group", rc)
+    return outs

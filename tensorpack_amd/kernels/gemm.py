@@ -405,8 +405,9 @@ def mtc_gemm_group(A, Bs, *, compute: str = "auto"):
     LinearMTCAdaptive.forward call, mtc/nn/layers.py:150-151).
 
     At decode sizes (fp32 path) matrices whose decode streams have a single row chunk run
-    MAX_GROUP at a time in one launch (mtc_gemv_f32_group); each result is bit-identical to
-    mtc_gemm(A, W_i). Other members, and the bf16 path, launch one matrix at a time.
+    MAX_GROUP at a time in one launch (mtc_gemv_f32_group); at prefill sizes (bf16 path)
+    MAX_GROUP at a time through one launch per kernel (mtc_gemm_bf16_group). Each result
+    is bit-identical to mtc_gemm(A, W_i); other members launch one matrix at a time.
     Returns a list in the order of Bs, each of the kind mtc_gemm returns.
     """
     import torch
@@ -456,5 +457,25 @@ def mtc_gemm_group(A, Bs, *, compute: str = "auto"):
             outs = [y.squeeze(0) for y in outs]
         if from_numpy:
             return [y.cpu().numpy() for y in outs]
+        return outs
+    if compute == "bf16" and M > 0:
+        from ..device import gemm_bf16_group
+        Xb = X if X.dtype in (torch.float32, torch.bfloat16) else X.float()
+        if Xb.stride(1) != 1:
+            Xb = Xb.contiguous()
+        tiles = [B.device_tiles(dev) for B in Bs]
+        # members that can share a launch: same scale format
+        groups: Dict[bool, list] = {}
+        for i, t in enumerate(tiles):
+            groups.setdefault(t.host.fp32_scales, []).append(i)
+        for idx in groups.values():
+            for j in range(0, len(idx), _abi.MAX_GROUP):
+                part = idx[j:j + _abi.MAX_GROUP]
+                for i, y in zip(part, gemm_bf16_group([tiles[i] for i in part], Xb)):
+                    outs[i] = y
+        if squeeze:
+            outs = [y.squeeze(0) for y in outs]
+        if from_numpy:
+            return [y.float().cpu().numpy() for y in outs]
         return outs
     return [mtc_gemm(A, B, compute=compute) for B in Bs]

@@ -143,6 +143,35 @@ def test_group_entry_rejects_bad_arguments_before_any_gpu_call(hip):
     assert f(descs(_desc(chunk_rows=256, n_chunks=1, abi_version=3)), 1, 0x10, 256, ys(1), lds(1), 1, None) == -7
 
 
+def test_group_prefill_entry_rejects_bad_arguments_before_any_gpu_call(hip):
+    a, b = _tdesc(), _tdesc(N=544, n_col_tiles=3)
+    D = _abi.TileDescP
+    descs = lambda *ds: (D * len(ds))(*[ctypes.pointer(x) for x in ds])
+    ys = lambda n: (ctypes.c_void_p * n)(*([0x10] * n))
+    lds = lambda n, v=600: (ctypes.c_int64 * n)(*([v] * n))
+    f = hip.mtc_gemm_bf16_group
+    assert f(None, 1, 0x10, 1, 256, ys(1), 0, lds(1), 4, None, 0, None) == -1
+    assert f(descs(a), 0, 0x10, 1, 256, ys(1), 0, lds(1), 4, None, 0, None) == -3
+    assert f(descs(*[a] * 5), 5, 0x10, 1, 256, ys(5), 0, lds(5), 4, None, 0, None) == -3
+    assert f(descs(a), 1, None, 1, 256, ys(1), 0, lds(1), 4, None, 0, None) == -1
+    assert f(descs(a), 1, 0x10, 5, 256, ys(1), 0, lds(1), 4, None, 0, None) == -4               # x dtype
+    assert f(descs(a), 1, 0x10, 1, 256, ys(1), 9, lds(1), 4, None, 0, None) == -4               # y dtype
+    assert f(descs(a), 1, 0x10, 1, 256, ys(1), 0, lds(1), 0, None, 0, None) == -3               # M
+    other_k = _tdesc(K=512, n_ksteps=8)
+    assert f(descs(a, other_k), 2, 0x10, 1, 512, ys(2), 0, lds(2), 4, None, 0, None) == -3      # different K
+    assert f(descs(a, _tdesc(flags=_abi.MTC_FLAG_FP32_SCALES)), 2, 0x10, 1, 256, ys(2), 0, lds(2), 4, None, 0,
+             None) == -3                                                                          # scale format
+    assert f(descs(a, b), 2, 0x10, 1, 100, ys(2), 0, lds(2), 4, None, 0, None) == -3           # ldx < K
+    assert f(descs(a, b), 2, 0x10, 1, 256, ys(2), 0, lds(2, 300), 4, None, 0, None) == -3      # ldy < N
+    assert f(descs(a), 1, 0x10, 1, 260, ys(1), 0, lds(1), 4, None, 0, None) == -3              # unaligned bf16 rows
+    need = hip.mtc_gemm_group_workspace_bytes(descs(a, b), 2, 4, 0)                             # fp32 X: staged per member
+    assert need == 2 * 4 * 256 * 2 + (256 - 4 * 256 * 2 % 256) % 256 * 2
+    assert f(descs(a, b), 2, 0x10, 0, 256, ys(2), 0, lds(2), 4, 0x20, need - 1, None) == -5    # workspace too small
+    assert f(descs(a, b), 2, 0x10, 0, 256, ys(2), 0, lds(2), 4, 0x20, need, None) == -5        # unaligned workspace
+    assert hip.mtc_gemm_group_workspace_bytes(descs(a, b), 2, 4, 1) == 0                       # bf16 X in place, no split
+    assert hip.mtc_gemm_group_workspace_bytes(None, 2, 4, 1) == 0
+
+
 def _tdesc(**kw):
     d = _abi.MtcTileDesc()
     d.abi_version = _abi.ABI_VERSION

@@ -123,3 +123,40 @@ def test_linear_layers(gpu, M):
     ys = g(torch.from_numpy(X).to(gpu))
     for lin, y in zip((q, k), ys):
         assert np.array_equal(y.cpu().numpy(), lin(X)), M
+
+
+@pytest.mark.parametrize("M,xdtype,ydtype", [(37, "f32", "f32"), (300, "bf16", "f32"), (600, "bf16", "bf16"),
+                                             (20, "f32", "bf16")])
+@pytest.mark.parametrize("pick", [(0, 1, 2), (0, 1, 2, 3, 4), (4, 3)])
+def test_prefill_group_matches_single_calls_bit_for_bit(gpu, members, M, xdtype, ydtype, pick):
+    import torch
+    _say("prefill group", pick, M, xdtype, ydtype)
+    X = np.random.RandomState(M + len(pick)).randn(M, 256).astype(np.float32)
+    Xd = torch.from_numpy(X).to(gpu)
+    if xdtype == "bf16":
+        Xd = Xd.to(torch.bfloat16)
+    odt = torch.bfloat16 if ydtype == "bf16" else torch.float32
+    from tensorpack_amd.device import gemm_bf16_group
+    tiles = [members[i][3].device_tiles(gpu) for i in pick]
+    for j in range(0, len(tiles), _abi.MAX_GROUP):
+        part = list(range(j, min(j + _abi.MAX_GROUP, len(tiles))))
+        ys = gemm_bf16_group([tiles[k] for k in part], Xd, out_dtype=odt)
+        torch.cuda.synchronize()
+        for k, y in zip(part, ys):
+            name, W, a, m = members[pick[k]]
+            single = mtc_gemm(Xd, m, compute="bf16", out_dtype=odt)
+            assert torch.equal(y, single), (name, M)
+            ref = O.qt_gemm_f64(O.bf16_round(X), _oracle_what(a, W))
+            err = O.relative_frobenius_error(ref, y.float().cpu().numpy())
+            assert err <= 2e-3 + (4e-3 if ydtype == "bf16" else 0.0), (name, M, err)
+
+
+def test_prefill_group_through_mtc_gemm_group(gpu, members):
+    import torch
+    _say("prefill group via mtc_gemm_group")
+    X = torch.from_numpy(np.random.RandomState(3).randn(200, 256).astype(np.float32)).to(gpu)
+    mats = [m for _, _, _, m in members]
+    ys = mtc_gemm_group(X, mats)                       # 200 rows: bf16 path, 5 members -> two launches
+    torch.cuda.synchronize()
+    for (name, W, a, m), y in zip(members, ys):
+        assert torch.equal(y, mtc_gemm(X, m)), name
