@@ -512,17 +512,34 @@ int check_tile_desc(const mtc_tile_desc* d) {
 bool needs_staging(const mtc_tile_desc* d, int x_dtype) { return d->row_perm || x_dtype == MTC_DTYPE_F32; }
 
 constexpr int kFillCUs = 256;             // blocks that fill the chip (one 256 x 256 tile block per CU)
-constexpr int kMinStepsPerSplit = 4;
+constexpr int kMinStepsPerSplit = 2;
+constexpr double kStepUs = 2.0;           // time of one K-step of a tile block (measured: 1.9-2.4 us)
+constexpr double kReduceBytesPerUs = 4.0e6;   // split-K partials written + read, bytes per microsecond
+constexpr double kReduceLaunchUs = 3.0;   // the reduction pass's own launch
 
-// K splits for M rows: enough blocks to fill the chip when the output has few tiles,
-// at least kMinStepsPerSplit K-steps per split. Returns the steps per split.
+// K splits for M rows when the output has fewer tiles than the chip has CUs: the split
+// count (at most enough blocks to fill the chip, at least kMinStepsPerSplit K-steps per
+// split) that minimises the estimated time, K-steps per block plus the split-K partial
+// traffic (written by the tile blocks, read by the reduction). Returns the steps per split.
 int split_steps(const mtc_tile_desc* d, int M, int* splits) {
   const int64_t n_tiles = (int64_t)((M + kTM - 1) / kTM) * d->n_col_tiles;
-  int want = n_tiles >= kFillCUs ? 1 : (int)((kFillCUs + n_tiles - 1) / n_tiles);
-  want = std::max(1, std::min(want, d->n_ksteps / kMinStepsPerSplit));
-  const int per = (d->n_ksteps + want - 1) / want;
-  *splits = (d->n_ksteps + per - 1) / per;
-  return per;
+  int max_s = n_tiles >= kFillCUs ? 1 : (int)((kFillCUs + n_tiles - 1) / n_tiles);
+  max_s = std::max(1, std::min(max_s, d->n_ksteps / kMinStepsPerSplit));
+  const double split_bytes = 2.0 * 4.0 * (double)M * d->N;     // one partial, written and read
+  int best_per = d->n_ksteps, best_s = 1;
+  double best = (double)d->n_ksteps * kStepUs;
+  for (int s = 2; s <= max_s; ++s) {
+    const int per = (d->n_ksteps + s - 1) / s;
+    const int s_eff = (d->n_ksteps + per - 1) / per;
+    const double t = per * kStepUs + s_eff * split_bytes / kReduceBytesPerUs + kReduceLaunchUs;
+    if (t < best) {
+      best = t;
+      best_per = per;
+      best_s = s_eff;
+    }
+  }
+  *splits = best_s;
+  return best_per;
 }
 
 size_t staging_bytes(const mtc_tile_desc* d, int M, int x_dtype) {
@@ -614,6 +631,8 @@ MTC_API int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, in
   const __bf16* xb = reinterpret_cast<const __bf16*>(X);
   int64_t ldb = ldx;
   const size_t stage = staging_bytes(d, M, x_dtype), need = stage + partial_bytes(d, M);
+  if (!stage && (ldx % 8 || (reinterpret_cast<uintptr_t>(X) & 15)))
+    return fail(MTC_E_SHAPE, "bf16 X read in place needs 16-byte aligned rows (ldx=%lld)", (long long)ldx);
   if (need && (!workspace || workspace_bytes < need))
     return fail(MTC_E_WORKSPACE, "prefill workspace of %zu bytes needed, %zu given", need, workspace ? workspace_bytes : 0);
   if (need && (reinterpret_cast<uintptr_t>(workspace) & 255))
@@ -627,8 +646,6 @@ MTC_API int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, in
     if (rc) return rc;
     xb = reinterpret_cast<const __bf16*>(workspace);
     ldb = d->K;
-  } else if (ldx % 8 || (reinterpret_cast<uintptr_t>(X) & 15)) {
-    return fail(MTC_E_SHAPE, "bf16 X read in place needs 16-byte aligned rows (ldx=%lld)", (long long)ldx);
   }
   const bool fs = d->flags & MTC_FLAG_FP32_SCALES;
   if (fs) {

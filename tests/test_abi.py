@@ -111,10 +111,11 @@ def test_entry_points_reject_bad_arguments_before_any_gpu_call(hip):
     assert hip.mtc_gemm_bf16(t, 0x10, 1, 256, 0x10, 0, 300, 0, None, 0, None) == -3
     assert hip.mtc_gemm_bf16(t, 0x10, 1, 260, 0x10, 0, 300, 4, None, 0, None) == -3      # unaligned bf16 rows
     need = hip.mtc_gemm_workspace_bytes(t, 4, 0)
-    assert need == 4 * 256 * 2 and hip.mtc_gemm_workspace_bytes(t, 4, 1) == 0
+    # fp32 X adds the staged bf16 copy (M x K x 2 bytes) to whatever the K splits need
+    assert need - hip.mtc_gemm_workspace_bytes(t, 4, 1) == 4 * 256 * 2
     assert hip.mtc_gemm_bf16(t, 0x10, 0, 256, 0x10, 0, 300, 4, 0x20, need - 1, None) == -5
     tp = ctypes.byref(_tdesc(row_perm=0x3000))
-    assert hip.mtc_gemm_workspace_bytes(tp, 4, 1) == 4 * 256 * 2
+    assert hip.mtc_gemm_workspace_bytes(tp, 4, 1) - hip.mtc_gemm_workspace_bytes(t, 4, 1) == 4 * 256 * 2   # a row permutation stages bf16 X too
 
 
 def test_group_entry_rejects_bad_arguments_before_any_gpu_call(hip):
@@ -165,10 +166,10 @@ def test_group_prefill_entry_rejects_bad_arguments_before_any_gpu_call(hip):
     assert f(descs(a, b), 2, 0x10, 1, 256, ys(2), 0, lds(2, 300), 4, None, 0, None) == -3      # ldy < N
     assert f(descs(a), 1, 0x10, 1, 260, ys(1), 0, lds(1), 4, None, 0, None) == -3              # unaligned bf16 rows
     need = hip.mtc_gemm_group_workspace_bytes(descs(a, b), 2, 4, 0)                             # fp32 X: staged per member
-    assert need == 2 * 4 * 256 * 2 + (256 - 4 * 256 * 2 % 256) % 256 * 2
+    assert need - hip.mtc_gemm_group_workspace_bytes(descs(a, b), 2, 4, 1) == 2 * 4 * 256 * 2
+    assert need == hip.mtc_gemm_workspace_bytes(ctypes.byref(a), 4, 0) + hip.mtc_gemm_workspace_bytes(ctypes.byref(b), 4, 0)
     assert f(descs(a, b), 2, 0x10, 0, 256, ys(2), 0, lds(2), 4, 0x20, need - 1, None) == -5    # workspace too small
     assert f(descs(a, b), 2, 0x10, 0, 256, ys(2), 0, lds(2), 4, 0x20, need, None) == -5        # unaligned workspace
-    assert hip.mtc_gemm_group_workspace_bytes(descs(a, b), 2, 4, 1) == 0                       # bf16 X in place, no split
     assert hip.mtc_gemm_group_workspace_bytes(None, 2, 4, 1) == 0
 
 
