@@ -455,19 +455,32 @@ __global__ __launch_bounds__(kStageThreads) void k_stage_x_group(const StageGrou
 }
 
 // Y[m, col_perm[n]] = sum over splits of part[z][m][n] (fixed order: deterministic).
+// Four consecutive outputs per thread (N % 4 == 0): element index i = 4 * thread.
+constexpr int kReducePer = 4;
 template <int kYDT>
-__device__ __forceinline__ void splitk_reduce_at(const int64_t i, const float* __restrict__ part, int splits, int M,
+__device__ __forceinline__ void splitk_reduce_at(const int64_t q, const float* __restrict__ part, int splits, int M,
                                                  int N, const int32_t* __restrict__ col_perm, void* __restrict__ Y,
                                                  int64_t ldy) {
+  const int64_t i = q * kReducePer;
   if (i >= (int64_t)M * N) return;
   const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
-  float v = 0.0f;
-  for (int z = 0; z < splits; ++z) v += part[(size_t)z * M * N + i];
-  const int col = col_perm ? col_perm[n] : n;
-  if (kYDT == MTC_DTYPE_F32)
-    reinterpret_cast<float*>(Y)[(int64_t)m * ldy + col] = v;
-  else
-    reinterpret_cast<__bf16*>(Y)[(int64_t)m * ldy + col] = (__bf16)v;
+  float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int z = 0; z < splits; ++z) {
+    const float4 p = *reinterpret_cast<const float4*>(part + (size_t)z * M * N + i);
+    v.x += p.x;
+    v.y += p.y;
+    v.z += p.z;
+    v.w += p.w;
+  }
+  const float vs[kReducePer] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int t = 0; t < kReducePer; ++t) {
+    const int col = col_perm ? col_perm[n + t] : n + t;
+    if (kYDT == MTC_DTYPE_F32)
+      reinterpret_cast<float*>(Y)[(int64_t)m * ldy + col] = vs[t];
+    else
+      reinterpret_cast<__bf16*>(Y)[(int64_t)m * ldy + col] = (__bf16)vs[t];
+  }
 }
 
 template <int kYDT>
@@ -574,7 +587,7 @@ int launch_tile(const mtc_tile_desc* d, const __bf16* X, int64_t ldx, void* Y, i
   int rc = check_launch("k_gemm_tile");
   if (rc || splits == 1) return rc;
   const int64_t n = (int64_t)M * d->N;
-  hipLaunchKernelGGL(k_splitk_reduce<kYDT>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, part, splits, M,
+  hipLaunchKernelGGL(k_splitk_reduce<kYDT>, dim3((unsigned)((n / kReducePer + 255) / 256)), dim3(256), 0, st, part, splits, M,
                      d->N, d->col_perm, Y, ldy);
   return check_launch("k_splitk_reduce");
 }
@@ -605,7 +618,8 @@ int launch_tile_group(GemmGroup& g, int n, int M, const ReduceGroup& rg, int n_r
   if (rc || n_red == 0) return rc;
   int64_t max_n = 0;
   for (int i = 0; i < n_red; ++i) max_n = std::max(max_n, (int64_t)M * rg.N[i]);
-  hipLaunchKernelGGL(k_splitk_reduce_group<kYDT>, dim3((unsigned)((max_n + 255) / 256), n_red), dim3(256), 0, st, rg, M);
+  hipLaunchKernelGGL(k_splitk_reduce_group<kYDT>, dim3((unsigned)((max_n / kReducePer + 255) / 256), n_red), dim3(256), 0,
+                     st, rg, M);
   return check_launch("k_splitk_reduce_group");
 }
 
