@@ -164,9 +164,13 @@ def gemv_f32_group(streams, X, outs=None):
     if any(s.device != dev for s in streams):
         raise ValueError("group members live on different devices")
     assert X.dim() == 2 and X.dtype == torch.float32 and X.stride(1) == 1, "X must be (M, K) fp32 row-major"
+    if X.device != dev:
+        raise ValueError(f"X is on {X.device}, the streams on {dev}")
     M = X.shape[0]
     if outs is None:
         outs = [torch.empty((M, s.N), dtype=torch.float32, device=dev) for s in streams]
+    if len(outs) != n or any(o.device != dev for o in outs):
+        raise ValueError("one output per member, on the members' device")
     for o, s in zip(outs, streams):
         assert o.dtype == torch.float32 and o.stride(1) == 1 and tuple(o.shape) == (M, s.N)
     descs = (_abi.DescP * n)(*[ctypes.pointer(s.desc) for s in streams])
@@ -261,10 +265,14 @@ def gemm_bf16_group(tiles, X, outs=None, out_dtype=None):
     if any(t.device != dev for t in tiles):
         raise ValueError("group members live on different devices")
     assert X.dim() == 2 and X.stride(1) == 1 and X.dtype in (torch.float32, torch.bfloat16)
+    if X.device != dev:
+        raise ValueError(f"X is on {X.device}, the streams on {dev}")
     M = X.shape[0]
     out_dtype = out_dtype or torch.float32
     if outs is None:
         outs = [torch.empty((M, t.N), dtype=out_dtype, device=dev) for t in tiles]
+    if len(outs) != n or any(o.device != dev for o in outs):
+        raise ValueError("one output per member, on the members' device")
     for o, t in zip(outs, tiles):
         assert o.dtype in (torch.float32, torch.bfloat16) and o.stride(1) == 1 and tuple(o.shape) == (M, t.N)
     if len({o.dtype for o in outs}) != 1:
