@@ -77,7 +77,7 @@ class DeviceStream:
         d.n_steps = 0 if ps.steps is None else int(ps.steps.shape[0])
         self.desc = d
         _abi.check(self.lib, "mtc_check_desc", self.lib.mtc_check_desc(ctypes.byref(d)))
-        self._ws: Dict[int, "object"] = {}
+        self._ws: Dict[int, tuple] = {}                # HIP stream handle -> (bytes, tensor)
 
     def clone(self) -> "DeviceStream":
         """A second device copy of the same stream (distinct buffers, same contents)."""
@@ -116,16 +116,18 @@ class DeviceStream:
         return self.host.nbytes()
 
     def workspace(self, M: int):
-        """Zero-initialised GEMV workspace for M rows (cached; counters self-reset)."""
+        """Zero-initialised GEMV workspace for M rows, one per HIP stream (its counters reset
+        themselves at the end of each call, so calls ordered on one stream can share it;
+        calls on different streams could overlap, so each stream gets its own)."""
         need = int(self.lib.mtc_gemv_workspace_bytes(ctypes.byref(self.desc), int(M)))
         if need == 0:
             return None, 0
-        ws = self._ws.get(need)
-        if ws is None:
+        key = current_stream_handle(self.device)
+        have = self._ws.get(key)
+        if have is None or have[0] != need:
             torch = _torch()
-            ws = torch.zeros(need, dtype=torch.uint8, device=self.device)
-            self._ws = {need: ws}
-        return ws, need
+            self._ws[key] = (need, torch.zeros(need, dtype=torch.uint8, device=self.device))
+        return self._ws[key][1], need
 
     # ---- launches -------------------------------------------------------------------
     def dequant(self, out=None):
@@ -208,7 +210,7 @@ class DeviceTiles:
         d.row_perm, d.col_perm = ptr(self.row_perm), ptr(self.col_perm)
         self.desc = d
         _abi.check(self.lib, "mtc_check_tile_desc", self.lib.mtc_check_tile_desc(ctypes.byref(d)))
-        self._ws = None
+        self._ws: Dict[int, "object"] = {}             # HIP stream handle -> workspace tensor
 
     @property
     def K(self) -> int:
@@ -226,10 +228,12 @@ class DeviceTiles:
         need = int(self.lib.mtc_gemm_workspace_bytes(ctypes.byref(self.desc), int(M), int(x_dtype)))
         if need == 0:
             return None, 0
-        if self._ws is None or self._ws.numel() < need:
+        key = current_stream_handle(self.device)       # one per stream: calls on two streams may overlap
+        ws = self._ws.get(key)
+        if ws is None or ws.numel() < need:
             torch = _torch()
-            self._ws = torch.empty(need, dtype=torch.uint8, device=self.device)
-        return self._ws, need
+            ws = self._ws[key] = torch.empty(need, dtype=torch.uint8, device=self.device)
+        return ws, need
 
     def gemm_bf16(self, X, out=None, out_dtype=None):
         torch = _torch()
@@ -255,7 +259,8 @@ _GROUP_WS: dict = {}
 def gemm_bf16_group(tiles, X, outs=None, out_dtype=None):
     """Y_i = X @ W_hat_i for 1..MAX_GROUP tile streams that share X (same K), one launch per
     kernel (mtc_gemm_bf16_group). Each Y_i is bit-identical to tiles[i].gemm_bf16(X). The
-    workspace is cached per device; calls on one device are ordered by its stream."""
+    workspace is cached per device and HIP stream (calls on one stream are ordered; calls on
+    two streams may overlap, so they do not share one)."""
     torch = _torch()
     tiles = list(tiles)
     n = len(tiles)
@@ -282,10 +287,10 @@ def gemm_bf16_group(tiles, X, outs=None, out_dtype=None):
     lib = tiles[0].lib
     descs = (_abi.TileDescP * n)(*[ctypes.pointer(t.desc) for t in tiles])
     need = int(lib.mtc_gemm_group_workspace_bytes(descs, n, M, xdt))
-    ws = _GROUP_WS.get(str(dev))
+    key = (str(dev), current_stream_handle(dev))
+    ws = _GROUP_WS.get(key)
     if need and (ws is None or ws.numel() < need):
-        ws = torch.empty(need, dtype=torch.uint8, device=dev)
-        _GROUP_WS[str(dev)] = ws
+        ws = _GROUP_WS[key] = torch.empty(need, dtype=torch.uint8, device=dev)
     ys = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
     lds = (ctypes.c_int64 * n)(*[o.stride(0) for o in outs])
     rc = lib.mtc_gemm_bf16_group(descs, n, X.data_ptr(), xdt, X.stride(0), ys, ydt, lds, M,

@@ -160,3 +160,28 @@ def test_prefill_group_through_mtc_gemm_group(gpu, members):
     torch.cuda.synchronize()
     for (name, W, a, m), y in zip(members, ys):
         assert torch.equal(y, mtc_gemm(X, m)), name
+
+
+def test_workspaces_are_per_stream(gpu, members):
+    """Calls on two HIP streams may overlap, so each stream gets its own workspace: split-K
+    decode (per-panel counters) and split-K prefill (staged X, partial tiles) interleaved on
+    two streams with no synchronisation between them all match a single-stream call."""
+    import torch
+    _say("workspaces per stream")
+    m = members[0][3]
+    ds = m.device_stream(64, gpu, 2)                                  # four row chunks
+    ts = m.device_tiles(gpu)
+    Xd = torch.from_numpy(np.random.RandomState(9).randn(2, 256).astype(np.float32)).to(gpu)
+    Xp = torch.from_numpy(np.random.RandomState(10).randn(300, 256).astype(np.float32)).to(gpu)
+    ref_d, ref_p = ds.gemv_f32(Xd), ts.gemm_bf16(Xp)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)]
+    outs = []
+    for _ in range(10):
+        for s in streams:
+            with torch.cuda.stream(s):
+                outs.append((ds.gemv_f32(Xd), ts.gemm_bf16(Xp)))
+    torch.cuda.synchronize()
+    for yd, yp in outs:
+        assert torch.equal(yd, ref_d) and torch.equal(yp, ref_p)
+    assert len(ds._ws) >= 2
