@@ -124,6 +124,26 @@ class _Levels:
         self.row_perm, self.col_perm = row_perm, col_perm
 
 
+class StoredQTAllocation:
+    """What a saved quadtree matrix keeps of its allocation: the leaf grids, modes and scales
+    per level (in the stored, permuted order), the permutations and the accounted bit count.
+    The weights are not kept; the codes travel with the matrix."""
+
+    def __init__(self, shape, sizes, leaf, modes, scales, total_bits, row_perm=None, col_perm=None):
+        self.shape = (int(shape[0]), int(shape[1]))
+        self.sizes = tuple(int(x) for x in sizes)
+        self.leaf, self.modes, self.scales = leaf, modes, scales
+        self.total_bits = int(total_bits)
+        self.row_perm, self.col_perm = row_perm, col_perm
+
+    @property
+    def permuted(self) -> bool:
+        return self.row_perm is not None
+
+
+SAVE_FORMAT = 1
+
+
 class MTCMatrix:
     """A packed (K x N) matrix: reduction along rows, as the right operand of Y = X * W."""
 
@@ -217,6 +237,72 @@ class MTCMatrix:
         a, b = rd_allocate_pair(matrix_a, matrix_b, bits_per_element, block_size)
         return (cls.from_allocation(matrix_a, a.modes, a.scales, block_size),
                 cls.from_allocation(matrix_b, b.modes, b.scales, block_size))
+
+    # ---- on-disk form ----------------------------------------------------------------------
+    def save(self, path) -> None:
+        """Write a quadtree matrix to one .npz of plain arrays (no pickled objects): per level
+        the leaf grid, modes and scales; the permutations; the accounted bit count; and the
+        code of every leaf element as one dense (K x N) int8 grid (int16 when a leaf is P16) in
+        the stored order. `load` rebuilds a matrix whose streams are byte-identical to this
+        one's without the allocator or the weights. (The reference keeps allocations in
+        memory only; the uniform-block form is its arena and is not written here.)"""
+        if self._levels is None:
+            raise ValueError("save() writes quadtree matrices; a uniform-block matrix is its arena")
+        lv = self._levels
+        K, N = self.shape
+        wide = any(bool(np.any(lv.modes[S][lv.leaf[S]] > 8)) for S in lv.sizes)
+        Q = np.zeros((K, N), np.int16 if wide else np.int8)
+        for S in lv.sizes:
+            blocks = Q.reshape(K // S, S, N // S, S)                  # view: [bi, r, bj, c]
+            for P in np.unique(lv.modes[S][lv.leaf[S]]):
+                if P == 0:
+                    continue
+                ii, jj = np.nonzero(lv.leaf[S] & (lv.modes[S] == P))
+                blocks[ii, :, jj, :] = np.asarray(lv.codes_of(S, int(P), ii, jj, lv.scales[S][ii, jj]))
+        arrays = {"format": np.array([SAVE_FORMAT]), "shape": np.array([K, N]), "sizes": np.array(lv.sizes),
+                  "total_bits": np.array([self.total_bits], np.int64), "codes": Q}
+        for S in lv.sizes:
+            arrays[f"leaf_{S}"] = np.asarray(lv.leaf[S], bool)
+            arrays[f"modes_{S}"] = np.asarray(lv.modes[S], np.uint8)
+            arrays[f"scales_{S}"] = np.asarray(lv.scales[S], np.float32)
+        if lv.row_perm is not None:
+            arrays["row_perm"] = np.asarray(lv.row_perm, np.int64)
+            arrays["col_perm"] = np.asarray(lv.col_perm, np.int64)
+        with open(path, "wb") as f:
+            np.savez_compressed(f, **arrays)
+
+    @classmethod
+    def load(cls, path) -> "MTCMatrix":
+        """Read a matrix written by `save` (plain arrays only: allow_pickle stays off)."""
+        with np.load(path, allow_pickle=False) as z:
+            if int(z["format"][0]) != SAVE_FORMAT:
+                raise ValueError(f"{path}: format {int(z['format'][0])}, expected {SAVE_FORMAT}")
+            K, N = (int(x) for x in z["shape"])
+            sizes = tuple(int(x) for x in z["sizes"])
+            leaf = {S: z[f"leaf_{S}"] for S in sizes}
+            modes = {S: z[f"modes_{S}"] for S in sizes}
+            scales = {S: z[f"scales_{S}"] for S in sizes}
+            Q = z["codes"]
+            pr = z["row_perm"] if "row_perm" in z.files else None
+            pc = z["col_perm"] if "col_perm" in z.files else None
+            total_bits = int(z["total_bits"][0])
+        if Q.shape != (K, N) or any(leaf[S].shape != (K // S, N // S) for S in sizes):
+            raise ValueError(f"{path}: array shapes do not match the ({K}, {N}) matrix")
+        views: Dict[int, np.ndarray] = {}
+
+        def codes_of(S, P, ii, jj, sc):
+            if S not in views:
+                views[S] = to_blocks(Q, S)
+            return views[S][ii, jj]
+
+        m = cls.__new__(cls)
+        m.shape = (K, N)
+        m.block_size = sizes[0]
+        m.arena = m.offsets = m.precisions = m.scales = m.pointer_tensor = None
+        m.allocation = StoredQTAllocation((K, N), sizes, leaf, modes, scales, total_bits, pr, pc)
+        m._levels = _Levels((K, N), sizes, leaf, modes, scales, codes_of, "bf16", pr, pc)
+        m._host, m._dev = {}, {}
+        return m
 
     # ---- reference properties ------------------------------------------------------------
     @property
