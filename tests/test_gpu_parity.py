@@ -82,7 +82,7 @@ def test_dequant_any_chunking(gpu, allocs, chunk_rows):
 
 
 @pytest.mark.parametrize("name", [c[0] for c in CASES])
-@pytest.mark.parametrize("M", [1, 2, 3, 5, 8, 16, 17, 40])
+@pytest.mark.parametrize("M", [1, 2, 3, 5, 8, 12, 16, 17, 40])
 def test_gemv_f32(gpu, allocs, name, M):
     import torch
     W, a, m = allocs[name]
