@@ -460,6 +460,16 @@ def main():
     copy_gbs = 2 * src.numel() * 4 * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9     # read + write bytes
     del src, dst
     log(f"device copy: {copy_gbs:.0f} GB/s (read + write)")
+    # the same for copies of the packed weight's size, rotated over ~1 GiB and replayed
+    # from a graph like the decode: what a launch of this size achieves on the copy path
+    n_el = int(packed) // 4
+    n_rot = max(2, (1 << 30) // (2 * 4 * n_el))
+    srcs = [torch.empty(n_el, dtype=torch.float32, device=dev) for _ in range(n_rot)]
+    dsts = [torch.empty_like(s) for s in srcs]
+    g = graph_of(torch, [lambda s=s, d=d: d.copy_(s) for s, d in zip(srcs, dsts)])
+    copy_small_us = time_replays(torch, g, 5) * 1e3 / n_rot
+    del g, srcs, dsts
+    log(f"device copy of {4 * n_el} B: {copy_small_us:.2f} us per copy ({n_rot} rotating pairs)")
 
     # ---------------- CPU baseline (bounded sample) ----------------
     cpu = None
@@ -542,6 +552,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": gbs / HBM_PEAK_GBS, "traffic": None if traffic is None else traffic["bytes"],
                      "copy_GBps": copy_gbs, "frac_of_copy": gbs / copy_gbs,
+                     "copy_same_bytes_us": copy_small_us, "us_per_call": ms * 1e3,
                      "kernel": "k_gemv<1>", "stream_GBps": per_copy / (ms * 1e-3) / 1e9,
                      "traffic_detail": traffic},
         "cpu_baseline": cpu,
