@@ -286,7 +286,9 @@ class MTCMatrix:
             pr = z["row_perm"] if "row_perm" in z.files else None
             pc = z["col_perm"] if "col_perm" in z.files else None
             total_bits = int(z["total_bits"][0])
-        if Q.shape != (K, N) or any(leaf[S].shape != (K // S, N // S) for S in sizes):
+        grids_ok = all(g[S].shape == (K // S, N // S) for g in (leaf, modes, scales) for S in sizes)
+        perms_ok = pr is None or (pc is not None and pr.shape == (K,) and pc.shape == (N,))
+        if Q.shape != (K, N) or not grids_ok or not perms_ok or any(K % S or N % S for S in sizes):
             raise ValueError(f"{path}: array shapes do not match the ({K}, {N}) matrix")
         views: Dict[int, np.ndarray] = {}
 
