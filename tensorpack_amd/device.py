@@ -24,7 +24,16 @@ def require_gpu(device=None):
     torch = _torch()
     if not torch.cuda.is_available():
         raise RuntimeError("mtc GPU path needs a ROCm GPU (torch.cuda.is_available() is False)")
-    return torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    if dev.type != "cuda":
+        raise ValueError(f"mtc GPU path runs on a cuda (ROCm) device, got {dev}")
+    return dev if dev.index is not None else torch.device("cuda", torch.cuda.current_device())
+
+
+def _need(ok: bool, what: str) -> None:
+    """Argument check that stays on under python -O: the kernels trust these shapes."""
+    if not ok:
+        raise ValueError(what)
 
 
 def current_stream_handle(device) -> int:
@@ -134,18 +143,21 @@ class DeviceStream:
         torch = _torch()
         if out is None:
             out = torch.empty((self.K, self.N), dtype=torch.float32, device=self.device)
-        assert out.is_contiguous() and out.dtype == torch.float32 and tuple(out.shape) == (self.K, self.N)
+        _need(out.is_contiguous() and out.dtype == torch.float32 and tuple(out.shape) == (self.K, self.N)
+              and out.device == self.device, f"out must be a contiguous ({self.K}, {self.N}) fp32 tensor on {self.device}")
         rc = self.lib.mtc_dequant(ctypes.byref(self.desc), out.data_ptr(), current_stream_handle(self.device))
         _abi.check(self.lib, "mtc_dequant", rc)
         return out
 
     def gemv_f32(self, X, out=None):
         torch = _torch()
-        assert X.dim() == 2 and X.dtype == torch.float32 and X.stride(1) == 1, "X must be (M, K) fp32 row-major"
+        _need(X.dim() == 2 and X.dtype == torch.float32 and X.stride(1) == 1 and X.shape[1] == self.K
+              and X.device == self.device, f"X must be (M, {self.K}) fp32 row-major on {self.device}")
         M = X.shape[0]
         if out is None:
             out = torch.empty((M, self.N), dtype=torch.float32, device=self.device)
-        assert out.dtype == torch.float32 and out.stride(1) == 1
+        _need(out.dtype == torch.float32 and out.stride(1) == 1 and tuple(out.shape) == (M, self.N)
+              and out.device == self.device, f"out must be ({M}, {self.N}) fp32 row-major on {self.device}")
         ws, nbytes = self.workspace(M)
         rc = self.lib.mtc_gemv_f32(ctypes.byref(self.desc), X.data_ptr(), X.stride(0), out.data_ptr(), out.stride(0),
                                    M, None if ws is None else ws.data_ptr(), nbytes,
@@ -165,7 +177,8 @@ def gemv_f32_group(streams, X, outs=None):
     dev = streams[0].device
     if any(s.device != dev for s in streams):
         raise ValueError("group members live on different devices")
-    assert X.dim() == 2 and X.dtype == torch.float32 and X.stride(1) == 1, "X must be (M, K) fp32 row-major"
+    _need(X.dim() == 2 and X.dtype == torch.float32 and X.stride(1) == 1 and X.shape[1] == streams[0].K,
+          f"X must be (M, {streams[0].K}) fp32 row-major")
     if X.device != dev:
         raise ValueError(f"X is on {X.device}, the streams on {dev}")
     M = X.shape[0]
@@ -174,7 +187,8 @@ def gemv_f32_group(streams, X, outs=None):
     if len(outs) != n or any(o.device != dev for o in outs):
         raise ValueError("one output per member, on the members' device")
     for o, s in zip(outs, streams):
-        assert o.dtype == torch.float32 and o.stride(1) == 1 and tuple(o.shape) == (M, s.N)
+        _need(o.dtype == torch.float32 and o.stride(1) == 1 and tuple(o.shape) == (M, s.N),
+              f"each output must be ({M}, N) fp32 row-major")
     descs = (_abi.DescP * n)(*[ctypes.pointer(s.desc) for s in streams])
     ys = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
     lds = (ctypes.c_int64 * n)(*[o.stride(0) for o in outs])
@@ -237,12 +251,14 @@ class DeviceTiles:
 
     def gemm_bf16(self, X, out=None, out_dtype=None):
         torch = _torch()
-        assert X.dim() == 2 and X.stride(1) == 1 and X.dtype in (torch.float32, torch.bfloat16)
+        _need(X.dim() == 2 and X.stride(1) == 1 and X.dtype in (torch.float32, torch.bfloat16) and X.shape[1] == self.K
+              and X.device == self.device, f"X must be (M, {self.K}) fp32 or bf16 row-major on {self.device}")
         M = X.shape[0]
         out_dtype = out_dtype or torch.float32
         if out is None:
             out = torch.empty((M, self.N), dtype=out_dtype, device=self.device)
-        assert out.dtype in (torch.float32, torch.bfloat16) and out.stride(1) == 1
+        _need(out.dtype in (torch.float32, torch.bfloat16) and out.stride(1) == 1 and tuple(out.shape) == (M, self.N)
+              and out.device == self.device, f"out must be ({M}, {self.N}) fp32 or bf16 row-major on {self.device}")
         xdt = _abi.MTC_DTYPE_BF16 if X.dtype == torch.bfloat16 else _abi.MTC_DTYPE_F32
         ydt = _abi.MTC_DTYPE_BF16 if out.dtype == torch.bfloat16 else _abi.MTC_DTYPE_F32
         ws, nbytes = self.workspace(M, xdt)
@@ -269,7 +285,8 @@ def gemm_bf16_group(tiles, X, outs=None, out_dtype=None):
     dev = tiles[0].device
     if any(t.device != dev for t in tiles):
         raise ValueError("group members live on different devices")
-    assert X.dim() == 2 and X.stride(1) == 1 and X.dtype in (torch.float32, torch.bfloat16)
+    _need(X.dim() == 2 and X.stride(1) == 1 and X.dtype in (torch.float32, torch.bfloat16) and X.shape[1] == tiles[0].K,
+          f"X must be (M, {tiles[0].K}) fp32 or bf16 row-major")
     if X.device != dev:
         raise ValueError(f"X is on {X.device}, the streams on {dev}")
     M = X.shape[0]
@@ -279,7 +296,8 @@ def gemm_bf16_group(tiles, X, outs=None, out_dtype=None):
     if len(outs) != n or any(o.device != dev for o in outs):
         raise ValueError("one output per member, on the members' device")
     for o, t in zip(outs, tiles):
-        assert o.dtype in (torch.float32, torch.bfloat16) and o.stride(1) == 1 and tuple(o.shape) == (M, t.N)
+        _need(o.dtype in (torch.float32, torch.bfloat16) and o.stride(1) == 1 and tuple(o.shape) == (M, t.N),
+              f"each output must be ({M}, N) fp32 or bf16 row-major")
     if len({o.dtype for o in outs}) != 1:
         raise ValueError("group outputs must share one dtype")
     xdt = _abi.MTC_DTYPE_BF16 if X.dtype == torch.bfloat16 else _abi.MTC_DTYPE_F32

@@ -185,3 +185,24 @@ def test_workspaces_are_per_stream(gpu, members):
     for yd, yp in outs:
         assert torch.equal(yd, ref_d) and torch.equal(yp, ref_p)
     assert len(ds._ws) >= 2
+
+
+def test_device_calls_check_their_arguments(gpu, members):
+    """The launch wrappers check shapes, dtypes and devices with real exceptions (not
+    asserts, which python -O removes): the kernels trust what they are given."""
+    import torch
+    _say("argument checks")
+    m = members[0][3]
+    ds, ts = m.device_stream(None, gpu, 1), m.device_tiles(gpu)
+    with pytest.raises(ValueError):
+        ds.gemv_f32(torch.zeros((1, 128), device=gpu))                       # K mismatch
+    with pytest.raises(ValueError):
+        ds.gemv_f32(torch.zeros((1, 256), device=gpu, dtype=torch.bfloat16))  # dtype
+    with pytest.raises(ValueError):
+        ds.gemv_f32(torch.zeros((2, 256), device=gpu), out=torch.empty((1, m.shape[1]), device=gpu))
+    with pytest.raises(ValueError):
+        ts.gemm_bf16(torch.zeros((40, 255), device=gpu))
+    with pytest.raises(ValueError):
+        ds.dequant(out=torch.empty((1, 1), device=gpu))
+    from tensorpack_amd.device import require_gpu
+    assert require_gpu("cuda").index is not None
