@@ -140,6 +140,12 @@ int mtc_check_desc(const mtc_stream_desc* d);
  * with +0.0 wherever a P0 leaf lies. */
 int mtc_dequant(const mtc_stream_desc* d, float* W_out, void* hip_stream);
 
+/* LDS bytes one decode block needs for M rows of X over a stream with these K and
+ * chunk_rows (has_row_perm: the stream has a row permutation); a packer shrinks
+ * chunk_rows until this fits the device's per-block LDS. Host arithmetic only (no HIP
+ * call, no GPU needed); 0 for non-positive arguments. */
+size_t mtc_gemv_lds_bytes(int K, int chunk_rows, int has_row_perm, int M);
+
 /* Bytes of GEMV workspace needed for M rows (0 if the stream has one chunk).
  * The workspace must be zero-filled once before first use; the kernels leave
  * its counters at zero again after every call. */

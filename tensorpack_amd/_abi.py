@@ -14,7 +14,7 @@ ERROR_NAMES = {
     -5: "MTC_E_WORKSPACE", -6: "MTC_E_LAUNCH", -7: "MTC_E_VERSION",
 }
 
-EXPORTED = ("mtc_abi_version", "mtc_last_error", "mtc_check_desc", "mtc_dequant",
+EXPORTED = ("mtc_abi_version", "mtc_last_error", "mtc_check_desc", "mtc_dequant", "mtc_gemv_lds_bytes",
             "mtc_gemv_workspace_bytes", "mtc_gemv_f32", "mtc_gemv_f32_group", "mtc_check_tile_desc", "mtc_gemm_workspace_bytes",
             "mtc_gemm_bf16", "mtc_gemm_group_workspace_bytes", "mtc_gemm_bf16_group")
 
@@ -83,6 +83,8 @@ def declare(lib: ctypes.CDLL) -> None:
     lib.mtc_check_desc.argtypes = [DescP]
     lib.mtc_dequant.restype = i32
     lib.mtc_dequant.argtypes = [DescP, vp, vp]
+    lib.mtc_gemv_lds_bytes.restype = sz
+    lib.mtc_gemv_lds_bytes.argtypes = [i32, i32, i32, i32]
     lib.mtc_gemv_workspace_bytes.restype = sz
     lib.mtc_gemv_workspace_bytes.argtypes = [DescP, i32]
     lib.mtc_gemv_f32.restype = i32

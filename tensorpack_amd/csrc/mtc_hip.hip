@@ -748,11 +748,14 @@ size_t gemv_ws_layout(const mtc_stream_desc* d, int M, size_t* counters_bytes) {
 
 // LDS of a decode block: X rows, their 4- and 8-row sums, the cross-wave reduction and,
 // for the LDS gather, whole X rows.
-size_t gemv_lds_bytes(const mtc_stream_desc* d, int MT) {
-  const size_t kc = (size_t)d->chunk_rows;
-  const size_t raw = gemv_lds_gather(MT, d->row_perm != nullptr, d->K) ? (size_t)MT * d->K : 0;
+size_t gemv_lds_bytes(int K, int chunk_rows, bool perm, int MT) {
+  const size_t kc = (size_t)chunk_rows;
+  const size_t raw = gemv_lds_gather(MT, perm, K) ? (size_t)MT * K : 0;
   return ((size_t)MT * (kc + (gemv_sum4(MT) ? kc / 4 : 0) + kc / 8) +
           (size_t)gemv_waves(MT) * kStepGroups * MT * kGroup + raw) * 4;
+}
+size_t gemv_lds_bytes(const mtc_stream_desc* d, int MT) {
+  return gemv_lds_bytes(d->K, d->chunk_rows, d->row_perm != nullptr, MT);
 }
 
 template <int MT>
@@ -831,6 +834,11 @@ MTC_API int mtc_dequant(const mtc_stream_desc* d, float* W_out, void* hip_stream
   if (rc) return rc;
   hipLaunchKernelGGL(k_dequant, dim3(d->n_panels * d->n_chunks), dim3(512), 0, st, *d, W_out);
   return check_launch("k_dequant");
+}
+
+MTC_API size_t mtc_gemv_lds_bytes(int K, int chunk_rows, int has_row_perm, int M) {
+  if (K <= 0 || chunk_rows <= 0 || M <= 0) return 0;
+  return gemv_lds_bytes(K, chunk_rows, has_row_perm != 0, gemv_mt(M));
 }
 
 MTC_API size_t mtc_gemv_workspace_bytes(const mtc_stream_desc* d, int M) {

@@ -17,7 +17,6 @@ semantics (gemm.py:541-574): C = A_hat @ B_hat in fp32.
 All arithmetic runs in libmtc_hip.so; without a GPU these calls raise.
 """
 
-import os
 from math import ceil
 from typing import Dict, Optional, Tuple
 
@@ -26,13 +25,17 @@ import numpy as np
 from ..core.allocation import QRANGE, quantize_blocks, rd_allocate_pair, to_blocks
 from ..core.arena import MemoryArena
 from ..core.permutation import PermutedQTAllocation
+from ..core.precision import (_BlockErrors, block_codes, block_scale, negotiate_joint_precision,
+                              select_independent_precision)
 from ..core.quadtree import QTAllocation
+from ..core.types import PrecisionMode
 from ..packer import PanelStream, pack_levels, weight_codes
 from ..tilestream import TileStream, pack_tiles
 
 DECODE_MAX_M = 16             # M at or below this takes the fp32 decode kernel under compute="auto"
 DECODE_X_LDS_BYTES = 64 * 1024   # on-chip budget for the gathered X rows of one decode block
 DECODE_LDS_BYTES = 160 * 1024    # per-block LDS of gfx950
+UNIFORM_BLOCK_SIZES = (4, 8, 16, 32)   # block sizes of the uniform form the device stream holds
 
 
 def _decode_mt(M: int) -> int:
@@ -50,11 +53,7 @@ def gemv_chunk_rows(K: int, N: int, M: int = 1) -> int:
     otherwise the fewest chunks that fit, of equal size (a 4864-row matrix splits 2432 +
     2432, not 4096 + 768). A matrix that needs a split anyway and has too few column panels
     to fill the chip (two blocks per unit) is cut into more chunks of at least
-    DECODE_MIN_SPLIT_ROWS rows. The environment variable MTC_GEMV_CHUNK_ROWS, when set,
-    overrides the choice (a multiple of 32; for layout experiments)."""
-    env = os.environ.get("MTC_GEMV_CHUNK_ROWS")
-    if env:
-        return int(env)
+    DECODE_MIN_SPLIT_ROWS rows."""
     cap = min(DECODE_X_LDS_BYTES // (4 * _decode_mt(M)) // 32 * 32, 4096)
     rows = -(-K // 32) * 32
     n = -(-rows // cap)
@@ -67,15 +66,10 @@ def gemv_chunk_rows(K: int, N: int, M: int = 1) -> int:
 
 
 def _decode_lds_need(ps: PanelStream, M: int) -> int:
-    """LDS bytes of one decode block: the gathered X rows, their 8-row (and, for M tiles
-    of 1-2 rows, 4-row) sums, the per-wave partial sums and, when X is gathered on chip,
-    whole X rows (mirrors gemv_lds_bytes in csrc/mtc_hip.hip; the payload streams through
-    registers)."""
-    mt = _decode_mt(M)
-    waves = 16 if mt <= 2 else 8
-    kc = ps.chunk_rows
-    raw = mt * ps.K if (ps.row_perm is not None and mt <= 2 and ps.K <= 4096) else 0   # LDS gather of X
-    return 4 * (mt * (kc + (kc // 4 if mt <= 2 else 0) + kc // 8) + waves * 4 * mt * 4 + raw)
+    """LDS bytes one decode block of this stream uses for M rows, as the library computes it
+    (mtc_gemv_lds_bytes)."""
+    from .._native import hip_lib
+    return int(hip_lib().mtc_gemv_lds_bytes(int(ps.K), int(ps.chunk_rows), int(ps.row_perm is not None), int(M)))
 
 
 # ---------------------------------------------------------------------------------------
@@ -229,6 +223,94 @@ class MTCMatrix:
             packed = arena_encode(q.reshape(q.shape[0], Bs * Bs), m)
             buf[offsets[sel].astype(np.int64)[:, None] + np.arange(packed.shape[1])] = packed
         return cls((H, W), Bs, arena, offsets, modes.copy(), np.where(modes == 0, 0.0, scales).astype(np.float32))
+
+    @classmethod
+    def _from_block_modes(cls, arr: np.ndarray, Bs: int, modes: np.ndarray, scales: Optional[np.ndarray],
+                          arena: Optional[MemoryArena]) -> "MTCMatrix":
+        """Uniform-block matrix whose block (i, j) is quantized at modes[i, j] the way
+        MicroTensor.from_array does (microtensor.py:63-160), with scales[i, j] or, where a
+        scale is NaN / scales is None, the block's own symmetric max-abs scale; blocks are
+        written in row-major order, P16 payloads on 2-byte boundaries."""
+        H, W = arr.shape
+        blocks = to_blocks(arr, Bs)
+        nbh, nbw = blocks.shape[:2]
+        if arena is None:
+            arena = MemoryArena(capacity_bytes=max(1024 * 1024, H * W * 2))
+        offsets = np.zeros((nbh, nbw), dtype=np.uint32)
+        sc32 = np.zeros((nbh, nbw), dtype=np.float32)
+        for bi in range(nbh):
+            for bj in range(nbw):
+                m = int(modes[bi, bj])
+                given = None if scales is None or np.isnan(scales[bi, bj]) else float(scales[bi, bj])
+                sc = block_scale(blocks[bi, bj], m, given)
+                q = block_codes(blocks[bi, bj], m, sc)
+                offsets[bi, bj] = arena.write_bytes(arena_encode(q.reshape(1, Bs * Bs), m),
+                                                    alignment=2 if m == 16 else 1)
+                sc32[bi, bj] = sc
+        return cls((H, W), Bs, arena, offsets, np.asarray(modes, dtype=np.uint8).copy(), sc32)
+
+    @classmethod
+    def from_numpy(cls, matrix: np.ndarray, block_size: int = 16, precision_mode=None, epsilon: float = 0.05,
+                   arena: Optional[MemoryArena] = None, use_pointer_hierarchy: bool = True) -> "MTCMatrix":
+        """Uniform-block matrix with one fixed precision or per-block adaptive precision
+        (gemm.py:255-328): with `precision_mode` every block uses that mode (P2, P4, P8 or
+        P16) and the scale max|block| / qmax (1.0 for a block whose max is <= 1e-7); without
+        it each block takes the lowest of P2/P4/P8 whose relative error is <= epsilon, else
+        P16 at scale 1.0. The pointer hierarchy (`PointerTensor`) is not built here:
+        `pointer_tensor` stays None whatever `use_pointer_hierarchy` says."""
+        arr = np.asarray(matrix, dtype=np.float32)
+        H, W = arr.shape
+        Bs = int(block_size)
+        assert H % Bs == 0 and W % Bs == 0, f"Dimensions ({H}, {W}) must be divisible by block_size {Bs}"
+        if Bs not in UNIFORM_BLOCK_SIZES:
+            raise ValueError(f"block_size {Bs} is not one of {UNIFORM_BLOCK_SIZES}")
+        blocks = to_blocks(arr, Bs)
+        nbh, nbw = blocks.shape[:2]
+        if precision_mode is not None:
+            mode = int(precision_mode)
+            if mode not in (2, 4, 8, 16):
+                raise ValueError(f"Unsupported precision: {PrecisionMode(mode)!r}")
+            modes = np.full((nbh, nbw), mode, dtype=np.uint8)
+            scales = None
+        else:
+            modes = np.zeros((nbh, nbw), dtype=np.uint8)
+            scales = np.zeros((nbh, nbw), dtype=np.float64)
+            for bi in range(nbh):
+                for bj in range(nbw):
+                    p, sc = select_independent_precision(blocks[bi, bj], epsilon)
+                    modes[bi, bj], scales[bi, bj] = int(p), sc
+        return cls._from_block_modes(arr, Bs, modes, scales, arena)
+
+    @classmethod
+    def from_numpy_joint(cls, matrix_a: np.ndarray, matrix_b: np.ndarray, block_size: int = 16,
+                         target_epsilon: float = 0.05, use_pointer_hierarchy: bool = True
+                         ) -> Tuple["MTCMatrix", "MTCMatrix"]:
+        """A and B of C = A @ B with block modes negotiated over every interacting block pair
+        (gemm.py:330-430): each of A's blocks (and B's) takes the highest mode any of its
+        pairs asked for (starting from P2), then is quantized at its own max-abs scale."""
+        A = np.asarray(matrix_a, dtype=np.float32)
+        B = np.asarray(matrix_b, dtype=np.float32)
+        M, K = A.shape
+        K2, N = B.shape
+        assert K == K2
+        Bs = int(block_size)
+        if Bs not in UNIFORM_BLOCK_SIZES:
+            raise ValueError(f"block_size {Bs} is not one of {UNIFORM_BLOCK_SIZES}")
+        ab, bb = to_blocks(A, Bs), to_blocks(B, Bs)
+        nbm, nbk, nbn = M // Bs, K // Bs, N // Bs
+        ea = [[_BlockErrors(ab[i, k]) for k in range(nbk)] for i in range(nbm)]
+        eb = [[_BlockErrors(bb[k, j]) for j in range(nbn)] for k in range(nbk)]
+        pa = np.full((nbm, nbk), 2, dtype=np.uint8)
+        pb = np.full((nbk, nbn), 2, dtype=np.uint8)
+        for k in range(nbk):
+            for i in range(nbm):
+                for j in range(nbn):
+                    a, b = negotiate_joint_precision(ea[i][k], eb[k][j], target_epsilon, nbk)
+                    pa[i, k] = max(pa[i, k], a)
+                    pb[k, j] = max(pb[k, j], b)
+        arena_a = MemoryArena(capacity_bytes=max(1024 * 1024, M * K * 2))
+        arena_b = MemoryArena(capacity_bytes=max(1024 * 1024, K * N * 2))
+        return cls._from_block_modes(A, Bs, pa, None, arena_a), cls._from_block_modes(B, Bs, pb, None, arena_b)
 
     @classmethod
     def from_numpy_rd_pair(cls, matrix_a: np.ndarray, matrix_b: np.ndarray, bits_per_element: float,
