@@ -165,6 +165,36 @@ int mtc_gemv_f32(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y
 int mtc_gemv_f32_group(const mtc_stream_desc* const* descs, int n, const float* X, int64_t ldx,
                        float* const* Y, const int64_t* ldy, int M, void* hip_stream);
 
+/* Batched decode: any number of matrices, each with its own X and Y (the same M), in ONE
+ * launch. Replaces a loop of mtc_gemv_f32 calls (the reference's per-layer
+ * LinearMTCAdaptive.forward, mtc/nn/layers.py:150-151, once per matrix of a decoder stack)
+ * when the inputs are known together. Each Y equals, bit for bit, what mtc_gemv_f32 writes
+ * for its matrix alone (same block code and chunking, fixed reduction order).
+ *
+ * 1. mtc_gemv_batch_plan(items, n, M, NULL, 0, NULL, 0, &plan_bytes, &ws_bytes) reports the
+ *    sizes (host only).
+ * 2. The caller provides a zero-filled device workspace of ws_bytes (256-byte aligned; split-K
+ *    partials and counters of the members with several row chunks; the kernels leave the
+ *    counters at zero again) and a 64-byte aligned host buffer of plan_bytes, and calls
+ *    mtc_gemv_batch_plan again with both: it writes the plan (descriptors, X/Y pointers,
+ *    workspace slices, the member of each grid block) into the host buffer.
+ * 3. The caller copies the plan byte for byte into a 64-byte aligned device buffer (and keeps
+ *    every array, X, Y and the workspace alive and unmoved while the plan is used).
+ * 4. mtc_gemv_f32_batch(host_plan, device_plan, stream) launches it (asynchronous; the host
+ *    plan is read during the call only). Launches that share a workspace must not overlap.
+ * All members must have the same scale format. */
+typedef struct mtc_gemv_batch_item {
+  const mtc_stream_desc* desc;   /* read while the plan is built */
+  const float* X;                /* M x K fp32, leading dim ldx */
+  int64_t ldx;
+  float* Y;                      /* M x N fp32, leading dim ldy */
+  int64_t ldy;
+} mtc_gemv_batch_item;
+
+int mtc_gemv_batch_plan(const mtc_gemv_batch_item* items, int n, int M, void* workspace, size_t workspace_bytes,
+                        void* plan, size_t plan_bytes, size_t* plan_needed, size_t* workspace_needed);
+int mtc_gemv_f32_batch(const void* host_plan, const void* device_plan, void* hip_stream);
+
 /*
  * Tile stream (prefill). Wp (K x N) is cut into steps of 64 reduction rows x
  * 256 output columns; step = col_tile * n_ksteps + kstep. A step holds 512

@@ -16,7 +16,8 @@ ERROR_NAMES = {
 
 EXPORTED = ("mtc_abi_version", "mtc_last_error", "mtc_check_desc", "mtc_dequant", "mtc_gemv_lds_bytes",
             "mtc_gemv_workspace_bytes", "mtc_gemv_f32", "mtc_gemv_f32_group", "mtc_check_tile_desc", "mtc_gemm_workspace_bytes",
-            "mtc_gemm_bf16", "mtc_gemm_group_workspace_bytes", "mtc_gemm_bf16_group")
+            "mtc_gemm_bf16", "mtc_gemm_group_workspace_bytes", "mtc_gemm_bf16_group", "mtc_gemv_batch_plan",
+            "mtc_gemv_f32_batch")
 
 
 class MtcStreamDesc(ctypes.Structure):
@@ -70,6 +71,16 @@ class MtcTileDesc(ctypes.Structure):
 TileDescP = ctypes.POINTER(MtcTileDesc)
 
 
+class MtcGemvBatchItem(ctypes.Structure):
+    _fields_ = [
+        ("desc", DescP),
+        ("X", ctypes.c_void_p),
+        ("ldx", ctypes.c_int64),
+        ("Y", ctypes.c_void_p),
+        ("ldy", ctypes.c_int64),
+    ]
+
+
 MAX_GROUP = 4                        # MTC_MAX_GROUP: matrices per mtc_gemv_f32_group launch
 
 
@@ -92,6 +103,11 @@ def declare(lib: ctypes.CDLL) -> None:
     lib.mtc_gemv_f32_group.restype = i32
     lib.mtc_gemv_f32_group.argtypes = [ctypes.POINTER(DescP), i32, vp, i64, ctypes.POINTER(vp),
                                        ctypes.POINTER(i64), i32, vp]
+    lib.mtc_gemv_batch_plan.restype = i32
+    lib.mtc_gemv_batch_plan.argtypes = [ctypes.POINTER(MtcGemvBatchItem), i32, i32, vp, sz, vp, sz,
+                                        ctypes.POINTER(sz), ctypes.POINTER(sz)]
+    lib.mtc_gemv_f32_batch.restype = i32
+    lib.mtc_gemv_f32_batch.argtypes = [vp, vp, vp]
     lib.mtc_check_tile_desc.restype = i32
     lib.mtc_check_tile_desc.argtypes = [TileDescP]
     lib.mtc_gemm_workspace_bytes.restype = sz

@@ -63,11 +63,31 @@ def hipcc_path():
 
 
 def build_hip(verbose=False):
+    """Compiles every source to an object in parallel (each holds its own gfx950 code
+    object; no device code crosses sources), then links the shared library."""
     os.makedirs(LIB_DIR, exist_ok=True)
     out = os.path.join(LIB_DIR, "libmtc_hip.so")
     tmp = _atomic_out(out)
-    srcs = [os.path.join(CSRC, s) for s in HIP_SOURCES]
-    _run([hipcc_path()] + HIPCC_FLAGS + ["-I", INCLUDE, "-I", CSRC] + srcs + ["-o", tmp], verbose)
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    objs, procs = [], []
+    for s in HIP_SOURCES:
+        obj = os.path.join(LIB_DIR, os.path.splitext(s)[0] + ".o.tmp%x" % os.getpid())
+        cmd = [hipcc_path()] + compile_flags + ["-I", INCLUDE, "-I", CSRC, "-c", os.path.join(CSRC, s), "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
+        objs.append(obj)
+    try:
+        for cmd, p in procs:
+            log, _ = p.communicate()
+            if p.returncode != 0:
+                sys.stderr.write(log)
+                raise RuntimeError(f"build step failed ({p.returncode}): {' '.join(cmd)}")
+        _run([hipcc_path(), "--offload-arch=gfx950", "-fPIC", "-shared"] + objs + ["-o", tmp], verbose)
+    finally:
+        for o in objs:
+            if os.path.exists(o):
+                os.remove(o)
     os.replace(tmp, out)
     return out
 

@@ -532,6 +532,11 @@ int check_tile_desc(const mtc_tile_desc* d) {
   if (d->flags & ~MTC_FLAG_FP32_SCALES) return fail(MTC_E_DESC, "unknown flags 0x%x", d->flags);
   if (!d->cells || !d->step_off || !d->payload) return fail(MTC_E_NULL, "tile stream arrays missing");
   if (d->payload_dwords < 4) return fail(MTC_E_DESC, "payload_dwords=%lld", (long long)d->payload_dwords);
+  // payload and cells are addressed with 32-bit byte offsets (buffer resources of at most 2 GiB)
+  const int64_t cell_bytes = (int64_t)d->n_ksteps * d->n_col_tiles * kCells * ((d->flags & MTC_FLAG_FP32_SCALES) ? 16 : 8);
+  if (d->payload_dwords > 0x7FFFFFFF / 4 || cell_bytes > 0x7FFFFFFF)
+    return fail(MTC_E_DESC, "tile stream arrays exceed 2 GiB (payload_dwords=%lld, %lld bytes of cells)",
+                (long long)d->payload_dwords, (long long)cell_bytes);
   return ok();
 }
 

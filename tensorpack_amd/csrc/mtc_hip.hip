@@ -197,6 +197,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, in
 // the buffer's end, which returns zeros without a memory access. Payload dwords 8-15 of
 // a P = 16 chunk are loaded when the chunk is decoded (gemv_load_p16_tail).
 constexpr uint32_t kOutOfRange = 0xFFFFFF00u;        // byte offset past any buffer's end
+constexpr int64_t kMaxArrayBytes = 0x7FFFFFFF;       // largest stream array a buffer resource covers
 
 template <bool FS>
 __device__ __forceinline__ void gemv_load(__amdgpu_buffer_rsrc_t pay_r, __amdgpu_buffer_rsrc_t lw_r,
@@ -370,11 +371,13 @@ __device__ __forceinline__ float slot_sum(float v) {
 
 
 // One decode block of matrix `d`: block id `bid` along the grid's x (the y index is the M tile),
-// NW waves.
+// NW waves. LG: the code for X rows gathered in LDS is present; lg: this matrix uses it
+// (gemv_lds_gather on the host; a constant true for kernels instantiated per matrix).
 template <int MT, bool FS, bool LG, int NW>
 __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int bid, const float* __restrict__ X,
                                            int64_t ldx, float* __restrict__ Y, int64_t ldy, int M,
-                                           float* __restrict__ part, uint32_t* __restrict__ counters) {
+                                           float* __restrict__ part, uint32_t* __restrict__ counters,
+                                           const bool lg = true) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   constexpr int W = NW, T = 64 * W, BPU = kGemvBlocksPerUnit;
   const int kc = d.chunk_rows;
@@ -409,7 +412,7 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
   constexpr int XG = kMaxChunkRows / (4 * T);        // 4-row groups per thread (kc <= kMaxChunkRows)
   constexpr int XR = kMaxChunkRows / T;              // whole-row X values per thread and M row
   const bool perm = d.row_perm != nullptr;
-  constexpr bool lds_gather = LG;                    // host: gemv_lds_gather(MT, perm, K)
+  const bool lds_gather = LG && lg;                  // host: gemv_lds_gather(MT, perm, K)
   int4 kk[XG];
 #pragma unroll
   for (int i = 0; i < XG; ++i) {
@@ -421,7 +424,7 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
     }
   }
   float xr[gemv_lds_gather_rows(MT)][XR];
-  if constexpr (lds_gather) {
+  if (lds_gather) {
 #pragma unroll
     for (int m = 0; m < gemv_lds_gather_rows(MT); ++m) {
       const float* xrow = X + (int64_t)min(m0 + m, M - 1) * ldx;
@@ -483,7 +486,7 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
     asm volatile("" ::"v"(f0.x), "v"(f1.x), "v"(f2.x));
 #pragma unroll
     for (int i = 0; i < XG; ++i) asm volatile("" ::"v"(kk[i].x));
-    if constexpr (lds_gather) {
+    if (lds_gather) {
 #pragma unroll
       for (int m = 0; m < gemv_lds_gather_rows(MT); ++m)
 #pragma unroll
@@ -495,7 +498,7 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
   }
 
   // ---- X rows of the unit (gathered) and their 4- and 8-row sums into LDS ----
-  if constexpr (lds_gather) {
+  if (lds_gather) {
 #pragma unroll
     for (int m = 0; m < gemv_lds_gather_rows(MT); ++m)
 #pragma unroll
@@ -510,7 +513,7 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
     const float* xrow = X + (int64_t)min(m0 + m, M - 1) * ldx;
     const bool mv = m0 + m < M;
     float4 xv[XG];
-    if constexpr (lds_gather) {
+    if (lds_gather) {
       const float* xl = xraw + m * d.K;
 #pragma unroll
       for (int i = 0; i < XG; ++i) {
@@ -678,6 +681,63 @@ __global__ __launch_bounds__(64 * NW, 4) void k_gemv_group(const GemvGroup g, co
   gemv_block<MT, FS, LG, NW>(g.d[i], (int)blockIdx.x - g.start[i], X, ldx, g.Y[i], g.ldy[i], M, nullptr, nullptr);
 }
 
+// Any number of matrices, each with its own X and Y, in one launch. The plan (built on the host
+// by mtc_gemv_batch_plan and copied byte for byte to the device by the caller) holds one
+// BatchItem per matrix and, per grid block, the index of its item. Item i owns grid blocks
+// [start, start + its blocks), a multiple of the XCD count, so each block runs the block code of
+// a launch of its own on the same XCD: every Y is bit-identical to the matrix's single call.
+struct BatchItem {
+  mtc_stream_desc d;
+  const float* X;
+  float* Y;
+  float* part;          // split-K partials and counters in the caller's workspace (n_chunks > 1)
+  uint32_t* counters;
+  int64_t ldx;
+  int64_t ldy;
+  int32_t start;        // first grid block of the item
+  int32_t lg;           // X rows gathered in LDS (gemv_lds_gather)
+};
+
+// Members run blocks of the wave count their own launch would use (gemv_waves_for), so the
+// blocks of 8-wave members come first in the grid table and one launch runs them, then one
+// launch runs the 16-wave members' blocks (their items' `start` counts from that launch's
+// first block).
+struct BatchHeader {
+  uint32_t magic;
+  uint32_t abi_version;
+  int32_t n_items;
+  int32_t n_blocks;     // all blocks: n_blocks8 of 8 waves, then the rest of 16 waves
+  int32_t M;
+  int32_t mt;           // rows per M tile
+  int32_t n_blocks8;
+  int32_t fs;           // fp32 leaf scales
+  uint64_t lds_bytes;
+  uint64_t items_off;   // byte offset of the BatchItem array
+  uint64_t block_item_off;
+  uint64_t plan_bytes;
+  uint64_t ws_bytes;
+  const void* workspace;
+};
+constexpr uint32_t kBatchMagic = 0x4D544342u;   // "BCTM"
+
+template <int MT, bool FS, int NW>
+__global__ __launch_bounds__(64 * NW, 4) void k_gemv_batch(const BatchItem* __restrict__ items,
+                                                        const uint32_t* __restrict__ block_item, int M) {
+  const int b = blockIdx.x;
+  const BatchItem& it = items[block_item[b]];
+  gemv_block<MT, FS, (MT <= 2), NW>(it.d, b - it.start, it.X, it.ldx, it.Y, it.ldy, M, it.part, it.counters,
+                                    it.lg != 0);
+}
+
+template <int MT>
+const void* gemv_batch_kernel(bool fs, int nw) {
+  if (nw == 16)
+    return fs ? reinterpret_cast<const void*>(&k_gemv_batch<MT, true, 16>)
+              : reinterpret_cast<const void*>(&k_gemv_batch<MT, false, 16>);
+  return fs ? reinterpret_cast<const void*>(&k_gemv_batch<MT, true, 8>)
+            : reinterpret_cast<const void*>(&k_gemv_batch<MT, false, 8>);
+}
+
 // The kernel instantiation for (M tile, scale format, LDS gather, waves).
 template <int MT, bool Group>
 const void* gemv_kernel(bool fs, bool lg, int nw) {
@@ -728,6 +788,11 @@ int check_desc(const mtc_stream_desc* d) {
                 (long long)d->n_steps);
   if ((reinterpret_cast<uintptr_t>(d->payload) | reinterpret_cast<uintptr_t>(d->row_perm)) % 16)
     return fail(MTC_E_DESC, "payload and row_perm must be 16-byte aligned");
+  // the kernels address payload, leaf words and step records with 32-bit byte offsets
+  if (d->payload_dwords < 0 || d->n_leaves < 0 || d->payload_dwords > kMaxArrayBytes / 4 ||
+      d->n_leaves > kMaxArrayBytes / 4 || d->n_steps > kMaxArrayBytes / (4 * kStepWords))
+    return fail(MTC_E_DESC, "stream arrays exceed 2 GiB (payload_dwords=%lld n_leaves=%lld n_steps=%lld)",
+                (long long)d->payload_dwords, (long long)d->n_leaves, (long long)d->n_steps);
   return ok();
 }
 
@@ -814,9 +879,147 @@ int launch_gemv_group(const GemvGroup& g, int n, const float* X, int64_t ldx, in
   return check_launch("k_gemv_group");
 }
 
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Plan of a batched decode launch (layout: BatchHeader, BatchItem[n], uint32 block_item[n_blocks]).
+// With plan == NULL only the sizes are reported.
+int build_batch_plan(const mtc_gemv_batch_item* items, int n, int M, void* workspace, size_t ws_bytes, void* plan,
+                     size_t plan_bytes, size_t* plan_needed, size_t* ws_needed) {
+  if (!items) return fail(MTC_E_NULL, "items is NULL");
+  if (n < 1) return fail(MTC_E_SHAPE, "batch of %d matrices", n);
+  if (M <= 0) return fail(MTC_E_SHAPE, "M=%d must be positive", M);
+  const int mt = gemv_mt(M);
+  bool fs = false;
+  size_t ws = 0, lds = 0;
+  int64_t blocks = 0, blocks8 = 0;
+  for (int i = 0; i < n; ++i) {
+    const mtc_stream_desc* d = items[i].desc;
+    int rc = check_desc(d);
+    if (rc) {
+      char why[400];
+      snprintf(why, sizeof(why), "%s", mtc::host::last_error());
+      return fail(rc, "batch item %d: %s", i, why);
+    }
+    if (!items[i].X || !items[i].Y) return fail(MTC_E_NULL, "batch item %d: X or Y is NULL", i);
+    if (items[i].ldx < d->K || items[i].ldy < d->N)
+      return fail(MTC_E_SHAPE, "batch item %d: ldx=%lld < K or ldy=%lld < N", i, (long long)items[i].ldx,
+                  (long long)items[i].ldy);
+    if ((M - 1) > (INT64_MAX / items[i].ldx)) return fail(MTC_E_SHAPE, "batch item %d: M * ldx overflows", i);
+    const bool fsi = d->leaf_scale != nullptr;
+    if (i == 0) fs = fsi;
+    if (fsi != fs) return fail(MTC_E_SHAPE, "batch item %d differs from item 0 in scale format", i);
+    lds = std::max(lds, gemv_lds_bytes(d, mt));
+    ws += align_up(gemv_ws_layout(d, M, nullptr), 256);
+    const int64_t nb = (int64_t)(d->n_panels * d->n_chunks + kXcds - 1) / kXcds * kXcds * kGemvBlocksPerUnit;
+    blocks += nb;
+    if (gemv_waves_for(mt, d->fixed_steps) == 8) blocks8 += nb;
+  }
+  if (blocks > (1 << 30)) return fail(MTC_E_SHAPE, "batch of %lld blocks", (long long)blocks);
+  const size_t items_off = align_up(sizeof(BatchHeader), 64);
+  const size_t block_off = align_up(items_off + (size_t)n * sizeof(BatchItem), 64);
+  const size_t need = block_off + (size_t)blocks * sizeof(uint32_t);
+  if (plan_needed) *plan_needed = need;
+  if (ws_needed) *ws_needed = ws;
+  if (!plan) return ok();
+  if (plan_bytes < need) return fail(MTC_E_WORKSPACE, "batch plan of %zu bytes needed, %zu given", need, plan_bytes);
+  if (ws && (!workspace || ws_bytes < ws))
+    return fail(MTC_E_WORKSPACE, "batch workspace of %zu bytes needed, %zu given", ws, workspace ? ws_bytes : 0);
+  if (reinterpret_cast<uintptr_t>(plan) % 64) return fail(MTC_E_WORKSPACE, "batch plan not 64-byte aligned");
+  const size_t limit = device_lds_limit();
+  if (lds > limit) return fail(MTC_E_SHAPE, "batch needs %zu B of LDS per block (limit %zu)", lds, limit);
+  unsigned char* base = reinterpret_cast<unsigned char*>(plan);
+  memset(base, 0, need);
+  BatchHeader* h = reinterpret_cast<BatchHeader*>(base);
+  BatchItem* it = reinterpret_cast<BatchItem*>(base + items_off);
+  uint32_t* block_item = reinterpret_cast<uint32_t*>(base + block_off);
+  h->magic = kBatchMagic;
+  h->abi_version = MTC_ABI_VERSION;
+  h->n_items = n;
+  h->n_blocks = (int32_t)blocks;
+  h->M = M;
+  h->mt = mt;
+  h->n_blocks8 = (int32_t)blocks8;
+  h->fs = fs;
+  h->lds_bytes = lds;
+  h->items_off = items_off;
+  h->block_item_off = block_off;
+  h->plan_bytes = need;
+  h->ws_bytes = ws;
+  h->workspace = workspace;
+  char* wsp = reinterpret_cast<char*>(workspace);
+  int start8 = 0, start16 = 0;                        // next block of each launch
+  for (int i = 0; i < n; ++i) {
+    const mtc_stream_desc* d = items[i].desc;
+    it[i].d = *d;
+    it[i].X = items[i].X;
+    it[i].Y = items[i].Y;
+    it[i].ldx = items[i].ldx;
+    it[i].ldy = items[i].ldy;
+    it[i].lg = gemv_lds_gather(mt, d->row_perm != nullptr, d->K);
+    size_t cb = 0;
+    const size_t wsi = gemv_ws_layout(d, M, &cb);
+    if (wsi) {
+      it[i].counters = reinterpret_cast<uint32_t*>(wsp);
+      it[i].part = reinterpret_cast<float*>(wsp + cb);
+      wsp += align_up(wsi, 256);
+    }
+    const int nb = (d->n_panels * d->n_chunks + kXcds - 1) / kXcds * kXcds * kGemvBlocksPerUnit;
+    const bool w8 = gemv_waves_for(mt, d->fixed_steps) == 8;
+    int& start = w8 ? start8 : start16;
+    uint32_t* table = block_item + (w8 ? 0 : blocks8);
+    it[i].start = start;
+    for (int b = 0; b < nb; ++b) table[start + b] = (uint32_t)i;
+    start += nb;
+  }
+  return ok();
+}
+
+int launch_gemv_batch(const void* host_plan, const void* device_plan, hipStream_t st) {
+  if (!host_plan || !device_plan) return fail(MTC_E_NULL, "host_plan or device_plan is NULL");
+  const BatchHeader* h = reinterpret_cast<const BatchHeader*>(host_plan);
+  if (h->magic != kBatchMagic || h->abi_version != MTC_ABI_VERSION)
+    return fail(MTC_E_DESC, "not a batch plan of this library (magic 0x%x, ABI %u)", h->magic, h->abi_version);
+  if (reinterpret_cast<uintptr_t>(device_plan) % 64) return fail(MTC_E_DESC, "device plan not 64-byte aligned");
+  const unsigned char* dp = reinterpret_cast<const unsigned char*>(device_plan);
+  const BatchItem* items = reinterpret_cast<const BatchItem*>(dp + h->items_off);
+  const uint32_t* block_item = reinterpret_cast<const uint32_t*>(dp + h->block_item_off);
+  int M = h->M;
+  const size_t shmem = h->lds_bytes;
+  for (int nw : {8, 16}) {                            // the 8-wave members' blocks, then the 16-wave ones
+    const int nblk = nw == 8 ? h->n_blocks8 : h->n_blocks - h->n_blocks8;
+    if (nblk == 0) continue;
+    const void* kern = h->mt == 1 ? gemv_batch_kernel<1>(h->fs, nw)
+                     : h->mt == 2 ? gemv_batch_kernel<2>(h->fs, nw)
+                                  : gemv_batch_kernel<4>(h->fs, 8);
+    if (shmem > 64 * 1024) {
+      hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
+      if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+    }
+    const uint32_t* table = block_item + (nw == 8 ? 0 : h->n_blocks8);
+    dim3 grid(nblk, (M + h->mt - 1) / h->mt);
+    const dim3 block(64 * nw);
+    void* args[] = {&items, &table, &M};
+    const hipError_t e = hipLaunchKernel(kern, grid, block, args, shmem, st);
+    if (e != hipSuccess) return fail(MTC_E_LAUNCH, "k_gemv_batch launch: %s", hipGetErrorString(e));
+    const int rc = check_launch("k_gemv_batch");
+    if (rc) return rc;
+  }
+  return ok();
+}
+
 }  // namespace
 
 MTC_API int mtc_abi_version(void) { return MTC_ABI_VERSION; }
+
+MTC_API int mtc_gemv_batch_plan(const mtc_gemv_batch_item* items, int n, int M, void* workspace,
+                                size_t workspace_bytes, void* plan, size_t plan_bytes, size_t* plan_needed,
+                                size_t* workspace_needed) {
+  return build_batch_plan(items, n, M, workspace, workspace_bytes, plan, plan_bytes, plan_needed, workspace_needed);
+}
+
+MTC_API int mtc_gemv_f32_batch(const void* host_plan, const void* device_plan, void* hip_stream) {
+  return launch_gemv_batch(host_plan, device_plan, as_stream(hip_stream));
+}
 
 MTC_API const char* mtc_last_error(void) { return mtc::host::last_error(); }
 

@@ -198,6 +198,67 @@ def gemv_f32_group(streams, X, outs=None):
     return outs
 
 
+def _aligned_host(nbytes: int, align: int = 64) -> np.ndarray:
+    raw = np.zeros(nbytes + align, dtype=np.uint8)
+    off = (-raw.ctypes.data) % align
+    return raw[off:off + nbytes]
+
+
+class GemvBatch:
+    """A prepared batched decode launch (mtc_gemv_batch_plan + mtc_gemv_f32_batch): Y_i = X_i @
+    W_hat_i for any number of streams, each with its own input and output, in one launch.
+
+    The plan records device addresses of every stream array, X_i, Y_i and the batch's own
+    workspace, so this object keeps them alive; `launch()` reruns the same products (new values
+    written into the same X tensors are picked up). Every Y_i is bit-identical to
+    streams[i].gemv_f32(X_i). Launches of one batch must not overlap in time (they share its
+    workspace): issue them on one stream."""
+
+    def __init__(self, streams, Xs, outs=None):
+        torch = _torch()
+        self.streams = list(streams)
+        n = len(self.streams)
+        if n < 1 or len(Xs) != n:
+            raise ValueError("one input per stream, at least one stream")
+        dev = self.streams[0].device
+        self.device = dev
+        M = Xs[0].shape[0]
+        for s, X in zip(self.streams, Xs):
+            if s.device != dev or X.device != dev:
+                raise ValueError("batch members, inputs and outputs live on one device")
+            _need(X.dim() == 2 and X.dtype == torch.float32 and X.stride(1) == 1 and X.shape == (M, s.K),
+                  f"each X must be (M={M}, K) fp32 row-major")
+        if outs is None:
+            outs = [torch.empty((M, s.N), dtype=torch.float32, device=dev) for s in self.streams]
+        if len(outs) != n:
+            raise ValueError("one output per stream")
+        for o, s in zip(outs, self.streams):
+            _need(o.device == dev and o.dtype == torch.float32 and o.stride(1) == 1 and tuple(o.shape) == (M, s.N),
+                  f"each output must be ({M}, N) fp32 row-major on {dev}")
+        self.Xs, self.outs, self.M = list(Xs), list(outs), M
+        lib = self.lib = self.streams[0].lib
+        items = (_abi.MtcGemvBatchItem * n)()
+        for it, s, X, o in zip(items, self.streams, self.Xs, self.outs):
+            it.desc = ctypes.pointer(s.desc)
+            it.X, it.ldx, it.Y, it.ldy = X.data_ptr(), X.stride(0), o.data_ptr(), o.stride(0)
+        plan_n, ws_n = ctypes.c_size_t(), ctypes.c_size_t()
+        _abi.check(lib, "mtc_gemv_batch_plan",
+                   lib.mtc_gemv_batch_plan(items, n, M, None, 0, None, 0, ctypes.byref(plan_n), ctypes.byref(ws_n)))
+        self.workspace = torch.zeros(ws_n.value, dtype=torch.uint8, device=dev) if ws_n.value else None
+        self.host_plan = _aligned_host(plan_n.value)
+        _abi.check(lib, "mtc_gemv_batch_plan",
+                   lib.mtc_gemv_batch_plan(items, n, M, None if self.workspace is None else self.workspace.data_ptr(),
+                                           ws_n.value, self.host_plan.ctypes.data, plan_n.value, None, None))
+        self.device_plan = torch.from_numpy(self.host_plan.copy()).to(dev)
+        torch.cuda.synchronize(dev)
+
+    def launch(self):
+        rc = self.lib.mtc_gemv_f32_batch(self.host_plan.ctypes.data, self.device_plan.data_ptr(),
+                                         current_stream_handle(self.device))
+        _abi.check(self.lib, "mtc_gemv_f32_batch", rc)
+        return self.outs
+
+
 class DeviceTiles:
     """A TileStream (prefill layout) uploaded to one GPU, plus its ctypes descriptor."""
 

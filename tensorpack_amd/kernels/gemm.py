@@ -29,7 +29,7 @@ from ..core.precision import (_BlockErrors, block_codes, block_scale, negotiate_
                               select_independent_precision)
 from ..core.quadtree import QTAllocation
 from ..core.types import PrecisionMode
-from ..packer import PanelStream, pack_levels, weight_codes
+from ..packer import PanelStream, check_permutation, pack_levels, weight_codes
 from ..tilestream import TileStream, pack_tiles
 
 DECODE_MAX_M = 16             # M at or below this takes the fp32 decode kernel under compute="auto"
@@ -138,6 +138,45 @@ class StoredQTAllocation:
 SAVE_FORMAT = 1
 
 
+def _check_stored(path, K, N, sizes, leaf, modes, scales, Q, pr, pc) -> None:
+    """Raise ValueError unless a saved quadtree matrix is one the packers may trust: grids of
+    the right shapes, leaf grids that tile the (K, N) matrix exactly once, modes in
+    {0} + the code widths, finite scales, every leaf element's code inside its mode's range,
+    and permutations of range(K) / range(N)."""
+    def bad(msg):
+        raise ValueError(f"{path}: {msg}")
+
+    if K <= 0 or N <= 0 or not sizes or any(S not in UNIFORM_BLOCK_SIZES or K % S or N % S for S in sizes):
+        bad(f"sizes {sizes} do not tile the ({K}, {N}) matrix")
+    if Q.shape != (K, N) or Q.dtype not in (np.int8, np.int16):
+        bad(f"codes must be an int8/int16 ({K}, {N}) grid, got {Q.dtype} {Q.shape}")
+    cover = np.zeros((K, N), np.int32)
+    for S in sizes:
+        g = (K // S, N // S)
+        if leaf[S].shape != g or modes[S].shape != g or scales[S].shape != g:
+            bad(f"level {S} grids are not {g}")
+        if leaf[S].dtype != bool or modes[S].dtype != np.uint8 or scales[S].dtype != np.float32:
+            bad(f"level {S} grids must be bool / uint8 / float32")
+        lf = leaf[S]
+        if not np.isin(modes[S][lf], (0,) + tuple(QRANGE)).all():
+            bad(f"level {S} has a mode outside {{0}} + {tuple(QRANGE)}")
+        if not np.isfinite(scales[S][lf]).all():
+            bad(f"level {S} has a non-finite scale")
+        cover += np.repeat(np.repeat(lf.astype(np.int32), S, axis=0), S, axis=1)
+        el_mode = np.repeat(np.repeat(np.where(lf, modes[S], 0), S, axis=0), S, axis=1)
+        for P, (lo, hi) in QRANGE.items():
+            sel = el_mode == P
+            if sel.any() and (Q[sel].min() < lo or Q[sel].max() > hi):
+                bad(f"level {S} P{P} codes outside [{lo}, {hi}]")
+    if not (cover == 1).all():
+        bad("leaf grids do not cover every element exactly once")
+    if (pr is None) != (pc is None):
+        bad("row_perm and col_perm come together")
+    if pr is not None:
+        check_permutation(pr, K, "row_perm")
+        check_permutation(pc, N, "col_perm")
+
+
 class MTCMatrix:
     """A packed (K x N) matrix: reduction along rows, as the right operand of Y = X * W."""
 
@@ -206,7 +245,10 @@ class MTCMatrix:
         assert H % Bs == 0 and W % Bs == 0, f"Dimensions ({H}, {W}) must be divisible by block_size {Bs}"
         blocks = to_blocks(arr, Bs)
         nbh, nbw = blocks.shape[:2]
-        modes = np.asarray(modes, dtype=np.uint8).reshape(nbh, nbw)
+        modes = np.asarray(modes).reshape(nbh, nbw)
+        if not np.isin(modes, (0,) + tuple(QRANGE)).all():
+            raise ValueError(f"modes must be in {{0}} + {tuple(QRANGE)}")
+        modes = modes.astype(np.uint8)
         scales = np.asarray(scales, dtype=np.float32).reshape(nbh, nbw)
         nbytes = (modes.astype(np.int64) * Bs * Bs) // 8
         starts = np.concatenate([[0], np.cumsum(nbytes.ravel())[:-1]])
@@ -368,10 +410,7 @@ class MTCMatrix:
             pr = z["row_perm"] if "row_perm" in z.files else None
             pc = z["col_perm"] if "col_perm" in z.files else None
             total_bits = int(z["total_bits"][0])
-        grids_ok = all(g[S].shape == (K // S, N // S) for g in (leaf, modes, scales) for S in sizes)
-        perms_ok = pr is None or (pc is not None and pr.shape == (K,) and pc.shape == (N,))
-        if Q.shape != (K, N) or not grids_ok or not perms_ok or any(K % S or N % S for S in sizes):
-            raise ValueError(f"{path}: array shapes do not match the ({K}, {N}) matrix")
+        _check_stored(path, K, N, sizes, leaf, modes, scales, Q, pr, pc)
         views: Dict[int, np.ndarray] = {}
 
         def codes_of(S, P, ii, jj, sc):
@@ -513,6 +552,18 @@ def _as_device_tensor(x, device):
     return torch.from_numpy(np.ascontiguousarray(arr)).to(device)
 
 
+def _kernel_layout(X):
+    """X itself when the kernels can read it in place (row-major rows: unit column stride, a
+    row stride of at least K, and for bf16 16-byte aligned rows), else a contiguous copy.
+    Views the reference accepts, such as X[:, 4:] or an expanded row, then run too."""
+    import torch
+    K = X.shape[1]
+    ok = X.stride(1) == 1 and X.stride(0) >= K
+    if ok and X.dtype == torch.bfloat16:
+        ok = X.stride(0) % 8 == 0 and X.data_ptr() % 16 == 0
+    return X if ok else X.contiguous()
+
+
 def mtc_gemm(A, B: MTCMatrix, *, compute: str = "auto", out_dtype=None):
     """Y = A @ W_hat.
 
@@ -549,16 +600,12 @@ def mtc_gemm(A, B: MTCMatrix, *, compute: str = "auto", out_dtype=None):
     if M == 0:
         Y = torch.zeros((0, B.shape[1]), dtype=out_dtype or torch.float32, device=dev)
     elif compute == "fp32":
-        Xf = X.float()
-        if Xf.stride(1) != 1:
-            Xf = Xf.contiguous()
+        Xf = _kernel_layout(X.float())
         Y = B.device_stream(None, dev, M).gemv_f32(Xf)
         if out_dtype is not None and out_dtype != torch.float32:
             Y = Y.to(out_dtype)
     elif compute == "bf16":
-        Xb = X if X.dtype in (torch.float32, torch.bfloat16) else X.float()
-        if Xb.stride(1) != 1:
-            Xb = Xb.contiguous()
+        Xb = _kernel_layout(X if X.dtype in (torch.float32, torch.bfloat16) else X.float())
         Y = B.device_tiles(dev).gemm_bf16(Xb, out_dtype=out_dtype)
     else:
         raise ValueError(f"compute must be 'auto', 'fp32' or 'bf16', got {compute!r}")
@@ -605,9 +652,7 @@ def mtc_gemm_group(A, Bs, *, compute: str = "auto"):
         compute = "fp32" if M <= DECODE_MAX_M else "bf16"
     outs = [None] * len(Bs)
     if compute == "fp32" and M > 0:
-        Xf = X.float()
-        if Xf.stride(1) != 1:
-            Xf = Xf.contiguous()
+        Xf = _kernel_layout(X.float())
         streams = [B.device_stream(None, dev, M) for B in Bs]
         # members that can share a launch: one row chunk, same scale format and permutation presence
         groups: Dict[Tuple[bool, bool], list] = {}
@@ -630,9 +675,7 @@ def mtc_gemm_group(A, Bs, *, compute: str = "auto"):
         return outs
     if compute == "bf16" and M > 0:
         from ..device import gemm_bf16_group
-        Xb = X if X.dtype in (torch.float32, torch.bfloat16) else X.float()
-        if Xb.stride(1) != 1:
-            Xb = Xb.contiguous()
+        Xb = _kernel_layout(X if X.dtype in (torch.float32, torch.bfloat16) else X.float())
         tiles = [B.device_tiles(dev) for B in Bs]
         # members that can share a launch: same scale format
         groups: Dict[bool, list] = {}

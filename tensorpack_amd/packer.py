@@ -44,6 +44,17 @@ MAX_FIXED_STEPS = 48                   # records per block stored at block-compu
 BLOCKS_PER_UNIT = 2                    # decode blocks (of STEP_GROUPS column groups) per unit
 _NULL_KEY = 3 | (2 << 8)               # kind of a record with no chunks (any valid kind)
 _LOG2 = {32: 5, 16: 4, 8: 3, 4: 2}
+MAX_DEVICE_ARRAY_BYTES = 0x7FFFFFFF    # the kernels address every stream array with 32-bit byte offsets
+
+
+def check_permutation(p, n: int, name: str) -> None:
+    """Raise ValueError unless p is an integer array holding each of 0 .. n-1 exactly once
+    (permutations index device memory directly: anything else reads or writes out of bounds)."""
+    a = np.asarray(p)
+    if a.shape != (n,) or not np.issubdtype(a.dtype, np.integer):
+        raise ValueError(f"{name} must be an integer array of shape ({n},), got {a.dtype} {a.shape}")
+    if n and (a.min() < 0 or a.max() >= n or np.bincount(a.astype(np.int64), minlength=n).max() != 1):
+        raise ValueError(f"{name} is not a permutation of range({n})")
 
 CodeSource = Callable[[int, int, np.ndarray, np.ndarray, np.ndarray], np.ndarray]
 
@@ -108,16 +119,96 @@ class PanelStream:
 
     @classmethod
     def load(cls, path) -> "PanelStream":
+        """Read a stream written by `save` and check it with `validate` (a file is not trusted:
+        its offsets and permutations become device addresses)."""
         with np.load(path, allow_pickle=False) as z:
             meta = [int(x) for x in z["meta"]]
             if meta[0] != STREAM_FORMAT:
                 raise ValueError(f"{path}: panel stream format {meta[0]}, this build reads {STREAM_FORMAT}")
             get = lambda k: np.array(z[k]) if k in z.files else None
             stats = dict(zip([str(k) for k in z["stats_keys"]], [float(v) for v in z["stats_vals"]]))
-            return cls(K=meta[1], N=meta[2], chunk_rows=meta[3], payload=get("payload"), buckets=get("buckets"),
-                       unit_hdr=get("unit_hdr"), leaf_word=get("leaf_word"), leaf_scale=get("leaf_scale"),
-                       steps=get("steps"), row_perm=get("row_perm"), col_perm=get("col_perm"), n_real_leaves=meta[4],
-                       max_unit_words=meta[5], max_unit_words4=meta[6], fixed_steps=meta[7], stats=stats)
+            ps = cls(K=meta[1], N=meta[2], chunk_rows=meta[3], payload=get("payload"), buckets=get("buckets"),
+                     unit_hdr=get("unit_hdr"), leaf_word=get("leaf_word"), leaf_scale=get("leaf_scale"),
+                     steps=get("steps"), row_perm=get("row_perm"), col_perm=get("col_perm"), n_real_leaves=meta[4],
+                     max_unit_words=meta[5], max_unit_words4=meta[6], fixed_steps=meta[7], stats=stats)
+        ps.validate()
+        return ps
+
+    def validate(self) -> None:
+        """Raise ValueError unless every index the kernels follow stays inside its array:
+        unit header ranges, bucket payload and leaf ranges, leaf rows within the unit's rows,
+        permutations of range(K) / range(N), array sizes the 32-bit device offsets reach."""
+        K, N, kc = int(self.K), int(self.N), int(self.chunk_rows)
+
+        def bad(msg):
+            raise ValueError(f"panel stream: {msg}")
+
+        if K <= 0 or N <= 0 or N % PANEL or K % 8:
+            bad(f"shape ({K}, {N}) (N must be a multiple of {PANEL}, K of 8)")
+        if kc % 32 or not 32 <= kc <= MAX_CHUNK_ROWS:
+            bad(f"chunk_rows={kc}")
+        arrays = {"payload": (self.payload, np.uint32), "leaf_word": (self.leaf_word, np.uint32),
+                  "unit_hdr": (self.unit_hdr, np.int32), "buckets": (self.buckets, np.uint32)}
+        for name, (a, dt) in arrays.items():
+            if not isinstance(a, np.ndarray) or a.dtype != dt:
+                bad(f"{name} must be a {np.dtype(dt).name} array")
+        n_units = self.n_units
+        if self.unit_hdr.shape != (n_units, UNIT_HDR_WORDS) or self.buckets.ndim != 2 or self.buckets.shape[1] != 4:
+            bad("unit_hdr / buckets shape")
+        for name, a in (("payload", self.payload), ("leaf_word", self.leaf_word)):
+            if a.ndim != 1 or a.size * 4 > MAX_DEVICE_ARRAY_BYTES:
+                bad(f"{name} of {a.size} words (at most {MAX_DEVICE_ARRAY_BYTES // 4})")
+        if self.leaf_scale is not None and (self.leaf_scale.dtype != np.float32 or self.leaf_scale.shape != self.leaf_word.shape):
+            bad("leaf_scale must be float32 with one scale per leaf word")
+        for name, p, n in (("row_perm", self.row_perm, K), ("col_perm", self.col_perm, N)):
+            if p is not None:
+                check_permutation(p, n, name)
+        if (self.row_perm is None) != (self.col_perm is None):
+            bad("row_perm and col_perm come together")
+        h = self.unit_hdr.astype(np.int64)
+        nb = self.buckets.shape[0]
+        if (h[:, 0] < 0).any() or (h[:, 0] % 4).any() or (h[:, 1] < h[:, 0]).any() or \
+                (h[:, 1] > self.payload.size - PAYLOAD_PAD).any():
+            bad("unit payload ranges")
+        if (h[:, 2] < 0).any() or (h[:, 3] < h[:, 2]).any() or (h[:, 3] > self.leaf_word.size).any():
+            bad("unit leaf-word ranges")
+        if (h[:, 4] < 0).any() or (h[:, 5] < h[:, 4]).any() or (h[:, 5] > nb).any() or \
+                (h[:, 8] != 0).any() or (np.diff(h[:, 8:17], axis=1) < 0).any() or (h[:, 16] != h[:, 5] - h[:, 4]).any():
+            bad("unit bucket ranges")
+        if nb:
+            unit = np.repeat(np.arange(n_units), (h[:, 5] - h[:, 4]))
+            if unit.size != nb:
+                bad("buckets not covered exactly once by the unit headers")
+            b = self.buckets.astype(np.int64)
+            ls, P = b[:, 3] & 0xFF, b[:, 3] >> 8
+            if not np.isin(ls, (2, 3, 4, 5)).all() or not np.isin(P, CODE_WIDTHS).all():
+                bad("bucket kind")
+            n = b[:, 2] & 0xFFFF
+            S = np.left_shift(1, ls)
+            if (b[:, 0] % 4).any() or (h[unit, 0] + b[:, 0] + n * P > h[unit, 1]).any():
+                bad("bucket payload outside its unit")
+            n_leaf = np.where(S == 4, 2 * n, -(-n * 8 // np.maximum(S, 8)))
+            first = h[unit, 2] + b[:, 1]
+            if (b[:, 1] < 0).any() or (first + n_leaf > h[unit, 3]).any():
+                bad("bucket leaf words outside its unit")
+            # every leaf of a bucket: its rows lie inside the unit's rows
+            idx = np.repeat(first - np.cumsum(n_leaf) + n_leaf, n_leaf) + np.arange(int(n_leaf.sum()))
+            size = np.repeat(S, n_leaf)
+            kb = np.repeat((unit % self.n_chunks) * kc, n_leaf)
+            w = self.leaf_word[idx].astype(np.int64)
+            row = (w & ((1 << ROW_BITS) - 1)) * 4
+            real = (w & LEAF_PAD) == 0
+            if (real & (row + size > np.minimum(kc, K - kb))).any():
+                bad("leaf rows outside their unit")
+        if self.steps is not None:
+            blocks = n_units * BLOCKS_PER_UNIT
+            if self.steps.ndim != 2 or self.steps.shape[1] != STEP_WORDS or \
+                    self.steps.shape[0] < blocks * int(self.fixed_steps) + 1 or self.steps.size * 4 > MAX_DEVICE_ARRAY_BYTES:
+                bad("step records shape")
+        elif nb:
+            bad("step records missing")
+        if self.fixed_steps not in (0, 16, 32, 48):
+            bad(f"fixed_steps={self.fixed_steps}")
 
 
 def pack_codes(codes: np.ndarray, P: int) -> np.ndarray:
@@ -416,6 +507,10 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
 
     stats = {"payload_bytes": float(total_dw * 4), "n_buckets": float(n_buckets), "n_leaves": float(n_real),
              "max_unit_bytes": float(4 * max_unit_words)}
+    for name, a in (("payload", payload), ("leaf words", leaf_word), ("step records", steps)):
+        if a is not None and a.nbytes > MAX_DEVICE_ARRAY_BYTES:
+            raise ValueError(f"panel stream {name} of {a.nbytes} bytes exceed the kernels' 32-bit offsets "
+                             f"({MAX_DEVICE_ARRAY_BYTES}); split the matrix by column panels")
     return PanelStream(K=K, N=N, chunk_rows=chunk_rows, payload=payload, buckets=buckets,
                        unit_hdr=hdr.astype(np.int32), leaf_word=leaf_word, leaf_scale=leaf_scale, steps=steps,
                        fixed_steps=F,

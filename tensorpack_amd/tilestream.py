@@ -154,8 +154,9 @@ def pack_tiles(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np.
     step_tot = per_step.sum(axis=1)
     off_in = (np.cumsum(per_step, axis=1) - per_step).reshape(-1)
     step_off = np.concatenate([[0], np.cumsum(step_tot)]).astype(np.int64)
-    if step_off[-1] >= 2 ** 32:
-        raise ValueError("tile stream payload too large for 32-bit step offsets")
+    if (step_off[-1] + PAYLOAD_PAD) * 4 > 0x7FFFFFFF or n_steps * CELLS * 4 * 4 > 0x7FFFFFFF:
+        raise ValueError("tile stream payload or cells exceed the kernels' 32-bit byte offsets (2 GiB); "
+                         "split the matrix by column tiles")
     # 8 dwords of tail padding: the device reads 32 bytes per cell whatever its class
     payload = np.zeros(int(step_off[-1]) + PAYLOAD_PAD, dtype=np.uint32)
 

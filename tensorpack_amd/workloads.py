@@ -116,3 +116,21 @@ def c3_matrices(n_layers: int = 24) -> List[MatrixWorkload]:
 
 
 CONFIGS = {"c1": c1, "c2": c2, "c4": c4, "c5": c5}
+
+
+def _allocate_one(w: MatrixWorkload):
+    return w.allocate(n_threads=1)
+
+
+def allocate_many(mats: List[MatrixWorkload], processes: int = 0) -> list:
+    """Allocations of many matrices at once: one forked worker process per CPU (at most 16, the
+    size of a GPU host's share), each running one matrix's allocator single-threaded. Results are
+    those of `w.allocate()` (the allocator is deterministic; its thread count does not change
+    its decisions). Fork only from a process that has not initialised the GPU yet."""
+    import multiprocessing as mp
+    import os
+    n = processes or min(16, len(os.sched_getaffinity(0)))
+    if n <= 1 or len(mats) <= 1:
+        return [w.allocate() for w in mats]
+    with mp.get_context("fork").Pool(min(n, len(mats))) as pool:
+        return pool.map(_allocate_one, mats, chunksize=1)

@@ -90,6 +90,12 @@ def test_descriptor_validation(hip):
     # the fixed record area of the 8 decode blocks plus the null record must be present
     assert hip.mtc_check_desc(ctypes.byref(_desc(fixed_steps=16, n_steps=129))) == 0
     assert hip.mtc_check_desc(ctypes.byref(_desc(fixed_steps=16, n_steps=128))) == -2
+    # arrays the kernels would address past 2 GiB with their 32-bit byte offsets are rejected
+    lim = 0x7FFFFFFF
+    assert hip.mtc_check_desc(ctypes.byref(_desc(payload_dwords=lim // 4))) == 0
+    assert hip.mtc_check_desc(ctypes.byref(_desc(payload_dwords=lim // 4 + 1))) == -2
+    assert hip.mtc_check_desc(ctypes.byref(_desc(n_leaves=lim // 4 + 1))) == -2
+    assert hip.mtc_check_desc(ctypes.byref(_desc(n_steps=lim // 64 + 1))) == -2
 
 
 def test_entry_points_reject_bad_arguments_before_any_gpu_call(hip):
@@ -204,6 +210,9 @@ def test_tile_descriptor_layout_and_validation(hip):
     for field, (val, code) in cases.items():
         assert hip.mtc_check_tile_desc(ctypes.byref(_tdesc(**{field: val}))) == code, field
     assert hip.mtc_check_tile_desc(None) == -1
+    # payload past 2 GiB (32-bit byte offsets) is rejected
+    assert hip.mtc_check_tile_desc(ctypes.byref(_tdesc(payload_dwords=0x7FFFFFFF // 4))) == 0
+    assert hip.mtc_check_tile_desc(ctypes.byref(_tdesc(payload_dwords=0x7FFFFFFF // 4 + 1))) == -2
 
 
 def test_rd_search_rejects_bad_block_size():
@@ -231,3 +240,41 @@ def test_gpu_path_fails_loudly_without_gpu():
         mtc_gemm(np.ones((1, 64), np.float32), m)
     with pytest.raises(RuntimeError, match="GPU"):
         m.to_array()
+
+
+def test_batch_plan_sizes_and_errors(hip):
+    """mtc_gemv_batch_plan is host arithmetic: sizes, the block -> member table, workspace
+    slices of the split-K members, and argument errors, all without a GPU."""
+    import numpy as np
+    d1 = _desc()                                           # 2 panels x 2 chunks: split-K member
+    d2 = _desc(K=256, chunk_rows=256, n_chunks=1)          # single chunk
+    items = (_abi.MtcGemvBatchItem * 2)()
+    for it, d in zip(items, (d1, d2)):
+        it.desc = ctypes.pointer(d)
+        it.X, it.ldx, it.Y, it.ldy = 0x10000, 256, 0x20000, 64
+    plan_n, ws_n = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip.mtc_gemv_batch_plan(items, 2, 1, None, 0, None, 0, ctypes.byref(plan_n), ctypes.byref(ws_n)) == 0
+    blocks = 16 + 16                                       # units padded to 8 XCDs x 2 blocks per unit
+    assert plan_n.value >= blocks * 4 and ws_n.value > 0 and ws_n.value % 256 == 0
+    raw = np.zeros(plan_n.value + 64, np.uint8)
+    off = (-raw.ctypes.data) % 64
+    plan = raw[off:off + plan_n.value]
+    ws = 0x100000
+    assert hip.mtc_gemv_batch_plan(items, 2, 1, ws, ws_n.value, plan.ctypes.data, plan_n.value, None, None) == 0
+    block_item = plan[-4 * blocks:].view(np.uint32)
+    assert (block_item[:16] == 0).all() and (block_item[16:] == 1).all()
+    # errors: empty batch, M = 0, missing X, mixed scale formats, plan or workspace too small
+    assert hip.mtc_gemv_batch_plan(items, 0, 1, None, 0, None, 0, ctypes.byref(plan_n), None) == -3
+    assert hip.mtc_gemv_batch_plan(items, 2, 0, None, 0, None, 0, ctypes.byref(plan_n), None) == -3
+    items[1].X = None
+    assert hip.mtc_gemv_batch_plan(items, 2, 1, None, 0, None, 0, ctypes.byref(plan_n), None) == -1
+    items[1].X = 0x10000
+    d3 = _desc(flags=_abi.MTC_FLAG_FP32_SCALES, leaf_scale=0x3000)
+    items[1].desc = ctypes.pointer(d3)
+    assert hip.mtc_gemv_batch_plan(items, 2, 1, None, 0, None, 0, ctypes.byref(plan_n), None) == -3
+    items[1].desc = ctypes.pointer(d2)
+    assert hip.mtc_gemv_batch_plan(items, 2, 1, ws, ws_n.value, plan.ctypes.data, 64, None, None) == -5
+    assert hip.mtc_gemv_batch_plan(items, 2, 1, None, 0, plan.ctypes.data, plan_n.value, None, None) == -5
+    assert hip.mtc_gemv_f32_batch(None, None, None) == -1
+    bogus = np.zeros(256, np.uint8)
+    assert hip.mtc_gemv_f32_batch(bogus.ctypes.data, 0x40000, None) == -2

@@ -101,3 +101,76 @@ def test_loaded_matrix_on_gpu(gpu, tmp_path):
         X = np.random.RandomState(M).randn(M, 256).astype(np.float32)
         assert np.array_equal(mtc_gemm(X, back), mtc_gemm(X, m)), M
     assert np.array_equal(back.to_array(), m.to_array())
+
+
+def _resave(src, dst, **changes):
+    """Copy an .npz, replacing the named arrays."""
+    with np.load(src, allow_pickle=False) as z:
+        arrays = {k: z[k] for k in z.files}
+    arrays.update(changes)
+    np.savez(dst, **arrays)
+
+
+@pytest.fixture(scope="module")
+def saved_qtp(tmp_path_factory):
+    K, N = 128, 96
+    W = outlier_matrix(11, K, N)
+    h = np.exp(np.random.RandomState(12).randn(K))
+    alloc = PermutedQuadtreeRD(W, h, (32, 16, 8, 4)).select(3.5)
+    m = MTCMatrix.from_quadtree(alloc, W)
+    d = tmp_path_factory.mktemp("qtp")
+    m.save(d / "w.npz")
+    m.panel_stream(64).save(d / "s.npz")
+    return d, m
+
+
+def test_load_rejects_corrupt_matrix(saved_qtp, tmp_path):
+    """Permutations and codes index device memory: a file whose permutations are not
+    permutations, whose modes or codes leave their ranges, or whose leaf grids overlap is
+    refused before anything reaches the GPU."""
+    d, m = saved_qtp
+    src = d / "w.npz"
+    with np.load(src, allow_pickle=False) as z:
+        pr, pc, codes, leaf8, modes8 = z["row_perm"], z["col_perm"], z["codes"], z["leaf_8"], z["modes_8"]
+    bad = {
+        "row_perm out of range": {"row_perm": np.where(pr == 0, 128, pr)},
+        "row_perm duplicate": {"row_perm": np.where(pr == 0, pr[1] if pr[0] != 0 else pr[0], pr)},
+        "col_perm negative": {"col_perm": np.where(pc == 5, -1, pc)},
+        "col_perm float": {"col_perm": pc.astype(np.float64)},
+        "mode 7": {"modes_8": np.where(leaf8, 7, modes8).astype(np.uint8)},
+        "overlapping leaves": {"leaf_8": np.ones_like(leaf8)},
+    }
+    wide = codes.astype(np.int16)
+    wide[0, 0] = 20000                                # outside every width's range but P16
+    bad["code out of range"] = {"codes": wide}
+    for name, change in bad.items():
+        dst = tmp_path / (name.replace(" ", "_") + ".npz")
+        _resave(src, dst, **change)
+        with pytest.raises(ValueError):
+            MTCMatrix.load(dst)
+    ok = tmp_path / "ok.npz"
+    _resave(src, ok)
+    assert MTCMatrix.load(ok).shape == m.shape
+
+
+def test_panel_stream_load_rejects_corrupt_stream(saved_qtp, tmp_path):
+    d, m = saved_qtp
+    src = d / "s.npz"
+    ps = PanelStream.load(src)
+    ps.validate()
+    hdr = ps.unit_hdr.copy()
+    hdr[0, 1] = ps.payload.size                       # unit payload past the array
+    bk = ps.buckets.copy()
+    bk[0, 0] += 4 * ps.payload.size                   # bucket payload outside its unit
+    bk2 = ps.buckets.copy()
+    bk2[0, 3] = 7 | (2 << 8)                          # no leaf size 128
+    lw = ps.leaf_word.copy()
+    lw[:] |= 1023                                     # leaf rows past the unit's rows
+    bad = {"hdr": {"unit_hdr": hdr}, "bucket payload": {"buckets": bk}, "bucket kind": {"buckets": bk2},
+           "leaf rows": {"leaf_word": lw}, "row_perm": {"row_perm": np.zeros_like(ps.row_perm)},
+           "col_perm": {"col_perm": ps.col_perm + 1}}
+    for name, change in bad.items():
+        dst = tmp_path / (name.replace(" ", "_") + ".npz")
+        _resave(src, dst, **change)
+        with pytest.raises(ValueError):
+            PanelStream.load(dst)
