@@ -342,14 +342,36 @@ __device__ __forceinline__ void gemv_chunk(const u32x16_t rw, uint32_t lw0, uint
 constexpr int kStepGroups = 4;              // column groups one decode step covers
 constexpr int kStepLanes = 16;              // lanes per column group in a step
 constexpr int kStepWords = 16;              // words per step record
-// waves per block: 16 for M tiles of 1-2 rows, 8 for 4 rows (more accumulators per lane).
-// Streams with at most kFewSteps records per block (small K) use 8-wave blocks for 1-2 rows
-// too: the 16-wave block would leave most waves without a record, and two 8-wave blocks
-// share a CU.
+// Most waves a decode block has (the LDS of the cross-wave reduction is sized for it).
 __host__ __device__ constexpr int gemv_waves(int MT) { return MT <= 2 ? 16 : 8; }
 constexpr int kFewSteps = 16;
-inline int gemv_waves_for(int MT, int fixed_steps) { return (MT <= 2 && fixed_steps <= kFewSteps) ? 8 : gemv_waves(MT); }
+constexpr int kSmallRows = 1024;
 constexpr int kGemvBlocksPerUnit = kGroups / kStepGroups;
+
+// Block shape of a matrix's decode blocks. The single, grouped and batched launches all take it
+// from gemv_shape, so a matrix's blocks run the same code (same waves, hence the same
+// summation order) in every launch:
+// - M tiles of 4 rows: 8 waves, three steps prefetched;
+// - 1-2 rows, more than kFewSteps records per block: 16 waves (one block fills a CU), three
+//   steps prefetched, X rows gathered in LDS when there is a row permutation and K <= 4096;
+// - 1-2 rows, at most kFewSteps records per block (small K): 4 waves with two steps
+//   prefetched, which keeps a wave near 69 registers so that seven blocks share a CU; the X
+//   staging is sized for kSmallRows rows when the chunk (and, for the LDS gather, K) fits in
+//   it, which keeps its registers few, else for kMaxChunkRows rows without the LDS gather.
+struct GemvShape {
+  int nw;        // waves per block
+  int kc;        // rows the X staging covers (kSmallRows or kMaxChunkRows)
+  bool lg_code;  // the kernel has the LDS-gather code
+  bool lg;       // this matrix gathers X in LDS
+};
+inline GemvShape gemv_shape(int MT, const mtc_stream_desc* d) {
+  const bool perm = d->row_perm != nullptr;
+  if (MT > 2) return {8, kMaxChunkRows, false, false};
+  if (d->fixed_steps > kFewSteps) return {16, kMaxChunkRows, true, perm && d->K <= kMaxChunkRows};
+  if (d->chunk_rows <= kSmallRows) return {4, kSmallRows, true, perm && d->K <= kSmallRows};
+  return {4, kMaxChunkRows, false, false};
+}
+__host__ __device__ constexpr int gemv_prefetch(int NW) { return NW == 4 ? 2 : 3; }
 constexpr int kMaxFixedSteps = 48;          // step records per block at block-computable positions
 constexpr int kXcds = 8;
 
@@ -373,7 +395,10 @@ __device__ __forceinline__ float slot_sum(float v) {
 // One decode block of matrix `d`: block id `bid` along the grid's x (the y index is the M tile),
 // NW waves. LG: the code for X rows gathered in LDS is present; lg: this matrix uses it
 // (gemv_lds_gather on the host; a constant true for kernels instantiated per matrix).
-template <int MT, bool FS, bool LG, int NW>
+// KC: rows the X staging covers (chunk_rows <= KC, and K <= KC when X is gathered in LDS).
+// PF (gemv_prefetch): steps whose loads a wave issues before the X staging; a wave executes
+// its records in the same order whatever PF is.
+template <int MT, bool FS, bool LG, int NW, int KC>
 __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int bid, const float* __restrict__ X,
                                            int64_t ldx, float* __restrict__ Y, int64_t ldy, int M,
                                            float* __restrict__ part, uint32_t* __restrict__ counters,
@@ -409,8 +434,10 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
   //      load level away and the decode can start before the last payload arrives;
   //      otherwise the permuted row indices are read here and X is gathered from memory
   //      after the payload loads are out. ----
-  constexpr int XG = kMaxChunkRows / (4 * T);        // 4-row groups per thread (kc <= kMaxChunkRows)
-  constexpr int XR = kMaxChunkRows / T;              // whole-row X values per thread and M row
+  static_assert(KC % T == 0, "the X staging loops cover KC rows");
+  constexpr int XG = (KC + 4 * T - 1) / (4 * T);     // 4-row groups per thread (kc <= KC)
+  constexpr int XR = KC / T;                         // whole-row X values per thread and M row (K <= KC)
+  constexpr int PF = gemv_prefetch(NW);
   const bool perm = d.row_perm != nullptr;
   const bool lds_gather = LG && lg;                  // host: gemv_lds_gather(MT, perm, K)
   int4 kk[XG];
@@ -482,8 +509,14 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
       const int i = wave + k * W;
       return slot_of(i < F ? (uint32_t)(blk * F + i) : null_rec);
     };
-    const u32x4_t f0 = fixed(0), f1 = fixed(1), f2 = fixed(2);
-    asm volatile("" ::"v"(f0.x), "v"(f1.x), "v"(f2.x));
+    static_assert(PF >= 1 && PF <= 3, "one to three prefetched steps");
+    const u32x4_t f0 = fixed(0);
+    u32x4_t f1 = {}, f2 = {};
+    if constexpr (PF >= 2) f1 = fixed(1);
+    if constexpr (PF >= 3) f2 = fixed(2);
+    asm volatile("" ::"v"(f0.x));
+    if constexpr (PF >= 2) asm volatile("" ::"v"(f1.x));
+    if constexpr (PF >= 3) asm volatile("" ::"v"(f2.x));
 #pragma unroll
     for (int i = 0; i < XG; ++i) asm volatile("" ::"v"(kk[i].x));
     if (lds_gather) {
@@ -493,8 +526,8 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
         for (int i = 0; i < XR; ++i) asm volatile("" ::"v"(xr[m][i]));
     }
     fetch(f0, r0);
-    fetch(f1, r1);
-    fetch(f2, r2);
+    if constexpr (PF >= 2) fetch(f1, r1);
+    if constexpr (PF >= 3) fetch(f2, r2);
   }
 
   // ---- X rows of the unit (gathered) and their 4- and 8-row sums into LDS ----
@@ -571,11 +604,11 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
     }
   };
   compute(r0);                                        // null records have no active lanes
-  compute(r1);
-  compute(r2);
+  if constexpr (PF >= 2) compute(r1);
+  if constexpr (PF >= 3) compute(r2);
   const int nrec = hdr[28 + 2 * cb];
   const uint32_t ovf = (uint32_t)hdr[27 + 2 * cb];
-  for (int i = wave + 3 * W; i < nrec; i += W) {
+  for (int i = wave + PF * W; i < nrec; i += W) {
     fetch(slot_of(i < F ? (uint32_t)(blk * F + i) : ovf + (uint32_t)(i - F)), r0);
     compute(r0);
   }
@@ -654,16 +687,16 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
 
 // At least 4 waves per SIMD: a 16-wave block fills a CU's 4 SIMDs; two 8-wave blocks
 // (M tiles of 4 rows) share one only if each wave keeps to 128 VGPRs.
-template <int MT, bool FS, bool LG, int NW>
+template <int MT, bool FS, bool LG, int NW, int KC>
 __global__ __launch_bounds__(64 * NW, 4) void k_gemv(const mtc_stream_desc d, const float* __restrict__ X,
                                                   int64_t ldx, float* __restrict__ Y, int64_t ldy, int M,
                                                   float* __restrict__ part, uint32_t* __restrict__ counters) {
-  gemv_block<MT, FS, LG, NW>(d, blockIdx.x, X, ldx, Y, ldy, M, part, counters);
+  gemv_block<MT, FS, LG, NW, KC>(d, blockIdx.x, X, ldx, Y, ldy, M, part, counters);
 }
 
-// Up to kMaxGroup single-chunk matrices that read the same X, in one launch: matrix i owns
-// grid blocks [start[i], start[i + 1]) (each range a whole number of XCD rounds, so a block's
-// XCD is the same as in a launch of its own).
+// Up to kMaxGroup single-chunk matrices of one block shape that read the same X, in one launch:
+// matrix i owns grid blocks [start[i], start[i + 1]) (each range a whole number of XCD rounds, so
+// a block's XCD is the same as in a launch of its own).
 constexpr int kMaxGroup = MTC_MAX_GROUP;
 struct GemvGroup {
   mtc_stream_desc d[kMaxGroup];
@@ -672,20 +705,23 @@ struct GemvGroup {
   int start[kMaxGroup + 1];
 };
 
-template <int MT, bool FS, bool LG, int NW>
+template <int MT, bool FS, bool LG, int NW, int KC>
 __global__ __launch_bounds__(64 * NW, 4) void k_gemv_group(const GemvGroup g, const float* __restrict__ X,
                                                         int64_t ldx, int M) {
   int i = 0;
 #pragma unroll
   for (int k = 1; k < kMaxGroup; ++k) i += (int)blockIdx.x >= g.start[k];
-  gemv_block<MT, FS, LG, NW>(g.d[i], (int)blockIdx.x - g.start[i], X, ldx, g.Y[i], g.ldy[i], M, nullptr, nullptr);
+  gemv_block<MT, FS, LG, NW, KC>(g.d[i], (int)blockIdx.x - g.start[i], X, ldx, g.Y[i], g.ldy[i], M, nullptr,
+                                 nullptr);
 }
 
-// Any number of matrices, each with its own X and Y, in one launch. The plan (built on the host
-// by mtc_gemv_batch_plan and copied byte for byte to the device by the caller) holds one
-// BatchItem per matrix and, per grid block, the index of its item. Item i owns grid blocks
-// [start, start + its blocks), a multiple of the XCD count, so each block runs the block code of
-// a launch of its own on the same XCD: every Y is bit-identical to the matrix's single call.
+// Any number of matrices, each with its own X and Y. The plan (built on the host by
+// mtc_gemv_batch_plan and copied byte for byte to the device by the caller) holds one BatchItem
+// per matrix and, per grid block, the index of its item. The members of each block shape
+// (gemv_shape) run in one launch of that shape's kernel, so each block runs the block code of a
+// launch of its own: every Y is bit-identical to the matrix's single call. Item i owns blocks
+// [start, start + its blocks) of its shape's launch, a multiple of the XCD count, so each block
+// also runs on the XCD it would run on alone.
 struct BatchItem {
   mtc_stream_desc d;
   const float* X;
@@ -694,23 +730,27 @@ struct BatchItem {
   uint32_t* counters;
   int64_t ldx;
   int64_t ldy;
-  int32_t start;        // first grid block of the item
-  int32_t lg;           // X rows gathered in LDS (gemv_lds_gather)
+  int32_t start;        // first block of the item in its shape's launch
+  int32_t lg;           // X rows gathered in LDS
 };
 
-// Members run blocks of the wave count their own launch would use (gemv_waves_for), so the
-// blocks of 8-wave members come first in the grid table and one launch runs them, then one
-// launch runs the 16-wave members' blocks (their items' `start` counts from that launch's
-// first block).
+// Shape classes of a batch, in the order of their blocks in the plan's block table:
+// 0: 4 waves, X staging of kSmallRows rows (LDS gather per member); 1: 4 waves, kMaxChunkRows
+// rows, no gather; 2: 16 waves, kMaxChunkRows rows (gather per member); 3: 8 waves (M tiles of
+// 4 rows), no gather.
+constexpr int kShapeClasses = 4;
+inline int shape_class(const GemvShape& s) { return s.nw == 8 ? 3 : s.nw == 16 ? 2 : s.kc == kSmallRows ? 0 : 1; }
+
 struct BatchHeader {
   uint32_t magic;
   uint32_t abi_version;
   int32_t n_items;
-  int32_t n_blocks;     // all blocks: n_blocks8 of 8 waves, then the rest of 16 waves
+  int32_t n_blocks;
   int32_t M;
   int32_t mt;           // rows per M tile
-  int32_t n_blocks8;
   int32_t fs;           // fp32 leaf scales
+  int32_t reserved;
+  int32_t class_blocks[kShapeClasses];
   uint64_t lds_bytes;
   uint64_t items_off;   // byte offset of the BatchItem array
   uint64_t block_item_off;
@@ -720,37 +760,46 @@ struct BatchHeader {
 };
 constexpr uint32_t kBatchMagic = 0x4D544342u;   // "BCTM"
 
-template <int MT, bool FS, int NW>
+template <int MT, bool FS, bool LG, int NW, int KC>
 __global__ __launch_bounds__(64 * NW, 4) void k_gemv_batch(const BatchItem* __restrict__ items,
                                                         const uint32_t* __restrict__ block_item, int M) {
   const int b = blockIdx.x;
   const BatchItem& it = items[block_item[b]];
-  gemv_block<MT, FS, (MT <= 2), NW>(it.d, b - it.start, it.X, it.ldx, it.Y, it.ldy, M, it.part, it.counters,
-                                    it.lg != 0);
+  gemv_block<MT, FS, LG, NW, KC>(it.d, b - it.start, it.X, it.ldx, it.Y, it.ldy, M, it.part, it.counters,
+                                 it.lg != 0);
 }
 
+// The batch kernel of a shape class (the LDS gather is a per-member flag there).
 template <int MT>
-const void* gemv_batch_kernel(bool fs, int nw) {
-  if (nw == 16)
-    return fs ? reinterpret_cast<const void*>(&k_gemv_batch<MT, true, 16>)
-              : reinterpret_cast<const void*>(&k_gemv_batch<MT, false, 16>);
-  return fs ? reinterpret_cast<const void*>(&k_gemv_batch<MT, true, 8>)
-            : reinterpret_cast<const void*>(&k_gemv_batch<MT, false, 8>);
+const void* gemv_batch_kernel(bool fs, int cls) {
+#define MTC_BATCH_K(LG_, NW_, KC_) \
+  (fs ? reinterpret_cast<const void*>(&k_gemv_batch<MT, true, LG_, NW_, KC_>) \
+      : reinterpret_cast<const void*>(&k_gemv_batch<MT, false, LG_, NW_, KC_>))
+  if constexpr (MT > 2) {
+    return MTC_BATCH_K(false, 8, kMaxChunkRows);
+  } else {
+    if (cls == 0) return MTC_BATCH_K(true, 4, kSmallRows);
+    if (cls == 1) return MTC_BATCH_K(false, 4, kMaxChunkRows);
+    return MTC_BATCH_K(true, 16, kMaxChunkRows);
+  }
+#undef MTC_BATCH_K
 }
 
-// The kernel instantiation for (M tile, scale format, LDS gather, waves).
+// The single-matrix (Group = false) or group kernel of an M tile, scale format and block shape.
 template <int MT, bool Group>
-const void* gemv_kernel(bool fs, bool lg, int nw) {
-  constexpr bool LG = MT <= 2;                        // the LDS gather exists for 1-2 row tiles only
-  constexpr int NW1 = gemv_waves(MT), NW2 = 8;
-#define MTC_GEMV_K(FS_, LG_, NW_) \
-  (Group ? reinterpret_cast<const void*>(&k_gemv_group<MT, FS_, LG_, NW_>) \
-         : reinterpret_cast<const void*>(&k_gemv<MT, FS_, LG_, NW_>))
-  if (nw == NW1)
-    return fs ? (lg ? MTC_GEMV_K(true, LG, NW1) : MTC_GEMV_K(true, false, NW1))
-              : (lg ? MTC_GEMV_K(false, LG, NW1) : MTC_GEMV_K(false, false, NW1));
-  return fs ? (lg ? MTC_GEMV_K(true, LG, NW2) : MTC_GEMV_K(true, false, NW2))
-            : (lg ? MTC_GEMV_K(false, LG, NW2) : MTC_GEMV_K(false, false, NW2));
+const void* gemv_kernel(bool fs, const GemvShape& s) {
+#define MTC_GEMV_K(LG_, NW_, KC_) \
+  (Group ? (fs ? reinterpret_cast<const void*>(&k_gemv_group<MT, true, LG_, NW_, KC_>) \
+               : reinterpret_cast<const void*>(&k_gemv_group<MT, false, LG_, NW_, KC_>)) \
+         : (fs ? reinterpret_cast<const void*>(&k_gemv<MT, true, LG_, NW_, KC_>) \
+               : reinterpret_cast<const void*>(&k_gemv<MT, false, LG_, NW_, KC_>)))
+  if constexpr (MT > 2) {
+    return MTC_GEMV_K(false, 8, kMaxChunkRows);
+  } else {
+    if (s.nw == 16) return s.lg ? MTC_GEMV_K(true, 16, kMaxChunkRows) : MTC_GEMV_K(false, 16, kMaxChunkRows);
+    if (s.kc == kSmallRows) return s.lg ? MTC_GEMV_K(true, 4, kSmallRows) : MTC_GEMV_K(false, 4, kSmallRows);
+    return MTC_GEMV_K(false, 4, kMaxChunkRows);
+  }
 #undef MTC_GEMV_K
 }
 
@@ -836,9 +885,8 @@ int launch_gemv(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y,
     return fail(MTC_E_SHAPE, "fp32 path: %d rows x chunk_rows=%d needs %zu B of LDS (limit %zu); "
                 "use a stream with smaller chunk_rows", MT, d->chunk_rows, shmem, limit);
   const bool fs = d->leaf_scale != nullptr;
-  const bool lg = gemv_lds_gather(MT, d->row_perm != nullptr, d->K);
-  const int nw = gemv_waves_for(MT, d->fixed_steps);
-  const void* kern = gemv_kernel<MT, false>(fs, lg, nw);
+  const GemvShape shape = gemv_shape(MT, d);
+  const void* kern = gemv_kernel<MT, false>(fs, shape);
   if (shmem > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
     if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
@@ -846,33 +894,29 @@ int launch_gemv(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y,
   const int n_units = d->n_panels * d->n_chunks;
   const int units_padded = (n_units + kXcds - 1) / kXcds * kXcds;
   dim3 grid(units_padded * kGemvBlocksPerUnit, (M + MT - 1) / MT);
-  const dim3 block(64 * nw);
+  const dim3 block(64 * shape.nw);
   void* args[] = {const_cast<mtc_stream_desc*>(d), &X, &ldx, &Y, &ldy, &M, &part, &counters};
   const hipError_t e = hipLaunchKernel(kern, grid, block, args, shmem, st);
   if (e != hipSuccess) return fail(MTC_E_LAUNCH, "k_gemv launch: %s", hipGetErrorString(e));
   return check_launch("k_gemv");
 }
 
+// One launch for group members of one block shape (g holds only those members).
 template <int MT>
-int launch_gemv_group(const GemvGroup& g, int n, const float* X, int64_t ldx, int M, hipStream_t st) {
+int launch_gemv_group(const GemvGroup& g, int n, const GemvShape& shape, const float* X, int64_t ldx, int M,
+                      hipStream_t st) {
   size_t shmem = 0;
   for (int i = 0; i < n; ++i) shmem = std::max(shmem, gemv_lds_bytes(&g.d[i], MT));
   const size_t limit = device_lds_limit();
   if (shmem > limit)
     return fail(MTC_E_SHAPE, "fp32 group: %d rows need %zu B of LDS (limit %zu)", MT, shmem, limit);
-  const mtc_stream_desc* d = &g.d[0];
-  const bool fs = d->leaf_scale != nullptr;
-  const bool lg = gemv_lds_gather(MT, d->row_perm != nullptr, d->K);
-  int max_fixed = 0;
-  for (int i = 0; i < n; ++i) max_fixed = std::max(max_fixed, g.d[i].fixed_steps);
-  const int nw = gemv_waves_for(MT, max_fixed);
-  const void* kern = gemv_kernel<MT, true>(fs, lg, nw);
+  const void* kern = gemv_kernel<MT, true>(g.d[0].leaf_scale != nullptr, shape);
   if (shmem > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
     if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
   }
   dim3 grid(g.start[n], (M + MT - 1) / MT);
-  const dim3 block(64 * nw);
+  const dim3 block(64 * shape.nw);
   void* args[] = {const_cast<GemvGroup*>(&g), &X, &ldx, &M};
   const hipError_t e = hipLaunchKernel(kern, grid, block, args, shmem, st);
   if (e != hipSuccess) return fail(MTC_E_LAUNCH, "k_gemv_group launch: %s", hipGetErrorString(e));
@@ -891,7 +935,7 @@ int build_batch_plan(const mtc_gemv_batch_item* items, int n, int M, void* works
   const int mt = gemv_mt(M);
   bool fs = false;
   size_t ws = 0, lds = 0;
-  int64_t blocks = 0, blocks8 = 0;
+  int64_t blocks = 0, class_blocks[kShapeClasses] = {0, 0, 0, 0};
   for (int i = 0; i < n; ++i) {
     const mtc_stream_desc* d = items[i].desc;
     int rc = check_desc(d);
@@ -912,7 +956,7 @@ int build_batch_plan(const mtc_gemv_batch_item* items, int n, int M, void* works
     ws += align_up(gemv_ws_layout(d, M, nullptr), 256);
     const int64_t nb = (int64_t)(d->n_panels * d->n_chunks + kXcds - 1) / kXcds * kXcds * kGemvBlocksPerUnit;
     blocks += nb;
-    if (gemv_waves_for(mt, d->fixed_steps) == 8) blocks8 += nb;
+    class_blocks[shape_class(gemv_shape(mt, d))] += nb;
   }
   if (blocks > (1 << 30)) return fail(MTC_E_SHAPE, "batch of %lld blocks", (long long)blocks);
   const size_t items_off = align_up(sizeof(BatchHeader), 64);
@@ -938,7 +982,7 @@ int build_batch_plan(const mtc_gemv_batch_item* items, int n, int M, void* works
   h->n_blocks = (int32_t)blocks;
   h->M = M;
   h->mt = mt;
-  h->n_blocks8 = (int32_t)blocks8;
+  for (int c = 0; c < kShapeClasses; ++c) h->class_blocks[c] = (int32_t)class_blocks[c];
   h->fs = fs;
   h->lds_bytes = lds;
   h->items_off = items_off;
@@ -947,7 +991,9 @@ int build_batch_plan(const mtc_gemv_batch_item* items, int n, int M, void* works
   h->ws_bytes = ws;
   h->workspace = workspace;
   char* wsp = reinterpret_cast<char*>(workspace);
-  int start8 = 0, start16 = 0;                        // next block of each launch
+  int start[kShapeClasses] = {0, 0, 0, 0};            // next block of each shape's launch
+  int64_t table_off[kShapeClasses] = {0, 0, 0, 0};    // first table entry of each shape's launch
+  for (int c = 1; c < kShapeClasses; ++c) table_off[c] = table_off[c - 1] + class_blocks[c - 1];
   for (int i = 0; i < n; ++i) {
     const mtc_stream_desc* d = items[i].desc;
     it[i].d = *d;
@@ -955,7 +1001,9 @@ int build_batch_plan(const mtc_gemv_batch_item* items, int n, int M, void* works
     it[i].Y = items[i].Y;
     it[i].ldx = items[i].ldx;
     it[i].ldy = items[i].ldy;
-    it[i].lg = gemv_lds_gather(mt, d->row_perm != nullptr, d->K);
+    const GemvShape shape = gemv_shape(mt, d);
+    const int cls = shape_class(shape);
+    it[i].lg = shape.lg;
     size_t cb = 0;
     const size_t wsi = gemv_ws_layout(d, M, &cb);
     if (wsi) {
@@ -964,12 +1012,10 @@ int build_batch_plan(const mtc_gemv_batch_item* items, int n, int M, void* works
       wsp += align_up(wsi, 256);
     }
     const int nb = (d->n_panels * d->n_chunks + kXcds - 1) / kXcds * kXcds * kGemvBlocksPerUnit;
-    const bool w8 = gemv_waves_for(mt, d->fixed_steps) == 8;
-    int& start = w8 ? start8 : start16;
-    uint32_t* table = block_item + (w8 ? 0 : blocks8);
-    it[i].start = start;
-    for (int b = 0; b < nb; ++b) table[start + b] = (uint32_t)i;
-    start += nb;
+    uint32_t* table = block_item + table_off[cls];
+    it[i].start = start[cls];
+    for (int b = 0; b < nb; ++b) table[start[cls] + b] = (uint32_t)i;
+    start[cls] += nb;
   }
   return ok();
 }
@@ -985,17 +1031,20 @@ int launch_gemv_batch(const void* host_plan, const void* device_plan, hipStream_
   const uint32_t* block_item = reinterpret_cast<const uint32_t*>(dp + h->block_item_off);
   int M = h->M;
   const size_t shmem = h->lds_bytes;
-  for (int nw : {8, 16}) {                            // the 8-wave members' blocks, then the 16-wave ones
-    const int nblk = nw == 8 ? h->n_blocks8 : h->n_blocks - h->n_blocks8;
+  int64_t first = 0;
+  for (int cls = 0; cls < kShapeClasses; ++cls) {      // one launch per block shape present
+    const int nblk = h->class_blocks[cls];
+    const uint32_t* table = block_item + first;
+    first += nblk;
     if (nblk == 0) continue;
-    const void* kern = h->mt == 1 ? gemv_batch_kernel<1>(h->fs, nw)
-                     : h->mt == 2 ? gemv_batch_kernel<2>(h->fs, nw)
-                                  : gemv_batch_kernel<4>(h->fs, 8);
+    const int nw = cls == 3 ? 8 : cls == 2 ? 16 : 4;
+    const void* kern = h->mt == 1 ? gemv_batch_kernel<1>(h->fs, cls)
+                     : h->mt == 2 ? gemv_batch_kernel<2>(h->fs, cls)
+                                  : gemv_batch_kernel<4>(h->fs, cls);
     if (shmem > 64 * 1024) {
       hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
       if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
     }
-    const uint32_t* table = block_item + (nw == 8 ? 0 : h->n_blocks8);
     dim3 grid(nblk, (M + h->mt - 1) / h->mt);
     const dim3 block(64 * nw);
     void* args[] = {&items, &table, &M};
@@ -1074,9 +1123,6 @@ MTC_API int mtc_gemv_f32_group(const mtc_stream_desc* const* descs, int n, const
   if (n < 1 || n > kMaxGroup) return fail(MTC_E_SHAPE, "group of %d matrices (1..%d)", n, kMaxGroup);
   if (!X) return fail(MTC_E_NULL, "X is NULL");
   if (M <= 0) return fail(MTC_E_SHAPE, "M=%d must be positive", M);
-  GemvGroup g;
-  memset(&g, 0, sizeof(g));
-  int blocks = 0;
   for (int i = 0; i < n; ++i) {
     const mtc_stream_desc* d = descs[i];
     int rc = check_desc(d);
@@ -1090,21 +1136,39 @@ MTC_API int mtc_gemv_f32_group(const mtc_stream_desc* const* descs, int n, const
       return fail(MTC_E_SHAPE, "group member %d differs from member 0 in scale format or row permutation", i);
     if (ldx < d->K || ldy[i] < d->N)
       return fail(MTC_E_SHAPE, "ldx=%lld < K or ldy[%d]=%lld < N", (long long)ldx, i, (long long)ldy[i]);
-    g.d[i] = *d;
-    g.Y[i] = Y[i];
-    g.ldy[i] = ldy[i];
-    g.start[i] = blocks;
-    const int units_padded = (d->n_panels + kXcds - 1) / kXcds * kXcds;
-    blocks += units_padded * kGemvBlocksPerUnit;
   }
-  for (int i = n; i <= kMaxGroup; ++i) g.start[i] = blocks;
   if ((M - 1) > (INT64_MAX / ldx)) return fail(MTC_E_SHAPE, "M * ldx overflows");
   hipStream_t st = as_stream(hip_stream);
-  switch (gemv_mt(M)) {
-    case 1: return launch_gemv_group<1>(g, n, X, ldx, M, st);
-    case 2: return launch_gemv_group<2>(g, n, X, ldx, M, st);
-    default: return launch_gemv_group<4>(g, n, X, ldx, M, st);
+  const int mt = gemv_mt(M);
+  // one launch per block shape among the members (usually one), so that every member's blocks
+  // run the code of its own launch
+  for (int cls = 0; cls < kShapeClasses; ++cls) {
+    GemvGroup g;
+    memset(&g, 0, sizeof(g));
+    GemvShape shape{};
+    int m = 0, blocks = 0;
+    for (int i = 0; i < n; ++i) {
+      const GemvShape si = gemv_shape(mt, descs[i]);
+      if (shape_class(si) != cls) continue;
+      shape = si;
+      g.d[m] = *descs[i];
+      g.Y[m] = Y[i];
+      g.ldy[m] = ldy[i];
+      g.start[m] = blocks;
+      blocks += (descs[i]->n_panels + kXcds - 1) / kXcds * kXcds * kGemvBlocksPerUnit;
+      ++m;
+    }
+    if (m == 0) continue;
+    for (int i = m; i <= kMaxGroup; ++i) g.start[i] = blocks;
+    int rc;
+    switch (mt) {
+      case 1: rc = launch_gemv_group<1>(g, m, shape, X, ldx, M, st); break;
+      case 2: rc = launch_gemv_group<2>(g, m, shape, X, ldx, M, st); break;
+      default: rc = launch_gemv_group<4>(g, m, shape, X, ldx, M, st); break;
+    }
+    if (rc) return rc;
   }
+  return ok();
 }
 
 // ---------------------------------------------------------------------------
