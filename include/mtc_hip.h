@@ -156,6 +156,20 @@ size_t mtc_gemv_workspace_bytes(const mtc_stream_desc* d, int M);
 int mtc_gemv_f32(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y, int64_t ldy, int M,
                  void* workspace, size_t workspace_bytes, void* hip_stream);
 
+/* mtc_gemv_f32 for callers that cannot allocate (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc). No counterpart in the reference. It takes no
+ * workspace: the split-K partials and counters of a stream with several row chunks live in
+ * a static per-device array of MTC_NOALLOC_SCRATCH_BYTES that the library holds until the
+ * process ends; a call that needs more fails with MTC_E_WORKSPACE before any launch. The
+ * call allocates nothing and clears the counters itself (a small fill kernel on hip_stream
+ * before the decode kernel). Every call on one GPU shares that GPU's array: calls that
+ * overlap in time on one GPU (two streams, or two threads) race. Y equals, bit for bit, what
+ * mtc_gemv_f32 writes. */
+#define MTC_NOALLOC_SCRATCH_BYTES (8u << 20)
+size_t mtc_gemv_noalloc_scratch_bytes(void);
+int mtc_gemv_f32_noalloc(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y, int64_t ldy, int M,
+                         void* hip_stream);
+
 /* fp32 path for n (1..MTC_MAX_GROUP) matrices that read the same X, in one launch:
  * Y[i] (M x N_i, leading dim ldy[i]) = X (M x K, leading dim ldx) * W_hat_i.
  * Every stream must have a single row chunk (n_chunks == 1, so no workspace), the

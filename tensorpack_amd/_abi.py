@@ -17,7 +17,7 @@ ERROR_NAMES = {
 EXPORTED = ("mtc_abi_version", "mtc_last_error", "mtc_check_desc", "mtc_dequant", "mtc_gemv_lds_bytes",
             "mtc_gemv_workspace_bytes", "mtc_gemv_f32", "mtc_gemv_f32_group", "mtc_check_tile_desc", "mtc_gemm_workspace_bytes",
             "mtc_gemm_bf16", "mtc_gemm_group_workspace_bytes", "mtc_gemm_bf16_group", "mtc_gemv_batch_plan",
-            "mtc_gemv_f32_batch")
+            "mtc_gemv_f32_batch", "mtc_gemv_noalloc_scratch_bytes", "mtc_gemv_f32_noalloc")
 
 
 class MtcStreamDesc(ctypes.Structure):
@@ -103,6 +103,10 @@ def declare(lib: ctypes.CDLL) -> None:
     lib.mtc_gemv_f32_group.restype = i32
     lib.mtc_gemv_f32_group.argtypes = [ctypes.POINTER(DescP), i32, vp, i64, ctypes.POINTER(vp),
                                        ctypes.POINTER(i64), i32, vp]
+    lib.mtc_gemv_noalloc_scratch_bytes.restype = sz
+    lib.mtc_gemv_noalloc_scratch_bytes.argtypes = []
+    lib.mtc_gemv_f32_noalloc.restype = i32
+    lib.mtc_gemv_f32_noalloc.argtypes = [DescP, vp, i64, vp, i64, i32, vp]
     lib.mtc_gemv_batch_plan.restype = i32
     lib.mtc_gemv_batch_plan.argtypes = [ctypes.POINTER(MtcGemvBatchItem), i32, i32, vp, sz, vp, sz,
                                         ctypes.POINTER(sz), ctypes.POINTER(sz)]

@@ -22,6 +22,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "mtc_hip.h"
 #include "mtc_decode.h"
@@ -1114,6 +1115,73 @@ MTC_API int mtc_gemv_f32(const mtc_stream_desc* d, const float* X, int64_t ldx, 
     case 1: return launch_gemv<1>(d, X, ldx, Y, ldy, M, workspace, st);
     case 2: return launch_gemv<2>(d, X, ldx, Y, ldy, M, workspace, st);
     default: return launch_gemv<4>(d, X, ldx, Y, ldy, M, workspace, st);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// decode without a caller workspace: split-K partials and counters in a static per-device array
+// ---------------------------------------------------------------------------
+namespace {
+constexpr size_t kScratchBytes = MTC_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+// In host code `scratch` names a host-side stand-in: kernels and copies get the device address
+// from scratch_address() instead.
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices] = {};
+
+// The address of the current device's `scratch`, looked up once per device (with that device
+// current) and kept.
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(MTC_E_LAUNCH, "device %d beyond the %d this library tracks", dev,
+                                                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return fail(MTC_E_LAUNCH, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *out = g_scratch_addr[dev];
+  return MTC_OK;
+}
+}  // namespace
+
+MTC_API size_t mtc_gemv_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+MTC_API int mtc_gemv_f32_noalloc(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y, int64_t ldy, int M,
+                                 void* hip_stream) {
+  int rc = check_desc(d);
+  if (rc) return rc;
+  if (!X || !Y) return fail(MTC_E_NULL, "X or Y is NULL");
+  if (M <= 0) return fail(MTC_E_SHAPE, "M=%d must be positive", M);
+  if (ldx < d->K || ldy < d->N) return fail(MTC_E_SHAPE, "ldx=%lld < K or ldy=%lld < N", (long long)ldx, (long long)ldy);
+  if ((M - 1) > (INT64_MAX / ldx)) return fail(MTC_E_SHAPE, "M * ldx overflows");
+  size_t counter_bytes = 0;
+  const size_t need = gemv_ws_layout(d, M, &counter_bytes);
+  if (need > kScratchBytes)
+    return fail(MTC_E_WORKSPACE, "M=%d over %d row chunks needs %zu bytes of split-K scratch; the static scratch "
+                "holds %zu (use mtc_gemv_f32 with a workspace)", M, d->n_chunks, need, kScratchBytes);
+  hipStream_t st = as_stream(hip_stream);
+  void* ws = nullptr;
+  if (need) {
+    rc = scratch_address(&ws);
+    if (rc) return rc;
+    // the counters start at zero (a fill kernel: no memset node if the caller captures this)
+    const int64_t words = (int64_t)(counter_bytes / sizeof(float));
+    hipLaunchKernelGGL(k_fill_zero, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st,
+                       reinterpret_cast<float*>(ws), words);
+    rc = check_launch("k_fill_zero");
+    if (rc) return rc;
+  }
+  switch (gemv_mt(M)) {
+    case 1: return launch_gemv<1>(d, X, ldx, Y, ldy, M, ws, st);
+    case 2: return launch_gemv<2>(d, X, ldx, Y, ldy, M, ws, st);
+    default: return launch_gemv<4>(d, X, ldx, Y, ldy, M, ws, st);
   }
 }
 

@@ -278,3 +278,18 @@ def test_batch_plan_sizes_and_errors(hip):
     assert hip.mtc_gemv_f32_batch(None, None, None) == -1
     bogus = np.zeros(256, np.uint8)
     assert hip.mtc_gemv_f32_batch(bogus.ctypes.data, 0x40000, None) == -2
+
+
+def test_noalloc_entry_rejects_before_any_gpu_call(hip):
+    """mtc_gemv_f32_noalloc checks arguments and the static scratch bound on the host."""
+    d = _desc()                                                  # 2 row chunks: needs split-K scratch
+    ref = ctypes.byref(d)
+    cap = hip.mtc_gemv_noalloc_scratch_bytes()
+    assert cap == 8 << 20
+    assert hip.mtc_gemv_f32_noalloc(ref, None, 256, 0x10, 64, 1, None) == -1
+    assert hip.mtc_gemv_f32_noalloc(ref, 0x10, 256, 0x10, 64, 0, None) == -3
+    assert hip.mtc_gemv_f32_noalloc(ref, 0x10, 100, 0x10, 64, 1, None) == -3
+    M = 1 << 16                                                  # partials far beyond the scratch
+    assert hip.mtc_gemv_workspace_bytes(ref, M) > cap
+    assert hip.mtc_gemv_f32_noalloc(ref, 0x10, 256, 0x10, 64, M, None) == -5
+    assert b"scratch" in hip.mtc_last_error()
