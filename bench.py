@@ -10,12 +10,16 @@ rotate so the weight is read from HBM, not the 256 MB Infinity Cache. The K
 timed calls are replayed from a HIP graph (launch-bound decode loops are
 graph-captured in serving too) between a synchronize on both sides.
 
-Also reported in the same JSON line: M = 16 on c2 (fp32-VALU bound) and the
-prefill kernel (bf16 MFMA) on c4 (8192 x 8192, QuadtreeRD @ 4.5, M = 4096),
-and the CPU baseline (C/OpenMP port of the reference block loop) on a bounded
-sample of the c2 M = 1 workload.
+Also reported in the same JSON line (`extra`), each with its own roofline object:
+M = 16 on c2; the prefill kernel (bf16 MFMA) on c4 (8192 x 8192, QuadtreeRD @
+4.5, M = 4096), its output checked on 64 sampled rows against the fp64 product;
+the 168-matrix c3 stack at M = 1 (one batched launch per pass) and M = 512; the
+adversarial c5 mix at M = 1 and M = 256. CPU baselines (C/OpenMP port of the
+reference block loop) run on bounded samples of c2, c3 and c5. All allocations
+(the c3 stack through forked worker processes) and the rocprofv3 counter passes
+run before this process initialises the GPU.
 
-    python bench.py [--steps K] [--warmup W] [--no-prefill] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--workload all|c2|c3|c5] [--no-cpu-baseline]
 """
 
 import argparse
@@ -53,10 +57,13 @@ def parse():
     ap.add_argument("--graph", type=int, default=1, help="replay the timed calls from a HIP graph")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH_SIZE/WRITE_SIZE passes")
     ap.add_argument("--pmc-child", help=argparse.SUPPRESS)
-    ap.add_argument("--workload", default="c2", choices=["c2", "c3", "c5"],
-                    help="c2 (default): the headline decode + c4 prefill run; c3: the 24-layer decoder "
-                         "stack (168 matrices) at M=1 and M=512; c5: the adversarial leaf mix at M=1 and M=256")
+    ap.add_argument("--workload", default="all", choices=["all", "c2", "c3", "c5"],
+                    help="all (default): the headline c2 decode plus c4 prefill, the c3 stack and c5; c2: c2 and "
+                         "c4 only; c3: the 24-layer decoder stack (168 matrices) at M=1 and M=512 with per-launch "
+                         "comparisons; c5: the adversarial leaf mix at M=1 and M=256")
     ap.add_argument("--c3-layers", type=int, default=24)
+    ap.add_argument("--no-c3", action="store_true")
+    ap.add_argument("--no-c5", action="store_true")
     return ap.parse_args()
 
 
@@ -210,85 +217,186 @@ def time_replays(torch, g, reps, warmup=2):
     return start.elapsed_time(stop) / reps          # ms per replay
 
 
-def run_c3(args):
-    """Qwen2.5-0.5B-shaped stack: 24 layers x (q, k, v, o, gate, up, down), QT-P @ 3.125 b/w
-    each; all 168 matrices back to back at M=1 (fp32 decode kernel) and at M=512 (bf16 MFMA
-    prefill), each pass captured as one HIP graph. At M=1 the pass runs once with one launch
-    per matrix and once with the matrices that read the same input grouped (q/k/v, gate/up:
-    4 launches per layer); the grouped pass is the reported value."""
+def rotating(stream, n_bytes_target):
+    """The stream plus clones of it totalling at least n_bytes_target device bytes, so that
+    timed calls cycling over them read the weight from HBM, not from the 256 MB MALL."""
+    n = max(1, int(np.ceil(n_bytes_target / stream.device_bytes())))
+    return [stream] + [stream.clone() for _ in range(n - 1)]
+
+
+def rel_frobenius(ref, got):
+    ref = np.asarray(ref, np.float64)
+    d = np.linalg.norm(ref - np.asarray(got, np.float64))
+    n = np.linalg.norm(ref)
+    return float(d if n < 1e-12 else d / n)
+
+
+def cpu_port_gbs(las, xs, packed_bytes, seconds, what):
+    """C/OpenMP port of the reference block loop (gemm.py:124-210) over the listed matrices,
+    timed on this host for about `seconds`: packed-weight GB/s and the sample it ran."""
+    from oracle import mtc_oracle as O
+    for la, x in zip(las, xs):
+        O.cpu_qt_gemm(x, la)
+    passes, t0 = 0, time.time()
+    while True:
+        for la, x in zip(las, xs):
+            O.cpu_qt_gemm(x, la)
+        passes += 1
+        if time.time() - t0 >= seconds and passes >= 3:
+            break
+    el = time.time() - t0
+    return {"value": packed_bytes * passes / el / 1e9, "unit": "GB/s", "cores": int(O.cpu_lib().oracle_threads()),
+            "kind": "port", "sample": f"{passes} passes of {what} in {el:.1f}s, C/OpenMP port of the reference "
+                                      f"block loop (gemm.py:124-210)"}
+
+
+def leaf_arena(alloc, W):
+    """The oracle's leaf list of an allocation (CPU baseline input)."""
+    from oracle import mtc_oracle as O
+    if hasattr(alloc, "inner"):
+        i = alloc.inner
+        return O.LeafArena(i.weights, i.sizes, i.leaf, i.modes, i.scales, alloc.row_perm, alloc.col_perm)
+    return O.LeafArena(W, alloc.sizes, alloc.leaf, alloc.modes, alloc.scales)
+
+
+# ----------------------------------------------------------------------------------------------
+# c2: the headline decode (M = 1), and M = 16
+# ----------------------------------------------------------------------------------------------
+def bench_c2(args, wl, alloc, traffic, dev):
+    import torch
+    from tensorpack_amd.kernels.gemm import MTCMatrix
+    m = MTCMatrix.from_quadtree(alloc, wl.W)
+    t0 = time.time()
+    ds = m.device_stream()
+    log(f"c2 packed in {time.time() - t0:.1f}s: chunk_rows={ds.host.chunk_rows} stream {ds.device_bytes()} B, "
+        f"accounted {m.packed_bytes:.0f} B")
+    packed = m.packed_bytes
+    copies = rotating(ds, args.rotate_gib * (1 << 30))
+    X1 = torch.from_numpy(wl.activations(1)).to(dev)
+    Y1 = torch.empty((1, wl.W.shape[1]), dtype=torch.float32, device=dev)
+    for c in copies:
+        c.workspace(1)
+        c.gemv_f32(X1, out=Y1)
+    torch.cuda.synchronize()
+    secs, ms = timed_calls(torch, [lambda c=c: c.gemv_f32(X1, out=Y1) for c in copies], args.steps, args.warmup,
+                           bool(args.graph))
+    gbs = packed / (ms * 1e-3) / 1e9
+    log(f"c2 M=1: {ms * 1e3:.2f} us/call, {gbs:.1f} GB/s packed ({len(copies)} copies)")
+    res = {"m": m, "ds": ds, "packed": packed, "ms": ms, "gbs": gbs, "n_copies": len(copies),
+           "y": Y1.cpu().numpy().copy(), "x": wl.activations(1)}
+    del copies
+    if not args.no_m16:
+        d16 = m.device_stream(None, dev, 16)
+        c16 = rotating(d16, args.rotate_gib * (1 << 30))
+        X16 = torch.from_numpy(wl.activations(16)).to(dev)
+        Y16 = torch.empty((16, wl.W.shape[1]), dtype=torch.float32, device=dev)
+        for c in c16:
+            c.workspace(16)
+            c.gemv_f32(X16, out=Y16)
+        torch.cuda.synchronize()
+        s16, ms16 = timed_calls(torch, [lambda c=c: c.gemv_f32(X16, out=Y16) for c in c16],
+                                max(args.steps // 4, len(c16)), args.warmup // 4, bool(args.graph))
+        flop16 = 2.0 * 16 * wl.W.shape[0] * wl.W.shape[1]
+        tf = flop16 / (ms16 * 1e-3) / 1e12
+        res["m16"] = {"us_per_call": ms16 * 1e3, "packed_GBps": packed / (ms16 * 1e-3) / 1e9, "TFLOPs": tf,
+                      "frac_fp32_peak": tf / FP32_PEAK_TFLOPS, "chunk_rows": d16.host.chunk_rows,
+                      "roofline": {"bound": "fp32", "achieved": tf, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                   "frac": tf / FP32_PEAK_TFLOPS, "traffic": None}}
+        log(f"c2 M=16: {ms16 * 1e3:.2f} us/call, {tf:.2f} TFLOP/s")
+        del c16
+    return res
+
+
+def device_copy_rates(dev, packed):
+    """A plain 1 GiB device copy (achievable HBM bandwidth) and graph-replayed copies of the
+    packed weight's size (what one launch of that size reaches on the copy path)."""
+    import torch
+    src = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    copy_gbs = 2 * src.numel() * 4 * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del src, dst
+    n_el = int(packed) // 4
+    n_rot = max(2, (1 << 30) // (2 * 4 * n_el))
+    srcs = [torch.empty(n_el, dtype=torch.float32, device=dev) for _ in range(n_rot)]
+    dsts = [torch.empty_like(s) for s in srcs]
+    g = graph_of(torch, [lambda s=s, d=d: d.copy_(s) for s, d in zip(srcs, dsts)])
+    small_us = time_replays(torch, g, 5) * 1e3 / n_rot
+    log(f"device copy: {copy_gbs:.0f} GB/s (read + write); copy of {4 * n_el} B: {small_us:.2f} us")
+    return copy_gbs, small_us
+
+
+# ----------------------------------------------------------------------------------------------
+# c4: prefill (bf16 MFMA), with its own output checked against a fp64 product
+# ----------------------------------------------------------------------------------------------
+def bench_c4(args, wl4, a4, dev):
+    import torch
+    from tensorpack_amd.kernels.gemm import MTCMatrix
+    m4 = MTCMatrix.from_quadtree(a4, wl4.W)
+    g4 = m4.device_tiles(dev)
+    M4 = 4096
+    X4 = torch.from_numpy(wl4.activations(M4)).to(dev).to(torch.bfloat16)
+    Y4 = torch.empty((M4, wl4.W.shape[1]), dtype=torch.float32, device=dev)
+    g4.gemm_bf16(X4, out=Y4)
+    torch.cuda.synchronize()
+    s4, ms4 = timed_calls(torch, [lambda: g4.gemm_bf16(X4, out=Y4)], args.prefill_steps, args.prefill_warmup, False)
+    flop4 = 2.0 * M4 * wl4.W.shape[0] * wl4.W.shape[1]
+    tf = flop4 / (ms4 * 1e-3) / 1e12
+    # the timed output: 4 rows of every 256-row tile, all 8192 columns (every column tile), against
+    # the fp64 product of the same bf16 X and the allocator's W_hat
+    rng = np.random.RandomState(4242)
+    rows = np.concatenate([rt * 256 + np.r_[0, 255, rng.choice(np.arange(1, 255), 2, replace=False)]
+                           for rt in range((M4 + 255) // 256)])
+    idx = torch.from_numpy(rows).to(dev)
+    Xs = X4[idx].float().cpu().numpy().astype(np.float64)
+    ref = Xs @ np.asarray(a4.dequant, np.float64)
+    rel = rel_frobenius(ref, Y4[idx].cpu().numpy())
+    log(f"c4 M=4096: {ms4:.3f} ms/call, {tf:.1f} TFLOP/s ({100 * tf / BF16_PEAK_TFLOPS:.1f}% of bf16 peak); "
+        f"{rows.size} sampled rows vs fp64: rel {rel:.2e}")
+    if not rel < 2e-3:
+        raise SystemExit(f"c4 prefill output differs from the fp64 product: rel {rel:.3e} >= 2e-3")
+    return {"M": M4, "ms_per_call": ms4, "TFLOPs": tf, "frac_bf16_peak": tf / BF16_PEAK_TFLOPS,
+            "packed_bytes": m4.packed_bytes,
+            "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": tf / BF16_PEAK_TFLOPS, "traffic": None, "kernel": "k_gemm_tile"},
+            "parity": {"rows": int(rows.size), "rel_frobenius_vs_fp64": rel, "tolerance": 2e-3}}
+
+
+# ----------------------------------------------------------------------------------------------
+# c3: the 168-matrix Qwen2.5-0.5B-shaped stack
+# ----------------------------------------------------------------------------------------------
+def bench_c3(args, mats, allocs, dev, detail=False):
+    """M = 1: all 168 matrices (each its own X and Y) in one batched launch per pass, over rotating
+    copies of the stack; M = 512: the prefill of every matrix, the q/k/v and gate/up groups sharing
+    their input (12 launches per layer), one HIP graph per pass. With `detail`, also the M = 1 pass
+    as one launch per matrix and as 96 grouped launches."""
     import torch
     from tensorpack_amd import workloads
+    from tensorpack_amd.device import GemvBatch, gemm_bf16_group, gemv_f32_group
     from tensorpack_amd.kernels.gemm import MTCMatrix
-    from tensorpack_amd.device import require_gpu
-    mats = workloads.c3_matrices(args.c3_layers)
-    t0 = time.time()
-    allocs = workloads.allocate_many(mats)
-    log(f"c3: {len(mats)} allocations in {time.time() - t0:.1f}s")
-    dev = require_gpu()
-    torch.cuda.set_device(dev)
     ms_ = [MTCMatrix.from_quadtree(a, w.W) for a, w in zip(allocs, mats)]
     packed = float(sum(m.packed_bytes for m in ms_))
     weights = sum(w.W.size for w in mats)
     xs = {}
+
     def x_of(K, M, dtype):
         key = (K, M, dtype)
         if key not in xs:
             xs[key] = torch.from_numpy(np.random.RandomState(3000 + K + M).randn(M, K).astype(np.float32)).to(dev).to(dtype)
         return xs[key]
-    # M = 1: each pass runs every matrix once; whole copies of the stack rotate so the weights come from HBM
-    streams = [m.device_stream() for m in ms_]
-    ys1 = [torch.empty((1, w.W.shape[1]), dtype=torch.float32, device=dev) for w in mats]
-    for s_, w, y in zip(streams, mats, ys1):
-        s_.workspace(1)
-        s_.gemv_f32(x_of(w.W.shape[0], 1, torch.float32), out=y)
-    torch.cuda.synchronize()
-    n_rot = max(1, int(np.ceil(args.rotate_gib * (1 << 30) / sum(s_.device_bytes() for s_ in streams))))
+
+    streams = [m.device_stream(None, dev, 1) for m in ms_]
+    stack_bytes = sum(s_.device_bytes() for s_ in streams)
+    n_rot = max(1, int(np.ceil(args.rotate_gib * (1 << 30) / stack_bytes)))
     sets = [streams] + [[s_.clone() for s_ in streams] for _ in range(n_rot - 1)]
-    for ss in sets[1:]:                              # workspaces exist before capture
-        for s_, w, y in zip(ss, mats, ys1):
-            s_.workspace(1)
-            s_.gemv_f32(x_of(w.W.shape[0], 1, torch.float32), out=y)
-    torch.cuda.synchronize()
-    from tensorpack_amd.device import gemv_f32_group
-
-    def time_m1(plan):
-        """Per rotating set, one graph of the pass; plan = list of index groups (one launch each)."""
-        def calls(ss):
-            out = []
-            for grp in plan:
-                if len(grp) == 1:
-                    i = grp[0]
-                    out.append(lambda s_=ss[i], w=mats[i], y=ys1[i]: s_.gemv_f32(x_of(w.W.shape[0], 1, torch.float32), out=y))
-                else:
-                    out.append(lambda g=[ss[i] for i in grp], K=mats[grp[0]].W.shape[0], ys=[ys1[i] for i in grp]:
-                               gemv_f32_group(g, x_of(K, 1, torch.float32), ys))
-            return out
-        graphs = [graph_of(torch, calls(ss)) for ss in sets]
-        for g in graphs:
-            g.replay()
-        torch.cuda.synchronize()
-        reps = max(2, 40 // len(graphs))
-        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(reps):
-            for g in graphs:
-                g.replay()
-        stop.record()
-        torch.cuda.synchronize()
-        return start.elapsed_time(stop) / (reps * len(graphs))
-
-    n_per = len(workloads.QWEN_LAYER)
-    # q, k, v read the layer input; gate and up read the post-attention input: one launch each
-    layer_groups = [[0, 1, 2], [3], [4, 5], [6]]
-    plan_grouped = [[L * n_per + i for i in grp] for L in range(args.c3_layers) for grp in layer_groups]
-    ms1_single = time_m1([[i] for i in range(len(mats))])
-    log(f"c3 M=1, one launch per matrix: {ms1_single * 1e3:.1f} us per pass of {len(mats)} matrices, "
-        f"{packed / (ms1_single * 1e-3) / 1e9:.1f} GB/s packed")
-    ms1_grouped = time_m1(plan_grouped)
-    log(f"c3 M=1, grouped ({len(plan_grouped)} launches): {ms1_grouped * 1e3:.1f} us per pass, "
-        f"{packed / (ms1_grouped * 1e-3) / 1e9:.1f} GB/s packed")
-    # the whole pass as ONE batched launch per rotating set (each matrix its own X and Y)
-    from tensorpack_amd.device import GemvBatch
+    ys1 = [torch.empty((1, w.W.shape[1]), dtype=torch.float32, device=dev) for w in mats]
     batches = [GemvBatch(ss, [x_of(w.W.shape[0], 1, torch.float32) for w in mats], ys1) for ss in sets]
     for b in batches:
         b.launch()
@@ -302,102 +410,143 @@ def run_c3(args):
     stop.record()
     torch.cuda.synchronize()
     ms1 = start.elapsed_time(stop) / (reps * len(batches))
-    log(f"c3 M=1, one batched launch: {ms1 * 1e3:.1f} us per pass, {packed / (ms1 * 1e-3) / 1e9:.1f} GB/s packed")
-    # parity of the timed pass: every output against its own single call
+    gbs = packed / (ms1 * 1e-3) / 1e9
     ref = [s_.gemv_f32(x_of(w.W.shape[0], 1, torch.float32)) for s_, w in zip(sets[-1], mats)]
     torch.cuda.synchronize()
-    batch_bit_identical = all(torch.equal(a_, b_) for a_, b_ in zip(ref, ys1))
-    log(f"c3 M=1 batched outputs bit-identical to single calls: {batch_bit_identical}")
+    identical = all(torch.equal(a_, b_) for a_, b_ in zip(ref, ys1))
+    log(f"c3 M=1, one batched launch per pass: {ms1 * 1e3:.1f} us, {gbs:.1f} GB/s packed "
+        f"({n_rot} rotating stacks); outputs bit-identical to single calls: {identical}")
+    if not identical:
+        raise SystemExit("c3 batched decode differs from the single-matrix calls")
+    out = {"workload": f"c3 Qwen2.5-0.5B-shaped stack, {len(mats) // 7} layers x 7 matrices, QT-P @ 3.125",
+           "matrices": len(mats), "weights": weights, "packed_bytes": packed, "rotating_stacks": n_rot,
+           "m1": {"us_per_pass": ms1 * 1e3, "GBps_packed": gbs, "launches": 1, "bit_identical_to_single_calls": True,
+                  "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                               "frac": gbs / HBM_PEAK_GBS, "traffic": None, "kernel": "k_gemv_batch"}}}
+    n_per = len(workloads.QWEN_LAYER)
+    layer_groups = [[0, 1, 2], [3], [4, 5], [6]]
+    plan_grouped = [[L * n_per + i for i in grp] for L in range(len(mats) // n_per) for grp in layer_groups]
+    if detail:
+        def time_m1(plan):
+            def calls(ss):
+                fns = []
+                for grp in plan:
+                    if len(grp) == 1:
+                        i = grp[0]
+                        fns.append(lambda s_=ss[i], w=mats[i], y=ys1[i]: s_.gemv_f32(x_of(w.W.shape[0], 1, torch.float32), out=y))
+                    else:
+                        fns.append(lambda g=[ss[i] for i in grp], K=mats[grp[0]].W.shape[0], ys=[ys1[i] for i in grp]:
+                                   gemv_f32_group(g, x_of(K, 1, torch.float32), ys))
+                return fns
+            for ss in sets:
+                for s_ in ss:
+                    s_.workspace(1)
+            graphs = [graph_of(torch, calls(ss)) for ss in sets]
+            for g in graphs:
+                g.replay()
+            torch.cuda.synchronize()
+            r = max(2, 40 // len(graphs))
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(r):
+                for g in graphs:
+                    g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) / (r * len(graphs))
+        out["m1"]["us_per_pass_one_launch_per_matrix"] = time_m1([[i] for i in range(len(mats))]) * 1e3
+        out["m1"]["us_per_pass_grouped_96_launches"] = time_m1(plan_grouped) * 1e3
+        log(f"c3 M=1: one launch per matrix {out['m1']['us_per_pass_one_launch_per_matrix']:.1f} us, "
+            f"96 grouped launches {out['m1']['us_per_pass_grouped_96_launches']:.1f} us")
     del sets, batches
-    # M = 512: prefill of every matrix
+    # M = 512 prefill
     M = 512
-    tiles = [m.device_tiles() for m in ms_]
+    tiles = [m.device_tiles(dev) for m in ms_]
     ysp = [torch.empty((M, w.W.shape[1]), dtype=torch.float32, device=dev) for w in mats]
-    from tensorpack_amd.device import gemm_bf16_group
-
-    def time_prefill(plan):
-        fns = []
-        for grp in plan:
-            K = mats[grp[0]].W.shape[0]
-            if len(grp) == 1:
-                i = grp[0]
-                fns.append(lambda t=tiles[i], K=K, y=ysp[i]: t.gemm_bf16(x_of(K, M, torch.bfloat16), out=y))
-            else:
-                fns.append(lambda ts=[tiles[i] for i in grp], K=K, ys=[ysp[i] for i in grp]:
-                           gemm_bf16_group(ts, x_of(K, M, torch.bfloat16), ys))
-        for f in fns:
-            f()
-        torch.cuda.synchronize()
-        return time_replays(torch, graph_of(torch, fns), 5)
-
-    flop = 2.0 * M * weights
-    msp_single = time_prefill([[i] for i in range(len(mats))])
-    log(f"c3 M=512, one matrix per launch: {msp_single:.3f} ms per pass, {flop / (msp_single * 1e-3) / 1e12:.1f} TFLOP/s")
-    msp = time_prefill(plan_grouped)
-    tf = flop / (msp * 1e-3) / 1e12
-    log(f"c3 M=512, grouped: {msp:.3f} ms per pass, {tf:.1f} TFLOP/s")
-    return {"metric": "packed-weight GB/s at M=1 over the 168-matrix stack (fp32 decode kernel)",
-            "value": packed / (ms1 * 1e-3) / 1e9, "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
-            "dtype": "f32", "data": "synthetic (seeded N(0, 0.02) weights per matrix, random-init)",
-            "config": {"workload": f"c3 Qwen2.5-0.5B-shaped stack, {args.c3_layers} layers, QT-P @ 3.125",
-                       "matrices": len(mats), "weights": weights, "packed_bytes": packed,
-                       "rotating_sets": n_rot},
-            "us_per_pass_m1": ms1 * 1e3, "launches_m1": 1, "batch_bit_identical": batch_bit_identical,
-            "us_per_pass_m1_grouped": ms1_grouped * 1e3, "launches_m1_grouped": len(plan_grouped),
-            "us_per_pass_m1_one_launch_per_matrix": ms1_single * 1e3,
-            "roofline": {"bound": "hbm", "achieved": packed / (ms1 * 1e-3) / 1e9, "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": packed / (ms1 * 1e-3) / 1e9 / HBM_PEAK_GBS},
-            "prefill_m512": {"ms_per_pass": msp, "TFLOPs": tf, "frac_bf16_peak": tf / BF16_PEAK_TFLOPS,
-                             "ms_per_pass_one_matrix_per_launch": msp_single}}
+    fns = []
+    for grp in plan_grouped:
+        K = mats[grp[0]].W.shape[0]
+        if len(grp) == 1:
+            fns.append(lambda t=tiles[grp[0]], K=K, y=ysp[grp[0]]: t.gemm_bf16(x_of(K, M, torch.bfloat16), out=y))
+        else:
+            fns.append(lambda ts=[tiles[i] for i in grp], K=K, ys=[ysp[i] for i in grp]:
+                       gemm_bf16_group(ts, x_of(K, M, torch.bfloat16), ys))
+    for f in fns:
+        f()
+    torch.cuda.synchronize()
+    msp = time_replays(torch, graph_of(torch, fns), 5)
+    tf = 2.0 * M * weights / (msp * 1e-3) / 1e12
+    # parity of the prefill pass: layer 0's matrices against the fp64 product with the allocator's W_hat
+    worst = 0.0
+    for i in range(n_per):
+        Xb = x_of(mats[i].W.shape[0], M, torch.bfloat16).float().cpu().numpy().astype(np.float64)
+        worst = max(worst, rel_frobenius(Xb @ np.asarray(allocs[i].dequant, np.float64), ysp[i].cpu().numpy()))
+    log(f"c3 M=512, {len(fns)} launches per pass: {msp:.3f} ms, {tf:.1f} TFLOP/s; layer 0 vs fp64: rel {worst:.2e}")
+    if not worst < 2e-3:
+        raise SystemExit(f"c3 prefill output differs from the fp64 product: rel {worst:.3e} >= 2e-3")
+    out["m512"] = {"ms_per_pass": msp, "TFLOPs": tf, "launches": len(fns), "rel_frobenius_layer0_vs_fp64": worst,
+                   "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                "frac": tf / BF16_PEAK_TFLOPS, "traffic": None}}
+    return out
 
 
-def run_c5(args):
-    """Adversarial leaf mix (QT @ 2.5 b/w, many 4x4 and P0 leaves): M=1 fp32 decode over
-    rotating copies, and M=256 through the bf16 MFMA path (fp32 X staged to bf16)."""
+def cpu_baseline_c3(args, mats, allocs):
+    """Bounded CPU sample of c3 at M=1: layer 0's seven matrices (the port's per-matrix cost scales
+    with the weights; every layer has the same shapes)."""
+    n_per = 7
+    las = [leaf_arena(allocs[i], mats[i].W) for i in range(n_per)]
+    xs = [np.random.RandomState(3000 + w.W.shape[0] + 1).randn(1, w.W.shape[0]).astype(np.float32)
+          for w in mats[:n_per]]
+    packed = float(sum(a.total_bits / 8.0 for a in allocs[:n_per]))
+    return cpu_port_gbs(las, xs, packed, args.cpu_seconds, "layer 0 of c3 (q, k, v, o, gate, up, down) at M=1")
+
+
+# ----------------------------------------------------------------------------------------------
+# c5: the adversarial leaf mix
+# ----------------------------------------------------------------------------------------------
+def bench_c5(args, wl, a, dev):
     import torch
-    from tensorpack_amd import workloads
     from tensorpack_amd.kernels.gemm import MTCMatrix
-    from tensorpack_amd.device import require_gpu
-    wl = workloads.c5()
-    t0 = time.time()
-    a = wl.allocate()
-    log(f"c5 allocation {time.time() - t0:.1f}s, {a.bits_per_element:.4f} b/w")
-    dev = require_gpu()
-    torch.cuda.set_device(dev)
     m = MTCMatrix.from_quadtree(a, wl.W)
-    ds = m.device_stream()
-    n_copies = max(1, int(np.ceil(args.rotate_gib * (1 << 30) / ds.device_bytes())))
-    copies = [ds] + [ds.clone() for _ in range(n_copies - 1)]
+    ds = m.device_stream(None, dev, 1)
+    copies = rotating(ds, args.rotate_gib * (1 << 30))
     X1 = torch.from_numpy(wl.activations(1)).to(dev)
     Y1 = torch.empty((1, wl.W.shape[1]), dtype=torch.float32, device=dev)
     for c in copies:
         c.workspace(1)
         c.gemv_f32(X1, out=Y1)
     torch.cuda.synchronize()
-    secs, ms = timed_calls(torch, [lambda c=c: c.gemv_f32(X1, out=Y1) for c in copies], args.steps, args.warmup,
-                           bool(args.graph))
+    s1, ms = timed_calls(torch, [lambda c=c: c.gemv_f32(X1, out=Y1) for c in copies], max(args.steps // 2, len(copies)),
+                         args.warmup // 2, bool(args.graph))
     gbs = m.packed_bytes / (ms * 1e-3) / 1e9
-    log(f"c5 M=1: {ms * 1e3:.2f} us/call, {gbs:.1f} GB/s packed")
+    rel1 = rel_frobenius(wl.activations(1).astype(np.float64) @ np.asarray(a.dequant, np.float64), Y1.cpu().numpy())
+    log(f"c5 M=1: {ms * 1e3:.2f} us/call, {gbs:.1f} GB/s packed; vs fp64 rel {rel1:.2e}")
+    if not rel1 < 1e-5:
+        raise SystemExit(f"c5 decode output differs from the fp64 product: rel {rel1:.3e}")
     M = 256
-    t = m.device_tiles()
+    t = m.device_tiles(dev)
     X = torch.from_numpy(wl.activations(M)).to(dev)
     Y = torch.empty((M, wl.W.shape[1]), dtype=torch.float32, device=dev)
     t.gemm_bf16(X, out=Y)
     torch.cuda.synchronize()
     s2, ms2 = timed_calls(torch, [lambda: t.gemm_bf16(X, out=Y)], 50, 5, bool(args.graph))
     tf = 2.0 * M * wl.W.size / (ms2 * 1e-3) / 1e12
-    log(f"c5 M=256: {ms2 * 1e3:.1f} us/call, {tf:.1f} TFLOP/s")
-    return {"metric": "packed-weight GB/s at M=1 (fp32 decode kernel)", "value": gbs, "unit": "GB/s",
-            "n_gpus": 1, "higher_is_better": True, "dtype": "f32",
-            "data": "synthetic (seeded np.random.RandomState weights/activations, random-init)",
-            "config": {"workload": wl.name + " M=1", "packed_bytes": m.packed_bytes,
-                       "stream_bytes": ds.device_bytes(), "rotating_copies": n_copies, "us_per_call": ms * 1e3},
-            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": gbs / HBM_PEAK_GBS},
-            "m256": {"us_per_call": ms2 * 1e3, "TFLOPs": tf, "frac_bf16_peak": tf / BF16_PEAK_TFLOPS,
-                     "x_dtype": "f32 (staged to bf16 by k_stage_x)"}}
+    Xb = X.to(torch.bfloat16).float().cpu().numpy().astype(np.float64)
+    rel2 = rel_frobenius(Xb @ np.asarray(a.dequant, np.float64), Y.cpu().numpy())
+    log(f"c5 M=256: {ms2 * 1e3:.1f} us/call, {tf:.1f} TFLOP/s; vs fp64 rel {rel2:.2e}")
+    if not rel2 < 2e-3:
+        raise SystemExit(f"c5 prefill output differs from the fp64 product: rel {rel2:.3e}")
+    return {"workload": wl.name, "packed_bytes": m.packed_bytes, "stream_bytes": ds.device_bytes(),
+            "m1": {"us_per_call": ms * 1e3, "GBps_packed": gbs, "rotating_copies": len(copies), "rel_vs_fp64": rel1,
+                   "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                "frac": gbs / HBM_PEAK_GBS, "traffic": None, "kernel": "k_gemv<1>"}},
+            "m256": {"us_per_call": ms2 * 1e3, "TFLOPs": tf, "x_dtype": "f32 (staged to bf16 by k_stage_x)",
+                     "rel_vs_fp64": rel2,
+                     "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                  "frac": tf / BF16_PEAK_TFLOPS, "traffic": None}}}
 
 
+# ----------------------------------------------------------------------------------------------
 def main():
     args = parse()
     if args.pmc_child:
@@ -407,153 +556,97 @@ def main():
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
         sys.exit(2)
-    if args.workload != "c2":
-        print(json.dumps(run_c3(args) if args.workload == "c3" else run_c5(args)), flush=True)
-        return
-    import torch
     from tensorpack_amd import workloads
     from tensorpack_amd.kernels.gemm import MTCMatrix
-    from tensorpack_amd.device import require_gpu
+    want = {"all": ("c2", "c4", "c3", "c5"), "c2": ("c2", "c4"), "c3": ("c3",), "c5": ("c5",)}[args.workload]
+    want = tuple(w for w in want if not (w == "c4" and args.no_prefill) and not (w == "c3" and args.no_c3)
+                 and not (w == "c5" and args.no_c5))
 
-    res = {}
-
-    # ---------------- c2 decode ----------------
-    wl = workloads.c2()
-    t0 = time.time()
-    alloc = wl.allocate()
-    log(f"c2 allocation {time.time() - t0:.1f}s, {alloc.bits_per_element:.4f} b/w")
-    m = MTCMatrix.from_quadtree(alloc, wl.W)
+    # ---- CPU phase: everything before this process initialises the GPU (the c3 pool forks) ----
+    A = {}
+    if "c3" in want:
+        mats = workloads.c3_matrices(args.c3_layers)
+        t0 = time.time()
+        A["c3"] = (mats, workloads.allocate_many(mats))
+        log(f"c3: {len(mats)} allocations in {time.time() - t0:.1f}s")
+    for name in ("c2", "c4", "c5"):
+        if name in want:
+            wl = workloads.CONFIGS[name]()
+            t0 = time.time()
+            A[name] = (wl, wl.allocate())
+            log(f"{name} allocation {time.time() - t0:.1f}s, {A[name][1].bits_per_element:.4f} b/w")
     traffic = None
-    if not args.no_traffic:
-        # counter passes run in child processes before this one initialises the GPU
+    if "c2" in want and not args.no_traffic:
+        wl, alloc = A["c2"]
+        m = MTCMatrix.from_quadtree(alloc, wl.W)
         traffic = traffic_passes(m.panel_stream(m.decode_chunk_rows(1)), wl.activations(1))
+
+    import torch
+    from tensorpack_amd.device import require_gpu
     dev = require_gpu()
     torch.cuda.set_device(dev)
-    t0 = time.time()
-    ds = m.device_stream()
-    log(f"c2 packed in {time.time() - t0:.1f}s: chunk_rows={ds.host.chunk_rows} stream {ds.device_bytes()} B, "
-        f"accounted {m.packed_bytes:.0f} B")
-    packed = m.packed_bytes
-    per_copy = ds.device_bytes()
-    n_copies = max(1, int(np.ceil(args.rotate_gib * (1 << 30) / per_copy)))
-    copies = [ds] + [ds.clone() for _ in range(n_copies - 1)]
-    X1 = torch.from_numpy(wl.activations(1)).to(dev)
-    Y1 = torch.empty((1, wl.W.shape[1]), dtype=torch.float32, device=dev)
-    for c in copies:
-        c.workspace(1)
-        c.gemv_f32(X1, out=Y1)
-    torch.cuda.synchronize()
-    launches = [lambda c=c: c.gemv_f32(X1, out=Y1) for c in copies]
-    secs, ms = timed_calls(torch, launches, args.steps, args.warmup, bool(args.graph))
-    gbs = packed / (ms * 1e-3) / 1e9
-    log(f"c2 M=1: {ms * 1e3:.2f} us/call, {gbs:.1f} GB/s packed ({n_copies} copies)")
-    y_gpu = Y1.cpu().numpy().copy()
+    if "c2" not in want:                                  # a single detail workload
+        if "c3" in want:
+            r = bench_c3(args, *A["c3"], dev, detail=True)
+            if not args.no_cpu_baseline:
+                r["cpu_baseline"] = cpu_baseline_c3(args, *A["c3"])
+        else:
+            r = bench_c5(args, *A["c5"], dev)
+            if not args.no_cpu_baseline:
+                wl, a = A["c5"]
+                r["cpu_baseline"] = cpu_port_gbs([leaf_arena(a, wl.W)], [wl.activations(1)], a.total_bits / 8.0,
+                                                 args.cpu_seconds, "c5 M=1 (full 4096x4096 matrix)")
+        print(json.dumps(r), flush=True)
+        return
 
-    if not args.no_m16:
-        d16 = m.device_stream(None, dev, 16)
-        c16 = [d16] + [d16.clone() for _ in range(max(1, int(np.ceil(args.rotate_gib * (1 << 30) / d16.device_bytes()))) - 1)]
-        X16 = torch.from_numpy(wl.activations(16)).to(dev)
-        Y16 = torch.empty((16, wl.W.shape[1]), dtype=torch.float32, device=dev)
-        for c in c16:
-            c.workspace(16)
-            c.gemv_f32(X16, out=Y16)
-        torch.cuda.synchronize()
-        l16 = [lambda c=c: c.gemv_f32(X16, out=Y16) for c in c16]
-        s16, ms16 = timed_calls(torch, l16, max(args.steps // 4, len(c16)), args.warmup // 4, bool(args.graph))
-        flop16 = 2.0 * 16 * wl.W.shape[0] * wl.W.shape[1]
-        res["c2_m16"] = {"us_per_call": ms16 * 1e3, "packed_GBps": packed / (ms16 * 1e-3) / 1e9,
-                         "TFLOPs": flop16 / (ms16 * 1e-3) / 1e12,
-                         "frac_fp32_peak": flop16 / (ms16 * 1e-3) / 1e12 / FP32_PEAK_TFLOPS,
-                         "chunk_rows": d16.host.chunk_rows}
-        del c16
-        log(f"c2 M=16: {ms16 * 1e3:.2f} us/call, {res['c2_m16']['TFLOPs']:.2f} TFLOP/s")
+    extra = {}
+    wl, alloc = A["c2"]
+    c2 = bench_c2(args, wl, alloc, traffic, dev)
+    if "m16" in c2:
+        extra["c2_m16"] = c2.pop("m16")
+    copy_gbs, copy_small_us = device_copy_rates(dev, c2["packed"])
+    if "c4" in want:
+        extra["c4_prefill"] = bench_c4(args, *A["c4"], dev)
+    if "c3" in want:
+        extra["c3"] = bench_c3(args, *A["c3"], dev)
+    if "c5" in want:
+        extra["c5"] = bench_c5(args, *A["c5"], dev)
 
-    # ---------------- achievable HBM bandwidth: a plain 1 GiB device copy ----------------
-    src = torch.empty(1 << 28, dtype=torch.float32, device=dev)
-    dst = torch.empty_like(src)
-    dst.copy_(src)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(10):
-        dst.copy_(src)
-    e1.record()
-    torch.cuda.synchronize()
-    copy_gbs = 2 * src.numel() * 4 * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9     # read + write bytes
-    del src, dst
-    log(f"device copy: {copy_gbs:.0f} GB/s (read + write)")
-    # the same for copies of the packed weight's size, rotated over ~1 GiB and replayed
-    # from a graph like the decode: what a launch of this size achieves on the copy path
-    n_el = int(packed) // 4
-    n_rot = max(2, (1 << 30) // (2 * 4 * n_el))
-    srcs = [torch.empty(n_el, dtype=torch.float32, device=dev) for _ in range(n_rot)]
-    dsts = [torch.empty_like(s) for s in srcs]
-    g = graph_of(torch, [lambda s=s, d=d: d.copy_(s) for s, d in zip(srcs, dsts)])
-    copy_small_us = time_replays(torch, g, 5) * 1e3 / n_rot
-    del g, srcs, dsts
-    log(f"device copy of {4 * n_el} B: {copy_small_us:.2f} us per copy ({n_rot} rotating pairs)")
-
-    # ---------------- CPU baseline (bounded sample) ----------------
+    # ---- CPU baselines (bounded samples on this host's cores) ----
     cpu = None
     if not args.no_cpu_baseline:
         from oracle import mtc_oracle as O
-        inner = alloc.inner
-        la = O.LeafArena(inner.weights, inner.sizes, inner.leaf, inner.modes, inner.scales,
-                         alloc.row_perm, alloc.col_perm)
-        x = wl.activations(1)
-        y_cpu = O.cpu_qt_gemm(x, la)
-        calls, t0 = 0, time.time()
-        while True:
-            O.cpu_qt_gemm(x, la)
-            calls += 1
-            if time.time() - t0 >= args.cpu_seconds and calls >= 3:
-                break
-        el = time.time() - t0
-        cores = int(O.cpu_lib().oracle_threads())
-        cpu = {"value": packed * calls / el / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
-               "sample": f"{calls} calls of c2 M=1 (full 4096x4096 matrix) in {el:.1f}s, C/OpenMP port of the "
-                         f"reference block loop (gemm.py:124-210)",
-               "gpu_vs_cpu_rel_frobenius": O.relative_frobenius_error(y_cpu, y_gpu)}
-        log(f"cpu baseline {cpu['value']:.3f} GB/s on {cores} threads; gpu-vs-cpu rel {cpu['gpu_vs_cpu_rel_frobenius']:.2e}")
+        la = leaf_arena(alloc, wl.W)
+        cpu = cpu_port_gbs([la], [c2["x"]], c2["packed"], args.cpu_seconds, "c2 M=1 (full 4096x4096 matrix)")
+        cpu["gpu_vs_cpu_rel_frobenius"] = O.relative_frobenius_error(O.cpu_qt_gemm(c2["x"], la), c2["y"])
+        log(f"cpu baseline c2 {cpu['value']:.3f} GB/s on {cpu['cores']} threads; gpu-vs-cpu rel "
+            f"{cpu['gpu_vs_cpu_rel_frobenius']:.2e}")
         # the reference's own inference path: X @ the cached dequantized weight (LinearMTCAdaptive.forward,
         # mtc/nn/layers.py:150-151), numpy BLAS over a dense fp32 W_hat
         w_hat = np.ascontiguousarray(alloc.dequant, dtype=np.float32)
+        x = c2["x"]
         x @ w_hat
         n_np, t0 = 0, time.time()
         while time.time() - t0 < 2.0 or n_np < 3:
             x @ w_hat
             n_np += 1
         el_np = time.time() - t0
-        cpu["numpy_dequant_matmul"] = {"ms_per_call": 1e3 * el_np / n_np,
-                                       "packed_GBps": packed * n_np / el_np / 1e9,
+        cpu["numpy_dequant_matmul"] = {"ms_per_call": 1e3 * el_np / n_np, "packed_GBps": c2["packed"] * n_np / el_np / 1e9,
                                        "dense_fp32_GBps": w_hat.nbytes * n_np / el_np / 1e9,
                                        "sample": f"{n_np} calls of x (1 x 4096) @ W_hat (4096 x 4096 fp32) in {el_np:.1f}s"}
-        log(f"cpu numpy X @ W_hat: {1e3 * el_np / n_np:.2f} ms/call")
         del w_hat
-
-    # ---------------- c4 prefill ----------------
-    if not args.no_prefill:
-        wl4 = workloads.c4()
-        t0 = time.time()
-        a4 = wl4.allocate()
-        log(f"c4 allocation {time.time() - t0:.1f}s, {a4.bits_per_element:.4f} b/w")
-        m4 = MTCMatrix.from_quadtree(a4, wl4.W)
-        t0 = time.time()
-        g4 = m4.device_tiles()
-        log(f"c4 packed in {time.time() - t0:.1f}s")
-        M4 = 4096
-        X4 = torch.from_numpy(wl4.activations(M4)).to(dev).to(torch.bfloat16)
-        Y4 = torch.empty((M4, wl4.W.shape[1]), dtype=torch.float32, device=dev)
-        g4.gemm_bf16(X4, out=Y4)
-        torch.cuda.synchronize()
-        s4, ms4 = timed_calls(torch, [lambda: g4.gemm_bf16(X4, out=Y4)], args.prefill_steps, args.prefill_warmup, False)
-        flop4 = 2.0 * M4 * wl4.W.shape[0] * wl4.W.shape[1]
-        tf = flop4 / (ms4 * 1e-3) / 1e12
-        res["c4_prefill"] = {"M": M4, "ms_per_call": ms4, "TFLOPs": tf, "frac_bf16_peak": tf / BF16_PEAK_TFLOPS,
-                             "packed_bytes": m4.packed_bytes}
-        log(f"c4 M=4096: {ms4:.3f} ms/call, {tf:.1f} TFLOP/s ({100 * tf / BF16_PEAK_TFLOPS:.1f}% of bf16 peak)")
+        if "c3" in extra:
+            extra["c3"]["cpu_baseline"] = cpu_baseline_c3(args, *A["c3"])
+            log(f"cpu baseline c3 {extra['c3']['cpu_baseline']['value']:.3f} GB/s")
+        if "c5" in extra:
+            wl5, a5 = A["c5"]
+            extra["c5"]["cpu_baseline"] = cpu_port_gbs([leaf_arena(a5, wl5.W)], [wl5.activations(1)],
+                                                       a5.total_bits / 8.0, args.cpu_seconds,
+                                                       "c5 M=1 (full 4096x4096 matrix)")
+            log(f"cpu baseline c5 {extra['c5']['cpu_baseline']['value']:.3f} GB/s")
 
     K, N = wl.W.shape
+    ms, gbs, ds = c2["ms"], c2["gbs"], c2["ds"]
     out = {
         "metric": "packed-weight GB/s at M=1 (fp32 decode kernel)",
         "value": gbs,
@@ -568,17 +661,17 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded np.random.RandomState weights/activations, random-init)",
         "config": {"workload": wl.name + " M=1", "K": K, "N": N, "M": 1, "budget_bits": wl.budget,
-                   "bits_per_weight": alloc.bits_per_element, "packed_bytes": packed,
-                   "stream_bytes": per_copy, "rotating_copies": n_copies,
+                   "bits_per_weight": alloc.bits_per_element, "packed_bytes": c2["packed"],
+                   "stream_bytes": ds.device_bytes(), "rotating_copies": c2["n_copies"],
                    "chunk_rows": ds.host.chunk_rows, "graph_replay": bool(args.graph)},
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": gbs / HBM_PEAK_GBS, "traffic": None if traffic is None else traffic["bytes"],
                      "copy_GBps": copy_gbs, "frac_of_copy": gbs / copy_gbs,
                      "copy_same_bytes_us": copy_small_us, "us_per_call": ms * 1e3,
-                     "kernel": "k_gemv<1>", "stream_GBps": per_copy / (ms * 1e-3) / 1e9,
+                     "kernel": "k_gemv<1>", "stream_GBps": ds.device_bytes() / (ms * 1e-3) / 1e9,
                      "traffic_detail": traffic},
         "cpu_baseline": cpu,
-        "extra": res,
+        "extra": extra,
     }
     print(json.dumps(out), flush=True)
 
