@@ -273,6 +273,30 @@ int mtc_gemm_bf16_group(const mtc_tile_desc* const* descs, int n, const void* X,
                         void* const* Y, int y_dtype, const int64_t* ldy, int M, void* workspace,
                         size_t workspace_bytes, void* hip_stream);
 
+/* Batched prefill: any number of matrices, each with its own X and Y (the same M, X dtype and
+ * Y dtype, and one scale format), in one X-staging launch, one tile launch and, if any
+ * member's K is split, one reduction launch. Replaces a loop of mtc_gemm_bf16 calls (the
+ * reference's per-layer LinearMTCAdaptive.forward, mtc/nn/layers.py:150-151, at prefill
+ * shapes) when the inputs are known together. The protocol is that of the decode batch:
+ * query sizes with plan == NULL, give a 256-byte aligned device workspace (staged bf16 X and
+ * split-K partials; no initialisation) and a 64-byte aligned host buffer, copy the plan byte
+ * for byte to a 64-byte aligned device buffer, launch with mtc_gemm_bf16_batch. When the
+ * members' output tiles together fill the chip no K is split; otherwise each member splits K
+ * as mtc_gemm_bf16 would, and its Y then equals that call's bit for bit. Results are
+ * deterministic. Launches that share a workspace must not overlap. */
+typedef struct mtc_gemm_batch_item {
+  const mtc_tile_desc* desc;     /* read while the plan is built */
+  const void* X;                 /* M x K, x_dtype, leading dim ldx */
+  int64_t ldx;
+  void* Y;                       /* M x N, y_dtype, leading dim ldy */
+  int64_t ldy;
+} mtc_gemm_batch_item;
+
+int mtc_gemm_batch_plan(const mtc_gemm_batch_item* items, int n, int M, int x_dtype, int y_dtype, void* workspace,
+                        size_t workspace_bytes, void* plan, size_t plan_bytes, size_t* plan_needed,
+                        size_t* workspace_needed);
+int mtc_gemm_bf16_batch(const void* host_plan, const void* device_plan, void* hip_stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,7 +17,8 @@ ERROR_NAMES = {
 EXPORTED = ("mtc_abi_version", "mtc_last_error", "mtc_check_desc", "mtc_dequant", "mtc_gemv_lds_bytes",
             "mtc_gemv_workspace_bytes", "mtc_gemv_f32", "mtc_gemv_f32_group", "mtc_check_tile_desc", "mtc_gemm_workspace_bytes",
             "mtc_gemm_bf16", "mtc_gemm_group_workspace_bytes", "mtc_gemm_bf16_group", "mtc_gemv_batch_plan",
-            "mtc_gemv_f32_batch", "mtc_gemv_noalloc_scratch_bytes", "mtc_gemv_f32_noalloc")
+            "mtc_gemv_f32_batch", "mtc_gemv_noalloc_scratch_bytes", "mtc_gemv_f32_noalloc", "mtc_gemm_batch_plan",
+            "mtc_gemm_bf16_batch")
 
 
 class MtcStreamDesc(ctypes.Structure):
@@ -81,6 +82,16 @@ class MtcGemvBatchItem(ctypes.Structure):
     ]
 
 
+class MtcGemmBatchItem(ctypes.Structure):
+    _fields_ = [
+        ("desc", TileDescP),
+        ("X", ctypes.c_void_p),
+        ("ldx", ctypes.c_int64),
+        ("Y", ctypes.c_void_p),
+        ("ldy", ctypes.c_int64),
+    ]
+
+
 MAX_GROUP = 4                        # MTC_MAX_GROUP: matrices per mtc_gemv_f32_group launch
 
 
@@ -112,6 +123,11 @@ def declare(lib: ctypes.CDLL) -> None:
                                         ctypes.POINTER(sz), ctypes.POINTER(sz)]
     lib.mtc_gemv_f32_batch.restype = i32
     lib.mtc_gemv_f32_batch.argtypes = [vp, vp, vp]
+    lib.mtc_gemm_batch_plan.restype = i32
+    lib.mtc_gemm_batch_plan.argtypes = [ctypes.POINTER(MtcGemmBatchItem), i32, i32, i32, i32, vp, sz, vp, sz,
+                                        ctypes.POINTER(sz), ctypes.POINTER(sz)]
+    lib.mtc_gemm_bf16_batch.restype = i32
+    lib.mtc_gemm_bf16_batch.argtypes = [vp, vp, vp]
     lib.mtc_check_tile_desc.restype = i32
     lib.mtc_check_tile_desc.argtypes = [TileDescP]
     lib.mtc_gemm_workspace_bytes.restype = sz

@@ -16,9 +16,11 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdio.h>
 #include <string.h>
 
 #include <algorithm>
+#include <vector>
 
 #include "mtc_hip.h"
 #include "mtc_host.h"
@@ -155,27 +157,39 @@ __device__ __forceinline__ void decode_cell(uint32_t cls, const u32x4_t* pw, flo
   }
 }
 
-// One output tile block of matrix `d`: tile-order index bx, K split by (the grid's x and y
-// for a launch of its own).
-template <bool kFS, int kYDT>
-__device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const int bx, const int by,
-                                                const __bf16* __restrict__ X, int64_t ldx, void* __restrict__ Y,
-                                                int64_t ldy, int M, int n_row_tiles, int tiles_per_xcd,
-                                                int steps_per_split, float* __restrict__ part) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-  constexpr int CW = kFS ? 4 : 2;
-
-  // Tile order: each XCD takes a contiguous range of tile ids; ids run over groups of
-  // kRowGroup row tiles, row tile fastest, so the blocks in flight on one XCD share
-  // column tiles (B) and row tiles (A) in its L2.
+// Output tile (rt, ct) of a launch of one matrix from its block index bx: each XCD (bx % 8)
+// takes a contiguous range of tile ids. Without an output column permutation the ids run
+// over groups of kRowGroup row tiles, row tile fastest, so the blocks in flight on one XCD
+// share column tiles (B) and row tiles (A) in its L2. With one (`row_major`), the ids run
+// row-major, so an XCD takes the column tiles of whole row tiles: the scattered 4-byte Y
+// writes of an output row then meet in one L2, which merges them into full lines before they
+// go to HBM (spread over XCDs they left partial lines: 3.7x the time of plain writes).
+// Returns false for a padding block.
+__device__ __forceinline__ bool tile_of_block(int bx, int n_row_tiles, int n_ct, int tiles_per_xcd, bool row_major,
+                                              int& rt, int& ct) {
   const int tile = (bx % kXcds) * tiles_per_xcd + bx / kXcds;
-  const int n_ct = d.n_col_tiles;
-  if (tile >= n_row_tiles * n_ct) return;
+  if (tile >= n_row_tiles * n_ct) return false;
+  if (row_major) {
+    rt = tile / n_ct;
+    ct = tile - rt * n_ct;
+    return true;
+  }
   const int per_group = kRowGroup * n_ct;
   const int grp = tile / per_group, in_grp = tile - grp * per_group;
   const int first = grp * kRowGroup;
   const int rows_in = min(n_row_tiles - first, kRowGroup);
-  const int rt = first + in_grp % rows_in, ct = in_grp / rows_in;
+  rt = first + in_grp % rows_in;
+  ct = in_grp / rows_in;
+  return true;
+}
+
+// One output tile block of matrix `d`: output tile (rt, ct), K split by.
+template <bool kFS, int kYDT>
+__device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const int rt, const int ct, const int by,
+                                                const __bf16* __restrict__ X, int64_t ldx, void* __restrict__ Y,
+                                                int64_t ldy, int M, int steps_per_split, float* __restrict__ part) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  constexpr int CW = kFS ? 4 : 2;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: keeps per-wave control scalar
@@ -389,8 +403,9 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, c
                                                         int64_t ldx, void* __restrict__ Y, int64_t ldy, int M,
                                                         int n_row_tiles, int tiles_per_xcd, int steps_per_split,
                                                         float* __restrict__ part) {
-  gemm_tile_block<kFS, kYDT>(d, (int)blockIdx.x, (int)blockIdx.y, X, ldx, Y, ldy, M, n_row_tiles, tiles_per_xcd,
-                             steps_per_split, part);
+  int rt, ct;
+  if (!tile_of_block((int)blockIdx.x, n_row_tiles, d.n_col_tiles, tiles_per_xcd, d.col_perm && !part, rt, ct)) return;
+  gemm_tile_block<kFS, kYDT>(d, rt, ct, (int)blockIdx.y, X, ldx, Y, ldy, M, steps_per_split, part);
 }
 
 // Up to kMaxGroup matrices that read the same X, in one launch of each kernel: member i owns
@@ -416,8 +431,12 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile_group(const GemmGroup g,
 #pragma unroll
   for (int k = 1; k < kMaxGroup; ++k) i += (int)blockIdx.x >= g.start[k];
   if ((int)blockIdx.y >= g.splits[i]) return;               // this member has fewer K splits
-  gemm_tile_block<kFS, kYDT>(g.d[i], (int)blockIdx.x - g.start[i], (int)blockIdx.y, g.X[i], g.ldx[i], g.Y[i], g.ldy[i],
-                             M, n_row_tiles, g.tiles_per_xcd[i], g.steps_per_split[i], g.part[i]);
+  int rt, ct;
+  if (!tile_of_block((int)blockIdx.x - g.start[i], n_row_tiles, g.d[i].n_col_tiles, g.tiles_per_xcd[i],
+                     g.d[i].col_perm && !g.part[i], rt, ct))
+    return;
+  gemm_tile_block<kFS, kYDT>(g.d[i], rt, ct, (int)blockIdx.y, g.X[i], g.ldx[i], g.Y[i], g.ldy[i], M,
+                             g.steps_per_split[i], g.part[i]);
 }
 
 // Xp[m, k] = bf16(X[m, row_perm[k]]) (identity without a permutation); 8 outputs per thread.
@@ -518,6 +537,53 @@ template <int kYDT>
 __global__ __launch_bounds__(kReduceThreads) void k_splitk_reduce_group(const ReduceGroup g, int M) {
   const int e = blockIdx.y;
   splitk_reduce_block<kYDT>((int)blockIdx.x, g.part[e], g.splits[e], M, g.N[e], g.col_perm[e], g.Y[e], g.ldy[e]);
+}
+
+// ---------------------------------------------------------------------------
+// Batched prefill: any number of matrices, each with its own X and Y (one M), in one staging
+// launch, one tile launch and, for the members whose K is split, one reduction launch. The plan
+// (built on the host by mtc_gemm_batch_plan, copied byte for byte to the device by the caller)
+// holds one GemmBatchItem per matrix and one entry per grid block: (item, row tile | column
+// tile << 12 | K split << 24), or kNoItem where an XCD's list is shorter than the longest.
+// ---------------------------------------------------------------------------
+struct GemmBatchItem {
+  mtc_tile_desc d;
+  const void* Xsrc;        // the caller's X
+  int64_t ldx_src;
+  const __bf16* X;         // what the tile blocks read: the staged bf16 copy, or the caller's bf16 X
+  int64_t ldx;
+  void* Y;
+  int64_t ldy;
+  float* part;             // split-K partial tiles (splits > 1)
+  int32_t steps_per_split;
+  int32_t splits;
+  int32_t stage;           // X is staged first (fp32 X, or a row permutation to gather)
+  int32_t reserved;
+};
+
+constexpr uint32_t kNoItem = 0xFFFFFFFFu;   // a block table entry with no work
+
+template <bool kFS, int kYDT>
+__global__ __launch_bounds__(kThreads) void k_gemm_tile_batch(const GemmBatchItem* __restrict__ items,
+                                                              const uint2* __restrict__ blocks, int M) {
+  const uint2 e = blocks[blockIdx.x];
+  if (e.x == kNoItem) return;                               // padding of an XCD's block list
+  const GemmBatchItem& it = items[e.x];
+  gemm_tile_block<kFS, kYDT>(it.d, (int)(e.y & 0xFFFu), (int)((e.y >> 12) & 0xFFFu), (int)(e.y >> 24), it.X, it.ldx,
+                             it.Y, it.ldy, M, it.steps_per_split, it.splits > 1 ? it.part : nullptr);
+}
+
+__global__ __launch_bounds__(kStageThreads) void k_stage_x_batch(const GemmBatchItem* __restrict__ items,
+                                                                 const uint32_t* __restrict__ list, int xdt) {
+  const GemmBatchItem& it = items[list[blockIdx.z]];
+  stage_x_row(it.Xsrc, xdt, it.ldx_src, it.d.row_perm, const_cast<__bf16*>(it.X), it.d.K);
+}
+
+template <int kYDT>
+__global__ __launch_bounds__(kReduceThreads) void k_splitk_reduce_batch(const GemmBatchItem* __restrict__ items,
+                                                                        const uint32_t* __restrict__ list, int M) {
+  const GemmBatchItem& it = items[list[blockIdx.y]];
+  splitk_reduce_block<kYDT>((int)blockIdx.x, it.part, it.splits, M, it.d.N, it.d.col_perm, it.Y, it.ldy);
 }
 
 int check_tile_desc(const mtc_tile_desc* d) {
@@ -639,7 +705,264 @@ int launch_tile_group(GemmGroup& g, int n, int M, const ReduceGroup& rg, int n_r
   return check_launch("k_splitk_reduce_group");
 }
 
+// ---- batched prefill plan: GemmBatchHeader, GemmBatchItem[n], uint2 blocks[n_blocks], stage list, reduce list ----
+struct GemmBatchHeader {
+  uint32_t magic;
+  uint32_t abi_version;
+  int32_t n_items;
+  int32_t n_blocks;
+  int32_t M;
+  int32_t x_dtype;
+  int32_t y_dtype;
+  int32_t fs;
+  int32_t n_stage;
+  int32_t n_reduce;
+  int32_t stage_blocks_x;
+  int32_t reduce_blocks_x;
+  uint64_t items_off;
+  uint64_t blocks_off;
+  uint64_t stage_off;
+  uint64_t reduce_off;
+  uint64_t plan_bytes;
+  uint64_t ws_bytes;
+  const void* workspace;
+};
+constexpr uint32_t kGemmBatchMagic = 0x4D544347u;   // "GCTM"
+
+size_t align64(size_t v) { return (v + 63) / 64 * 64; }
+
+int build_gemm_batch_plan(const mtc_gemm_batch_item* items, int n, int M, int x_dtype, int y_dtype, void* workspace,
+                          size_t ws_bytes, void* plan, size_t plan_bytes, size_t* plan_needed, size_t* ws_needed) {
+  if (!items) return fail(MTC_E_NULL, "items is NULL");
+  if (n < 1 || n > (1 << 16)) return fail(MTC_E_SHAPE, "batch of %d matrices", n);
+  if (M <= 0 || M > 65535) return fail(MTC_E_SHAPE, "M=%d must be in [1, 65535]", M);
+  if (x_dtype != MTC_DTYPE_F32 && x_dtype != MTC_DTYPE_BF16) return fail(MTC_E_DTYPE, "x_dtype=%d", x_dtype);
+  if (y_dtype != MTC_DTYPE_F32 && y_dtype != MTC_DTYPE_BF16) return fail(MTC_E_DTYPE, "y_dtype=%d", y_dtype);
+  const int n_row_tiles = (M + kTM - 1) / kTM;
+  int64_t total_tiles = 0;
+  bool fs = false;
+  for (int i = 0; i < n; ++i) {
+    const mtc_tile_desc* d = items[i].desc;
+    int rc = check_tile_desc(d);
+    if (rc) {
+      char why[400];
+      snprintf(why, sizeof(why), "%s", mtc::host::last_error());
+      return fail(rc, "batch item %d: %s", i, why);
+    }
+    if (!items[i].X || !items[i].Y) return fail(MTC_E_NULL, "batch item %d: X or Y is NULL", i);
+    if (items[i].ldx < d->K || items[i].ldy < d->N)
+      return fail(MTC_E_SHAPE, "batch item %d: ldx=%lld < K or ldy=%lld < N", i, (long long)items[i].ldx,
+                  (long long)items[i].ldy);
+    const bool fsi = (d->flags & MTC_FLAG_FP32_SCALES) != 0;
+    if (i == 0) fs = fsi;
+    if (fsi != fs) return fail(MTC_E_SHAPE, "batch item %d differs from item 0 in scale format", i);
+    if (!needs_staging(d, x_dtype) && (items[i].ldx % 8 || (reinterpret_cast<uintptr_t>(items[i].X) & 15)))
+      return fail(MTC_E_SHAPE, "batch item %d: bf16 X read in place needs 16-byte aligned rows", i);
+    const int64_t ldx_used = needs_staging(d, x_dtype) ? d->K : items[i].ldx;
+    if (ldx_used >= ((int64_t)1 << 31) / (2 * kTM))
+      return fail(MTC_E_SHAPE, "batch item %d: ldx=%lld too large for 32-bit X tile offsets", i, (long long)ldx_used);
+    total_tiles += (int64_t)n_row_tiles * d->n_col_tiles;
+  }
+  // the K split of a single call when the batch alone would leave CUs idle; none when it fills them
+  const bool fill = total_tiles >= kFillCUs;
+  std::vector<int> splits(n), per(n);
+  size_t ws = 0;
+  int n_stage = 0, n_reduce = 0, stage_bx = 1, reduce_bx = 1;
+  // Block placement. Grid block g runs on XCD g % 8, so the table is 8 interleaved lists, one
+  // per XCD. Work goes to the lists in groups: the column tiles of one row tile for an unsplit
+  // item with an output column permutation (its scattered Y writes of a row then meet in one
+  // L2), else the row tiles of one column tile and K split (they share the column tile's
+  // weights in L2). Groups go, longest first, to the least loaded list (load = block K-steps);
+  // within a list the blocks with the most K-steps come first.
+  struct Blk {
+    uint32_t item, code;
+    int steps;
+  };
+  struct Group {
+    std::vector<Blk> blks;
+    int64_t cost;
+  };
+  std::vector<Group> groups;
+  for (int i = 0; i < n; ++i) {
+    const mtc_tile_desc* d = items[i].desc;
+    int s = 1;
+    per[i] = fill ? d->n_ksteps : split_steps(d, M, &s);
+    splits[i] = s;
+    if (n_row_tiles >= 4096 || d->n_col_tiles >= 4096 || s > 256)
+      return fail(MTC_E_SHAPE, "batch item %d: %d x %d tiles, %d splits exceed the block table fields", i, n_row_tiles,
+                  d->n_col_tiles, s);
+    const int steps = std::min(per[i], d->n_ksteps);
+    auto code = [](int rt, int ct, int by) { return (uint32_t)rt | (uint32_t)ct << 12 | (uint32_t)by << 24; };
+    if (d->col_perm && s == 1) {
+      for (int rt = 0; rt < n_row_tiles; ++rt) {
+        Group g{{}, 0};
+        for (int ct = 0; ct < d->n_col_tiles; ++ct) g.blks.push_back({(uint32_t)i, code(rt, ct, 0), steps});
+        g.cost = (int64_t)steps * d->n_col_tiles;
+        groups.push_back(std::move(g));
+      }
+    } else {
+      for (int by = 0; by < s; ++by)
+        for (int ct = 0; ct < d->n_col_tiles; ++ct) {
+          Group g{{}, 0};
+          const int st = std::min(per[i], d->n_ksteps - by * per[i]);
+          for (int rt = 0; rt < n_row_tiles; ++rt) g.blks.push_back({(uint32_t)i, code(rt, ct, by), st});
+          g.cost = (int64_t)st * n_row_tiles;
+          groups.push_back(std::move(g));
+        }
+    }
+    ws += round256(staging_bytes(d, M, x_dtype)) + round256(s > 1 ? (size_t)s * M * d->N * 4 : 0);
+    if (needs_staging(d, x_dtype)) {
+      ++n_stage;
+      stage_bx = std::max(stage_bx, (d->K / 8 + kStageThreads - 1) / kStageThreads);
+    }
+    if (s > 1) {
+      ++n_reduce;
+      reduce_bx = std::max(reduce_bx, reduce_blocks(M, d->N, d->col_perm != nullptr));
+    }
+  }
+  std::stable_sort(groups.begin(), groups.end(), [](const Group& a, const Group& b) { return a.cost > b.cost; });
+  std::vector<Blk> lists[kXcds];
+  int64_t load[kXcds] = {};
+  for (const Group& g : groups) {
+    const int x = (int)(std::min_element(load, load + kXcds) - load);
+    load[x] += g.cost;
+    lists[x].insert(lists[x].end(), g.blks.begin(), g.blks.end());
+  }
+  size_t longest = 0;
+  for (auto& l : lists) {
+    std::stable_sort(l.begin(), l.end(), [](const Blk& a, const Blk& b) { return a.steps > b.steps; });
+    longest = std::max(longest, l.size());
+  }
+  const int64_t blocks = (int64_t)longest * kXcds;
+  if (blocks > (1 << 30)) return fail(MTC_E_SHAPE, "batch of %lld blocks", (long long)blocks);
+  const size_t items_off = align64(sizeof(GemmBatchHeader));
+  const size_t blocks_off = align64(items_off + (size_t)n * sizeof(GemmBatchItem));
+  const size_t stage_off = align64(blocks_off + (size_t)blocks * sizeof(uint2));
+  const size_t reduce_off = align64(stage_off + (size_t)n_stage * sizeof(uint32_t));
+  const size_t need = reduce_off + (size_t)n_reduce * sizeof(uint32_t);
+  if (plan_needed) *plan_needed = need;
+  if (ws_needed) *ws_needed = ws;
+  if (!plan) return ok();
+  if (plan_bytes < need) return fail(MTC_E_WORKSPACE, "batch plan of %zu bytes needed, %zu given", need, plan_bytes);
+  if (reinterpret_cast<uintptr_t>(plan) % 64) return fail(MTC_E_WORKSPACE, "batch plan not 64-byte aligned");
+  if (ws && (!workspace || ws_bytes < ws))
+    return fail(MTC_E_WORKSPACE, "batch workspace of %zu bytes needed, %zu given", ws, workspace ? ws_bytes : 0);
+  if (ws && (reinterpret_cast<uintptr_t>(workspace) & 255)) return fail(MTC_E_WORKSPACE, "workspace not 256-byte aligned");
+  unsigned char* base = reinterpret_cast<unsigned char*>(plan);
+  memset(base, 0, need);
+  GemmBatchHeader* h = reinterpret_cast<GemmBatchHeader*>(base);
+  GemmBatchItem* it = reinterpret_cast<GemmBatchItem*>(base + items_off);
+  uint2* table = reinterpret_cast<uint2*>(base + blocks_off);
+  uint32_t* stage_list = reinterpret_cast<uint32_t*>(base + stage_off);
+  uint32_t* reduce_list = reinterpret_cast<uint32_t*>(base + reduce_off);
+  h->magic = kGemmBatchMagic;
+  h->abi_version = MTC_ABI_VERSION;
+  h->n_items = n;
+  h->n_blocks = (int32_t)blocks;
+  h->M = M;
+  h->x_dtype = x_dtype;
+  h->y_dtype = y_dtype;
+  h->fs = fs;
+  h->n_stage = n_stage;
+  h->n_reduce = n_reduce;
+  h->stage_blocks_x = stage_bx;
+  h->reduce_blocks_x = reduce_bx;
+  h->items_off = items_off;
+  h->blocks_off = blocks_off;
+  h->stage_off = stage_off;
+  h->reduce_off = reduce_off;
+  h->plan_bytes = need;
+  h->ws_bytes = ws;
+  h->workspace = workspace;
+  char* wsp = reinterpret_cast<char*>(workspace);
+  n_stage = n_reduce = 0;
+  for (int i = 0; i < n; ++i) {
+    const mtc_tile_desc* d = items[i].desc;
+    GemmBatchItem& e = it[i];
+    e.d = *d;
+    e.Xsrc = items[i].X;
+    e.ldx_src = items[i].ldx;
+    e.Y = items[i].Y;
+    e.ldy = items[i].ldy;
+    e.steps_per_split = per[i];
+    e.splits = splits[i];
+    e.stage = needs_staging(d, x_dtype);
+    if (e.stage) {
+      e.X = reinterpret_cast<const __bf16*>(wsp);
+      e.ldx = d->K;
+      wsp += round256(staging_bytes(d, M, x_dtype));
+      stage_list[n_stage++] = (uint32_t)i;
+    } else {
+      e.X = reinterpret_cast<const __bf16*>(items[i].X);
+      e.ldx = items[i].ldx;
+    }
+    if (splits[i] > 1) {
+      e.part = reinterpret_cast<float*>(wsp);
+      wsp += round256((size_t)splits[i] * M * d->N * 4);
+      reduce_list[n_reduce++] = (uint32_t)i;
+    }
+  }
+  for (int x = 0; x < kXcds; ++x)
+    for (size_t p = 0; p < longest; ++p)
+      table[p * kXcds + x] = p < lists[x].size() ? uint2{lists[x][p].item, lists[x][p].code} : uint2{kNoItem, 0u};
+  return ok();
+}
+
+template <bool kFS, int kYDT>
+int launch_tile_batch(const GemmBatchHeader* h, const GemmBatchItem* items, const uint2* blocks,
+                      const uint32_t* reduce_list, hipStream_t st) {
+  if ((size_t)kLdsBytes > mtc::host::device_lds_limit())
+    return fail(MTC_E_SHAPE, "prefill kernel needs %d B of LDS per block, device has %zu", kLdsBytes,
+                mtc::host::device_lds_limit());
+  const void* fn = reinterpret_cast<const void*>(&k_gemm_tile_batch<kFS, kYDT>);
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+  if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+  hipLaunchKernelGGL((k_gemm_tile_batch<kFS, kYDT>), dim3((unsigned)h->n_blocks), dim3(kThreads), kLdsBytes, st, items,
+                     blocks, h->M);
+  int rc = check_launch("k_gemm_tile_batch");
+  if (rc || h->n_reduce == 0) return rc;
+  hipLaunchKernelGGL(k_splitk_reduce_batch<kYDT>, dim3((unsigned)h->reduce_blocks_x, (unsigned)h->n_reduce),
+                     dim3(kReduceThreads), 0, st, items, reduce_list, h->M);
+  return check_launch("k_splitk_reduce_batch");
+}
+
+int launch_gemm_batch(const void* host_plan, const void* device_plan, hipStream_t st) {
+  if (!host_plan || !device_plan) return fail(MTC_E_NULL, "host_plan or device_plan is NULL");
+  const GemmBatchHeader* h = reinterpret_cast<const GemmBatchHeader*>(host_plan);
+  if (h->magic != kGemmBatchMagic || h->abi_version != MTC_ABI_VERSION)
+    return fail(MTC_E_DESC, "not a prefill batch plan of this library (magic 0x%x, ABI %u)", h->magic,
+                h->abi_version);
+  if (reinterpret_cast<uintptr_t>(device_plan) % 64) return fail(MTC_E_DESC, "device plan not 64-byte aligned");
+  const unsigned char* dp = reinterpret_cast<const unsigned char*>(device_plan);
+  const GemmBatchItem* items = reinterpret_cast<const GemmBatchItem*>(dp + h->items_off);
+  const uint2* blocks = reinterpret_cast<const uint2*>(dp + h->blocks_off);
+  const uint32_t* stage_list = reinterpret_cast<const uint32_t*>(dp + h->stage_off);
+  const uint32_t* reduce_list = reinterpret_cast<const uint32_t*>(dp + h->reduce_off);
+  if (h->n_stage) {
+    hipLaunchKernelGGL(k_stage_x_batch, dim3((unsigned)h->stage_blocks_x, (unsigned)h->M, (unsigned)h->n_stage),
+                       dim3(kStageThreads), 0, st, items, stage_list, h->x_dtype);
+    const int rc = check_launch("k_stage_x_batch");
+    if (rc) return rc;
+  }
+  if (h->fs)
+    return h->y_dtype == MTC_DTYPE_F32 ? launch_tile_batch<true, MTC_DTYPE_F32>(h, items, blocks, reduce_list, st)
+                                       : launch_tile_batch<true, MTC_DTYPE_BF16>(h, items, blocks, reduce_list, st);
+  return h->y_dtype == MTC_DTYPE_F32 ? launch_tile_batch<false, MTC_DTYPE_F32>(h, items, blocks, reduce_list, st)
+                                     : launch_tile_batch<false, MTC_DTYPE_BF16>(h, items, blocks, reduce_list, st);
+}
+
 }  // namespace
+
+MTC_API int mtc_gemm_batch_plan(const mtc_gemm_batch_item* items, int n, int M, int x_dtype, int y_dtype,
+                                void* workspace, size_t workspace_bytes, void* plan, size_t plan_bytes,
+                                size_t* plan_needed, size_t* workspace_needed) {
+  return build_gemm_batch_plan(items, n, M, x_dtype, y_dtype, workspace, workspace_bytes, plan, plan_bytes,
+                               plan_needed, workspace_needed);
+}
+
+MTC_API int mtc_gemm_bf16_batch(const void* host_plan, const void* device_plan, void* hip_stream) {
+  return launch_gemm_batch(host_plan, device_plan, reinterpret_cast<hipStream_t>(hip_stream));
+}
 
 MTC_API int mtc_check_tile_desc(const mtc_tile_desc* d) { return check_tile_desc(d); }
 

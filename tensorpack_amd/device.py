@@ -330,6 +330,72 @@ class DeviceTiles:
         return out
 
 
+class GemmBatch:
+    """A prepared batched prefill (mtc_gemm_batch_plan + mtc_gemm_bf16_batch): Y_i = X_i @ W_hat_i
+    for any number of tile streams, each with its own input and output (one M, X dtype and Y
+    dtype), in one staging, one tile and at most one reduction launch. The plan records the
+    device addresses of the streams, inputs, outputs and the batch's workspace, so this object
+    keeps them alive; `launch()` reruns the same products. Launches of one batch must not
+    overlap in time (they share its workspace)."""
+
+    def __init__(self, tiles, Xs, outs=None, out_dtype=None):
+        torch = _torch()
+        self.tiles = list(tiles)
+        n = len(self.tiles)
+        if n < 1 or len(Xs) != n:
+            raise ValueError("one input per matrix, at least one matrix")
+        dev = self.tiles[0].device
+        self.device = dev
+        M = Xs[0].shape[0]
+        xdt_t = Xs[0].dtype
+        for t, X in zip(self.tiles, Xs):
+            if t.device != dev or X.device != dev:
+                raise ValueError("batch members, inputs and outputs live on one device")
+            _need(X.dim() == 2 and X.dtype == xdt_t and X.dtype in (torch.float32, torch.bfloat16)
+                  and X.stride(1) == 1 and tuple(X.shape) == (M, t.K),
+                  f"each X must be (M={M}, K) row-major, all fp32 or all bf16")
+        out_dtype = out_dtype or torch.float32
+        if outs is None:
+            outs = [torch.empty((M, t.N), dtype=out_dtype, device=dev) for t in self.tiles]
+        if len(outs) != n or len({o.dtype for o in outs}) != 1:
+            raise ValueError("one output per matrix, all of one dtype")
+        for o, t in zip(outs, self.tiles):
+            _need(o.device == dev and o.dtype in (torch.float32, torch.bfloat16) and o.stride(1) == 1
+                  and tuple(o.shape) == (M, t.N), f"each output must be ({M}, N) row-major on {dev}")
+        self.Xs, self.outs, self.M = list(Xs), list(outs), M
+        xdt = _abi.MTC_DTYPE_BF16 if xdt_t == torch.bfloat16 else _abi.MTC_DTYPE_F32
+        ydt = _abi.MTC_DTYPE_BF16 if outs[0].dtype == torch.bfloat16 else _abi.MTC_DTYPE_F32
+        lib = self.lib = self.tiles[0].lib
+        items = (_abi.MtcGemmBatchItem * n)()
+        for it, t, X, o in zip(items, self.tiles, self.Xs, self.outs):
+            it.desc = ctypes.pointer(t.desc)
+            it.X, it.ldx, it.Y, it.ldy = X.data_ptr(), X.stride(0), o.data_ptr(), o.stride(0)
+        plan_n, ws_n = ctypes.c_size_t(), ctypes.c_size_t()
+        _abi.check(lib, "mtc_gemm_batch_plan", lib.mtc_gemm_batch_plan(items, n, M, xdt, ydt, None, 0, None, 0,
+                                                                       ctypes.byref(plan_n), ctypes.byref(ws_n)))
+        self.workspace = torch.empty(ws_n.value, dtype=torch.uint8, device=dev) if ws_n.value else None
+        self.host_plan = _aligned_host(plan_n.value)
+        _abi.check(lib, "mtc_gemm_batch_plan",
+                   lib.mtc_gemm_batch_plan(items, n, M, xdt, ydt,
+                                           None if self.workspace is None else self.workspace.data_ptr(), ws_n.value,
+                                           self.host_plan.ctypes.data, plan_n.value, None, None))
+        self.device_plan = torch.from_numpy(self.host_plan.copy()).to(dev)
+        torch.cuda.synchronize(dev)
+
+    @property
+    def launches(self) -> int:
+        """Kernel launches per launch(): X staging if any member stages, the tile launch, and a
+        reduction if any member splits K (header fields n_stage and n_reduce)."""
+        n_stage, n_reduce = np.frombuffer(self.host_plan, dtype=np.int32, count=2, offset=32)
+        return 1 + int(n_stage > 0) + int(n_reduce > 0)
+
+    def launch(self):
+        rc = self.lib.mtc_gemm_bf16_batch(self.host_plan.ctypes.data, self.device_plan.data_ptr(),
+                                          current_stream_handle(self.device))
+        _abi.check(self.lib, "mtc_gemm_bf16_batch", rc)
+        return self.outs
+
+
 _GROUP_WS: dict = {}
 
 
