@@ -146,19 +146,24 @@ int mtc_dequant(const mtc_stream_desc* d, float* W_out, void* hip_stream);
  * call, no GPU needed); 0 for non-positive arguments. */
 size_t mtc_gemv_lds_bytes(int K, int chunk_rows, int has_row_perm, int M);
 
-/* Bytes of GEMV workspace needed for M rows (0 if the stream has one chunk).
- * The workspace must be zero-filled once before first use; the kernels leave
- * its counters at zero again after every call. */
+/* Bytes of GEMV workspace needed for M rows: split-K partials and counters when the stream has
+ * several row chunks, and, for M >= 5 (matrix-core M tiles of 8 or 16 rows), X gathered through
+ * the row permutation once per call (M tiles x chunk-padded K x tile rows fp32); 0 for a
+ * single-chunk stream at M <= 4. The workspace must be zero-filled once before first use; the
+ * kernels leave its counters at zero again after every call. */
 size_t mtc_gemv_workspace_bytes(const mtc_stream_desc* d, int M);
 
 /* fp32 path: Y (M x N fp32, leading dim ldy) = X (M x K fp32, leading dim ldx) * W_hat.
- * Any M >= 1; tuned for decode (M <= 16). Deterministic. */
+ * Any M >= 1; tuned for decode (M <= 16): M <= 4 on the vector units, M >= 5 on the matrix
+ * core (v_mfma_f32_4x4x1_16b_f32, fp32 products and sums) after a small X staging launch.
+ * Deterministic; the rows of a call at any M >= 5 equal those of any other call at M >= 5
+ * bit for bit. */
 int mtc_gemv_f32(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y, int64_t ldy, int M,
                  void* workspace, size_t workspace_bytes, void* hip_stream);
 
 /* mtc_gemv_f32 for callers that cannot allocate (code under HIP graph capture, serving
  * loops, harnesses that forbid hipMalloc). No counterpart in the reference. It takes no
- * workspace: the split-K partials and counters of a stream with several row chunks live in
+ * workspace: what mtc_gemv_workspace_bytes counts (split-K partials and counters, staged X) lives in
  * a static per-device array of MTC_NOALLOC_SCRATCH_BYTES that the library holds until the
  * process ends; a call that needs more fails with MTC_E_WORKSPACE before any launch. The
  * call allocates nothing and clears the counters itself (a small fill kernel on hip_stream
@@ -172,7 +177,8 @@ int mtc_gemv_f32_noalloc(const mtc_stream_desc* d, const float* X, int64_t ldx, 
 
 /* fp32 path for n (1..MTC_MAX_GROUP) matrices that read the same X, in one launch:
  * Y[i] (M x N_i, leading dim ldy[i]) = X (M x K, leading dim ldx) * W_hat_i.
- * Every stream must have a single row chunk (n_chunks == 1, so no workspace), the
+ * No workspace: at M >= 5 each block gathers its own X rows (no staging launch).
+ * Every stream must have a single row chunk (n_chunks == 1), the
  * same K, and the same scale format and row-permutation presence. Each Y[i] equals,
  * bit for bit, what mtc_gemv_f32 writes for matrix i alone. */
 #define MTC_MAX_GROUP 4
@@ -180,7 +186,7 @@ int mtc_gemv_f32_group(const mtc_stream_desc* const* descs, int n, const float* 
                        float* const* Y, const int64_t* ldy, int M, void* hip_stream);
 
 /* Batched decode: any number of matrices, each with its own X and Y (the same M), in ONE
- * launch. Replaces a loop of mtc_gemv_f32 calls (the reference's per-layer
+ * launch per block shape (plus one X staging launch for M >= 5). Replaces a loop of mtc_gemv_f32 calls (the reference's per-layer
  * LinearMTCAdaptive.forward, mtc/nn/layers.py:150-151, once per matrix of a decoder stack)
  * when the inputs are known together. Each Y equals, bit for bit, what mtc_gemv_f32 writes
  * for its matrix alone (same block code and chunking, fixed reduction order).
@@ -188,8 +194,8 @@ int mtc_gemv_f32_group(const mtc_stream_desc* const* descs, int n, const float* 
  * 1. mtc_gemv_batch_plan(items, n, M, NULL, 0, NULL, 0, &plan_bytes, &ws_bytes) reports the
  *    sizes (host only).
  * 2. The caller provides a zero-filled device workspace of ws_bytes (256-byte aligned; split-K
- *    partials and counters of the members with several row chunks; the kernels leave the
- *    counters at zero again) and a 64-byte aligned host buffer of plan_bytes, and calls
+ *    partials and counters of the members with several row chunks, and X staged for M >= 5;
+ *    the kernels leave the counters at zero again) and a 64-byte aligned host buffer of plan_bytes, and calls
  *    mtc_gemv_batch_plan again with both: it writes the plan (descriptors, X/Y pointers,
  *    workspace slices, the member of each grid block) into the host buffer.
  * 3. The caller copies the plan byte for byte into a 64-byte aligned device buffer (and keeps

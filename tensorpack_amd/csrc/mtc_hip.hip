@@ -344,7 +344,7 @@ constexpr int kStepGroups = 4;              // column groups one decode step cov
 constexpr int kStepLanes = 16;              // lanes per column group in a step
 constexpr int kStepWords = 16;              // words per step record
 // Most waves a decode block has (the LDS of the cross-wave reduction is sized for it).
-__host__ __device__ constexpr int gemv_waves(int MT) { return MT <= 2 ? 16 : 8; }
+__host__ __device__ constexpr int gemv_waves(int MT) { return MT == 4 ? 8 : 16; }
 constexpr int kFewSteps = 16;
 constexpr int kSmallRows = 1024;
 constexpr int kGemvBlocksPerUnit = kGroups / kStepGroups;
@@ -367,6 +367,7 @@ struct GemvShape {
 };
 inline GemvShape gemv_shape(int MT, const mtc_stream_desc* d) {
   const bool perm = d->row_perm != nullptr;
+  if (MT > 4) return {16, kMaxChunkRows, false, false};   // matrix core
   if (MT > 2) return {8, kMaxChunkRows, false, false};
   if (d->fixed_steps > kFewSteps) return {16, kMaxChunkRows, true, perm && d->K <= kMaxChunkRows};
   if (d->chunk_rows <= kSmallRows) return {4, kSmallRows, true, perm && d->K <= kSmallRows};
@@ -392,6 +393,85 @@ __device__ __forceinline__ float slot_sum(float v) {
   return v;
 }
 
+
+// The block's outputs from the cross-wave reduction buffer red[wave][slot][m][c] (all waves'
+// values in place, after a barrier). The block covers H column halves of its unit's panel
+// (16 columns each, from half cb; its waves split evenly over them): Y directly for a
+// single-chunk stream; otherwise the block's partial, and the last block of each (M tile,
+// panel) sums the unit partials into Y.
+template <int MT, int W, int H>
+__device__ __forceinline__ void gemv_store(const mtc_stream_desc& d, const float* red, const int u, const int cb,
+                                           float* __restrict__ Y, int64_t ldy, int M, float* __restrict__ part,
+                                           uint32_t* __restrict__ counters) {
+  constexpr int T = 64 * W, WH = W / H, CH = kStepGroups * kGroup;   // waves and columns per half
+  constexpr int blocks_per_chunk = kGemvBlocksPerUnit / H;
+  const int tid = threadIdx.x;
+  const int mt = blockIdx.y, m0 = mt * MT;
+  const int n_units = d.n_panels * d.n_chunks;
+  const int panel = u / d.n_chunks;
+  constexpr int nout = MT * H * CH;
+  auto sum_of = [&](int i, int& m, int& pc) __attribute__((always_inline)) {
+    m = i / (H * CH);
+    const int rest = i - m * (H * CH);
+    const int hh = rest / CH, gc = rest - hh * CH;
+    const int g2 = gc / kGroup, c = gc - g2 * kGroup;
+    pc = (cb + hh) * CH + gc;                          // column within the panel
+    float v = 0.0f;
+#pragma unroll
+    for (int w2 = 0; w2 < WH; ++w2) v += red[(((hh * WH + w2) * kStepGroups + g2) * MT + m) * kGroup + c];
+    return v;
+  };
+
+  if (d.n_chunks == 1) {
+    for (int i = tid; i < nout; i += T) {
+      int m, pc;
+      const float v = sum_of(i, m, pc);
+      if (m0 + m < M) {
+        int col = panel * kPanel + pc;
+        if (d.col_perm) col = d.col_perm[col];
+        Y[(int64_t)(m0 + m) * ldy + col] = v;
+      }
+    }
+    return;
+  }
+
+  // split-K over chunks: deterministic last-block reduction per (M tile, panel).
+  // Partials and the counter use relaxed device-scope atomics, which the hardware performs
+  // past the XCD-private L2s; ordering comes from waiting for the partial stores to complete
+  // before the counter add. (Acquire/release fences at device scope would write back and
+  // invalidate the whole L2 of the XCD instead, costing tens of microseconds per call.)
+  constexpr int n_part = MT * kPanel;
+  float* mine = part + ((size_t)mt * n_units + u) * n_part;
+  for (int i = tid; i < nout; i += T) {
+    int m, pc;
+    const float v = sum_of(i, m, pc);
+    __hip_atomic_store(mine + m * kPanel + pc, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores are complete
+  __syncthreads();
+  __shared__ int last;
+  if (tid == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(&counters[mt * d.n_panels + panel], 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    last = (prev == (uint32_t)(d.n_chunks * blocks_per_chunk - 1));
+  }
+  __syncthreads();
+  if (!last) return;
+  const float* pp = part + ((size_t)mt * n_units + (size_t)panel * d.n_chunks) * n_part;
+  for (int i = tid; i < n_part; i += T) {
+    float v = 0.0f;
+    for (int c = 0; c < d.n_chunks; ++c)
+      v += __hip_atomic_load(pp + (size_t)c * n_part + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int m = i / kPanel, cc = i - m * kPanel;
+    if (m0 + m < M) {
+      int col = panel * kPanel + cc;
+      if (d.col_perm) col = d.col_perm[col];
+      Y[(int64_t)(m0 + m) * ldy + col] = v;
+    }
+  }
+  if (tid == 0)
+    __hip_atomic_store(&counters[mt * d.n_panels + panel], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // One decode block of matrix `d`: block id `bid` along the grid's x (the y index is the M tile),
 // NW waves. LG: the code for X rows gathered in LDS is present; lg: this matrix uses it
@@ -626,64 +706,370 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
       for (int c = 0; c < kGroup; ++c) red[((wave * kStepGroups + g) * MT + m) * kGroup + c] = acc[m][c];
   }
   __syncthreads();
+  gemv_store<MT, W, 1>(d, red, u, cb, Y, ldy, M, part, counters);
+}
 
-  constexpr int nout = MT * kStepGroups * kGroup;
-  if (d.n_chunks == 1) {
-    for (int i = tid; i < nout; i += T) {
-      const int m = i / (kStepGroups * kGroup), gc = i - m * (kStepGroups * kGroup);
-      const int g2 = gc / kGroup, c = gc - g2 * kGroup;
-      float v = 0.0f;
+// ---------------------------------------------------------------------------
+// Decode blocks for M tiles of 8 or 16 rows, on the matrix core.
+// v_mfma_f32_4x4x1_16b_f32 runs 16 independent 4x4 outer products per wave: block b (lanes
+// 4b .. 4b+3) adds A_b (x) B_b to its 4x4 accumulator, with A_b[i] from lane 4b + i, B_b[j]
+// from lane 4b + j, and D_b[i][j] held by lane 4b + j in accumulator register i. A lane
+// chunk (8 rows x 4 columns of one column group, rows chosen by its leaf) is one such block:
+// lane 4b + j decodes the chunk's column j (8 codes) into weights s * q and, for row r =
+// 0..7 in turn, multiplies them with X[m0 + 4h + j][row r] for every 4-row slice h of the M
+// tile (one accumulator per slice, so consecutive MFMAs are independent). A step record's
+// 4 slots x 16 chunks take four passes of 16 chunks: in pass p, lane (slot g, li) takes
+// chunk 4p + li / 4 of slot g's bucket, column li % 4. The weights equal the dequantized
+// W_hat (one fma rounding of s * (u - 2^(P-1)), exact in q), and every product accumulates
+// in fp32. The lane -> chunk order, and so every sum, is the same for M tiles of 8 and 16
+// rows: the tile height only sets how many X rows one block stages.
+// X is staged in LDS as xs[r][j][h] = X[m0 + 4h + j][row r of the unit], so the slices a
+// lane needs for one row are adjacent (one 16- or 8-byte read). A staging launch writes X
+// transposed into that order once per call (xt[k][j][h], in the workspace), so a block
+// gathers each of its rows (through row_perm) as one 32- or 64-byte piece; without it
+// (grouped launches) each block gathers its rows from X itself, 4 bytes at a time.
+// One block covers a whole unit (both 16-column halves of its panel, waves 0-7 and 8-15),
+// so that a unit's X rows are staged once.
+// ---------------------------------------------------------------------------
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+constexpr int kMfmaWaves = 16;
+// 16-byte X pieces per thread when a block stages its rows: kc * MT floats fit the LDS next to
+// the reduction buffer (at most 144 KB for 16-row tiles), over 1024 threads.
+constexpr int kMfmaStageIters = 9;
+
+// X of one M tile transposed for the matrix core: xt[k][j][h] = X[m0 + 4h + j][k] (original
+// row order, k < K; M rows past M are zero). Thread k of the launch writes row k's MT values.
+__device__ __forceinline__ int mfma_slot(int m, int MT) { return (m & 3) * (MT / 4) + (m >> 2); }
+constexpr int kStageThreads = 64;
+
+template <int MT>
+__device__ __forceinline__ void stage_xt_block(int K, const float* __restrict__ X, int64_t ldx, int M,
+                                               float* __restrict__ xt) {
+  const int k = (int)blockIdx.x * kStageThreads + (int)threadIdx.x;
+  if (k >= K) return;
+  const int m0 = (int)blockIdx.y * MT;
+  float v[MT];
 #pragma unroll
-      for (int w2 = 0; w2 < W; ++w2) v += red[((w2 * kStepGroups + g2) * MT + m) * kGroup + c];
-      if (m0 + m < M) {
-        int col = panel * kPanel + (cb * kStepGroups + g2) * kGroup + c;
-        if (d.col_perm) col = d.col_perm[col];
-        Y[(int64_t)(m0 + m) * ldy + col] = v;
+  for (int m = 0; m < MT; ++m) v[mfma_slot(m, MT)] = m0 + m < M ? X[(int64_t)(m0 + m) * ldx + k] : 0.0f;
+  float4* o = reinterpret_cast<float4*>(xt + ((size_t)blockIdx.y * K + k) * MT);
+#pragma unroll
+  for (int i = 0; i < MT / 4; ++i) o[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+}
+
+template <int MT>
+__global__ __launch_bounds__(kStageThreads) void k_gemv_stage_x(int K, const float* __restrict__ X, int64_t ldx,
+                                                                int M, float* __restrict__ xt) {
+  stage_xt_block<MT>(K, X, ldx, M, xt);
+}
+
+// A lane's loads of one pass: the 64-bit window(s) holding its column's codes (two loads for
+// every kind: leaf 0's and leaf 1's windows for two 4x4 leaves; the two halves of a 128-bit
+// window for P = 16; the window and a load past the buffer's end, which reads zeros, for
+// other widths), the leaf word(s) and, with fp32 scales, the leaf scale(s). Same load count
+// for every kind, so the compiler's in-order waits stay exact.
+struct MfmaPass {
+  u32x4_t w;
+  uint32_t lw0, lw1;
+  float fs0, fs1;
+};
+
+template <bool FS>
+__device__ __forceinline__ void mfma_load(__amdgpu_buffer_rsrc_t pay_r, __amdgpu_buffer_rsrc_t lw_r,
+                                          __amdgpu_buffer_rsrc_t fs_r, uint32_t key, uint32_t pay, uint32_t leaf,
+                                          uint32_t t, uint32_t j, MfmaPass& r) {
+  const uint32_t P = key >> 8, ls = key & 0xFFu;
+  const uint32_t ob = (pay + t * P) << 2;            // payload byte offset of the chunk
+  uint32_t o0, o1;
+  if (ls == 2) {                                     // codes 4j.. of leaf 0 and 16 + 4j.. of leaf 1
+    o0 = ob + (((4 * j * P) >> 5) << 2);
+    o1 = ob + ((((16 + 4 * j) * P) >> 5) << 2);
+  } else if (P == 16) {                              // codes 8j .. 8j + 7: 128 bits at dword 4j
+    o0 = ob + 16 * j;
+    o1 = o0 + 8;
+  } else {                                           // codes 8j .. 8j + 7: 8P <= 64 bits
+    o0 = ob + (((8 * j * P) >> 5) << 2);
+    o1 = kOutOfRange;
+  }
+  const u32x2_t a = __builtin_amdgcn_raw_buffer_load_b64(pay_r, o0, 0, kNT);
+  const u32x2_t b = __builtin_amdgcn_raw_buffer_load_b64(pay_r, o1, 0, kNT);
+  r.w = u32x4_t{a.x, a.y, b.x, b.y};
+  const uint32_t l0 = leaf + (ls == 2 ? 2 * t : t >> (ls - 3));
+  const uint32_t b1 = ls == 2 ? (l0 + 1) << 2 : kOutOfRange;   // second 4x4 leaf, if any
+  r.lw0 = __builtin_amdgcn_raw_buffer_load_b32(lw_r, l0 << 2, 0, 0);
+  r.lw1 = __builtin_amdgcn_raw_buffer_load_b32(lw_r, b1, 0, 0);
+  if constexpr (FS) {
+    r.fs0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(fs_r, l0 << 2, 0, 0));
+    r.fs1 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(fs_r, b1, 0, 0));
+  } else {
+    r.fs0 = r.fs1 = 0.0f;
+  }
+}
+
+// NC codes of width P, the first at bit `o` (0..31) of the 64-bit window (lo, hi), as floats.
+// Z: o is known to be 0 for this kind.
+template <int P, int NC, bool Z>
+__device__ __forceinline__ void window_codes(uint32_t lo, uint32_t hi, uint32_t o, float* u) {
+  const uint32_t a = Z ? lo : __builtin_amdgcn_alignbit(hi, lo, o);   // window bits o .. o + 31
+  const uint32_t b = Z ? hi : hi >> o;                                // window bits o + 32 .. 63
+  constexpr uint32_t mask = (1u << P) - 1u;
+#pragma unroll
+  for (int r = 0; r < NC; ++r) {
+    const int s = r * P;
+    uint32_t v;
+    if (s + P <= 32) v = (a >> s) & mask;
+    else if (s >= 32) v = (b >> (s - 32)) & mask;
+    else v = __builtin_amdgcn_alignbit(b, a, s) & mask;
+    u[r] = (float)v;
+  }
+}
+
+// A lane's column of its chunk in one pass of kind (S, P): the 8 weights (zero when the
+// lane's chunk is not in the bucket, `on` false, or its leaf is padding) and the unit rows
+// they sit on (rows row0 .. row0 + 3 and row1 .. row1 + 3).
+template <int S, int P>
+__device__ __forceinline__ void mfma_decode(const MfmaPass& r, bool on, uint32_t t, uint32_t j, uint32_t rb_mask,
+                                            bool fp32_scales, float (&wq)[8], int& row0, int& row1) {
+  static_assert(S == 4 || S == 8, "leaf sizes 16 and 32 take the S = 8 path");
+  constexpr float off = (float)(1 << (P - 1));
+  float u[8];
+  float s0, s1;
+  if constexpr (S == 4) {
+    window_codes<P, 4, (P >= 8)>(r.w.x, r.w.y, (4 * j * P) & 31u, u);
+    window_codes<P, 4, (P >= 8)>(r.w.z, r.w.w, ((16 + 4 * j) * P) & 31u, u + 4);
+    const LeafInfo a = leaf_info_v(r.lw0, fp32_scales, r.fs0), b = leaf_info_v(r.lw1, fp32_scales, r.fs1);
+    row0 = a.row;
+    row1 = b.row;
+    s0 = (on && !a.pad) ? a.scale : 0.0f;
+    s1 = (on && !b.pad) ? b.scale : 0.0f;
+  } else {
+    if constexpr (P == 16) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        u[2 * k] = (float)(r.w[k] & 0xFFFFu);
+        u[2 * k + 1] = (float)(r.w[k] >> 16);
+      }
+    } else {
+      window_codes<P, 8, (P == 4 || P == 8)>(r.w.x, r.w.y, (8 * j * P) & 31u, u);
+    }
+    const LeafInfo a = leaf_info_v(r.lw0, fp32_scales, r.fs0);
+    row0 = a.row + 8 * (int)(t & rb_mask);
+    row1 = row0 + 4;
+    s0 = s1 = (on && !a.pad) ? a.scale : 0.0f;
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const float s = k < 4 ? s0 : s1;
+    wq[k] = __builtin_fmaf(u[k], s, -(s * off));     // s * (u - off): s * off is exact
+  }
+}
+
+// LDS of a matrix-core decode block: X rows [kc][MT] and the cross-wave reduction.
+__host__ __device__ constexpr size_t gemv_mfma_lds_floats(int MT, int kc) {
+  return (size_t)MT * kc + (size_t)kMfmaWaves * kStepGroups * MT * kGroup;
+}
+
+template <int MT, bool FS>
+__device__ __forceinline__ void gemv_block_mfma(const mtc_stream_desc& d, const int bid, const float* __restrict__ X,
+                                                int64_t ldx, float* __restrict__ Y, int64_t ldy, int M,
+                                                float* __restrict__ part, uint32_t* __restrict__ counters,
+                                                const float* __restrict__ xt) {
+  static_assert(MT == 8 || MT == 16, "M tiles of 8 or 16 rows");
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  constexpr int W = kMfmaWaves, T = 64 * W, BPU = kGemvBlocksPerUnit, NP = kStepLanes / 4, Q = MT / 4;
+  constexpr int WH = W / BPU;                         // waves per column half
+  const int kc = d.chunk_rows;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n_units = d.n_panels * d.n_chunks;
+  const int u = bid;                                  // grid x: one block per unit
+  if (u >= n_units) return;                           // padding block of the XCD rounding
+  const int cb = wave / WH, wl = wave % WH;           // this wave's column half, its index there
+  const int m0 = blockIdx.y * MT;
+  const int chunk = u % d.n_chunks;
+  const int kb = chunk * kc;
+  const int rows = min(kc, d.K - kb);
+  float* xs = smem;                                   // [kc][4 j][Q h]
+  float* red = xs + MT * kc;                          // [waves][4 slots][MT][4]
+  const ci32p hdr = (ci32p)(d.unit_hdr + kUnitHdr * u);
+
+  const int F = d.fixed_steps;
+  const int blk = u * BPU + cb;
+  const uint32_t null_rec = (uint32_t)(n_units * BPU) * (uint32_t)F;
+  const int g = lane / kStepLanes, li = lane % kStepLanes;
+  const uint32_t j = (uint32_t)(li & 3), cq = (uint32_t)(li >> 2);   // column in the chunk, chunk in the pass
+  const __amdgpu_buffer_rsrc_t rec_r = buffer_of(d.steps, d.n_steps * kStepWords * 4);
+  const __amdgpu_buffer_rsrc_t pay_r = buffer_of(d.payload, d.payload_dwords * 4);
+  const __amdgpu_buffer_rsrc_t lw_r = buffer_of(d.leaf_word, d.n_leaves * 4);
+  const __amdgpu_buffer_rsrc_t fs_r =
+      buffer_of(FS ? static_cast<const void*>(d.leaf_scale) : static_cast<const void*>(d.leaf_word), d.n_leaves * 4);
+  const int nrec = hdr[28 + 2 * cb];
+  const uint32_t ovf = (uint32_t)hdr[27 + 2 * cb];
+  // record index of the block's i-th record: the first F at block-computable places, the rest
+  // (F = 48 only) in the unit's overflow list; past the block's end, the null record
+  auto rec_of = [&](int i) __attribute__((always_inline)) {
+    return i < F ? (uint32_t)(blk * F + i) : i < nrec ? ovf + (uint32_t)(i - F) : null_rec;
+  };
+  auto slot_of = [&](uint32_t r) __attribute__((always_inline)) {
+    return __builtin_amdgcn_raw_buffer_load_b128(rec_r, (r * kStepWords + 4 * g) * 4, 0, 0);
+  };
+  struct Rec {
+    MfmaPass p[NP];
+    uint32_t key, J, valid;
+  };
+  auto fetch = [&](const u32x4_t f, Rec& r) __attribute__((always_inline)) {
+    r.key = __builtin_amdgcn_readfirstlane(f.w & 0xFFFFu);
+    r.J = f.w >> 16;
+    r.valid = f.z;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const uint32_t c = 4 * p + cq;
+      const uint32_t t = c < f.z ? kStepLanes * r.J + c : 0u;
+      mfma_load<FS>(pay_r, lw_r, fs_r, r.key, f.x, f.y, t, j, r.p[p]);
+    }
+  };
+
+  // ---- the first records' loads, then X rows of the unit into LDS ----
+  const u32x4_t f0 = slot_of(rec_of(wl));
+  u32x4_t f1 = slot_of(rec_of(wl + WH));
+  Rec cur, nxt;
+  fetch(f0, cur);
+  if (xt) {                                           // transposed X: one MT-float piece per row
+    // All of a thread's row indices are loaded, then all its pieces, then stored: the loads
+    // overlap instead of running one dependent pair at a time. kc * MT fits the LDS, so a
+    // thread has at most kMfmaStageIters pieces.
+    constexpr int L = MT / 4;                         // threads per row (16 bytes each)
+    const float* src = xt + (size_t)blockIdx.y * d.K * MT;
+    int kr[kMfmaStageIters];
+#pragma unroll
+    for (int it = 0; it < kMfmaStageIters; ++it) {
+      const int i = it * T + tid, r = i / L;
+      kr[it] = r < rows ? (d.row_perm ? d.row_perm[kb + r] : kb + r) : -1;
+    }
+    float4 v[kMfmaStageIters];
+#pragma unroll
+    for (int it = 0; it < kMfmaStageIters; ++it) {
+      const int i = it * T + tid, part4 = i % L;
+      v[it] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (kr[it] >= 0) v[it] = *reinterpret_cast<const float4*>(src + (size_t)kr[it] * MT + 4 * part4);
+    }
+#pragma unroll
+    for (int it = 0; it < kMfmaStageIters; ++it) {
+      const int i = it * T + tid;
+      if (i < kc * L) *reinterpret_cast<float4*>(xs + 4 * i) = v[it];
+    }
+  } else {
+    const int r4 = 4 * tid;                           // this thread's 4 rows (kc <= 4096 = 4T)
+    if (r4 < kc) {
+      int4 kk = make_int4(kb + r4, kb + r4 + 1, kb + r4 + 2, kb + r4 + 3);
+      if (d.row_perm && r4 < rows) kk = *reinterpret_cast<const int4*>(d.row_perm + kb + r4);
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const float* xrow = X + (int64_t)min(m0 + m, M - 1) * ldx;
+        float4 xv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (r4 < rows && m0 + m < M) xv = make_float4(xrow[kk.x], xrow[kk.y], xrow[kk.z], xrow[kk.w]);
+        float* o = xs + r4 * MT + mfma_slot(m, MT);
+        o[0] = xv.x;
+        o[MT] = xv.y;
+        o[2 * MT] = xv.z;
+        o[3 * MT] = xv.w;
       }
     }
-    return;
+  }
+  lds_barrier();                                      // record loads stay in flight
+
+  f32x4_t acc[Q];
+#pragma unroll
+  for (int h = 0; h < Q; ++h) acc[h] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const float* xl = xs + (int)j * Q;                  // this lane's M rows m0 + 4h + j
+  auto compute = [&](const Rec& r) __attribute__((always_inline)) {
+    // passes holding any chunk of the record (slots share a kind, not a chunk count)
+    const uint32_t vmax = max(max(__builtin_amdgcn_readlane(r.valid, 0), __builtin_amdgcn_readlane(r.valid, 16)),
+                              max(__builtin_amdgcn_readlane(r.valid, 32), __builtin_amdgcn_readlane(r.valid, 48)));
+    const uint32_t key = r.key, ls = key & 0xFFu;
+    const uint32_t rb_mask = ls > 3 ? (1u << (ls - 3)) - 1u : 0u;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      if ((uint32_t)(4 * p) >= vmax) break;
+      const uint32_t c = 4 * p + cq;
+      const bool on = c < r.valid;
+      const uint32_t t = on ? kStepLanes * r.J + c : 0u;
+      float wq[8];
+      int row0 = 0, row1 = 0;
+      switch (ls == 2 ? key : (key & ~0xFFu) | 3u) {   // sizes 8, 16, 32 share a case
+#define MTC_CASE(S, P) \
+  case MTC_BUCKET_KEY(S, P): \
+    mfma_decode<S, P>(r.p[p], on, t, j, rb_mask, FS, wq, row0, row1); \
+    break;
+        MTC_FOR_EACH_WIDTH(8, MTC_CASE)
+        MTC_FOR_EACH_WIDTH(4, MTC_CASE)
+#undef MTC_CASE
+        default:
+#pragma unroll
+          for (int k = 0; k < 8; ++k) wq[k] = 0.0f;
+          break;
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int row = k < 4 ? row0 + k : row1 + (k - 4);
+        if constexpr (Q == 4) {
+          const float4 xq = *reinterpret_cast<const float4*>(xl + row * MT);
+          acc[0] = __builtin_amdgcn_mfma_f32_4x4x1f32(xq.x, wq[k], acc[0], 0, 0, 0);
+          acc[1] = __builtin_amdgcn_mfma_f32_4x4x1f32(xq.y, wq[k], acc[1], 0, 0, 0);
+          acc[2] = __builtin_amdgcn_mfma_f32_4x4x1f32(xq.z, wq[k], acc[2], 0, 0, 0);
+          acc[3] = __builtin_amdgcn_mfma_f32_4x4x1f32(xq.w, wq[k], acc[3], 0, 0, 0);
+        } else {
+          const float2 xq = *reinterpret_cast<const float2*>(xl + row * MT);
+          acc[0] = __builtin_amdgcn_mfma_f32_4x4x1f32(xq.x, wq[k], acc[0], 0, 0, 0);
+          acc[1] = __builtin_amdgcn_mfma_f32_4x4x1f32(xq.y, wq[k], acc[1], 0, 0, 0);
+        }
+      }
+    }
+  };
+  // two records in flight: while one is computed the next one's loads (and the record
+  // after that's slot) are outstanding
+  for (int i = wl; i < nrec; i += 2 * WH) {
+    u32x4_t f2 = slot_of(rec_of(i + 2 * WH));
+    fetch(f1, nxt);
+    compute(cur);
+    if (i + WH >= nrec) break;
+    f1 = slot_of(rec_of(i + 3 * WH));
+    fetch(f2, cur);
+    compute(nxt);
   }
 
-  // split-K over chunks: deterministic last-block reduction per (M tile, panel).
-  // Partials and the counter use relaxed device-scope atomics, which the hardware performs
-  // past the XCD-private L2s; ordering comes from waiting for the partial stores to complete
-  // before the counter add. (Acquire/release fences at device scope would write back and
-  // invalidate the whole L2 of the XCD instead, costing tens of microseconds per call.)
-  constexpr int n_part = MT * kPanel;
-  float* mine = part + ((size_t)mt * n_units + u) * n_part;
-  for (int i = tid; i < nout; i += T) {
-    const int m = i / (kStepGroups * kGroup), gc = i - m * (kStepGroups * kGroup);
-    const int g2 = gc / kGroup, c = gc - g2 * kGroup;
-    float v = 0.0f;
+  // ---- reduce: the 4 chunks of each slot (lanes li, li + 4, li + 8, li + 12), then the waves ----
 #pragma unroll
-    for (int w2 = 0; w2 < W; ++w2) v += red[((w2 * kStepGroups + g2) * MT + m) * kGroup + c];
-    __hip_atomic_store(mine + m * kPanel + (cb * kStepGroups + g2) * kGroup + c, v, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores are complete
-  __syncthreads();
-  __shared__ int last;
-  if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(&counters[mt * d.n_panels + panel], 1u, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-    last = (prev == (uint32_t)(d.n_chunks * BPU - 1));
-  }
-  __syncthreads();
-  if (!last) return;
-  const float* pp = part + ((size_t)mt * n_units + (size_t)panel * d.n_chunks) * n_part;
-  for (int i = tid; i < n_part; i += T) {
-    float v = 0.0f;
-    for (int c = 0; c < d.n_chunks; ++c)
-      v += __hip_atomic_load(pp + (size_t)c * n_part + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int m = i / kPanel, cc = i - m * kPanel;
-    if (m0 + m < M) {
-      int col = panel * kPanel + cc;
-      if (d.col_perm) col = d.col_perm[col];
-      Y[(int64_t)(m0 + m) * ldy + col] = v;
+  for (int h = 0; h < Q; ++h)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = acc[h][i];
+      v += row_shr<4>(v);
+      v += row_shr<8>(v);
+      acc[h][i] = v;
     }
+  if (li >= kStepLanes - 4) {
+#pragma unroll
+    for (int h = 0; h < Q; ++h)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[((wave * kStepGroups + g) * MT + 4 * h + i) * kGroup + (int)j] = acc[h][i];
   }
-  if (tid == 0)
-    __hip_atomic_store(&counters[mt * d.n_panels + panel], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  gemv_store<MT, W, BPU>(d, red, u, 0, Y, ldy, M, part, counters);
+}
+
+// The block code of an M tile: the matrix core for tiles of 8 or 16 rows (X staged transposed
+// in xt, or gathered by the block from X when xt is null), else the vector path.
+template <int MT, bool FS, bool LG, int NW, int KC>
+__device__ __forceinline__ void gemv_any(const mtc_stream_desc& d, const int bid, const float* __restrict__ X,
+                                         int64_t ldx, float* __restrict__ Y, int64_t ldy, int M,
+                                         float* __restrict__ part, uint32_t* __restrict__ counters, const bool lg,
+                                         const float* __restrict__ xt) {
+  if constexpr (MT >= 8) {
+    static_assert(NW == kMfmaWaves, "matrix-core decode blocks have 16 waves");
+    gemv_block_mfma<MT, FS>(d, bid, X, ldx, Y, ldy, M, part, counters, xt);
+  } else {
+    gemv_block<MT, FS, LG, NW, KC>(d, bid, X, ldx, Y, ldy, M, part, counters, lg);
+  }
 }
 
 // At least 4 waves per SIMD: a 16-wave block fills a CU's 4 SIMDs; two 8-wave blocks
@@ -691,8 +1077,9 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
 template <int MT, bool FS, bool LG, int NW, int KC>
 __global__ __launch_bounds__(64 * NW, 4) void k_gemv(const mtc_stream_desc d, const float* __restrict__ X,
                                                   int64_t ldx, float* __restrict__ Y, int64_t ldy, int M,
-                                                  float* __restrict__ part, uint32_t* __restrict__ counters) {
-  gemv_block<MT, FS, LG, NW, KC>(d, blockIdx.x, X, ldx, Y, ldy, M, part, counters);
+                                                  float* __restrict__ part, uint32_t* __restrict__ counters,
+                                                  const float* __restrict__ xt) {
+  gemv_any<MT, FS, LG, NW, KC>(d, blockIdx.x, X, ldx, Y, ldy, M, part, counters, true, xt);
 }
 
 // Up to kMaxGroup single-chunk matrices of one block shape that read the same X, in one launch:
@@ -712,8 +1099,8 @@ __global__ __launch_bounds__(64 * NW, 4) void k_gemv_group(const GemvGroup g, co
   int i = 0;
 #pragma unroll
   for (int k = 1; k < kMaxGroup; ++k) i += (int)blockIdx.x >= g.start[k];
-  gemv_block<MT, FS, LG, NW, KC>(g.d[i], (int)blockIdx.x - g.start[i], X, ldx, g.Y[i], g.ldy[i], M, nullptr,
-                                 nullptr);
+  gemv_any<MT, FS, LG, NW, KC>(g.d[i], (int)blockIdx.x - g.start[i], X, ldx, g.Y[i], g.ldy[i], M, nullptr,
+                               nullptr, true, nullptr);
 }
 
 // Any number of matrices, each with its own X and Y. The plan (built on the host by
@@ -729,6 +1116,7 @@ struct BatchItem {
   float* Y;
   float* part;          // split-K partials and counters in the caller's workspace (n_chunks > 1)
   uint32_t* counters;
+  float* xt;            // X staged for the matrix core (M tiles of 8 or 16 rows)
   int64_t ldx;
   int64_t ldy;
   int32_t start;        // first block of the item in its shape's launch
@@ -750,7 +1138,7 @@ struct BatchHeader {
   int32_t M;
   int32_t mt;           // rows per M tile
   int32_t fs;           // fp32 leaf scales
-  int32_t reserved;
+  int32_t stage_blocks_x;   // grid x of the X staging (matrix-core M tiles)
   int32_t class_blocks[kShapeClasses];
   uint64_t lds_bytes;
   uint64_t items_off;   // byte offset of the BatchItem array
@@ -766,8 +1154,15 @@ __global__ __launch_bounds__(64 * NW, 4) void k_gemv_batch(const BatchItem* __re
                                                         const uint32_t* __restrict__ block_item, int M) {
   const int b = blockIdx.x;
   const BatchItem& it = items[block_item[b]];
-  gemv_block<MT, FS, LG, NW, KC>(it.d, b - it.start, it.X, it.ldx, it.Y, it.ldy, M, it.part, it.counters,
-                                 it.lg != 0);
+  gemv_any<MT, FS, LG, NW, KC>(it.d, b - it.start, it.X, it.ldx, it.Y, it.ldy, M, it.part, it.counters,
+                               it.lg != 0, it.xt);
+}
+
+// X of every member staged for the matrix core (grid z: the member).
+template <int MT>
+__global__ __launch_bounds__(kStageThreads) void k_gemv_stage_x_batch(const BatchItem* __restrict__ items, int M) {
+  const BatchItem& it = items[blockIdx.z];
+  stage_xt_block<MT>(it.d.K, it.X, it.ldx, M, it.xt);
 }
 
 // The batch kernel of a shape class (the LDS gather is a per-member flag there).
@@ -776,7 +1171,9 @@ const void* gemv_batch_kernel(bool fs, int cls) {
 #define MTC_BATCH_K(LG_, NW_, KC_) \
   (fs ? reinterpret_cast<const void*>(&k_gemv_batch<MT, true, LG_, NW_, KC_>) \
       : reinterpret_cast<const void*>(&k_gemv_batch<MT, false, LG_, NW_, KC_>))
-  if constexpr (MT > 2) {
+  if constexpr (MT > 4) {
+    return MTC_BATCH_K(false, 16, kMaxChunkRows);
+  } else if constexpr (MT > 2) {
     return MTC_BATCH_K(false, 8, kMaxChunkRows);
   } else {
     if (cls == 0) return MTC_BATCH_K(true, 4, kSmallRows);
@@ -794,7 +1191,9 @@ const void* gemv_kernel(bool fs, const GemvShape& s) {
                : reinterpret_cast<const void*>(&k_gemv_group<MT, false, LG_, NW_, KC_>)) \
          : (fs ? reinterpret_cast<const void*>(&k_gemv<MT, true, LG_, NW_, KC_>) \
                : reinterpret_cast<const void*>(&k_gemv<MT, false, LG_, NW_, KC_>)))
-  if constexpr (MT > 2) {
+  if constexpr (MT > 4) {
+    return MTC_GEMV_K(false, 16, kMaxChunkRows);
+  } else if constexpr (MT > 2) {
     return MTC_GEMV_K(false, 8, kMaxChunkRows);
   } else {
     if (s.nw == 16) return s.lg ? MTC_GEMV_K(true, 16, kMaxChunkRows) : MTC_GEMV_K(false, 16, kMaxChunkRows);
@@ -850,20 +1249,48 @@ hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 using mtc::host::device_lds_limit;
 
-int gemv_mt(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : 4; }
+// Rows per M tile: 1, 2 or 4 on the vector path; 8, or 16 when 16 staged X rows of a unit fit
+// on chip (chunk_rows <= kMfmaTile16Rows), on the matrix core (the sums are the same for both).
+constexpr int kMfmaTile16Rows = 2048;
+int gemv_mt(int M, int chunk_rows) {
+  return M <= 2 ? M : M <= 4 ? 4 : (M <= 8 || chunk_rows > kMfmaTile16Rows) ? 8 : 16;
+}
 
-size_t gemv_ws_layout(const mtc_stream_desc* d, int M, size_t* counters_bytes) {
-  const int mt = gemv_mt(M);
+// Workspace of a decode call: split-K counters (counters_bytes, from offset 0) and partials when
+// K is split over row chunks, then, for matrix-core M tiles, X staged per M tile (from xt_off).
+size_t gemv_ws_layout(const mtc_stream_desc* d, int M, int mt, size_t* counters_bytes, size_t* xt_off = nullptr) {
   const size_t n_mt = (size_t)((M + mt - 1) / mt);
   const size_t cb = ((n_mt * d->n_panels * sizeof(uint32_t)) + 255) & ~(size_t)255;
   if (counters_bytes) *counters_bytes = cb;
-  if (d->n_chunks == 1) return 0;
-  return cb + n_mt * (size_t)d->n_panels * d->n_chunks * mt * kPanel * sizeof(float);
+  size_t end = d->n_chunks == 1 ? 0 : cb + n_mt * (size_t)d->n_panels * d->n_chunks * mt * kPanel * sizeof(float);
+  if (mt > 4) {
+    end = (end + 255) & ~(size_t)255;
+    if (xt_off) *xt_off = end;
+    end += n_mt * (size_t)d->K * mt * sizeof(float);
+  }
+  return end;
+}
+
+// A matrix-core block stages at most kMfmaStageIters 16-byte X pieces per thread.
+bool mfma_rows_fit(int mt, int chunk_rows) {
+  return mt <= 4 || (size_t)chunk_rows * (mt / 4) <= (size_t)kMfmaStageIters * 64 * kMfmaWaves;
+}
+
+// Grid x of the X staging of one M tile.
+unsigned stage_x_blocks(const mtc_stream_desc* d) { return (unsigned)((d->K + kStageThreads - 1) / kStageThreads); }
+
+// Decode blocks of one M tile: one per unit on the matrix core; two per unit on the vector
+// path, with the unit count rounded up to whole XCD rounds.
+int gemv_blocks(const mtc_stream_desc* d, int mt) {
+  const int n_units = d->n_panels * d->n_chunks;
+  if (mt > 4) return n_units;
+  return (n_units + kXcds - 1) / kXcds * kXcds * kGemvBlocksPerUnit;
 }
 
 // LDS of a decode block: X rows, their 4- and 8-row sums, the cross-wave reduction and,
 // for the LDS gather, whole X rows.
 size_t gemv_lds_bytes(int K, int chunk_rows, bool perm, int MT) {
+  if (MT > 4) return gemv_mfma_lds_floats(MT, chunk_rows) * 4;
   const size_t kc = (size_t)chunk_rows;
   const size_t raw = gemv_lds_gather(MT, perm, K) ? (size_t)MT * K : 0;
   return ((size_t)MT * (kc + (gemv_sum4(MT) ? kc / 4 : 0) + kc / 8) +
@@ -876,13 +1303,21 @@ size_t gemv_lds_bytes(const mtc_stream_desc* d, int MT) {
 template <int MT>
 int launch_gemv(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y, int64_t ldy, int M, void* ws,
                 hipStream_t st) {
-  size_t cb = 0;
-  gemv_ws_layout(d, M, &cb);
+  size_t cb = 0, xt_off = 0;
+  gemv_ws_layout(d, M, MT, &cb, &xt_off);
   uint32_t* counters = reinterpret_cast<uint32_t*>(ws);
   float* part = ws ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + cb) : nullptr;
+  float* xt = nullptr;
+  if constexpr (MT > 4) {
+    xt = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + xt_off);
+    hipLaunchKernelGGL(k_gemv_stage_x<MT>, dim3(stage_x_blocks(d), (M + MT - 1) / MT), dim3(kStageThreads), 0, st,
+                       d->K, X, ldx, M, xt);
+    const int rc = check_launch("k_gemv_stage_x");
+    if (rc) return rc;
+  }
   const size_t shmem = gemv_lds_bytes(d, MT);
   const size_t limit = device_lds_limit();
-  if (shmem > limit)
+  if (shmem > limit || !mfma_rows_fit(MT, d->chunk_rows))
     return fail(MTC_E_SHAPE, "fp32 path: %d rows x chunk_rows=%d needs %zu B of LDS (limit %zu); "
                 "use a stream with smaller chunk_rows", MT, d->chunk_rows, shmem, limit);
   const bool fs = d->leaf_scale != nullptr;
@@ -892,11 +1327,9 @@ int launch_gemv(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y,
     hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
     if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
   }
-  const int n_units = d->n_panels * d->n_chunks;
-  const int units_padded = (n_units + kXcds - 1) / kXcds * kXcds;
-  dim3 grid(units_padded * kGemvBlocksPerUnit, (M + MT - 1) / MT);
+  dim3 grid(gemv_blocks(d, MT), (M + MT - 1) / MT);
   const dim3 block(64 * shape.nw);
-  void* args[] = {const_cast<mtc_stream_desc*>(d), &X, &ldx, &Y, &ldy, &M, &part, &counters};
+  void* args[] = {const_cast<mtc_stream_desc*>(d), &X, &ldx, &Y, &ldy, &M, &part, &counters, &xt};
   const hipError_t e = hipLaunchKernel(kern, grid, block, args, shmem, st);
   if (e != hipSuccess) return fail(MTC_E_LAUNCH, "k_gemv launch: %s", hipGetErrorString(e));
   return check_launch("k_gemv");
@@ -907,7 +1340,10 @@ template <int MT>
 int launch_gemv_group(const GemvGroup& g, int n, const GemvShape& shape, const float* X, int64_t ldx, int M,
                       hipStream_t st) {
   size_t shmem = 0;
-  for (int i = 0; i < n; ++i) shmem = std::max(shmem, gemv_lds_bytes(&g.d[i], MT));
+  for (int i = 0; i < n; ++i) {
+    shmem = std::max(shmem, gemv_lds_bytes(&g.d[i], MT));
+    if (!mfma_rows_fit(MT, g.d[i].chunk_rows)) shmem = SIZE_MAX;
+  }
   const size_t limit = device_lds_limit();
   if (shmem > limit)
     return fail(MTC_E_SHAPE, "fp32 group: %d rows need %zu B of LDS (limit %zu)", MT, shmem, limit);
@@ -933,7 +1369,11 @@ int build_batch_plan(const mtc_gemv_batch_item* items, int n, int M, void* works
   if (!items) return fail(MTC_E_NULL, "items is NULL");
   if (n < 1) return fail(MTC_E_SHAPE, "batch of %d matrices", n);
   if (M <= 0) return fail(MTC_E_SHAPE, "M=%d must be positive", M);
-  const int mt = gemv_mt(M);
+  int max_rows = 0;
+  for (int i = 0; i < n; ++i)
+    if (items[i].desc) max_rows = std::max(max_rows, items[i].desc->chunk_rows);
+  const int mt = gemv_mt(M, max_rows);
+  if (mt > 4 && n > 65535) return fail(MTC_E_SHAPE, "batch of %d matrices at M=%d (at most 65535 above M=4)", n, M);
   bool fs = false;
   size_t ws = 0, lds = 0;
   int64_t blocks = 0, class_blocks[kShapeClasses] = {0, 0, 0, 0};
@@ -953,9 +1393,9 @@ int build_batch_plan(const mtc_gemv_batch_item* items, int n, int M, void* works
     const bool fsi = d->leaf_scale != nullptr;
     if (i == 0) fs = fsi;
     if (fsi != fs) return fail(MTC_E_SHAPE, "batch item %d differs from item 0 in scale format", i);
-    lds = std::max(lds, gemv_lds_bytes(d, mt));
-    ws += align_up(gemv_ws_layout(d, M, nullptr), 256);
-    const int64_t nb = (int64_t)(d->n_panels * d->n_chunks + kXcds - 1) / kXcds * kXcds * kGemvBlocksPerUnit;
+    lds = std::max(lds, mfma_rows_fit(mt, d->chunk_rows) ? gemv_lds_bytes(d, mt) : SIZE_MAX);
+    ws += align_up(gemv_ws_layout(d, M, mt, nullptr), 256);
+    const int64_t nb = gemv_blocks(d, mt);
     blocks += nb;
     class_blocks[shape_class(gemv_shape(mt, d))] += nb;
   }
@@ -992,6 +1432,7 @@ int build_batch_plan(const mtc_gemv_batch_item* items, int n, int M, void* works
   h->ws_bytes = ws;
   h->workspace = workspace;
   char* wsp = reinterpret_cast<char*>(workspace);
+  unsigned stage_bx = 0;
   int start[kShapeClasses] = {0, 0, 0, 0};            // next block of each shape's launch
   int64_t table_off[kShapeClasses] = {0, 0, 0, 0};    // first table entry of each shape's launch
   for (int c = 1; c < kShapeClasses; ++c) table_off[c] = table_off[c - 1] + class_blocks[c - 1];
@@ -1005,19 +1446,24 @@ int build_batch_plan(const mtc_gemv_batch_item* items, int n, int M, void* works
     const GemvShape shape = gemv_shape(mt, d);
     const int cls = shape_class(shape);
     it[i].lg = shape.lg;
-    size_t cb = 0;
-    const size_t wsi = gemv_ws_layout(d, M, &cb);
+    size_t cb = 0, xt_off = 0;
+    const size_t wsi = gemv_ws_layout(d, M, mt, &cb, &xt_off);
     if (wsi) {
-      it[i].counters = reinterpret_cast<uint32_t*>(wsp);
-      it[i].part = reinterpret_cast<float*>(wsp + cb);
+      if (d->n_chunks > 1) {
+        it[i].counters = reinterpret_cast<uint32_t*>(wsp);
+        it[i].part = reinterpret_cast<float*>(wsp + cb);
+      }
+      if (mt > 4) it[i].xt = reinterpret_cast<float*>(wsp + xt_off);
       wsp += align_up(wsi, 256);
     }
-    const int nb = (d->n_panels * d->n_chunks + kXcds - 1) / kXcds * kXcds * kGemvBlocksPerUnit;
+    stage_bx = std::max(stage_bx, stage_x_blocks(d));
+    const int nb = gemv_blocks(d, mt);
     uint32_t* table = block_item + table_off[cls];
     it[i].start = start[cls];
     for (int b = 0; b < nb; ++b) table[start[cls] + b] = (uint32_t)i;
     start[cls] += nb;
   }
+  h->stage_blocks_x = (int32_t)stage_bx;
   return ok();
 }
 
@@ -1032,6 +1478,13 @@ int launch_gemv_batch(const void* host_plan, const void* device_plan, hipStream_
   const uint32_t* block_item = reinterpret_cast<const uint32_t*>(dp + h->block_item_off);
   int M = h->M;
   const size_t shmem = h->lds_bytes;
+  if (h->mt > 4) {                                     // X of every member staged for the matrix core
+    const dim3 grid((unsigned)h->stage_blocks_x, (unsigned)((M + h->mt - 1) / h->mt), (unsigned)h->n_items);
+    if (h->mt == 8) hipLaunchKernelGGL(k_gemv_stage_x_batch<8>, grid, dim3(kStageThreads), 0, st, items, M);
+    else hipLaunchKernelGGL(k_gemv_stage_x_batch<16>, grid, dim3(kStageThreads), 0, st, items, M);
+    const int rc = check_launch("k_gemv_stage_x_batch");
+    if (rc) return rc;
+  }
   int64_t first = 0;
   for (int cls = 0; cls < kShapeClasses; ++cls) {      // one launch per block shape present
     const int nblk = h->class_blocks[cls];
@@ -1039,9 +1492,11 @@ int launch_gemv_batch(const void* host_plan, const void* device_plan, hipStream_
     first += nblk;
     if (nblk == 0) continue;
     const int nw = cls == 3 ? 8 : cls == 2 ? 16 : 4;
-    const void* kern = h->mt == 1 ? gemv_batch_kernel<1>(h->fs, cls)
-                     : h->mt == 2 ? gemv_batch_kernel<2>(h->fs, cls)
-                                  : gemv_batch_kernel<4>(h->fs, cls);
+    const void* kern = h->mt == 1   ? gemv_batch_kernel<1>(h->fs, cls)
+                     : h->mt == 2   ? gemv_batch_kernel<2>(h->fs, cls)
+                     : h->mt == 4   ? gemv_batch_kernel<4>(h->fs, cls)
+                     : h->mt == 8   ? gemv_batch_kernel<8>(h->fs, cls)
+                                    : gemv_batch_kernel<16>(h->fs, cls);
     if (shmem > 64 * 1024) {
       hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
       if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
@@ -1091,12 +1546,12 @@ MTC_API int mtc_dequant(const mtc_stream_desc* d, float* W_out, void* hip_stream
 
 MTC_API size_t mtc_gemv_lds_bytes(int K, int chunk_rows, int has_row_perm, int M) {
   if (K <= 0 || chunk_rows <= 0 || M <= 0) return 0;
-  return gemv_lds_bytes(K, chunk_rows, has_row_perm != 0, gemv_mt(M));
+  return gemv_lds_bytes(K, chunk_rows, has_row_perm != 0, gemv_mt(M, chunk_rows));
 }
 
 MTC_API size_t mtc_gemv_workspace_bytes(const mtc_stream_desc* d, int M) {
   if (check_desc(d) || M <= 0) return 0;
-  return gemv_ws_layout(d, M, nullptr);
+  return gemv_ws_layout(d, M, gemv_mt(M, d->chunk_rows), nullptr);
 }
 
 MTC_API int mtc_gemv_f32(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y, int64_t ldy, int M,
@@ -1107,14 +1562,17 @@ MTC_API int mtc_gemv_f32(const mtc_stream_desc* d, const float* X, int64_t ldx, 
   if (M <= 0) return fail(MTC_E_SHAPE, "M=%d must be positive", M);
   if (ldx < d->K || ldy < d->N) return fail(MTC_E_SHAPE, "ldx=%lld < K or ldy=%lld < N", (long long)ldx, (long long)ldy);
   if ((M - 1) > (INT64_MAX / ldx)) return fail(MTC_E_SHAPE, "M * ldx overflows");
-  const size_t need = gemv_ws_layout(d, M, nullptr);
+  const int mt = gemv_mt(M, d->chunk_rows);
+  const size_t need = gemv_ws_layout(d, M, mt, nullptr);
   if (need && (!workspace || workspace_bytes < need))
     return fail(MTC_E_WORKSPACE, "GEMV workspace of %zu bytes needed, %zu given", need, workspace ? workspace_bytes : 0);
   hipStream_t st = as_stream(hip_stream);
-  switch (gemv_mt(M)) {
+  switch (mt) {
     case 1: return launch_gemv<1>(d, X, ldx, Y, ldy, M, workspace, st);
     case 2: return launch_gemv<2>(d, X, ldx, Y, ldy, M, workspace, st);
-    default: return launch_gemv<4>(d, X, ldx, Y, ldy, M, workspace, st);
+    case 4: return launch_gemv<4>(d, X, ldx, Y, ldy, M, workspace, st);
+    case 8: return launch_gemv<8>(d, X, ldx, Y, ldy, M, workspace, st);
+    default: return launch_gemv<16>(d, X, ldx, Y, ldy, M, workspace, st);
   }
 }
 
@@ -1162,7 +1620,8 @@ MTC_API int mtc_gemv_f32_noalloc(const mtc_stream_desc* d, const float* X, int64
   if (ldx < d->K || ldy < d->N) return fail(MTC_E_SHAPE, "ldx=%lld < K or ldy=%lld < N", (long long)ldx, (long long)ldy);
   if ((M - 1) > (INT64_MAX / ldx)) return fail(MTC_E_SHAPE, "M * ldx overflows");
   size_t counter_bytes = 0;
-  const size_t need = gemv_ws_layout(d, M, &counter_bytes);
+  const int mt = gemv_mt(M, d->chunk_rows);
+  const size_t need = gemv_ws_layout(d, M, mt, &counter_bytes);
   if (need > kScratchBytes)
     return fail(MTC_E_WORKSPACE, "M=%d over %d row chunks needs %zu bytes of split-K scratch; the static scratch "
                 "holds %zu (use mtc_gemv_f32 with a workspace)", M, d->n_chunks, need, kScratchBytes);
@@ -1178,10 +1637,12 @@ MTC_API int mtc_gemv_f32_noalloc(const mtc_stream_desc* d, const float* X, int64
     rc = check_launch("k_fill_zero");
     if (rc) return rc;
   }
-  switch (gemv_mt(M)) {
+  switch (mt) {
     case 1: return launch_gemv<1>(d, X, ldx, Y, ldy, M, ws, st);
     case 2: return launch_gemv<2>(d, X, ldx, Y, ldy, M, ws, st);
-    default: return launch_gemv<4>(d, X, ldx, Y, ldy, M, ws, st);
+    case 4: return launch_gemv<4>(d, X, ldx, Y, ldy, M, ws, st);
+    case 8: return launch_gemv<8>(d, X, ldx, Y, ldy, M, ws, st);
+    default: return launch_gemv<16>(d, X, ldx, Y, ldy, M, ws, st);
   }
 }
 
@@ -1207,7 +1668,9 @@ MTC_API int mtc_gemv_f32_group(const mtc_stream_desc* const* descs, int n, const
   }
   if ((M - 1) > (INT64_MAX / ldx)) return fail(MTC_E_SHAPE, "M * ldx overflows");
   hipStream_t st = as_stream(hip_stream);
-  const int mt = gemv_mt(M);
+  int max_rows = 0;
+  for (int i = 0; i < n; ++i) max_rows = std::max(max_rows, descs[i]->chunk_rows);
+  const int mt = gemv_mt(M, max_rows);
   // one launch per block shape among the members (usually one), so that every member's blocks
   // run the code of its own launch
   for (int cls = 0; cls < kShapeClasses; ++cls) {
@@ -1223,7 +1686,7 @@ MTC_API int mtc_gemv_f32_group(const mtc_stream_desc* const* descs, int n, const
       g.Y[m] = Y[i];
       g.ldy[m] = ldy[i];
       g.start[m] = blocks;
-      blocks += (descs[i]->n_panels + kXcds - 1) / kXcds * kXcds * kGemvBlocksPerUnit;
+      blocks += gemv_blocks(descs[i], mt);
       ++m;
     }
     if (m == 0) continue;
@@ -1232,7 +1695,9 @@ MTC_API int mtc_gemv_f32_group(const mtc_stream_desc* const* descs, int n, const
     switch (mt) {
       case 1: rc = launch_gemv_group<1>(g, m, shape, X, ldx, M, st); break;
       case 2: rc = launch_gemv_group<2>(g, m, shape, X, ldx, M, st); break;
-      default: rc = launch_gemv_group<4>(g, m, shape, X, ldx, M, st); break;
+      case 4: rc = launch_gemv_group<4>(g, m, shape, X, ldx, M, st); break;
+      case 8: rc = launch_gemv_group<8>(g, m, shape, X, ldx, M, st); break;
+      default: rc = launch_gemv_group<16>(g, m, shape, X, ldx, M, st); break;
     }
     if (rc) return rc;
   }

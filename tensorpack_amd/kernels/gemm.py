@@ -33,18 +33,40 @@ from ..packer import PanelStream, check_permutation, pack_levels, weight_codes
 from ..tilestream import TileStream, pack_tiles
 
 DECODE_MAX_M = 16             # M at or below this takes the fp32 decode kernel under compute="auto"
-DECODE_X_LDS_BYTES = 64 * 1024   # on-chip budget for the gathered X rows of one decode block
+DECODE_X_LDS_BYTES = 64 * 1024   # on-chip budget for the gathered X rows of one vector-path decode block
+DECODE_MFMA_X_LDS_BYTES = 128 * 1024   # the same for a matrix-core decode block (M tiles of 8 or 16 rows)
 DECODE_LDS_BYTES = 160 * 1024    # per-block LDS of gfx950
 UNIFORM_BLOCK_SIZES = (4, 8, 16, 32)   # block sizes of the uniform form the device stream holds
 
 
 def _decode_mt(M: int) -> int:
-    """Rows of X per decode block (larger M runs several blocks along M)."""
-    return 1 if M <= 1 else 2 if M <= 2 else 4
+    """Rows of X per decode block (larger M runs several blocks along M): 1, 2 or 4 on the
+    vector path; 8 or 16 on the matrix core (the library takes 8 when a unit's 16 rows of X
+    would not fit on chip)."""
+    return M if M <= 2 else 4 if M <= 4 else 8 if M <= 8 else 16
+
+
+def _decode_x_budget(mt: int) -> int:
+    """On-chip bytes for one decode block's staged X rows."""
+    return DECODE_X_LDS_BYTES if mt <= 4 else DECODE_MFMA_X_LDS_BYTES
 
 
 DECODE_FILL_BLOCKS = 256      # decode blocks that fill the chip (one 16-wave block per CU)
 DECODE_MIN_SPLIT_ROWS = 512   # no row chunk below this when splitting only to fill the chip
+DECODE_MFMA_MAX_ROWS = 2048   # row chunks of the matrix-core layout (16 X rows of one fit on chip)
+
+
+def _decode_row_cap(M: int) -> int:
+    """Largest row chunk of the decode layout for M rows."""
+    mt = _decode_mt(M)
+    cap = min(_decode_x_budget(mt) // (4 * mt) // 32 * 32, 4096)
+    return cap if mt <= 4 else min(cap, DECODE_MFMA_MAX_ROWS)
+
+
+def _decode_blocks_per_unit(M: int) -> int:
+    """Decode blocks per unit: one per 16-column half on the vector path, one per unit on the
+    matrix core."""
+    return 2 if _decode_mt(M) <= 4 else 1
 
 
 def gemv_chunk_rows(K: int, N: int, M: int = 1) -> int:
@@ -52,14 +74,14 @@ def gemv_chunk_rows(K: int, N: int, M: int = 1) -> int:
     (M_tile x rows fp32) fit the on-chip budget, so no block needs a cross-block reduction;
     otherwise the fewest chunks that fit, of equal size (a 4864-row matrix splits 2432 +
     2432, not 4096 + 768). A matrix that needs a split anyway and has too few column panels
-    to fill the chip (two blocks per unit) is cut into more chunks of at least
-    DECODE_MIN_SPLIT_ROWS rows."""
-    cap = min(DECODE_X_LDS_BYTES // (4 * _decode_mt(M)) // 32 * 32, 4096)
+    to fill the chip (_decode_blocks_per_unit blocks per unit) is cut into more chunks of at
+    least DECODE_MIN_SPLIT_ROWS rows."""
+    cap = _decode_row_cap(M)
     rows = -(-K // 32) * 32
     n = -(-rows // cap)
     if n > 1:
         panels = max(1, N // 32)
-        fill = -(-DECODE_FILL_BLOCKS // (2 * panels))
+        fill = -(-DECODE_FILL_BLOCKS // (_decode_blocks_per_unit(M) * panels))
         n = max(n, min(fill, rows // DECODE_MIN_SPLIT_ROWS))
     chunk = -(-(-(-rows // n)) // 32) * 32
     return int(max(32, min(chunk, cap)))

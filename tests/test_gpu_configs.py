@@ -97,13 +97,18 @@ def test_c2_decode(gpu, M):
     if M == 1:
         _check_dequant("c2", m, W_hat)
     ds = m.device_stream(None, gpu, M)              # the bench's decode layout
-    assert ds.host.chunk_rows == 4096 and ds.host.n_chunks == 1 and ds.host.row_perm is not None
+    # M = 1: whole 4096-row units; M = 16 (matrix core, 16-row M tile): 2048-row units, split K
+    assert ds.host.chunk_rows == (4096 if M == 1 else 2048) and ds.host.row_perm is not None
     X = wl.activations(M)
     _say(f"c2 M={M} decode, chunk_rows {ds.host.chunk_rows}")
     Y = ds.gemv_f32(torch.from_numpy(X).to(gpu))
     _check_f32(f"c2 M={M}", X, Y, W_hat)
     Y2 = mtc_gemm(torch.from_numpy(X).to(gpu), m)
     assert torch.equal(Y, Y2)
+    if M == 16:                                     # the M = 1 layout at M = 16: two 8-row M tiles
+        _say("c2 M=16 decode, chunk_rows 4096")
+        _check_f32("c2 M=16 (4096-row units)", X, m.device_stream(4096, gpu).gemv_f32(torch.from_numpy(X).to(gpu)),
+                   W_hat)
 
 
 def test_c4_prefill(gpu):

@@ -95,17 +95,33 @@ def test_gemv_f32(gpu, allocs, name, M):
 
 
 @pytest.mark.parametrize("chunk_rows", [32, 64, 96, 512])
-def test_gemv_split_k_chunkings(gpu, allocs, chunk_rows):
+@pytest.mark.parametrize("M", [4, 12])
+def test_gemv_split_k_chunkings(gpu, allocs, chunk_rows, M):
     import torch
     W, a, m = allocs["outlier-qt-2.5"]
-    _say("gemv chunking", chunk_rows)
-    X = np.random.RandomState(7).randn(4, W.shape[0]).astype(np.float32)
+    _say("gemv chunking", chunk_rows, M)
+    X = np.random.RandomState(7).randn(M, W.shape[0]).astype(np.float32)
     ds = m.device_stream(chunk_rows)
     Y1 = ds.gemv_f32(torch.from_numpy(X).to(gpu)).cpu().numpy()
     Y2 = ds.gemv_f32(torch.from_numpy(X).to(gpu)).cpu().numpy()
     assert np.array_equal(Y1, Y2), "fp32 path must be deterministic (counters must self-reset)"
     err = O.relative_frobenius_error(O.qt_gemm_f64(X, _oracle_what(a, W)), Y1)
     assert err <= TOL_F32, err
+
+
+@pytest.mark.parametrize("name", [c[0] for c in CASES])
+def test_gemv_matrix_core_tile_heights_agree(gpu, allocs, name):
+    # M tiles of 8 and 16 rows run the same lane -> chunk order: the rows both compute are
+    # bit-identical, and every M from 5 to 16 matches the 16-row call's rows
+    import torch
+    W, a, m = allocs[name]
+    ds = m.device_stream(512, gpu)
+    X = torch.from_numpy(np.random.RandomState(11).randn(16, W.shape[0]).astype(np.float32)).to(gpu)
+    _say("gemv tile heights", name)
+    Y16 = ds.gemv_f32(X).cpu().numpy()
+    for M in (5, 8, 9, 13):
+        Y = ds.gemv_f32(X[:M].contiguous()).cpu().numpy()
+        assert np.array_equal(_bits(Y), _bits(Y16[:M])), (name, M)
 
 
 @pytest.mark.parametrize("M,permuted,ydt", [(100, False, "f32"), (300, True, "f32"), (37, True, "bf16")])

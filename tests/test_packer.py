@@ -238,11 +238,12 @@ def test_step_records_survive_save_load(tmp_path):
                                    (4864, 896, 16), (896, 896, 1), (896, 4864, 1), (896, 128, 1), (10000, 64, 1),
                                    (100, 64, 1)])
 def test_decode_row_chunks_are_even_and_fill_the_chip(K, N, M):
-    from tensorpack_amd.kernels.gemm import DECODE_FILL_BLOCKS, DECODE_MIN_SPLIT_ROWS, DECODE_X_LDS_BYTES, \
-        _decode_mt, gemv_chunk_rows
+    from tensorpack_amd.kernels.gemm import DECODE_FILL_BLOCKS, DECODE_MIN_SPLIT_ROWS, _decode_blocks_per_unit, \
+        _decode_mt, _decode_row_cap, _decode_x_budget, gemv_chunk_rows
     c = gemv_chunk_rows(K, N, M)
     rows = -(-K // 32) * 32
-    cap = min(DECODE_X_LDS_BYTES // (4 * _decode_mt(M)) // 32 * 32, 4096)
+    cap = _decode_row_cap(M)
+    assert cap * 4 * _decode_mt(M) <= _decode_x_budget(_decode_mt(M))   # the staged X rows fit on chip
     n = -(-rows // c)
     assert c % 32 == 0 and 32 <= c <= cap
     if rows <= cap:
@@ -253,4 +254,5 @@ def test_decode_row_chunks_are_even_and_fill_the_chip(K, N, M):
         assert rows - (n - 1) * c > 0 and (n - 1) * c < rows      # every chunk holds rows
         assert c - (rows - (n - 1) * c) < 32 * n        # chunks are equal up to 32-row rounding
         if n > need:                                    # a split beyond the minimum only to fill the chip
-            assert 2 * (N // 32) * (n - 1) < DECODE_FILL_BLOCKS and c >= DECODE_MIN_SPLIT_ROWS - 32
+            assert _decode_blocks_per_unit(M) * (N // 32) * (n - 1) < DECODE_FILL_BLOCKS \
+                and c >= DECODE_MIN_SPLIT_ROWS - 32
