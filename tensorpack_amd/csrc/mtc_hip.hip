@@ -773,14 +773,21 @@ struct MfmaPass {
   float fs0, fs1;
 };
 
-template <bool FS>
-__device__ __forceinline__ void mfma_load(__amdgpu_buffer_rsrc_t pay_r, __amdgpu_buffer_rsrc_t lw_r,
-                                          __amdgpu_buffer_rsrc_t fs_r, uint32_t key, uint32_t pay, uint32_t leaf,
-                                          uint32_t t, uint32_t j, MfmaPass& r) {
+// The loads of a record's four passes. Pass p of lane (slot, chunk cq, column j) takes chunk
+// t0 + 4p of the slot's bucket, t0 = 16 * step + cq, so every offset is pass 0's plus a
+// wave-uniform step per pass: 4 chunks of P dwords of payload, and the leaf words of 4
+// chunks (8 for two 4x4 leaves per chunk, 4 >> (log2 S - 3) for larger leaves). Chunks past the bucket's
+// end are read in place (the stream's next chunks, or zeros past a buffer's end) and masked
+// by the caller.
+template <bool FS, int NP>
+__device__ __forceinline__ void mfma_load_rec(__amdgpu_buffer_rsrc_t pay_r, __amdgpu_buffer_rsrc_t lw_r,
+                                              __amdgpu_buffer_rsrc_t fs_r, uint32_t key, uint32_t pay,
+                                              uint32_t leaf, uint32_t t0, uint32_t j, MfmaPass (&r)[NP]) {
   const uint32_t P = key >> 8, ls = key & 0xFFu;
-  const uint32_t ob = (pay + t * P) << 2;            // payload byte offset of the chunk
+  const uint32_t ob = (pay + t0 * P) << 2;           // payload byte offset of pass 0's chunk
+  const bool two = ls == 2;                          // two 4x4 leaves per chunk
   uint32_t o0, o1;
-  if (ls == 2) {                                     // codes 4j.. of leaf 0 and 16 + 4j.. of leaf 1
+  if (two) {                                         // codes 4j.. of leaf 0 and 16 + 4j.. of leaf 1
     o0 = ob + (((4 * j * P) >> 5) << 2);
     o1 = ob + ((((16 + 4 * j) * P) >> 5) << 2);
   } else if (P == 16) {                              // codes 8j .. 8j + 7: 128 bits at dword 4j
@@ -790,18 +797,26 @@ __device__ __forceinline__ void mfma_load(__amdgpu_buffer_rsrc_t pay_r, __amdgpu
     o0 = ob + (((8 * j * P) >> 5) << 2);
     o1 = kOutOfRange;
   }
-  const u32x2_t a = __builtin_amdgcn_raw_buffer_load_b64(pay_r, o0, 0, kNT);
-  const u32x2_t b = __builtin_amdgcn_raw_buffer_load_b64(pay_r, o1, 0, kNT);
-  r.w = u32x4_t{a.x, a.y, b.x, b.y};
-  const uint32_t l0 = leaf + (ls == 2 ? 2 * t : t >> (ls - 3));
-  const uint32_t b1 = ls == 2 ? (l0 + 1) << 2 : kOutOfRange;   // second 4x4 leaf, if any
-  r.lw0 = __builtin_amdgcn_raw_buffer_load_b32(lw_r, l0 << 2, 0, 0);
-  r.lw1 = __builtin_amdgcn_raw_buffer_load_b32(lw_r, b1, 0, 0);
-  if constexpr (FS) {
-    r.fs0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(fs_r, l0 << 2, 0, 0));
-    r.fs1 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(fs_r, b1, 0, 0));
-  } else {
-    r.fs0 = r.fs1 = 0.0f;
+  const bool o1_used = two || P == 16;
+  const uint32_t sh = ls >= 3 ? ls - 3 : 0u;         // leaf sizes 8, 16, 32 (the null record has ls = 0)
+  const uint32_t l0 = leaf + (two ? 2 * t0 : t0 >> sh);
+  const uint32_t pstep = 16 * P;                     // bytes of 4 chunks (P dwords each)
+  const uint32_t lstep = 4 * (two ? 8u : 4u >> sh);  // bytes of the leaf words of 4 chunks
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const uint32_t a = o0 + p * pstep, b = o1_used ? o1 + p * pstep : kOutOfRange;
+    const u32x2_t x = __builtin_amdgcn_raw_buffer_load_b64(pay_r, a, 0, kNT);
+    const u32x2_t y = __builtin_amdgcn_raw_buffer_load_b64(pay_r, b, 0, kNT);
+    r[p].w = u32x4_t{x.x, x.y, y.x, y.y};
+    const uint32_t w0 = (l0 << 2) + p * lstep, w1 = two ? w0 + 4 : kOutOfRange;
+    r[p].lw0 = __builtin_amdgcn_raw_buffer_load_b32(lw_r, w0, 0, 0);
+    r[p].lw1 = __builtin_amdgcn_raw_buffer_load_b32(lw_r, w1, 0, 0);
+    if constexpr (FS) {
+      r[p].fs0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(fs_r, w0, 0, 0));
+      r[p].fs1 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(fs_r, w1, 0, 0));
+    } else {
+      r[p].fs0 = r[p].fs1 = 0.0f;
+    }
   }
 }
 
@@ -825,10 +840,11 @@ __device__ __forceinline__ void window_codes(uint32_t lo, uint32_t hi, uint32_t 
 
 // A lane's column of its chunk in one pass of kind (S, P): the 8 weights (zero when the
 // lane's chunk is not in the bucket, `on` false, or its leaf is padding) and the unit rows
-// they sit on (rows row0 .. row0 + 3 and row1 .. row1 + 3).
+// they sit on (rows row0 .. row0 + 3 and row1 .. row1 + 3; row_off: the chunk's 8-row block
+// within a leaf of 16 or 32 rows).
 template <int S, int P>
-__device__ __forceinline__ void mfma_decode(const MfmaPass& r, bool on, uint32_t t, uint32_t j, uint32_t rb_mask,
-                                            bool fp32_scales, float (&wq)[8], int& row0, int& row1) {
+__device__ __forceinline__ void mfma_decode(const MfmaPass& r, bool on, int row_off, uint32_t j, bool fp32_scales,
+                                            float (&wq)[8], int& row0, int& row1) {
   static_assert(S == 4 || S == 8, "leaf sizes 16 and 32 take the S = 8 path");
   constexpr float off = (float)(1 << (P - 1));
   float u[8];
@@ -837,8 +853,8 @@ __device__ __forceinline__ void mfma_decode(const MfmaPass& r, bool on, uint32_t
     window_codes<P, 4, (P >= 8)>(r.w.x, r.w.y, (4 * j * P) & 31u, u);
     window_codes<P, 4, (P >= 8)>(r.w.z, r.w.w, ((16 + 4 * j) * P) & 31u, u + 4);
     const LeafInfo a = leaf_info_v(r.lw0, fp32_scales, r.fs0), b = leaf_info_v(r.lw1, fp32_scales, r.fs1);
-    row0 = a.row;
-    row1 = b.row;
+    row0 = on ? a.row : 0;                           // a masked lane's leaf may be any unit's
+    row1 = on ? b.row : 0;
     s0 = (on && !a.pad) ? a.scale : 0.0f;
     s1 = (on && !b.pad) ? b.scale : 0.0f;
   } else {
@@ -852,7 +868,7 @@ __device__ __forceinline__ void mfma_decode(const MfmaPass& r, bool on, uint32_t
       window_codes<P, 8, (P == 4 || P == 8)>(r.w.x, r.w.y, (8 * j * P) & 31u, u);
     }
     const LeafInfo a = leaf_info_v(r.lw0, fp32_scales, r.fs0);
-    row0 = a.row + 8 * (int)(t & rb_mask);
+    row0 = on ? a.row + row_off : 0;                 // a masked lane's leaf may be any unit's
     row1 = row0 + 4;
     s0 = s1 = (on && !a.pad) ? a.scale : 0.0f;
   }
@@ -914,44 +930,43 @@ __device__ __forceinline__ void gemv_block_mfma(const mtc_stream_desc& d, const 
   };
   struct Rec {
     MfmaPass p[NP];
-    uint32_t key, J, valid;
+    uint32_t key, valid;
   };
   auto fetch = [&](const u32x4_t f, Rec& r) __attribute__((always_inline)) {
     r.key = __builtin_amdgcn_readfirstlane(f.w & 0xFFFFu);
-    r.J = f.w >> 16;
     r.valid = f.z;
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      const uint32_t c = 4 * p + cq;
-      const uint32_t t = c < f.z ? kStepLanes * r.J + c : 0u;
-      mfma_load<FS>(pay_r, lw_r, fs_r, r.key, f.x, f.y, t, j, r.p[p]);
-    }
+    mfma_load_rec<FS, NP>(pay_r, lw_r, fs_r, r.key, f.x, f.y, kStepLanes * (f.w >> 16) + cq, j, r.p);
   };
 
-  // ---- the first records' loads, then X rows of the unit into LDS ----
-  const u32x4_t f0 = slot_of(rec_of(wl));
-  u32x4_t f1 = slot_of(rec_of(wl + WH));
-  Rec cur, nxt;
-  fetch(f0, cur);
-  if (xt) {                                           // transposed X: one MT-float piece per row
-    // All of a thread's row indices are loaded, then all its pieces, then stored: the loads
-    // overlap instead of running one dependent pair at a time. kc * MT fits the LDS, so a
-    // thread has at most kMfmaStageIters pieces.
-    constexpr int L = MT / 4;                         // threads per row (16 bytes each)
-    const float* src = xt + (size_t)blockIdx.y * d.K * MT;
-    int kr[kMfmaStageIters];
+  // ---- X rows of the unit into LDS, overlapped with the first records' loads. The compiler
+  //      waits for loads in issue order, so the order is: row indices, record slots, X pieces,
+  //      then the first record's payload; the LDS stores wait for the X pieces only and the
+  //      payload stays in flight. With xt, each row is one MT-float piece (16 bytes per
+  //      thread); kc * MT fits the LDS, so a thread has at most kMfmaStageIters pieces. ----
+  constexpr int L = MT / 4;                           // threads per row
+  int kr[kMfmaStageIters];
+  if (xt) {
 #pragma unroll
     for (int it = 0; it < kMfmaStageIters; ++it) {
-      const int i = it * T + tid, r = i / L;
+      const int r = (it * T + tid) / L;
       kr[it] = r < rows ? (d.row_perm ? d.row_perm[kb + r] : kb + r) : -1;
     }
-    float4 v[kMfmaStageIters];
+  }
+  const u32x4_t f0 = slot_of(rec_of(wl));
+  u32x4_t f1 = slot_of(rec_of(wl + WH));
+  float4 v[kMfmaStageIters];
+  if (xt) {
+    const float* src = xt + (size_t)blockIdx.y * d.K * MT;
 #pragma unroll
     for (int it = 0; it < kMfmaStageIters; ++it) {
-      const int i = it * T + tid, part4 = i % L;
+      const int part4 = (it * T + tid) % L;
       v[it] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       if (kr[it] >= 0) v[it] = *reinterpret_cast<const float4*>(src + (size_t)kr[it] * MT + 4 * part4);
     }
+  }
+  Rec cur, nxt;
+  fetch(f0, cur);
+  if (xt) {
 #pragma unroll
     for (int it = 0; it < kMfmaStageIters; ++it) {
       const int i = it * T + tid;
@@ -986,19 +1001,19 @@ __device__ __forceinline__ void gemv_block_mfma(const mtc_stream_desc& d, const 
     const uint32_t vmax = max(max(__builtin_amdgcn_readlane(r.valid, 0), __builtin_amdgcn_readlane(r.valid, 16)),
                               max(__builtin_amdgcn_readlane(r.valid, 32), __builtin_amdgcn_readlane(r.valid, 48)));
     const uint32_t key = r.key, ls = key & 0xFFu;
-    const uint32_t rb_mask = ls > 3 ? (1u << (ls - 3)) - 1u : 0u;
+    // 8-row block of the chunk within its leaf (chunk t is block t & (S/8 - 1); t = 16 step +
+    // 4p + cq, so only cq matters)
+    const int row_off = ls > 3 ? 8 * (int)(cq & ((1u << (ls - 3)) - 1u)) : 0;
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       if ((uint32_t)(4 * p) >= vmax) break;
-      const uint32_t c = 4 * p + cq;
-      const bool on = c < r.valid;
-      const uint32_t t = on ? kStepLanes * r.J + c : 0u;
+      const bool on = 4 * p + cq < r.valid;
       float wq[8];
       int row0 = 0, row1 = 0;
       switch (ls == 2 ? key : (key & ~0xFFu) | 3u) {   // sizes 8, 16, 32 share a case
 #define MTC_CASE(S, P) \
   case MTC_BUCKET_KEY(S, P): \
-    mfma_decode<S, P>(r.p[p], on, t, j, rb_mask, FS, wq, row0, row1); \
+    mfma_decode<S, P>(r.p[p], on, row_off, j, FS, wq, row0, row1); \
     break;
         MTC_FOR_EACH_WIDTH(8, MTC_CASE)
         MTC_FOR_EACH_WIDTH(4, MTC_CASE)
@@ -1029,11 +1044,11 @@ __device__ __forceinline__ void gemv_block_mfma(const mtc_stream_desc& d, const 
   // after that's slot) are outstanding
   for (int i = wl; i < nrec; i += 2 * WH) {
     u32x4_t f2 = slot_of(rec_of(i + 2 * WH));
-    fetch(f1, nxt);
+    if (i + WH < nrec) fetch(f1, nxt);
     compute(cur);
     if (i + WH >= nrec) break;
     f1 = slot_of(rec_of(i + 3 * WH));
-    fetch(f2, cur);
+    if (i + 2 * WH < nrec) fetch(f2, cur);
     compute(nxt);
   }
 
