@@ -462,6 +462,62 @@ __global__ __launch_bounds__(kStageThreads) void k_stage_x(const void* __restric
   stage_x_row(X, xdt, ldx, row_perm, Xp, K);
 }
 
+// Rows m0 .. m0 + R - 1 of Xp = bf16(X[:, row_perm]) (identity without a permutation),
+// R * K bf16 values of LDS: each row is first copied into LDS as bf16 (coalesced reads, the
+// same round-to-nearest-even conversion as stage_x_row), then each thread gathers 8 consecutive
+// outputs through row_perm from LDS and writes them as one 16-byte store. A gather from global
+// memory instead touches a cache line per lane (the permutation scatters a row's columns).
+constexpr int kStageLdsMaxBytes = 64 * 1024;
+__device__ __forceinline__ void stage_x_rows(const void* __restrict__ X, int xdt, int64_t ldx,
+                                             const int32_t* __restrict__ row_perm, __bf16* __restrict__ Xp,
+                                             int K, int M, int m0, int R) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t xl[];   // [R][K] bf16 bits
+  const int tid = threadIdx.x;
+  const int rows = min(R, M - m0);
+  for (int r = 0; r < rows; ++r) {
+    const int64_t base = (int64_t)(m0 + r) * ldx;
+    if (xdt == MTC_DTYPE_F32) {
+      const float* x = reinterpret_cast<const float*>(X) + base;
+      for (int k = tid; k < K; k += kStageThreads) xl[r * K + k] = (uint16_t)pk_bf16(x[k], 0.0f);
+    } else {
+      const uint16_t* x = reinterpret_cast<const uint16_t*>(X) + base;
+      for (int k = tid; k < K; k += kStageThreads) xl[r * K + k] = x[k];
+    }
+  }
+  __syncthreads();
+  const int units = K / 8;
+  for (int r = 0; r < rows; ++r) {
+    const uint16_t* src = xl + r * K;
+    __bf16* dst = Xp + (int64_t)(m0 + r) * K;
+    for (int u = tid; u < units; u += kStageThreads) {
+      const int k0 = 8 * u;
+      int4 a = make_int4(k0, k0 + 1, k0 + 2, k0 + 3), b = make_int4(k0 + 4, k0 + 5, k0 + 6, k0 + 7);
+      if (row_perm) {
+        a = *reinterpret_cast<const int4*>(row_perm + k0);   // 16-byte aligned: k0 % 8 == 0
+        b = *reinterpret_cast<const int4*>(row_perm + k0 + 4);
+      }
+      const u32x4_t o{(uint32_t)src[a.x] | (uint32_t)src[a.y] << 16, (uint32_t)src[a.z] | (uint32_t)src[a.w] << 16,
+                      (uint32_t)src[b.x] | (uint32_t)src[b.y] << 16, (uint32_t)src[b.z] | (uint32_t)src[b.w] << 16};
+      *reinterpret_cast<u32x4_t*>(dst + k0) = o;
+    }
+  }
+}
+
+// Rows per staging block: up to 4 while R * K bf16 fit kStageLdsMaxBytes and the grid keeps
+// at least 1024 blocks; 0 when one row does not fit (the global-gather kernel then stages).
+int stage_rows_for(int max_k, int64_t rows_total) {
+  if ((int64_t)max_k * 2 > kStageLdsMaxBytes) return 0;
+  int r = 1;
+  while (r < 4 && (int64_t)2 * r * max_k * 2 <= kStageLdsMaxBytes && rows_total / (2 * r) >= 1024) r *= 2;
+  return r;
+}
+
+__global__ __launch_bounds__(kStageThreads) void k_stage_x_rows(const void* __restrict__ X, int xdt, int64_t ldx,
+                                                                const int32_t* __restrict__ row_perm,
+                                                                __bf16* __restrict__ Xp, int K, int M, int R) {
+  stage_x_rows(X, xdt, ldx, row_perm, Xp, K, M, (int)blockIdx.x * R, R);
+}
+
 // Staging for the members of a group that need it (grid z = entry).
 struct StageGroup {
   const int32_t* row_perm[kMaxGroup];
@@ -577,6 +633,15 @@ __global__ __launch_bounds__(kStageThreads) void k_stage_x_batch(const GemmBatch
                                                                  const uint32_t* __restrict__ list, int xdt) {
   const GemmBatchItem& it = items[list[blockIdx.z]];
   stage_x_row(it.Xsrc, xdt, it.ldx_src, it.d.row_perm, const_cast<__bf16*>(it.X), it.d.K);
+}
+
+// The same through LDS, R rows per block (grid: row groups x members that stage).
+__global__ __launch_bounds__(kStageThreads) void k_stage_x_rows_batch(const GemmBatchItem* __restrict__ items,
+                                                                      const uint32_t* __restrict__ list, int xdt,
+                                                                      int M, int R) {
+  const GemmBatchItem& it = items[list[blockIdx.y]];
+  stage_x_rows(it.Xsrc, xdt, it.ldx_src, it.d.row_perm, const_cast<__bf16*>(it.X), it.d.K, M, (int)blockIdx.x * R,
+               R);
 }
 
 template <int kYDT>
@@ -719,6 +784,8 @@ struct GemmBatchHeader {
   int32_t n_reduce;
   int32_t stage_blocks_x;
   int32_t reduce_blocks_x;
+  int32_t stage_rows;     // rows per LDS staging block (0: global gather)
+  int32_t stage_max_k;
   uint64_t items_off;
   uint64_t blocks_off;
   uint64_t stage_off;
@@ -866,6 +933,11 @@ int build_gemm_batch_plan(const mtc_gemm_batch_item* items, int n, int M, int x_
   h->n_stage = n_stage;
   h->n_reduce = n_reduce;
   h->stage_blocks_x = stage_bx;
+  int max_k = 0;
+  for (int i = 0; i < n; ++i)
+    if (needs_staging(items[i].desc, x_dtype)) max_k = std::max(max_k, items[i].desc->K);
+  h->stage_max_k = max_k;
+  h->stage_rows = n_stage ? stage_rows_for(max_k, (int64_t)M * n_stage) : 0;
   h->reduce_blocks_x = reduce_bx;
   h->items_off = items_off;
   h->blocks_off = blocks_off;
@@ -939,8 +1011,15 @@ int launch_gemm_batch(const void* host_plan, const void* device_plan, hipStream_
   const uint32_t* stage_list = reinterpret_cast<const uint32_t*>(dp + h->stage_off);
   const uint32_t* reduce_list = reinterpret_cast<const uint32_t*>(dp + h->reduce_off);
   if (h->n_stage) {
-    hipLaunchKernelGGL(k_stage_x_batch, dim3((unsigned)h->stage_blocks_x, (unsigned)h->M, (unsigned)h->n_stage),
-                       dim3(kStageThreads), 0, st, items, stage_list, h->x_dtype);
+    const int R = h->stage_rows;
+    if (R) {
+      hipLaunchKernelGGL(k_stage_x_rows_batch, dim3((unsigned)((h->M + R - 1) / R), (unsigned)h->n_stage),
+                         dim3(kStageThreads), (size_t)R * h->stage_max_k * 2, st, items, stage_list, h->x_dtype,
+                         h->M, R);
+    } else {
+      hipLaunchKernelGGL(k_stage_x_batch, dim3((unsigned)h->stage_blocks_x, (unsigned)h->M, (unsigned)h->n_stage),
+                         dim3(kStageThreads), 0, st, items, stage_list, h->x_dtype);
+    }
     const int rc = check_launch("k_stage_x_batch");
     if (rc) return rc;
   }
@@ -992,9 +1071,16 @@ MTC_API int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, in
     return fail(MTC_E_WORKSPACE, "workspace not 256-byte aligned");
   float* part = need > stage ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + stage) : nullptr;
   if (stage) {
-    dim3 grid((d->K / 8 + kStageThreads - 1) / kStageThreads, M);
-    hipLaunchKernelGGL(k_stage_x, grid, dim3(kStageThreads), 0, st, X, x_dtype, ldx, d->row_perm,
-                       reinterpret_cast<__bf16*>(workspace), d->K);
+    const int R = stage_rows_for(d->K, M);
+    if (R) {
+      hipLaunchKernelGGL(k_stage_x_rows, dim3((unsigned)((M + R - 1) / R)), dim3(kStageThreads),
+                         (size_t)R * d->K * 2, st, X, x_dtype, ldx, d->row_perm, reinterpret_cast<__bf16*>(workspace),
+                         d->K, M, R);
+    } else {
+      dim3 grid((d->K / 8 + kStageThreads - 1) / kStageThreads, M);
+      hipLaunchKernelGGL(k_stage_x, grid, dim3(kStageThreads), 0, st, X, x_dtype, ldx, d->row_perm,
+                         reinterpret_cast<__bf16*>(workspace), d->K);
+    }
     rc = check_launch("k_stage_x");
     if (rc) return rc;
     xb = reinterpret_cast<const __bf16*>(workspace);
