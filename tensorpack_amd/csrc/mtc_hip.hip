@@ -353,12 +353,14 @@ constexpr int kGemvBlocksPerUnit = kGroups / kStepGroups;
 // from gemv_shape, so a matrix's blocks run the same code (same waves, hence the same
 // summation order) in every launch:
 // - M tiles of 4 rows: 8 waves, three steps prefetched;
-// - 1-2 rows, more than kFewSteps records per block: 16 waves (one block fills a CU), three
-//   steps prefetched, X rows gathered in LDS when there is a row permutation and K <= 4096;
-// - 1-2 rows, at most kFewSteps records per block (small K): 4 waves with two steps
-//   prefetched, which keeps a wave near 69 registers so that seven blocks share a CU; the X
-//   staging is sized for kSmallRows rows when the chunk (and, for the LDS gather, K) fits in
-//   it, which keeps its registers few, else for kMaxChunkRows rows without the LDS gather.
+// - 1-2 rows, units of at most kSmallRows rows: 4 waves with two steps prefetched, which
+//   keeps a wave near 69 registers so that seven blocks share a CU; the X staging is sized
+//   for kSmallRows rows (with the LDS gather when K fits it too);
+// - 1-2 rows, larger units with more than kFewSteps records per block: 16 waves (one block
+//   fills a CU), three steps prefetched, X rows gathered in LDS when there is a row
+//   permutation and K <= 4096;
+// - 1-2 rows, larger units with at most kFewSteps records per block: 4 waves, X staging
+//   for kMaxChunkRows rows without the LDS gather.
 struct GemvShape {
   int nw;        // waves per block
   int kc;        // rows the X staging covers (kSmallRows or kMaxChunkRows)
@@ -369,8 +371,8 @@ inline GemvShape gemv_shape(int MT, const mtc_stream_desc* d) {
   const bool perm = d->row_perm != nullptr;
   if (MT > 4) return {16, kMaxChunkRows, false, false};   // matrix core
   if (MT > 2) return {8, kMaxChunkRows, false, false};
-  if (d->fixed_steps > kFewSteps) return {16, kMaxChunkRows, true, perm && d->K <= kMaxChunkRows};
   if (d->chunk_rows <= kSmallRows) return {4, kSmallRows, true, perm && d->K <= kSmallRows};
+  if (d->fixed_steps > kFewSteps) return {16, kMaxChunkRows, true, perm && d->K <= kMaxChunkRows};
   return {4, kMaxChunkRows, false, false};
 }
 __host__ __device__ constexpr int gemv_prefetch(int NW) { return NW == 4 ? 2 : 3; }
