@@ -298,11 +298,17 @@ def bench_c2(args, wl, alloc, traffic, dev):
                                 max(args.steps // 4, len(c16)), args.warmup // 4, bool(args.graph))
         flop16 = 2.0 * 16 * wl.W.shape[0] * wl.W.shape[1]
         tf = flop16 / (ms16 * 1e-3) / 1e12
+        # the timed output against the fp64 product with the allocator's W_hat
+        rel16 = rel_frobenius(wl.activations(16).astype(np.float64) @ np.asarray(alloc.dequant, np.float64),
+                              Y16.cpu().numpy())
+        if not rel16 < 1e-5:
+            raise SystemExit(f"c2 M=16 output differs from the fp64 product: rel {rel16:.3e} >= 1e-5")
         res["m16"] = {"us_per_call": ms16 * 1e3, "packed_GBps": packed / (ms16 * 1e-3) / 1e9, "TFLOPs": tf,
                       "frac_fp32_peak": tf / FP32_PEAK_TFLOPS, "chunk_rows": d16.host.chunk_rows,
+                      "rel_frobenius_vs_fp64": rel16,
                       "roofline": {"bound": "fp32", "achieved": tf, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
                                    "frac": tf / FP32_PEAK_TFLOPS, "traffic": None}}
-        log(f"c2 M=16: {ms16 * 1e3:.2f} us/call, {tf:.2f} TFLOP/s")
+        log(f"c2 M=16: {ms16 * 1e3:.2f} us/call, {tf:.2f} TFLOP/s; vs fp64 rel {rel16:.2e}")
         del c16
     return res
 
@@ -336,6 +342,14 @@ def device_copy_rates(dev, packed):
 # ----------------------------------------------------------------------------------------------
 # c4: prefill (bf16 MFMA), with its own output checked against a fp64 product
 # ----------------------------------------------------------------------------------------------
+def p0_area_fraction(a):
+    """Fraction of the matrix's weights in P0 leaves (flop counts are dense-equivalent: the
+    kernels skip those leaves' work, the metric does not subtract it)."""
+    q = getattr(a, "inner", a)
+    area = sum(float(((q.leaf[s] & (q.modes[s] == 0))).sum()) * s * s for s in q.sizes)
+    return area / float(q.shape[0] * q.shape[1])
+
+
 def bench_c4(args, wl4, a4, dev):
     import torch
     from tensorpack_amd.kernels.gemm import MTCMatrix
@@ -363,7 +377,7 @@ def bench_c4(args, wl4, a4, dev):
     if not rel < 2e-3:
         raise SystemExit(f"c4 prefill output differs from the fp64 product: rel {rel:.3e} >= 2e-3")
     return {"M": M4, "ms_per_call": ms4, "TFLOPs": tf, "frac_bf16_peak": tf / BF16_PEAK_TFLOPS,
-            "packed_bytes": m4.packed_bytes,
+            "packed_bytes": m4.packed_bytes, "p0_area_fraction": p0_area_fraction(a4),
             "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": tf / BF16_PEAK_TFLOPS, "traffic": None, "kernel": "k_gemm_tile"},
             "parity": {"rows": int(rows.size), "rel_frobenius_vs_fp64": rel, "tolerance": 2e-3}}
@@ -674,12 +688,14 @@ def main():
         "config": {"workload": wl.name + " M=1", "K": K, "N": N, "M": 1, "budget_bits": wl.budget,
                    "bits_per_weight": alloc.bits_per_element, "packed_bytes": c2["packed"],
                    "stream_bytes": ds.device_bytes(), "rotating_copies": c2["n_copies"],
+                   "algorithmic_bytes": c2["packed"] + 4.0 * (K + N),
                    "chunk_rows": ds.host.chunk_rows, "graph_replay": bool(args.graph)},
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": gbs / HBM_PEAK_GBS, "traffic": None if traffic is None else traffic["bytes"],
                      "copy_GBps": copy_gbs, "frac_of_copy": gbs / copy_gbs,
                      "copy_same_bytes_us": copy_small_us, "us_per_call": ms * 1e3,
                      "kernel": "k_gemv<1>", "stream_GBps": ds.device_bytes() / (ms * 1e-3) / 1e9,
+                     "algorithmic_GBps": (c2["packed"] + 4.0 * (K + N)) / (ms * 1e-3) / 1e9,
                      "traffic_detail": traffic},
         "cpu_baseline": cpu,
         "extra": extra,
