@@ -686,13 +686,22 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
       }
     }
   };
-  compute(r0);                                        // null records have no active lanes
-  if constexpr (PF >= 2) compute(r1);
-  if constexpr (PF >= 3) compute(r2);
+  // Records past the prefetched ones, in the same order: each one's slot is loaded a record
+  // ahead (while the previous record computes), so only its payload load is waited for.
   const int nrec = hdr[28 + 2 * cb];
   const uint32_t ovf = (uint32_t)hdr[27 + 2 * cb];
-  for (int i = wave + PF * W; i < nrec; i += W) {
-    fetch(slot_of(i < F ? (uint32_t)(blk * F + i) : ovf + (uint32_t)(i - F)), r0);
+  auto rec = [&](int i) __attribute__((always_inline)) {
+    return i < F ? (uint32_t)(blk * F + i) : ovf + (uint32_t)(i - F);
+  };
+  int i = wave + PF * W;
+  compute(r0);                                        // null records have no active lanes
+  u32x4_t nxt = {};                                   // loaded once r0's registers are free
+  if (i < nrec) nxt = slot_of(rec(i));
+  if constexpr (PF >= 2) compute(r1);
+  if constexpr (PF >= 3) compute(r2);
+  for (; i < nrec; i += W) {
+    fetch(nxt, r0);
+    if (i + W < nrec) nxt = slot_of(rec(i + W));
     compute(r0);
   }
 
