@@ -82,7 +82,8 @@ def test_batch_matches_single_calls(gpu, members, M):
         assert torch.equal(y, s.gemv_f32(X)), (s.K, s.N)
 
 
-def test_batch_strided_outputs_and_uniform_members(gpu):
+@pytest.mark.parametrize("M", [3, 12])
+def test_batch_strided_outputs_and_uniform_members(gpu, M):
     """fp32-scale (uniform-block) members batch together; outputs may be row-strided views."""
     import torch
     from tensorpack_amd.core.allocation import rd_allocate
@@ -92,7 +93,6 @@ def test_batch_strided_outputs_and_uniform_members(gpu):
         W = outlier_matrix(40 + i, K, N)
         a = rd_allocate(W, 4.0, None, 16)
         mats.append((MTCMatrix.from_allocation(W, a.modes, a.scales, 16), a.dequant))
-    M = 3
     streams = [m.device_stream(None, gpu, M) for m, _ in mats]
     Xs = [torch.randn(M, s.K, device=gpu) for s in streams]
     big = [torch.zeros(M, s.N + 32, device=gpu) for s in streams]

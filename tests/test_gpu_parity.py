@@ -293,12 +293,13 @@ def test_uniform_form_packed_kernel_matches_simulation(gpu):
         assert Bm.total_bytes_allocated * 8 == b.payload_bits
 
 
-def test_uniform_form_dense_x(gpu):
+@pytest.mark.parametrize("M", [3, 9, 16])          # vector decode; matrix core at 9 and 16
+def test_uniform_form_dense_x(gpu, M):
     rng = np.random.RandomState(8)
     W = rng.randn(256, 128).astype(np.float32)
     al = rd_allocate(W, 4.0, None, 32)
     m = MTCMatrix.from_allocation(W, al.modes, al.scales, 32)
-    X = rng.randn(3, 256).astype(np.float32)
+    X = rng.randn(M, 256).astype(np.float32)
     assert O.relative_frobenius_error(O.qt_gemm_f64(X, al.dequant), mtc_gemm(X, m)) <= TOL_F32
 
 
