@@ -144,7 +144,10 @@ def traffic_passes(ps, x, kernel="k_gemv"):
 
 
 def timed_calls(torch, launch_list, steps, warmup, use_graph):
-    """Time exactly `steps` calls cycling over launch_list; returns (seconds, per-call ms)."""
+    """Time exactly `steps` calls cycling over launch_list; returns (seconds, per-call ms). With a
+    graph, timed_calls.last_median_ms is the median per-call ms over 10 segments of the replays
+    (the last segment also holds the remainder calls)."""
+    timed_calls.last_median_ms = None
     n = len(launch_list)
     stream = torch.cuda.current_stream()
     if use_graph:
@@ -169,13 +172,28 @@ def timed_calls(torch, launch_list, steps, warmup, use_graph):
             g.replay()
         torch.cuda.synchronize()
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        # one event per tenth of the replays as well, for the median of 10 segments; recording
+        # an event between replays adds no work to the timed stream
+        reps = steps // n
+        marks = sorted({(reps * j) // 10 for j in range(1, 10)} - {0, reps})
+        seg = [torch.cuda.Event(enable_timing=True) for _ in marks]
         start.record(stream)
-        for _ in range(steps // n):
+        k = 0
+        for r in range(reps):
+            if k < len(marks) and r == marks[k]:
+                seg[k].record(stream)
+                k += 1
             g.replay()
         if gt is not None:
             gt.replay()
         stop.record(stream)
         torch.cuda.synchronize()
+        if len(marks) == 9:
+            ev = [start] + seg + [stop]
+            cuts = [0] + marks + [reps]
+            calls = [(cuts[j + 1] - cuts[j]) * n + (tail if j == 9 else 0) for j in range(10)]
+            per = sorted(ev[j].elapsed_time(ev[j + 1]) / calls[j] for j in range(10) if calls[j] > 0)
+            timed_calls.last_median_ms = per[len(per) // 2]
     else:
         for i in range(warmup):
             launch_list[i % n]()
@@ -280,9 +298,10 @@ def bench_c2(args, wl, alloc, traffic, dev):
     torch.cuda.synchronize()
     secs, ms = timed_calls(torch, [lambda c=c: c.gemv_f32(X1, out=Y1) for c in copies], args.steps, args.warmup,
                            bool(args.graph))
+    ms_median = timed_calls.last_median_ms
     gbs = packed / (ms * 1e-3) / 1e9
     log(f"c2 M=1: {ms * 1e3:.2f} us/call, {gbs:.1f} GB/s packed ({len(copies)} copies)")
-    res = {"m": m, "ds": ds, "packed": packed, "ms": ms, "gbs": gbs, "n_copies": len(copies),
+    res = {"m": m, "ds": ds, "packed": packed, "ms": ms, "gbs": gbs, "n_copies": len(copies), "ms_median": ms_median,
            "y": Y1.cpu().numpy().copy(), "x": wl.activations(1)}
     del copies
     if not args.no_m16:
@@ -694,6 +713,7 @@ def main():
                      "frac": gbs / HBM_PEAK_GBS, "traffic": None if traffic is None else traffic["bytes"],
                      "copy_GBps": copy_gbs, "frac_of_copy": gbs / copy_gbs,
                      "copy_same_bytes_us": copy_small_us, "us_per_call": ms * 1e3,
+                     "us_per_call_median_of_10": None if c2["ms_median"] is None else c2["ms_median"] * 1e3,
                      "kernel": "k_gemv<1>", "stream_GBps": ds.device_bytes() / (ms * 1e-3) / 1e9,
                      "algorithmic_GBps": (c2["packed"] + 4.0 * (K + N)) / (ms * 1e-3) / 1e9,
                      "traffic_detail": traffic},
