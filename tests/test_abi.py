@@ -280,6 +280,38 @@ def test_batch_plan_sizes_and_errors(hip):
     assert hip.mtc_gemv_f32_batch(bogus.ctypes.data, 0x40000, None) == -2
 
 
+def test_decode_workspace_and_lds_by_m_tile(hip):
+    """Decode sizes are host arithmetic. M <= 4 runs one tile of 1, 2 or 4 rows on the vector
+    path. 5 <= M <= 8 runs tiles of 8 rows on the matrix core, and so does M > 8 when a chunk is
+    longer than 2048 rows. Otherwise M > 8 runs tiles of 16 rows. Matrix-core tiles add a
+    staged copy of X, K x tile rows fp32 per tile, after the split-K area, 256-aligned.
+    Expected byte counts are worked out by hand for K = 256, 2 panels x 2 chunks of 128 rows."""
+    ref = ctypes.byref(_desc())
+    # counters: 256 (one aligned line); partials: tiles x 2 panels x 2 chunks x rows x 32 x 4 B
+    expect = {1: 256 + 512, 2: 256 + 1024, 4: 256 + 2048,
+              5: 256 + 4096 + 256 * 8 * 4, 8: 256 + 4096 + 256 * 8 * 4,
+              9: 256 + 8192 + 256 * 16 * 4, 16: 256 + 8192 + 256 * 16 * 4,
+              17: 256 + 16384 + 2 * 256 * 16 * 4}
+    for M, n in expect.items():
+        assert hip.mtc_gemv_workspace_bytes(ref, M) == n, M
+    # one chunk: no split-K area, only the staged X of the matrix-core tiles
+    one = ctypes.byref(_desc(chunk_rows=256, n_chunks=1))
+    assert hip.mtc_gemv_workspace_bytes(one, 4) == 0
+    assert hip.mtc_gemv_workspace_bytes(one, 16) == 256 * 16 * 4
+    # chunks of 4096 rows keep 8-row tiles at M = 16: two tiles
+    big = ctypes.byref(_desc(K=8192, chunk_rows=4096, n_chunks=2))
+    assert hip.mtc_gemv_workspace_bytes(big, 16) == 256 + 2 * 2 * 2 * 8 * 32 * 4 + 2 * 8192 * 8 * 4
+    lds = hip.mtc_gemv_lds_bytes
+    # the on-chip X of a matrix-core block is tile rows x chunk rows fp32, the rest is fixed
+    for mt_m in (5, 16):
+        assert lds(4096, 2048, 0, mt_m) - lds(4096, 1024, 0, mt_m) == (8 if mt_m == 5 else 16) * 1024 * 4
+    assert lds(4096, 2048, 0, 9) == lds(4096, 2048, 0, 16) != lds(4096, 2048, 0, 8)
+    assert lds(8192, 4096, 0, 16) == lds(8192, 4096, 0, 8)
+    assert lds(4096, 2048, 1, 16) == lds(4096, 2048, 0, 16)     # no gather of X on the matrix core
+    assert max(lds(4096, 2048, 0, 16), lds(8192, 4096, 0, 8)) <= 160 * 1024
+    assert lds(0, 128, 0, 1) == lds(256, 128, 0, 0) == 0
+
+
 def test_noalloc_entry_rejects_before_any_gpu_call(hip):
     """mtc_gemv_f32_noalloc checks arguments and the static scratch bound on the host."""
     d = _desc()                                                  # 2 row chunks: needs split-K scratch
