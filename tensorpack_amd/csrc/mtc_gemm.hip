@@ -1,7 +1,9 @@
 // gfx950 prefill kernel: Y = X * W_hat with W_hat decoded from the tile stream
 // into bf16 LDS tiles and multiplied on v_mfma_f32_32x32x16_bf16 (fp32 accumulate).
 //
-//   k_stage_x   : X -> bf16 Xp = X[:, row_perm] (only for fp32 X or a row permutation)
+//   k_stage_x_rows / k_stage_x : X -> bf16 Xp = X[:, row_perm] (only for fp32 X or a row
+//                 permutation); 1-4 rows per block gathered through LDS, or, for rows
+//                 wider than the LDS holds, one element per lane from global memory
 //   k_gemm_tile : one 256 x 256 output tile per block, K in steps of 64. Warp-specialized:
 //                 8 consumer waves (2 x 4 of 128 x 64 outputs) copy X tiles straight
 //                 into LDS (buffer loads with the LDS destination, two steps ahead into
