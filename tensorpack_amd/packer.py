@@ -272,15 +272,92 @@ def _kind_rank(S: int, P: int) -> int:
 _KIND_S = np.array([LEAF_SIZES[r // len(CODE_WIDTHS)] for r in range(len(LEAF_SIZES) * len(CODE_WIDTHS))])
 _KIND_P = np.array([CODE_WIDTHS[r % len(CODE_WIDTHS)] for r in range(len(LEAF_SIZES) * len(CODE_WIDTHS))])
 
+# Payload bytes a merge of two kinds may add per decode step record it saves (besides the
+# record's own 64 bytes, which it also saves).
+MERGE_BYTES_PER_RECORD = 256
+# Bits a leaf's codes may be widened by. The fp32 decode sums x * u - 2^(P-1) * sum(x), so a
+# code stored d bits wider carries an offset 2^d times larger through the same sums: its
+# rounding error grows by up to 2^d.
+MERGE_MAX_WIDEN = 2
+
+
+def _block_records(chunks: np.ndarray) -> np.ndarray:
+    """Decode step records of one kind per unit: (U, 8) lane chunks per column group ->
+    (U,) records over the unit's two blocks of 4 column groups (16 chunks per slot)."""
+    return (-(-chunks.reshape(-1, BLOCKS_PER_UNIT, STEP_GROUPS).max(axis=2) // STEP_LANES)).sum(axis=1)
+
+
+def storage_widths(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np.ndarray],
+                   modes: Dict[int, np.ndarray], chunk_rows: int) -> Dict[int, np.ndarray]:
+    """Per level S, the code width each leaf is stored at: its mode P, or a wider width P' of
+    the same leaf size in the same unit.
+
+    The decode runs one kind (S, P) per step record of 4 column groups x 16 chunks, so a kind
+    with a few chunks in a block still costs a whole record. Signed codes q of width P fit any
+    wider offset-binary width (u' = q + 2^(P'-1)) and decode to the same q * s, so W_hat is
+    unchanged. Per unit and leaf size, kinds are taken narrowest first; each is merged into
+    the narrowest wider kind present in the unit when that saves records, adds at most
+    MERGE_BYTES_PER_RECORD payload bytes per record saved and widens no leaf it holds (its
+    own or merged into it earlier) by more than MERGE_MAX_WIDEN bits."""
+    K, N = (int(x) for x in shape)
+    n_chunks = -(-K // chunk_rows)
+    n_units = (N // PANEL) * n_chunks
+    widths = np.array(CODE_WIDTHS)
+    out: Dict[int, np.ndarray] = {}
+    for S in (int(s) for s in sizes):
+        mode = np.asarray(modes[S])
+        stored = np.asarray(leaf[S], dtype=bool) & np.isin(mode, widths)
+        pw = np.where(stored, mode, 0).astype(np.int64)
+        out[S] = pw
+        ii, jj = np.nonzero(stored)
+        if ii.size == 0:
+            continue
+        p_idx = np.searchsorted(widths, mode[ii, jj])
+        unit = ((jj * S) // PANEL) * n_chunks + (ii * S) // chunk_rows
+        ncg = max(1, S // GROUP)
+        g0 = (jj * S % PANEL) // GROUP
+        per_cg = 1 if S <= 8 else S // 8            # chunks per covered column group (S = 4: leaves)
+        cnt = np.zeros((n_units, len(widths), N_GROUPS), dtype=np.int64)
+        for c in range(ncg):
+            np.add.at(cnt, (unit, p_idx, g0 + c), per_cg)
+
+        def chunks(x):
+            return -(-x // 2) if S == 4 else x       # two 4x4 leaves per chunk
+
+        target = np.tile(np.arange(len(widths)), (n_units, 1))
+        narrowest = np.tile(widths, (n_units, 1))      # narrowest mode each kind holds
+        for p in range(len(widths) - 1):
+            undecided = cnt[:, p].sum(axis=1) > 0
+            for q in range(p + 1, len(widths)):
+                cand = undecided & (cnt[:, q].sum(axis=1) > 0)
+                if not cand.any():
+                    continue
+                merged = cnt[:, p] + cnt[:, q]
+                saved = (_block_records(chunks(cnt[:, p])) + _block_records(chunks(cnt[:, q])) -
+                         _block_records(chunks(merged)))
+                extra = chunks(cnt[:, p]).sum(axis=1) * 4 * (widths[q] - widths[p])     # 32 codes per chunk
+                ok = cand & (saved > 0) & (extra <= MERGE_BYTES_PER_RECORD * saved) & \
+                    (widths[q] - narrowest[:, p] <= MERGE_MAX_WIDEN)
+                cnt[ok, q] = merged[ok]
+                cnt[ok, p] = 0
+                narrowest[ok, q] = np.minimum(narrowest[ok, q], narrowest[ok, p])
+                target[ok, p] = q
+                undecided &= ~ok
+        for p in range(len(widths) - 2, -1, -1):     # follow merges of merged kinds
+            target[:, p] = np.where(target[:, p] != p, target[np.arange(n_units), target[:, p]], p)
+        pw[ii, jj] = widths[target[unit, p_idx]]
+    return out
+
 
 def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np.ndarray],
                 modes: Dict[int, np.ndarray], scales: Dict[int, np.ndarray], codes_of: CodeSource,
                 chunk_rows: int = 512, scale_format: str = "bf16", row_perm: Optional[np.ndarray] = None,
-                col_perm: Optional[np.ndarray] = None) -> PanelStream:
+                col_perm: Optional[np.ndarray] = None, merge_kinds: bool = True) -> PanelStream:
     """Pack the leaves given per level s (leaf mask, mode grid, scale grid) of a K x N weight.
 
     `codes_of(S, P, ii, jj, scales)` returns the (n, S, S) integer codes of the
-    listed leaves (see weight_codes).
+    listed leaves (see weight_codes). With `merge_kinds`, rare kinds are stored at a wider
+    width of the same leaf size (storage_widths); W_hat is the same either way.
     """
     K, N = (int(x) for x in shape)
     if N % PANEL or K % 8:
@@ -297,14 +374,20 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
     ch_unit, ch_cg, ch_kind, ch_row, ch_leaf, ch_words = [], [], [], [], [], []
     n_real = 0
     n_lw = 0
-    for S in sorted((int(s) for s in sizes), reverse=True):
-        if S not in LEAF_SIZES:
+    for S in sizes:
+        if int(S) not in LEAF_SIZES:
             raise ValueError(f"leaf size {S} not supported by the panel stream (sizes {LEAF_SIZES})")
+    if merge_kinds:
+        store_w = storage_widths((K, N), sizes, leaf, modes, chunk_rows)
+    else:
+        store_w = {int(S): np.asarray(modes[S]) for S in sizes}
+    for S in sorted((int(s) for s in sizes), reverse=True):
         lv_leaf = np.asarray(leaf[S], dtype=bool)
         lv_mode = np.asarray(modes[S])
+        lv_store = store_w[S]
         lv_scale = np.asarray(scales[S], dtype=np.float32)
-        for P in CODE_WIDTHS:
-            ii, jj = np.nonzero(lv_leaf & (lv_mode == P))
+        for P in CODE_WIDTHS:                          # storage width: the kind's P
+            ii, jj = np.nonzero(lv_leaf & np.isin(lv_mode, CODE_WIDTHS) & (lv_store == P))
             if ii.size == 0:
                 continue
             kr = _kind_rank(S, P)
@@ -314,7 +397,11 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
             order = np.lexsort((k0, c0, unit))
             ii, jj, k0, c0, unit = ii[order], jj[order], k0[order], c0[order], unit[order]
             sc = lv_scale[ii, jj]
-            q = np.asarray(codes_of(S, P, ii, jj, sc)).astype(np.int32)          # (n, S, S) row-major
+            q = np.empty((ii.size, S, S), dtype=np.int32)                         # (n, S, S) row-major
+            qm = lv_mode[ii, jj]
+            for Pq in np.unique(qm):                   # codes quantized at each leaf's own width
+                sel = np.flatnonzero(qm == Pq)
+                q[sel] = np.asarray(codes_of(S, int(Pq), ii[sel], jj[sel], sc[sel])).astype(np.int32)
             n_real += ii.size
             words = ((k0 % chunk_rows) // 4).astype(np.uint32)
             if scale_format == "bf16":

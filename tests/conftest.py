@@ -43,7 +43,8 @@ def outlier_matrix(seed=0, n=128, m=None):
 def kind_mix_stream(K=4096, N=32, seed=24):
     """Panel stream of 4x4 leaves whose code width changes with the column group (random
     codes, power-of-two scales, 30 % P0): the 4 column groups of a decode block step
-    through different kinds, so a block has more step records than the fixed area holds."""
+    through different kinds, so a block has more step records than the fixed area holds
+    (kinds are stored at their own widths: no merging into wider kinds)."""
     from tensorpack_amd.packer import pack_levels
     rng = np.random.RandomState(seed)
     widths = np.array([2, 3, 4, 5, 6, 8, 16, 2])
@@ -52,4 +53,4 @@ def kind_mix_stream(K=4096, N=32, seed=24):
     leaf4 = np.ones((K // 4, N // 4), bool)
     scales4 = (2.0 ** rng.randint(-8, 0, size=(K // 4, N // 4))).astype(np.float32)
     codes = lambda S, P, ii, jj, sc: rng.randint(-(1 << (P - 1)), 1 << (P - 1), size=(ii.size, S, S))
-    return pack_levels((K, N), (4,), {4: leaf4}, {4: modes4}, {4: scales4}, codes, chunk_rows=K)
+    return pack_levels((K, N), (4,), {4: leaf4}, {4: modes4}, {4: scales4}, codes, chunk_rows=K, merge_kinds=False)

@@ -13,7 +13,7 @@ from tensorpack_amd.core.quadtree import QuadtreeRD
 from tensorpack_amd.kernels.gemm import MTCMatrix, arena_decode, arena_encode
 from tensorpack_amd.packer import (BLOCKS_PER_UNIT, LEAF_PAD, MAX_FIXED_STEPS, N_GROUPS, STEP_GROUPS, STEP_LANES,
                                    decode_stream, decode_steps, pack_codes, pack_levels, step_record_index,
-                                   unpack_codes)
+                                   storage_widths, unpack_codes)
 
 from conftest import kind_mix_stream, outlier_matrix
 
@@ -89,15 +89,27 @@ def test_stream_layout_invariants():
                 start += ps.buckets[k, 2] & 0xFFFF
 
 
-def test_payload_accounting_matches_allocator_bits():
+@pytest.mark.parametrize("merge", [False, True])
+def test_payload_accounting_matches_allocator_bits(merge):
+    """Unmerged, the chunk words hold exactly the allocator's payload bits (plus S = 4 pad
+    leaves); merged, every leaf is stored at its storage width, which is at least its mode."""
     W = outlier_matrix(12, 256, 256)
     a = QuadtreeRD(W, None, (32, 16, 8, 4)).select(4.0)
-    ps = MTCMatrix.from_quadtree(a, W).panel_stream(256)
-    payload_bits = sum(int((a.leaf[s] & (a.modes[s] == m)).sum()) * s * s * m
+    lv = MTCMatrix.from_quadtree(a, W)._levels
+    ps = pack_levels(lv.shape, lv.sizes, lv.leaf, lv.modes, lv.scales, lv.codes_of, 256, lv.scale_format,
+                     lv.row_perm, lv.col_perm, merge_kinds=merge)
+    widths = storage_widths((256, 256), a.sizes, a.leaf, a.modes, 256) if merge else a.modes
+    for s in a.sizes:
+        stored = a.leaf[s] & (a.modes[s] > 0)
+        assert (widths[s][stored] >= a.modes[s][stored]).all()
+    payload_bits = sum(int((a.leaf[s] & (a.modes[s] > 0) & (widths[s] == m)).sum()) * s * s * m
                        for s in a.sizes for m in (2, 3, 4, 5, 6, 8, 16))
+    if not merge:
+        assert payload_bits == sum(int((a.leaf[s] & (a.modes[s] == m)).sum()) * s * s * m
+                                   for s in a.sizes for m in (2, 3, 4, 5, 6, 8, 16))
     b = ps.buckets[:ps.n_buckets]
     n, P = (b[:, 2] & 0xFFFF).astype(np.int64), (b[:, 3] >> 8).astype(np.int64)
-    # chunk words = allocator payload + the zero codes of S=4 pad leaves (16 codes each)
+    # chunk words = stored payload + the zero codes of S=4 pad leaves (16 codes each)
     pad_bits = 0
     for k in np.flatnonzero((b[:, 3] & 0xFF) == 2):
         u = int(np.searchsorted(ps.unit_hdr[:, 5], k, side="right"))
@@ -221,6 +233,57 @@ def test_step_records_overflow_past_the_fixed_area():
     assert n.max() > MAX_FIXED_STEPS and ps.fixed_steps == MAX_FIXED_STEPS
     assert ps.steps.shape[0] > ps.n_units * BLOCKS_PER_UNIT * MAX_FIXED_STEPS + 1
     assert np.array_equal(_bits(decode_steps(ps)), _bits(decode_stream(ps)))
+
+
+def _records(ps):
+    st = ps.steps.reshape(-1, STEP_GROUPS, 4)
+    return int((st[:, :, 2].sum(axis=1) > 0).sum())
+
+
+def test_storage_widths_merge_rare_kinds_within_the_byte_limit():
+    """One unit of 256 rows x 32 columns of 8x8 leaves (leaf (i, j): rows 8i.., column groups
+    2j, 2j + 1; blocks of 4 column groups). Worked by hand: a lone P2 leaf among 31 P3 leaves
+    of its column pair costs a record of its own; stored at P3 it fits the P3 records (32
+    chunks per group either way: 2 records), so it is merged. Fifteen P2 leaves (one full
+    record) and one P16 leaf: merged they fit one record, but the 30 P2 chunks would grow by
+    14 bits per code, 1680 bytes for one record saved, so they stay."""
+    shape, S = (256, 32), 8
+    leaf = {S: np.ones((32, 4), bool)}
+    modes = {S: np.zeros((32, 4), np.int64)}
+    modes[S][:, 0] = 3
+    modes[S][0, 0] = 2
+    w = storage_widths(shape, (S,), leaf, modes, 256)[S]
+    assert w[0, 0] == 3 and (w[1:, 0] == 3).all() and (w[:, 1:] == 0).all()
+    modes[S][:, 0] = 0
+    modes[S][:15, 1] = 2
+    modes[S][15, 1] = 16
+    w = storage_widths(shape, (S,), leaf, modes, 256)[S]
+    assert (w[:15, 1] == 2).all() and w[15, 1] == 16
+    # the decision covers the unit: a P2 leaf in the other block (column groups 4-7) keeps
+    # its record either way (2 + 1 records before, 2 merged: one saved for 32 chunks x 56
+    # bytes), so nothing is merged
+    modes[S][0, 2] = 2
+    w = storage_widths(shape, (S,), leaf, modes, 256)[S]
+    assert (w[:15, 1] == 2).all() and w[15, 1] == 16 and w[0, 2] == 2
+
+
+@pytest.mark.parametrize("budget,chunk_rows,perm", [(2.5, 128, False), (3.25, 256, True), (4.0, 64, True)])
+def test_merged_kinds_decode_to_the_same_w_hat(budget, chunk_rows, perm):
+    """Merged and unmerged streams of one allocation decode to the same W_hat bit for bit, by
+    the bucket walk and by the step-record walk; merging never adds records."""
+    W = outlier_matrix(31, 512, 256)
+    h = np.exp(np.random.RandomState(5).randn(512))
+    a = (PermutedQuadtreeRD(W, h, (32, 16, 8, 4)) if perm else QuadtreeRD(W, None, (32, 16, 8, 4))).select(budget)
+    lv = MTCMatrix.from_quadtree(a, W)._levels
+    args = (lv.shape, lv.sizes, lv.leaf, lv.modes, lv.scales, lv.codes_of, chunk_rows, lv.scale_format,
+            lv.row_perm, lv.col_perm)
+    p0, p1 = pack_levels(*args, merge_kinds=False), pack_levels(*args, merge_kinds=True)
+    ref = _bits(decode_stream(p0))
+    assert np.array_equal(_bits(decode_stream(p1)), ref)
+    assert np.array_equal(_bits(decode_steps(p1)), ref)
+    assert _records(p1) <= _records(p0)
+    widths = storage_widths(lv.shape, lv.sizes, lv.leaf, lv.modes, chunk_rows)
+    assert any((widths[s] != np.where(lv.leaf[s] & (lv.modes[s] > 0), lv.modes[s], 0)).any() for s in lv.sizes)
 
 
 def test_step_records_survive_save_load(tmp_path):
