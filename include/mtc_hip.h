@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MTC_ABI_VERSION 7
+#define MTC_ABI_VERSION 8
 
 enum {
   MTC_OK = 0,
@@ -93,9 +93,11 @@ enum { MTC_DTYPE_F32 = 0, MTC_DTYPE_BF16 = 1 };
  * chunks with 16-byte loads that may run up to 3 dwords past a chunk's end); leaf_word
  * holds at least one word.
  *
- * A lane chunk is 32 codes in P dwords: code i occupies bits [i*P, i*P+P) of
- * the little-endian bit string, stored offset-binary (u = q + 2^(P-1), so the
- * signed code q = u - 2^(P-1)). Every chunk lands in the 4
+ * A lane chunk is 32 codes in P dwords, stored offset-binary (u = q + 2^(P-1), so
+ * the signed code q = u - 2^(P-1)). For P != 3 code i occupies bits [i*P, i*P+P)
+ * of the chunk's little-endian bit string. For P = 3 the codes sit in byte lanes:
+ * byte b of dwords 0, 1, 2 (dword 0's byte lowest) is a 24-bit string holding
+ * codes 8b .. 8b+7, code 8b + a at bits [3a, 3a+3). Every chunk lands in the 4
  * columns of its cg: for S >= 8 it is 4 columns x 8 rows of one leaf, code i
  * at column i/8, row i%8, and chunk t of a bucket is leaf t/(S/8), row block
  * t%(S/8); for S = 4 it is leaves 2t and 2t+1 (16 codes each, column-major; an

@@ -2,7 +2,7 @@
 
 import ctypes
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 MTC_OK = 0
 MTC_DTYPE_F32 = 0

@@ -1,11 +1,13 @@
 // Device-side decoding of the panel stream (layout documented in include/mtc_hip.h).
 //
-// A lane chunk is 32 offset-binary codes u = q + 2^(P-1) of P bits packed
-// LSB-first into P dwords. After full unrolling every bit position is a
-// compile-time constant: byte-aligned fields (P = 2, 4 after one mask per 4 or 8
-// codes, P = 8 directly) convert with v_cvt_f32_ubyteN, other widths with one
-// v_bfe_u32 (or v_alignbit + v_and when a code straddles a dword) and one
-// v_cvt_f32_u32.
+// A lane chunk is 32 offset-binary codes u = q + 2^(P-1) of P bits in P dwords:
+// LSB-first for every width but 3; 3-bit codes sit in byte lanes (byte b of the 3
+// dwords is a 24-bit string holding codes 8b .. 8b+7, 3 bits each), so one shift
+// and mask (two, and an or, where a code crosses a byte) bring a code of every lane
+// into its own byte. After full unrolling every bit position is a compile-time
+// constant: byte-aligned fields (P = 2, 3, 4 after one mask per 4 or 8 codes, P = 8
+// directly) convert with v_cvt_f32_ubyteN, P = 5 and 6 with one v_bfe_u32 (or
+// v_alignbit + v_and when a code straddles a dword) and one v_cvt_f32_u32.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -83,7 +85,7 @@ __device__ __forceinline__ uint32_t opaque(uint32_t x) {
 
 __device__ __forceinline__ float ubyte(uint32_t x, int k) { return (float)((x >> (8 * k)) & 0xFFu); }
 
-// Offset-binary code i (0..31) of a chunk.
+// Offset-binary code i (0..31) of a chunk (LSB-first widths, P != 3).
 template <int P>
 __device__ __forceinline__ uint32_t chunk_ucode(const uint32_t (&w)[P], int i) {
   const int b = i * P, j = b >> 5, o = b & 31;
@@ -118,6 +120,23 @@ __device__ __forceinline__ void decode_chunk_u(const uint32_t (&w)[P], float (&u
 #pragma unroll
         for (int k = 0; k < 4; ++k) u[16 * j + 4 * k + s] = ubyte(f, k);
       }
+  } else if constexpr (P == 3) {
+    // byte k of f[a] is code 8k + a (bits 3a .. 3a+2 of byte lane k)
+    uint32_t f[8];
+    f[0] = w[0] & 0x07070707u;
+    f[1] = (w[0] >> 3) & 0x07070707u;
+    f[2] = ((w[0] >> 6) & 0x03030303u) | ((w[1] << 2) & 0x04040404u);
+    f[3] = (w[1] >> 1) & 0x07070707u;
+    f[4] = (w[1] >> 4) & 0x07070707u;
+    f[5] = ((w[1] >> 7) & 0x01010101u) | ((w[2] << 1) & 0x06060606u);
+    f[6] = (w[2] >> 2) & 0x07070707u;
+    f[7] = (w[2] >> 5) & 0x07070707u;
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+      const uint32_t v = opaque(f[a]);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) u[8 * k + a] = ubyte(v, k);
+    }
   } else if constexpr (P == 16) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) {

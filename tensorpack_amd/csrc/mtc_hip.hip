@@ -775,9 +775,10 @@ __global__ __launch_bounds__(kStageThreads) void k_gemv_stage_x(int K, const flo
 
 // A lane's loads of one pass: the 64-bit window(s) holding its column's codes (two loads for
 // every kind: leaf 0's and leaf 1's windows for two 4x4 leaves; the two halves of a 128-bit
-// window for P = 16; the window and a load past the buffer's end, which reads zeros, for
-// other widths), the leaf word(s) and, with fp32 scales, the leaf scale(s). Same load count
-// for every kind, so the compiler's in-order waits stay exact.
+// window for P = 16; the whole 3-dword chunk and the dword after it for P = 3, whose codes sit
+// in byte lanes; the window and a load past the buffer's end, which reads zeros, for other
+// widths), the leaf word(s) and, with fp32 scales, the leaf scale(s). Same load count for
+// every kind, so the compiler's in-order waits stay exact.
 struct MfmaPass {
   u32x4_t w;
   uint32_t lw0, lw1;
@@ -798,7 +799,10 @@ __device__ __forceinline__ void mfma_load_rec(__amdgpu_buffer_rsrc_t pay_r, __am
   const uint32_t ob = (pay + t0 * P) << 2;           // payload byte offset of pass 0's chunk
   const bool two = ls == 2;                          // two 4x4 leaves per chunk
   uint32_t o0, o1;
-  if (two) {                                         // codes 4j.. of leaf 0 and 16 + 4j.. of leaf 1
+  if (P == 3) {                                      // byte lanes: every column spans the chunk
+    o0 = ob;
+    o1 = ob + 8;
+  } else if (two) {                                  // codes 4j.. of leaf 0 and 16 + 4j.. of leaf 1
     o0 = ob + (((4 * j * P) >> 5) << 2);
     o1 = ob + ((((16 + 4 * j) * P) >> 5) << 2);
   } else if (P == 16) {                              // codes 8j .. 8j + 7: 128 bits at dword 4j
@@ -808,7 +812,7 @@ __device__ __forceinline__ void mfma_load_rec(__amdgpu_buffer_rsrc_t pay_r, __am
     o0 = ob + (((8 * j * P) >> 5) << 2);
     o1 = kOutOfRange;
   }
-  const bool o1_used = two || P == 16;
+  const bool o1_used = two || P == 16 || P == 3;
   const uint32_t sh = ls >= 3 ? ls - 3 : 0u;         // leaf sizes 8, 16, 32 (the null record has ls = 0)
   const uint32_t l0 = leaf + (two ? 2 * t0 : t0 >> sh);
   const uint32_t pstep = 16 * P;                     // bytes of 4 chunks (P dwords each)
@@ -849,6 +853,13 @@ __device__ __forceinline__ void window_codes(uint32_t lo, uint32_t hi, uint32_t 
   }
 }
 
+// Byte lane b (0..3) of a 3-bit chunk (dwords w0, w1, w2) as one 24-bit string: codes 8b ..
+// 8b + 7 at bits 0, 3, .., 21. Two byte permutes.
+__device__ __forceinline__ uint32_t p3_lane(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t b) {
+  const uint32_t lo = __builtin_amdgcn_perm(w1, w0, b | ((4u + b) << 8) | 0x0C0C0000u);   // w0.b, w1.b, 0, 0
+  return __builtin_amdgcn_perm(w2, lo, 0x0C000100u | ((4u + b) << 16));                   // lo.0, lo.1, w2.b, 0
+}
+
 // A lane's column of its chunk in one pass of kind (S, P): the 8 weights (zero when the
 // lane's chunk is not in the bucket, `on` false, or its leaf is padding) and the unit rows
 // they sit on (rows row0 .. row0 + 3 and row1 .. row1 + 3; row_off: the chunk's 8-row block
@@ -860,24 +871,42 @@ __device__ __forceinline__ void mfma_decode(const MfmaPass& r, bool on, int row_
   constexpr float off = (float)(1 << (P - 1));
   float u[8];
   float s0, s1;
-  if constexpr (S == 4) {
+  // the column's 8 codes
+  if constexpr (P == 3) {
+    if constexpr (S == 4) {
+      // codes 4j + k (leaf 0) and 16 + 4j + k (leaf 1): byte lanes j/2 and 2 + j/2, from bit 12 (j & 1)
+      const uint32_t l0 = p3_lane(r.w.x, r.w.y, r.w.z, j >> 1), l1 = p3_lane(r.w.x, r.w.y, r.w.z, 2u + (j >> 1));
+      const uint32_t o = 12u * (j & 1u);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        u[k] = (float)__builtin_amdgcn_ubfe(l0, o + 3u * k, 3u);
+        u[4 + k] = (float)__builtin_amdgcn_ubfe(l1, o + 3u * k, 3u);
+      }
+    } else {
+      const uint32_t l = p3_lane(r.w.x, r.w.y, r.w.z, j);   // codes 8j .. 8j + 7: byte lane j
+#pragma unroll
+      for (int k = 0; k < 8; ++k) u[k] = (float)((l >> (3 * k)) & 7u);
+    }
+  } else if constexpr (S == 4) {
     window_codes<P, 4, (P >= 8)>(r.w.x, r.w.y, (4 * j * P) & 31u, u);
     window_codes<P, 4, (P >= 8)>(r.w.z, r.w.w, ((16 + 4 * j) * P) & 31u, u + 4);
+  } else if constexpr (P == 16) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      u[2 * k] = (float)(r.w[k] & 0xFFFFu);
+      u[2 * k + 1] = (float)(r.w[k] >> 16);
+    }
+  } else {
+    window_codes<P, 8, (P == 4 || P == 8)>(r.w.x, r.w.y, (8 * j * P) & 31u, u);
+  }
+  // their leaves: rows and scales
+  if constexpr (S == 4) {
     const LeafInfo a = leaf_info_v(r.lw0, fp32_scales, r.fs0), b = leaf_info_v(r.lw1, fp32_scales, r.fs1);
     row0 = on ? a.row : 0;                           // a masked lane's leaf may be any unit's
     row1 = on ? b.row : 0;
     s0 = (on && !a.pad) ? a.scale : 0.0f;
     s1 = (on && !b.pad) ? b.scale : 0.0f;
   } else {
-    if constexpr (P == 16) {
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        u[2 * k] = (float)(r.w[k] & 0xFFFFu);
-        u[2 * k + 1] = (float)(r.w[k] >> 16);
-      }
-    } else {
-      window_codes<P, 8, (P == 4 || P == 8)>(r.w.x, r.w.y, (8 * j * P) & 31u, u);
-    }
     const LeafInfo a = leaf_info_v(r.lw0, fp32_scales, r.fs0);
     row0 = on ? a.row + row_off : 0;                 // a masked lane's leaf may be any unit's
     row1 = row0 + 4;

@@ -35,7 +35,7 @@ LEAF_PAD = 1 << 13
 ROW_BITS = 10                          # leaf word: row/4 in bits 0-9
 MAX_CHUNK_ROWS = 4 << ROW_BITS         # 4096
 UNIT_HDR_WORDS = 32
-STREAM_FORMAT = 7                      # panel stream layout version (matches the C-ABI version)
+STREAM_FORMAT = 8                      # panel stream layout version (matches the C-ABI version)
 PAYLOAD_PAD = 4                        # dwords after the last bucket
 STEP_GROUPS = 4                        # column groups one decode step covers
 STEP_LANES = 16                        # lanes (chunks) per column group in a step
@@ -211,20 +211,41 @@ class PanelStream:
             bad(f"fixed_steps={self.fixed_steps}")
 
 
+def _code_bits(P: int, i: int):
+    """Where code i of a chunk lives: [(dword, shift, bits of the code taken, shift into the
+    code)], one entry per dword it touches. P = 3 uses byte lanes: byte b of the 3 dwords,
+    dword 0's byte lowest, is a 24-bit string holding codes 8b .. 8b+7 at bits 3a (a = i % 8),
+    so a shift and a mask extract one code of every lane at once. Other widths run code i
+    over bits [i*P, i*P+P) of the chunk's little-endian bit string."""
+    if P == 3:
+        b, s = i // 8, 3 * (i % 8)
+        k, o = s // 8, s % 8
+        first = min(3, 8 - o)
+        parts = [(k, 8 * b + o, first, 0)]
+        if first < 3:
+            parts.append((k + 1, 8 * b, 3 - first, first))
+        return parts
+    bit = i * P
+    j, sh = bit >> 5, bit & 31
+    first = min(P, 32 - sh)
+    parts = [(j, sh, first, 0)]
+    if first < P:
+        parts.append((j + 1, 0, P - first, first))
+    return parts
+
+
 def pack_codes(codes: np.ndarray, P: int) -> np.ndarray:
-    """(n, 32) signed codes q -> (n, P) uint32 of offset-binary codes u = q + 2^(P-1);
-    code i at bits [i*P, i*P+P) of the chunk."""
+    """(n, 32) signed codes q -> (n, P) uint32 of offset-binary codes u = q + 2^(P-1),
+    placed as _code_bits says."""
     n = codes.shape[0]
     u = (codes.astype(np.int64) + (1 << (P - 1))).astype(np.uint64)
     if np.any(u >> np.uint64(P)):
         raise ValueError(f"codes outside the signed {P}-bit range")
     out = np.zeros((n, P), dtype=np.uint64)
     for i in range(32):
-        bit = i * P
-        j, sh = bit >> 5, bit & 31
-        out[:, j] |= (u[:, i] << np.uint64(sh)) & np.uint64(0xFFFFFFFF)
-        if sh + P > 32:
-            out[:, j + 1] |= u[:, i] >> np.uint64(32 - sh)
+        for k, sh, nb, lo in _code_bits(P, i):
+            part = (u[:, i] >> np.uint64(lo)) & np.uint64((1 << nb) - 1)
+            out[:, k] |= part << np.uint64(sh)
     return out.astype(np.uint32)
 
 
@@ -232,15 +253,11 @@ def unpack_codes(words: np.ndarray, P: int) -> np.ndarray:
     """Inverse of pack_codes: (n, P) uint32 -> (n, 32) int32."""
     w = words.astype(np.uint64)
     n = w.shape[0]
-    out = np.empty((n, 32), dtype=np.int64)
-    mask = np.uint64((1 << P) - 1)
+    out = np.zeros((n, 32), dtype=np.int64)
     for i in range(32):
-        bit = i * P
-        j, sh = bit >> 5, bit & 31
-        v = w[:, j] >> np.uint64(sh)
-        if sh + P > 32:
-            v |= w[:, j + 1] << np.uint64(32 - sh)
-        v &= mask
+        v = np.zeros(n, dtype=np.uint64)
+        for k, sh, nb, lo in _code_bits(P, i):
+            v |= ((w[:, k] >> np.uint64(sh)) & np.uint64((1 << nb) - 1)) << np.uint64(lo)
         out[:, i] = v.astype(np.int64) - (1 << (P - 1))
     return out.astype(np.int32)
 

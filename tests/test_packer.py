@@ -37,6 +37,7 @@ def test_pack_codes_round_trip_and_bit_order(P):
     assert w.shape == (9, P)
     assert np.array_equal(unpack_codes(w, P), q)
     # offset-binary: q = -2^(P-1) packs to all-zero bits; u = 1 for code 1 starts at bit P
+    # (P = 3 too: code 1 is byte lane 0's second code, at bit 3 of dword 0)
     one = np.full((1, 32), lo, np.int64)
     one[0, 1] = lo + 1
     w1 = pack_codes(one, P)
@@ -44,6 +45,16 @@ def test_pack_codes_round_trip_and_bit_order(P):
     assert np.all(pack_codes(np.zeros((1, 32), np.int64), P)[0] != 0)
     with pytest.raises(ValueError):
         pack_codes(np.full((1, 32), hi + 1), P)
+    # every code read back from where the layout puts it, by explicit bit strings
+    u = q + (1 << (P - 1))
+    for n in range(q.shape[0]):
+        if P == 3:          # byte lane b of the 3 dwords: codes 8b .. 8b+7 at bits 3a
+            for b in range(4):
+                lane = sum(((int(w[n, k]) >> (8 * b)) & 0xFF) << (8 * k) for k in range(3))
+                assert [(lane >> (3 * a)) & 7 for a in range(8)] == list(u[n, 8 * b: 8 * b + 8])
+        else:               # LSB-first over the chunk
+            bits = sum(int(w[n, k]) << (32 * k) for k in range(P))
+            assert [(bits >> (i * P)) & ((1 << P) - 1) for i in range(32)] == list(u[n])
 
 
 CASES = [(QuadtreeRD, 2.2), (QuadtreeRD, 4.25), (QuadtreeRD, 9.0), (QuadtreeRD, 15.0),
