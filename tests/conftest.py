@@ -40,6 +40,21 @@ def outlier_matrix(seed=0, n=128, m=None):
     return W
 
 
+def kind_grid_stream(S, K=512, N=64, seed=31, merge_kinds=False):
+    """Panel stream of S x S leaves only, each leaf's code width picked at random from every
+    width (about 1 in 8 leaves P0), with random codes and power-of-two scales: every (S, P)
+    kind occurs in every unit, so every decode path of that leaf size runs."""
+    from tensorpack_amd.packer import CODE_WIDTHS, pack_levels
+    rng = np.random.RandomState(seed + S)
+    g = (K // S, N // S)
+    modes = np.array((0,) + tuple(CODE_WIDTHS))[rng.randint(0, len(CODE_WIDTHS) + 1, size=g)]
+    leaf = np.ones(g, bool)
+    scales = (2.0 ** rng.randint(-9, -2, size=g)).astype(np.float32)
+    codes = lambda S_, P, ii, jj, sc: rng.randint(-(1 << (P - 1)), 1 << (P - 1), size=(ii.size, S_, S_))
+    return pack_levels((K, N), (S,), {S: leaf}, {S: modes}, {S: scales}, codes, chunk_rows=K,
+                       merge_kinds=merge_kinds)
+
+
 def kind_mix_stream(K=4096, N=32, seed=24):
     """Panel stream of 4x4 leaves whose code width changes with the column group (random
     codes, power-of-two scales, 30 % P0): the 4 column groups of a decode block step

@@ -17,7 +17,7 @@ from tensorpack_amd.core.permutation import PermutedQuadtreeRD
 from tensorpack_amd.core.quadtree import QuadtreeRD
 from tensorpack_amd.kernels.gemm import MTCMatrix, mtc_gemm
 
-from conftest import kind_mix_stream, outlier_matrix
+from conftest import kind_grid_stream, kind_mix_stream, outlier_matrix
 
 pytestmark = pytest.mark.gpu
 
@@ -162,6 +162,31 @@ def test_gemv_step_records_past_the_fixed_area(gpu, M):
     Y = DeviceStream(ps, gpu).gemv_f32(torch.from_numpy(X).to(gpu)).cpu().numpy()
     err = O.relative_frobenius_error(O.qt_gemm_f64(X, decode_stream(ps)), Y)
     assert err <= TOL_F32, err
+
+
+@pytest.mark.parametrize("S", [8, 16, 32])
+@pytest.mark.parametrize("merge", [False, True])
+def test_every_kind_of_a_leaf_size(gpu, S, merge):
+    """Every code width at leaf size S in every unit (kind_grid_stream), stored at its own
+    width or merged into wider ones: the dequant is bit-exact against the host decode of the
+    same stream, and Y is within the fp32 bar on the vector path (M = 1, 2) and on the matrix
+    core (M = 5, 16)."""
+    import torch
+    from tensorpack_amd.device import DeviceStream
+    from tensorpack_amd.packer import decode_stream
+    ps = kind_grid_stream(S, merge_kinds=merge)
+    kinds = {(int(k) & 0xFF, int(k) >> 8) for k in ps.buckets[:ps.n_buckets, 3]}
+    assert merge or len(kinds) == 7, kinds                 # every width present unmerged
+    ref = decode_stream(ps)
+    ds = DeviceStream(ps, gpu)
+    _say("every kind", S, merge)
+    got = ds.dequant().cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    for M in (1, 2, 5, 16):
+        X = np.random.RandomState(M + S).randn(M, ps.K).astype(np.float32)
+        Y = ds.gemv_f32(torch.from_numpy(X).to(gpu)).cpu().numpy()
+        err = O.relative_frobenius_error(O.qt_gemm_f64(X, ref), Y)
+        assert err <= TOL_F32, (S, merge, M, err)
 
 
 @pytest.mark.parametrize("name", [c[0] for c in CASES])
