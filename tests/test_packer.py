@@ -297,6 +297,47 @@ def test_merged_kinds_decode_to_the_same_w_hat(budget, chunk_rows, perm):
     assert any((widths[s] != np.where(lv.leaf[s] & (lv.modes[s] > 0), lv.modes[s], 0)).any() for s in lv.sizes)
 
 
+@settings(max_examples=20, deadline=None)
+@given(seed=st.integers(0, 10 ** 6), rows=st.sampled_from([64, 128, 256]), chunk=st.sampled_from([32, 64, 128]),
+       sizes=st.sampled_from([(32, 16, 8, 4), (16, 8, 4), (8, 4), (4,), (32,)]))
+def test_fuzz_storage_widths(seed, rows, chunk, sizes):
+    """Random leaf mixes: a stored width is never narrower than the mode and at most
+    MERGE_MAX_WIDEN bits wider, P0 leaves are never stored, and the merged stream decodes to
+    the unmerged stream's W_hat bit for bit (bucket walk and step-record walk) with no more
+    step records."""
+    from tensorpack_amd.packer import CODE_WIDTHS, MERGE_MAX_WIDEN
+    rng = np.random.RandomState(seed)
+    K, N = rows, 64
+    chunk = min(chunk, K)
+    # a random quadtree-like cover: each 32 x 32 root tile is split to one leaf size of `sizes`
+    leaf = {s: np.zeros((K // s, N // s), bool) for s in sizes}
+    modes = {s: np.zeros((K // s, N // s), np.int64) for s in sizes}
+    scales = {s: (2.0 ** rng.randint(-8, 0, size=(K // s, N // s))).astype(np.float32) for s in sizes}
+    widths_all = np.array((0,) + tuple(CODE_WIDTHS))
+    for i in range(K // 32):
+        for j in range(N // 32):
+            s = int(rng.choice(sizes))
+            r = 32 // s
+            leaf[s][i * r:(i + 1) * r, j * r:(j + 1) * r] = True
+            modes[s][i * r:(i + 1) * r, j * r:(j + 1) * r] = widths_all[rng.randint(0, len(widths_all), size=(r, r))]
+    # codes a fixed function of the leaf (packing calls it per kind, in any grouping)
+    base = {s: rng.randint(0, 1 << 16, size=(K // s, N // s, s, s)) for s in sizes}
+    codes = lambda S, P, ii, jj, sc: base[S][ii, jj] % (1 << P) - (1 << (P - 1))
+    args = ((K, N), sizes, leaf, modes, scales, codes, chunk)
+    w = storage_widths((K, N), sizes, leaf, modes, chunk)
+    for s in sizes:
+        stored = leaf[s] & (modes[s] > 0)
+        assert (w[s][~stored] == 0).all()
+        d = w[s][stored] - modes[s][stored]
+        assert (d >= 0).all() and (d <= MERGE_MAX_WIDEN).all()
+        assert np.isin(w[s][stored], CODE_WIDTHS).all()
+    p0, p1 = pack_levels(*args, merge_kinds=False), pack_levels(*args, merge_kinds=True)
+    ref = _bits(decode_stream(p0))
+    assert np.array_equal(_bits(decode_stream(p1)), ref)
+    assert np.array_equal(_bits(decode_steps(p1)), ref)
+    assert _records(p1) <= _records(p0)
+
+
 def test_step_records_survive_save_load(tmp_path):
     W = outlier_matrix(22, 128, 64)
     a = QuadtreeRD(W, None, (32, 16, 8, 4)).select(4.0)
