@@ -55,6 +55,35 @@ def kind_grid_stream(S, K=512, N=64, seed=31, merge_kinds=False):
                        merge_kinds=merge_kinds)
 
 
+def signed_scale_levels(seed=7, K=256, N=128, sizes=(32, 16, 8, 4)):
+    """A random quadtree-like cover (each 32 x 32 root tile one leaf size), random code
+    widths (about 1 in 8 leaves P0), bf16 power-of-two scales of random sign, and codes a
+    fixed function of the leaf. Returns the pack_levels arguments and W_hat computed from the
+    grids directly (q * s + 0.0 per leaf, so a zero code under a negative scale is +0.0)."""
+    from tensorpack_amd.packer import CODE_WIDTHS
+    rng = np.random.RandomState(seed)
+    leaf = {s: np.zeros((K // s, N // s), bool) for s in sizes}
+    modes = {s: np.zeros((K // s, N // s), np.int64) for s in sizes}
+    scales = {s: ((2.0 ** rng.randint(-9, -1, size=(K // s, N // s))) *
+                  rng.choice([-1.0, 1.0], size=(K // s, N // s))).astype(np.float32) for s in sizes}
+    widths = np.array((0,) + tuple(CODE_WIDTHS))
+    for i in range(K // 32):
+        for j in range(N // 32):
+            s = int(rng.choice(sizes))
+            r = 32 // s
+            leaf[s][i * r:(i + 1) * r, j * r:(j + 1) * r] = True
+            modes[s][i * r:(i + 1) * r, j * r:(j + 1) * r] = widths[rng.randint(0, len(widths), size=(r, r))]
+    base = {s: rng.randint(0, 1 << 16, size=(K // s, N // s, s, s)) for s in sizes}
+    codes = lambda S, P, ii, jj, sc: base[S][ii, jj] % (1 << P) - (1 << (P - 1))
+    W_hat = np.zeros((K, N), np.float32)
+    for s in sizes:
+        for i, j in zip(*np.nonzero(leaf[s] & (modes[s] > 0))):
+            P = int(modes[s][i, j])
+            q = (base[s][i, j] % (1 << P) - (1 << (P - 1))).astype(np.float32)
+            W_hat[i * s:(i + 1) * s, j * s:(j + 1) * s] = q * scales[s][i, j] + np.float32(0.0)
+    return ((K, N), sizes, leaf, modes, scales, codes), W_hat
+
+
 def kind_mix_stream(K=4096, N=32, seed=24):
     """Panel stream of 4x4 leaves whose code width changes with the column group (random
     codes, power-of-two scales, 30 % P0): the 4 column groups of a decode block step

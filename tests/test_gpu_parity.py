@@ -17,7 +17,7 @@ from tensorpack_amd.core.permutation import PermutedQuadtreeRD
 from tensorpack_amd.core.quadtree import QuadtreeRD
 from tensorpack_amd.kernels.gemm import MTCMatrix, mtc_gemm
 
-from conftest import kind_grid_stream, kind_mix_stream, outlier_matrix
+from conftest import kind_grid_stream, kind_mix_stream, outlier_matrix, signed_scale_levels
 
 pytestmark = pytest.mark.gpu
 
@@ -187,6 +187,32 @@ def test_every_kind_of_a_leaf_size(gpu, S, merge):
         Y = ds.gemv_f32(torch.from_numpy(X).to(gpu)).cpu().numpy()
         err = O.relative_frobenius_error(O.qt_gemm_f64(X, ref), Y)
         assert err <= TOL_F32, (S, merge, M, err)
+
+
+def test_negative_scales(gpu):
+    """Scales may be negative (any sign of s gives W_hat = q * s): the dequant is bit-exact
+    against W_hat built from the leaf grids directly, the decode is within the fp32 bar on
+    the vector path and the matrix core, and the prefill within the bf16 bar."""
+    import torch
+    from tensorpack_amd.device import DeviceStream, DeviceTiles
+    from tensorpack_amd.packer import pack_levels
+    from tensorpack_amd.tilestream import pack_tiles
+    args, W_hat = signed_scale_levels()
+    _say("negative scales")
+    ds = DeviceStream(pack_levels(*args, chunk_rows=256), gpu)
+    got = ds.dequant().cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), W_hat.view(np.uint32))
+    for M in (1, 2, 5, 16):
+        X = np.random.RandomState(M + 70).randn(M, W_hat.shape[0]).astype(np.float32)
+        Y = ds.gemv_f32(torch.from_numpy(X).to(gpu)).cpu().numpy()
+        err = O.relative_frobenius_error(O.qt_gemm_f64(X, W_hat), Y)
+        assert err <= TOL_F32, (M, err)
+    dt = DeviceTiles(pack_tiles(*args), gpu)
+    for M in (1, 64, 300):
+        X = np.random.RandomState(M + 80).randn(M, W_hat.shape[0]).astype(np.float32)
+        Y = dt.gemm_bf16(torch.from_numpy(X).to(gpu).to(torch.bfloat16)).float().cpu().numpy()
+        err = O.relative_frobenius_error(O.qt_gemm_f64(O.bf16_round(X), W_hat), Y)
+        assert err <= TOL_BF16, (M, err)
 
 
 @pytest.mark.parametrize("name", [c[0] for c in CASES])

@@ -338,6 +338,21 @@ def test_fuzz_storage_widths(seed, rows, chunk, sizes):
     assert _records(p1) <= _records(p0)
 
 
+@pytest.mark.parametrize("chunk", [64, 256])
+def test_negative_scales_decode_exactly(chunk):
+    """Scales may be negative: both host walks of the panel stream, and the tile stream's
+    host decode, give W_hat = q * s (+0.0 for a zero code) from the grids directly."""
+    from tensorpack_amd.tilestream import decode_tiles, pack_tiles
+    from conftest import signed_scale_levels
+    args, W_hat = signed_scale_levels()
+    assert any((args[4][s] < 0).any() for s in args[1])
+    ps = pack_levels(*args, chunk_rows=chunk)
+    assert np.array_equal(_bits(decode_stream(ps)), _bits(W_hat))
+    assert np.array_equal(_bits(decode_steps(ps)), _bits(W_hat))
+    ts = pack_tiles(*args)
+    assert np.array_equal(_bits(decode_tiles(ts) + np.float32(0.0)), _bits(O.bf16_round(W_hat) + np.float32(0.0)))
+
+
 def test_step_records_survive_save_load(tmp_path):
     W = outlier_matrix(22, 128, 64)
     a = QuadtreeRD(W, None, (32, 16, 8, 4)).select(4.0)
