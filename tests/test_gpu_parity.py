@@ -189,6 +189,37 @@ def test_every_kind_of_a_leaf_size(gpu, S, merge):
         assert err <= TOL_F32, (S, merge, M, err)
 
 
+def test_all_p0_matrix_and_empty_x(gpu, allocs):
+    """A matrix whose every leaf is P0 stores no codes (no buckets, only the null record): the
+    dequant is all +0.0 and Y is all zero on the vector path, the matrix core and the prefill.
+    An X of M = 0 rows gives a (0, N) Y on the decode and the prefill paths."""
+    import torch
+    from tensorpack_amd.device import DeviceStream, DeviceTiles
+    from tensorpack_amd.packer import pack_levels
+    from tensorpack_amd.tilestream import pack_tiles
+    _say("all P0 / empty X")
+    K, N = 256, 96
+    grids = ((K, N), (16, 4), {16: np.ones((K // 16, N // 16), bool), 4: np.zeros((K // 4, N // 4), bool)},
+             {16: np.zeros((K // 16, N // 16), np.int64), 4: np.zeros((K // 4, N // 4), np.int64)},
+             {16: np.ones((K // 16, N // 16), np.float32), 4: np.ones((K // 4, N // 4), np.float32)},
+             lambda *a: None)
+    ps = pack_levels(*grids, chunk_rows=128)
+    assert ps.n_buckets == 0
+    ds = DeviceStream(ps, gpu)
+    w = ds.dequant().cpu().numpy()
+    assert np.array_equal(w.view(np.uint32), np.zeros((K, N), np.uint32))
+    for M in (1, 3, 9):
+        X = torch.from_numpy(np.random.RandomState(M).randn(M, K).astype(np.float32)).to(gpu)
+        Y = ds.gemv_f32(X).cpu().numpy()
+        assert Y.shape == (M, N) and not Y.any(), M
+    Yb = DeviceTiles(pack_tiles(*grids), gpu).gemm_bf16(torch.ones((40, K), device=gpu, dtype=torch.bfloat16))
+    assert Yb.shape == (40, N) and not Yb.float().cpu().numpy().any()
+    W, a, m = allocs[CASES[0][0]]
+    for compute in ("fp32", "bf16"):
+        Y0 = mtc_gemm(torch.zeros((0, W.shape[0]), device=gpu), m, compute=compute)
+        assert tuple(Y0.shape) == (0, W.shape[1]), compute
+
+
 def test_negative_scales(gpu):
     """Scales may be negative (any sign of s gives W_hat = q * s): the dequant is bit-exact
     against W_hat built from the leaf grids directly, the decode is within the fp32 bar on
