@@ -57,6 +57,7 @@ def parse():
     ap.add_argument("--graph", type=int, default=1, help="replay the timed calls from a HIP graph")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH_SIZE/WRITE_SIZE passes")
     ap.add_argument("--pmc-child", help=argparse.SUPPRESS)
+    ap.add_argument("--pmc-child-batch", help=argparse.SUPPRESS)
     ap.add_argument("--workload", default="all", choices=["all", "c2", "c3", "c5"],
                     help="all (default): the headline c2 decode plus c4 prefill, the c3 stack and c5; c2: c2 and "
                          "c4 only; c3: the 24-layer decoder stack (168 matrices) at M=1 and M=512 with per-launch "
@@ -70,6 +71,16 @@ def parse():
 COPY_BYTES = 256 << 20
 
 
+def pmc_copies(torch):
+    """The counter calibration: four plain device copies of COPY_BYTES."""
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
 def pmc_child(path):
     """Body of one counter pass: a plain device copy of known size, then the decode kernel."""
     import torch
@@ -78,11 +89,7 @@ def pmc_child(path):
     ps = PanelStream.load(path)
     with np.load(path.replace(".npz", "_x.npz")) as z:
         x = z["x"]
-    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
-    dst = torch.empty_like(src)
-    torch.cuda.synchronize()
-    for _ in range(4):
-        dst.copy_(src)
+    pmc_copies(torch)
     ds = DeviceStream(ps)
     copies = [ds] + [ds.clone() for _ in range(7)]
     X = torch.from_numpy(x).cuda()
@@ -97,29 +104,79 @@ def pmc_child(path):
     print("pmc child done", flush=True)
 
 
+def pmc_child_batch(folder):
+    """Body of one counter pass of the batched decode: the calibration copies, then four
+    launches of one batch over the streams saved in `folder` (stream_NNN.npz; one input per
+    K in x.npz, shared by every stream of that K)."""
+    import torch
+    from tensorpack_amd.device import DeviceStream, GemvBatch
+    from tensorpack_amd.packer import PanelStream
+    with np.load(os.path.join(folder, "x.npz")) as z:
+        xs = {int(k[1:]): z[k] for k in z.files}
+    n = len([f for f in os.listdir(folder) if f.startswith("stream_")])
+    pss = [PanelStream.load(os.path.join(folder, f"stream_{i:03d}.npz")) for i in range(n)]
+    pmc_copies(torch)
+    streams = [DeviceStream(ps) for ps in pss]
+    X = {K: torch.from_numpy(x).cuda() for K, x in xs.items()}
+    batch = GemvBatch(streams, [X[s.K] for s in streams])
+    torch.cuda.synchronize()
+    for _ in range(4):
+        batch.launch()
+    torch.cuda.synchronize()
+    print("pmc child done", flush=True)
+
+
 def traffic_passes(ps, x, kernel="k_gemv"):
-    """HBM bytes per decode launch from two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE).
+    """HBM bytes per decode launch of one stream (`ps`, input `x`); see counter_passes."""
+    import tempfile
+    tmp = tempfile.mkdtemp(prefix="mtc_pmc_")
+    path = os.path.join(tmp, "stream.npz")
+    ps.save(path)
+    np.savez(os.path.join(tmp, "stream_x.npz"), x=x)
+    return counter_passes(tmp, ["--pmc-child", path], kernel)
+
+
+def traffic_passes_batch(pss, xs, kernel="k_gemv_batch"):
+    """HBM bytes per batched decode launch over the streams `pss` (`xs`: one input per K);
+    see counter_passes."""
+    import tempfile
+    tmp = tempfile.mkdtemp(prefix="mtc_pmc_")
+    for i, ps in enumerate(pss):
+        ps.save(os.path.join(tmp, f"stream_{i:03d}.npz"))
+    np.savez(os.path.join(tmp, "x.npz"), **{f"k{K}": x for K, x in xs.items()})
+    return counter_passes(tmp, ["--pmc-child-batch", tmp], kernel, launches=4)
+
+
+def counter_passes(tmp, child_args, kernel, launches=None):
+    """HBM bytes per launch of `kernel` from two rocprofv3 --pmc passes (FETCH_SIZE, then
+    WRITE_SIZE) over a child run of this script (`child_args`, inputs saved in `tmp`).
+    With `launches`, the child's dispatches of `kernel` are summed and divided by that
+    many launches (a batched launch may dispatch once per block shape); otherwise the
+    mean over dispatches is taken.
 
     Each counter is scaled by what it reads for a device copy of COPY_BYTES in the
     same pass (bytes moved / counter bytes), so unit or per-instance conventions of
     the counter cancel. Runs before this process touches the GPU; returns None
     when rocprofv3 is unavailable or a pass fails."""
     import shutil
-    import subprocess
-    import tempfile
-    from tensorpack_amd.profiling import dispatch_values
     exe = shutil.which("rocprofv3")
     if exe is None:
         log("traffic: rocprofv3 not found")
+        shutil.rmtree(tmp, ignore_errors=True)
         return None
-    tmp = tempfile.mkdtemp(prefix="mtc_pmc_")
-    path = os.path.join(tmp, "stream.npz")
-    ps.save(path)
-    np.savez(os.path.join(tmp, "stream_x.npz"), x=x)
+    try:
+        return _counter_passes(exe, tmp, child_args, kernel, launches)
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+
+def _counter_passes(exe, tmp, child_args, kernel, launches):
+    import subprocess
+    from tensorpack_amd.profiling import dispatch_values
     res = {}
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
         cmd = ["timeout", "-s", "KILL", "120", exe, "--pmc", counter, "-d", tmp, "-o", counter, "--",
-               sys.executable, os.path.abspath(__file__), "--pmc-child", path]
+               sys.executable, os.path.abspath(__file__)] + child_args
         log("traffic pass: " + " ".join(cmd[3:]))
         r = subprocess.run(cmd, capture_output=True, text=True, env=dict(os.environ, TMPDIR="/tmp"))
         db = os.path.join(tmp, counter + "_results.db")
@@ -134,11 +191,10 @@ def traffic_passes(ps, x, kernel="k_gemv"):
             log(f"traffic pass {counter}: kernel or copy dispatches missing")
             return None
         copy_kib = sum(copy) / len(copy)
-        res[counter] = {"kernel_kib": sum(kern) / len(kern), "copy_kib": copy_kib,
+        res[counter] = {"kernel_kib": sum(kern) / (launches or len(kern)), "copy_kib": copy_kib,
                         "factor": COPY_BYTES / (copy_kib * 1024.0), "copy_spread": max(copy) / min(copy)}
     fetch = res["FETCH_SIZE"]["kernel_kib"] * 1024.0 * res["FETCH_SIZE"]["factor"]
     write = res["WRITE_SIZE"]["kernel_kib"] * 1024.0 * res["WRITE_SIZE"]["factor"]
-    shutil.rmtree(tmp, ignore_errors=True)
     return {"bytes": fetch + write, "fetch_bytes": fetch, "write_bytes": write,
             "fetch_factor": res["FETCH_SIZE"]["factor"], "write_factor": res["WRITE_SIZE"]["factor"]}
 
@@ -405,16 +461,23 @@ def bench_c4(args, wl4, a4, dev):
 # ----------------------------------------------------------------------------------------------
 # c3: the 168-matrix Qwen2.5-0.5B-shaped stack
 # ----------------------------------------------------------------------------------------------
-def bench_c3(args, mats, allocs, dev, detail=False):
+def c3_x(K, M):
+    """The c3 input of K columns and M rows (every matrix of that K shares it)."""
+    return np.random.RandomState(3000 + K + M).randn(M, K).astype(np.float32)
+
+
+def bench_c3(args, mats, allocs, dev, detail=False, ms_=None, traffic=None):
     """M = 1: all 168 matrices (each its own X and Y) in one batched launch per pass, over rotating
     copies of the stack; M = 512: the prefill of every matrix, the q/k/v and gate/up groups sharing
     their input (12 launches per layer), one HIP graph per pass. With `detail`, also the M = 1 pass
-    as one launch per matrix and as 96 grouped launches."""
+    as one launch per matrix and as 96 grouped launches. `ms_`: the MTCMatrix of each allocation,
+    if already built; `traffic`: counter bytes of one batched M = 1 launch (traffic_passes_batch)."""
     import torch
     from tensorpack_amd import workloads
     from tensorpack_amd.device import GemvBatch, gemm_bf16_group, gemv_f32_group
     from tensorpack_amd.kernels.gemm import MTCMatrix
-    ms_ = [MTCMatrix.from_quadtree(a, w.W) for a, w in zip(allocs, mats)]
+    if ms_ is None:
+        ms_ = [MTCMatrix.from_quadtree(a, w.W) for a, w in zip(allocs, mats)]
     packed = float(sum(m.packed_bytes for m in ms_))
     weights = sum(w.W.size for w in mats)
     xs = {}
@@ -422,7 +485,7 @@ def bench_c3(args, mats, allocs, dev, detail=False):
     def x_of(K, M, dtype):
         key = (K, M, dtype)
         if key not in xs:
-            xs[key] = torch.from_numpy(np.random.RandomState(3000 + K + M).randn(M, K).astype(np.float32)).to(dev).to(dtype)
+            xs[key] = torch.from_numpy(c3_x(K, M)).to(dev).to(dtype)
         return xs[key]
 
     streams = [m.device_stream(None, dev, 1) for m in ms_]
@@ -455,7 +518,11 @@ def bench_c3(args, mats, allocs, dev, detail=False):
            "matrices": len(mats), "weights": weights, "packed_bytes": packed, "rotating_stacks": n_rot,
            "m1": {"us_per_pass": ms1 * 1e3, "GBps_packed": gbs, "launches": 1, "bit_identical_to_single_calls": True,
                   "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                               "frac": gbs / HBM_PEAK_GBS, "traffic": None, "kernel": "k_gemv_batch"}}}
+                               "frac": gbs / HBM_PEAK_GBS, "traffic": None if traffic is None else traffic["bytes"],
+                               "kernel": "k_gemv_batch"}}}
+    if traffic is not None:
+        out["m1"]["roofline"]["traffic_detail"] = dict(traffic, traffic_over_packed=traffic["bytes"] / packed)
+        log(f"c3 M=1 traffic {traffic['bytes'] / 1e6:.2f} MB per launch = {traffic['bytes'] / packed:.3f}x packed")
     n_per = len(workloads.QWEN_LAYER)
     layer_groups = [[0, 1, 2], [3], [4, 5], [6]]
     plan_grouped = [[L * n_per + i for i in grp] for L in range(len(mats) // n_per) for grp in layer_groups]
@@ -596,6 +663,9 @@ def main():
     if args.pmc_child:
         pmc_child(args.pmc_child)
         return
+    if args.pmc_child_batch:
+        pmc_child_batch(args.pmc_child_batch)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
@@ -619,6 +689,13 @@ def main():
             t0 = time.time()
             A[name] = (wl, wl.allocate())
             log(f"{name} allocation {time.time() - t0:.1f}s, {A[name][1].bits_per_element:.4f} b/w")
+    c3_ms, c3_traffic = None, None
+    if "c3" in want:
+        mats, allocs = A["c3"]
+        c3_ms = [MTCMatrix.from_quadtree(a, w.W) for a, w in zip(allocs, mats)]
+        if not args.no_traffic:
+            c3_traffic = traffic_passes_batch([m.panel_stream(m.decode_chunk_rows(1)) for m in c3_ms],
+                                              {w.W.shape[0]: c3_x(w.W.shape[0], 1) for w in mats})
     traffic = None
     if "c2" in want and not args.no_traffic:
         wl, alloc = A["c2"]
@@ -631,7 +708,7 @@ def main():
     torch.cuda.set_device(dev)
     if "c2" not in want:                                  # a single detail workload
         if "c3" in want:
-            r = bench_c3(args, *A["c3"], dev, detail=True)
+            r = bench_c3(args, *A["c3"], dev, detail=True, ms_=c3_ms, traffic=c3_traffic)
             if not args.no_cpu_baseline:
                 r["cpu_baseline"] = cpu_baseline_c3(args, *A["c3"])
         else:
@@ -652,7 +729,7 @@ def main():
     if "c4" in want:
         extra["c4_prefill"] = bench_c4(args, *A["c4"], dev)
     if "c3" in want:
-        extra["c3"] = bench_c3(args, *A["c3"], dev)
+        extra["c3"] = bench_c3(args, *A["c3"], dev, ms_=c3_ms, traffic=c3_traffic)
     if "c5" in want:
         extra["c5"] = bench_c5(args, *A["c5"], dev)
 
