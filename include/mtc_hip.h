@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MTC_ABI_VERSION 8
+#define MTC_ABI_VERSION 9
 
 enum {
   MTC_OK = 0,
@@ -77,18 +77,21 @@ enum { MTC_DTYPE_F32 = 0, MTC_DTYPE_BF16 = 1 };
  *  leaf_word[l]     : bits 0-9 row offset in the unit / 4, bit 13 pad leaf (ignored),
  *                     bits 16-31 bf16 scale
  *  leaf_scale[l]    : fp32 scale (only with MTC_FLAG_FP32_SCALES)
- *  steps[16*r + ..] : decode step records. Decode block B = 2*u + b (unit u, block b of 4
+ *  steps[8*r + ..]  : decode step records. Decode block B = 2*u + b (unit u, block b of 4
  *                     column groups) owns count = unit_hdr[32*u + 28 + 2b] records, ordered by
  *                     bucket kind, then 16-chunk step j. Its record i < F = fixed_steps is
  *                     steps record B*F + i; record i >= F is record overflow_start + i - F.
  *                     Record n_blocks*F (n_blocks = 2 * n_units) and unused fixed places are
- *                     null records (no valid chunks). A record is 4 slots, one per column
- *                     group of the block; slot g = words 4g..4g+3: absolute payload offset
- *                     (dwords) of the kind's bucket in that column group, its absolute first
- *                     leaf-word index, the bucket's chunks in this step, min(max(n - 16j, 0),
- *                     16) (0: no bucket of the kind; the offsets then name another existing
- *                     bucket, or payload dword 0 and leaf word 0), and kind key | j << 16.
- *
+ *                     null records (no chunks). Word 2g (g = 0..3, column group 4b + g) names
+ *                     the step's first chunk, chunk 16j of the kind's bucket in that column
+ *                     group, relative to the unit: bits 0-15 its payload offset in dwords / 4
+ *                     (from unit_hdr[32*u + 0]), bits 16-31 its first leaf word (from
+ *                     unit_hdr[32*u + 2]; the bucket's first leaf + 32j for S = 4, + 16j >>
+ *                     (log2 S - 3) otherwise); 0 when the slot has no chunks. Words 2g + 1
+ *                     (all four equal): bits 0-2 log2 S, bits 3-7 P, bits 8+5g .. 12+5g the
+ *                     chunks of slot g in this step, min(max(n - 16j, 0), 16) for a bucket
+ *                     of n chunks (0 without one).
+
  * The payload array extends at least 4 dwords past the last bucket (the kernels read
  * chunks with 16-byte loads that may run up to 3 dwords past a chunk's end); leaf_word
  * holds at least one word.
@@ -128,7 +131,7 @@ typedef struct mtc_stream_desc {
   const float* leaf_scale;
   const int32_t* row_perm;
   const int32_t* col_perm;
-  const uint32_t* steps;   /* n_steps step records of 16 words */
+  const uint32_t* steps;   /* n_steps step records of 8 words */
   int64_t n_steps;
 } mtc_stream_desc;
 

@@ -2,7 +2,7 @@
 
 import ctypes
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 MTC_OK = 0
 MTC_DTYPE_F32 = 0

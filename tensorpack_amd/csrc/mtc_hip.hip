@@ -342,7 +342,19 @@ __device__ __forceinline__ void gemv_chunk(const u32x16_t rw, uint32_t lw0, uint
 
 constexpr int kStepGroups = 4;              // column groups one decode step covers
 constexpr int kStepLanes = 16;              // lanes per column group in a step
-constexpr int kStepWords = 16;              // words per step record
+constexpr int kStepWords = 8;               // words per step record: (slot word, kind and counts) x 4
+
+// Slot g's word of record r and the record's kind-and-counts word (words 2g, 2g + 1).
+__device__ __forceinline__ u32x2_t record_slot(__amdgpu_buffer_rsrc_t rec_r, uint32_t r, int g) {
+  return __builtin_amdgcn_raw_buffer_load_b64(rec_r, r * (kStepWords * 4) + 8 * g, 0, 0);
+}
+// Bucket key (log2 S | P << 8) of a record's kind field (log2 S | P << 3); wave-uniform.
+__device__ __forceinline__ uint32_t record_key(uint32_t kc) {
+  const uint32_t k = __builtin_amdgcn_readfirstlane(kc);
+  return (k & 7u) | (((k >> 3) & 31u) << 8);
+}
+// Chunks of slot g in the record's step (0-16).
+__device__ __forceinline__ uint32_t record_count(uint32_t kc, int g) { return (kc >> (8 + 5 * g)) & 31u; }
 // Most waves a decode block has (the LDS of the cross-wave reduction is sized for it).
 __host__ __device__ constexpr int gemv_waves(int MT) { return MT == 4 ? 8 : 16; }
 constexpr int kFewSteps = 16;
@@ -548,24 +560,26 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
 
   // ---- this wave's step records: records wave, wave + W, wave + 2W, ... of the block's list.
   //      A block's first F records sit at block-computable places, so the first three steps'
-  //      records are read without waiting for the unit header. ----
+  //      records are read while the unit header (whose payload and leaf-word starts the
+  //      records' offsets are relative to) is still in flight. ----
   const int F = d.fixed_steps;
   const int blk = u * BPU + cb;
   const uint32_t null_rec = (uint32_t)(d.n_panels * d.n_chunks * BPU) * (uint32_t)F;
   const int g = lane / kStepLanes, li = lane % kStepLanes;   // column-group slot, lane in slot
 
-  // A lane's slot of a record: [payload offset, first leaf, valid chunks, kind | j << 16]
-  // (16 bytes; the 16 lanes of a slot read the same words).
+  // A lane's view of a record: its slot's word (where the step starts in the column group's
+  // bucket, relative to the unit) and the record's kind-and-counts word; the 16 lanes of a
+  // slot read the same words.
   const __amdgpu_buffer_rsrc_t rec_r = buffer_of(d.steps, d.n_steps * kStepWords * 4);
   const __amdgpu_buffer_rsrc_t pay_r = buffer_of(d.payload, d.payload_dwords * 4);
   const __amdgpu_buffer_rsrc_t lw_r = buffer_of(d.leaf_word, d.n_leaves * 4);
   const __amdgpu_buffer_rsrc_t fs_r =
       buffer_of(FS ? static_cast<const void*>(d.leaf_scale) : static_cast<const void*>(d.leaf_word), d.n_leaves * 4);
-  auto slot_of = [&](uint32_t r) __attribute__((always_inline)) {
-    return __builtin_amdgcn_raw_buffer_load_b128(rec_r, (r * kStepWords + 4 * g) * 4, 0, 0);
-  };
-  // A step's per-lane view: chunk t of this slot's bucket, active if li < valid chunks.
-  // Inactive lanes load chunk 0 of the bucket (every referenced bucket has one).
+  const uint32_t pay0 = (uint32_t)hdr[0], leaf0 = (uint32_t)hdr[2];   // the unit's payload and leaf words
+  auto slot_of = [&](uint32_t r) __attribute__((always_inline)) { return record_slot(rec_r, r, g); };
+  // A step's per-lane view: chunk t = li of the step in this slot's column group, active if
+  // li is below the slot's chunk count. Inactive lanes load the step's chunk 0 (a slot without
+  // chunks names the unit's first payload dword and leaf word) and use nothing they load.
   struct Regs {
     u32x16_t w;
     uint32_t ob, lw0, lw1;
@@ -573,11 +587,12 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
     uint32_t t, key;
     bool on;
   };
-  auto fetch = [&](const u32x4_t f, Regs& r) __attribute__((always_inline)) {
-    r.key = __builtin_amdgcn_readfirstlane(f.w & 0xFFFFu);   // one kind per record
-    r.on = (uint32_t)li < f.z;
-    r.t = r.on ? kStepLanes * (f.w >> 16) + li : 0u;
-    gemv_load<FS>(pay_r, lw_r, fs_r, r.key, f.x, f.y, r.t, r.w, r.ob, r.lw0, r.lw1, r.fs0, r.fs1);
+  auto fetch = [&](const u32x2_t f, Regs& r) __attribute__((always_inline)) {
+    r.key = record_key(f.y);                          // one kind per record
+    r.on = (uint32_t)li < record_count(f.y, g);
+    r.t = r.on ? (uint32_t)li : 0u;
+    gemv_load<FS>(pay_r, lw_r, fs_r, r.key, pay0 + ((f.x & 0xFFFFu) << 2), leaf0 + (f.x >> 16), r.t, r.w, r.ob,
+                  r.lw0, r.lw1, r.fs0, r.fs1);
   };
 
   // The first three steps: block record wave + k*W is a fixed record (or the null record:
@@ -593,13 +608,14 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
       return slot_of(i < F ? (uint32_t)(blk * F + i) : null_rec);
     };
     static_assert(PF >= 1 && PF <= 3, "one to three prefetched steps");
-    const u32x4_t f0 = fixed(0);
-    u32x4_t f1 = {}, f2 = {};
+    const u32x2_t f0 = fixed(0);
+    u32x2_t f1 = {}, f2 = {};
     if constexpr (PF >= 2) f1 = fixed(1);
     if constexpr (PF >= 3) f2 = fixed(2);
     asm volatile("" ::"v"(f0.x));
     if constexpr (PF >= 2) asm volatile("" ::"v"(f1.x));
     if constexpr (PF >= 3) asm volatile("" ::"v"(f2.x));
+    asm volatile("" ::"s"(pay0), "s"(leaf0));         // the unit's starts, read beside the records
 #pragma unroll
     for (int i = 0; i < XG; ++i) asm volatile("" ::"v"(kk[i].x));
     if (lds_gather) {
@@ -695,7 +711,7 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
   };
   int i = wave + PF * W;
   compute(r0);                                        // null records have no active lanes
-  u32x4_t nxt = {};                                   // loaded once r0's registers are free
+  u32x2_t nxt = {};                                   // loaded once r0's registers are free
   if (i < nrec) nxt = slot_of(rec(i));
   if constexpr (PF >= 2) compute(r1);
   if constexpr (PF >= 3) compute(r2);
@@ -786,7 +802,8 @@ struct MfmaPass {
 };
 
 // The loads of a record's four passes. Pass p of lane (slot, chunk cq, column j) takes chunk
-// t0 + 4p of the slot's bucket, t0 = 16 * step + cq, so every offset is pass 0's plus a
+// t0 + 4p of the step (t0 = cq; pay and leaf name the step's first chunk and its first leaf
+// word in the slot's column group), so every offset is pass 0's plus a
 // wave-uniform step per pass: 4 chunks of P dwords of payload, and the leaf words of 4
 // chunks (8 for two 4x4 leaves per chunk, 4 >> (log2 S - 3) for larger leaves). Chunks past the bucket's
 // end are read in place (the stream's next chunks, or zeros past a buffer's end) and masked
@@ -965,17 +982,16 @@ __device__ __forceinline__ void gemv_block_mfma(const mtc_stream_desc& d, const 
   auto rec_of = [&](int i) __attribute__((always_inline)) {
     return i < F ? (uint32_t)(blk * F + i) : i < nrec ? ovf + (uint32_t)(i - F) : null_rec;
   };
-  auto slot_of = [&](uint32_t r) __attribute__((always_inline)) {
-    return __builtin_amdgcn_raw_buffer_load_b128(rec_r, (r * kStepWords + 4 * g) * 4, 0, 0);
-  };
+  const uint32_t pay0 = (uint32_t)hdr[0], leaf0 = (uint32_t)hdr[2];   // the unit's payload and leaf words
+  auto slot_of = [&](uint32_t r) __attribute__((always_inline)) { return record_slot(rec_r, r, g); };
   struct Rec {
     MfmaPass p[NP];
     uint32_t key, valid;
   };
-  auto fetch = [&](const u32x4_t f, Rec& r) __attribute__((always_inline)) {
-    r.key = __builtin_amdgcn_readfirstlane(f.w & 0xFFFFu);
-    r.valid = f.z;
-    mfma_load_rec<FS, NP>(pay_r, lw_r, fs_r, r.key, f.x, f.y, kStepLanes * (f.w >> 16) + cq, j, r.p);
+  auto fetch = [&](const u32x2_t f, Rec& r) __attribute__((always_inline)) {
+    r.key = record_key(f.y);
+    r.valid = record_count(f.y, g);
+    mfma_load_rec<FS, NP>(pay_r, lw_r, fs_r, r.key, pay0 + ((f.x & 0xFFFFu) << 2), leaf0 + (f.x >> 16), cq, j, r.p);
   };
 
   // ---- X rows of the unit into LDS, overlapped with the first records' loads. The compiler
@@ -992,8 +1008,8 @@ __device__ __forceinline__ void gemv_block_mfma(const mtc_stream_desc& d, const 
       kr[it] = r < rows ? (d.row_perm ? d.row_perm[kb + r] : kb + r) : -1;
     }
   }
-  const u32x4_t f0 = slot_of(rec_of(wl));
-  u32x4_t f1 = slot_of(rec_of(wl + WH));
+  const u32x2_t f0 = slot_of(rec_of(wl));
+  u32x2_t f1 = slot_of(rec_of(wl + WH));
   float4 v[kMfmaStageIters];
   if (xt) {
     const float* src = xt + (size_t)blockIdx.y * d.K * MT;
@@ -1041,8 +1057,8 @@ __device__ __forceinline__ void gemv_block_mfma(const mtc_stream_desc& d, const 
     const uint32_t vmax = max(max(__builtin_amdgcn_readlane(r.valid, 0), __builtin_amdgcn_readlane(r.valid, 16)),
                               max(__builtin_amdgcn_readlane(r.valid, 32), __builtin_amdgcn_readlane(r.valid, 48)));
     const uint32_t key = r.key, ls = key & 0xFFu;
-    // 8-row block of the chunk within its leaf (chunk t is block t & (S/8 - 1); t = 16 step +
-    // 4p + cq, so only cq matters)
+    // 8-row block of the chunk within its leaf (chunk t of the bucket is block t & (S/8 - 1);
+    // t = 16 step + 4p + cq, so only cq matters)
     const int row_off = ls > 3 ? 8 * (int)(cq & ((1u << (ls - 3)) - 1u)) : 0;
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
@@ -1083,7 +1099,7 @@ __device__ __forceinline__ void gemv_block_mfma(const mtc_stream_desc& d, const 
   // two records in flight: while one is computed the next one's loads (and the record
   // after that's slot) are outstanding
   for (int i = wl; i < nrec; i += 2 * WH) {
-    u32x4_t f2 = slot_of(rec_of(i + 2 * WH));
+    u32x2_t f2 = slot_of(rec_of(i + 2 * WH));
     if (i + WH < nrec) fetch(f1, nxt);
     compute(cur);
     if (i + WH >= nrec) break;

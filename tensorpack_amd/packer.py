@@ -20,7 +20,7 @@ device dequantization q * s reproduces W_hat bit for bit.
 """
 
 from dataclasses import dataclass, field
-from typing import Callable, Dict, Optional, Sequence, Tuple
+from typing import Callable, Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
 
@@ -35,14 +35,15 @@ LEAF_PAD = 1 << 13
 ROW_BITS = 10                          # leaf word: row/4 in bits 0-9
 MAX_CHUNK_ROWS = 4 << ROW_BITS         # 4096
 UNIT_HDR_WORDS = 32
-STREAM_FORMAT = 8                      # panel stream layout version (matches the C-ABI version)
+STREAM_FORMAT = 9                      # panel stream layout version (matches the C-ABI version)
 PAYLOAD_PAD = 4                        # dwords after the last bucket
 STEP_GROUPS = 4                        # column groups one decode step covers
 STEP_LANES = 16                        # lanes (chunks) per column group in a step
-STEP_WORDS = 16                        # words per step record
+STEP_WORDS = 8                         # words per step record: (slot word, kind-and-counts word) x 4
 MAX_FIXED_STEPS = 48                   # records per block stored at block-computable positions
 BLOCKS_PER_UNIT = 2                    # decode blocks (of STEP_GROUPS column groups) per unit
 _NULL_KEY = 3 | (2 << 8)               # kind of a record with no chunks (any valid kind)
+SLOT_OFFSET_LIMIT = 1 << 16            # step payload offset / 4 and first leaf, relative to the unit
 _LOG2 = {32: 5, 16: 4, 8: 3, 4: 2}
 MAX_DEVICE_ARRAY_BYTES = 0x7FFFFFFF    # the kernels address every stream array with 32-bit byte offsets
 
@@ -553,11 +554,14 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
     # A block's records, in (kind, step) order, are split into its first F ("fixed") records,
     # stored at records [b*F, b*F + F) of the table (b = unit * 2 + block; unused places hold
     # null records), and the rest ("overflow"), stored after the fixed area and one null
-    # record at index n_blocks * F. Offsets are absolute: payload dwords and leaf-word index.
+    # record at index n_blocks * F. Word 2g (column group 4 * block + g) holds where the step
+    # starts in that column group's bucket of the kind, relative to the unit: payload dwords / 4
+    # (bits 0-15) and leaf-word index (bits 16-31), 0 for a slot without chunks; words 2g + 1
+    # all hold the kind (log2 S | P << 3) and each slot's chunk count in this step (5 bits at
+    # 8 + 5g), so that a lane of slot g reads its two words with one aligned 8-byte load.
     n_blocks = n_units * BLOCKS_PER_UNIT
-    null_rec = np.zeros((STEP_GROUPS, 4), dtype=np.int64)
-    null_rec[:, 3] = _NULL_KEY
-    null_rec = null_rec.reshape(STEP_WORDS)
+    null_rec = np.zeros(STEP_WORDS, dtype=np.int64)
+    null_rec[1::2] = record_kind(_NULL_KEY)
     recs = np.zeros((0, STEP_WORDS), dtype=np.int64)
     blk_begin = np.zeros(n_blocks + 1, dtype=np.int64)
     if n_buckets:
@@ -578,13 +582,21 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
         rec_g = np.repeat(np.arange(n_grp), g_steps)
         j = np.arange(rec_g.size) - np.repeat(np.concatenate([[0], np.cumsum(g_steps)[:-1]]), g_steps)
         bb = gb[rec_g]
-        recs = np.zeros((rec_g.size, STEP_GROUPS, 4), dtype=np.int64)      # slot g = words 4g .. 4g+3
-        b_key = np.array([_LOG2[int(v)] for v in b_S], dtype=np.int64) | (b_P.astype(np.int64) << 8)
-        recs[:, :, 0] = b_pay[bb]
-        recs[:, :, 1] = b_leaf[bb]
-        recs[:, :, 2] = np.clip(g_n[rec_g] - STEP_LANES * j[:, None], 0, STEP_LANES)
-        recs[:, :, 3] = (b_key[bb[:, 0]] | (j << 16))[:, None]
-        recs = recs.reshape(rec_g.size, STEP_WORDS)
+        b_ls = np.array([_LOG2[int(v)] for v in b_S], dtype=np.int64)
+        nv = np.clip(g_n[rec_g] - STEP_LANES * j[:, None], 0, STEP_LANES)
+        # the step's first chunk, 16 j, and its first leaf (two 4x4 leaves per chunk, else
+        # one leaf per S / 8 chunks)
+        pay_rel = b_pay[bb] - hdr[b_unit[bb], 0] + STEP_LANES * j[:, None] * b_P[bb].astype(np.int64)
+        leaf_rel = b_leaf[bb] - hdr[b_unit[bb], 2] + np.where(
+            b_ls[bb] == 2, 2 * STEP_LANES * j[:, None], (STEP_LANES * j[:, None]) >> np.maximum(b_ls[bb] - 3, 0))
+        on = nv > 0
+        if np.any(pay_rel[on] % 4) or pay_rel[on].max(initial=0) >= 4 * SLOT_OFFSET_LIMIT or \
+                leaf_rel[on].max(initial=0) >= SLOT_OFFSET_LIMIT:
+            raise ValueError("a unit's payload or leaf words exceed the step records' 16-bit offsets")
+        recs = np.zeros((rec_g.size, STEP_WORDS), dtype=np.int64)
+        recs[:, 0::2] = np.where(on, (pay_rel >> 2) | (leaf_rel << 16), 0)
+        kind = b_ls[bb[:, 0]] | (b_P[bb[:, 0]].astype(np.int64) << 3)
+        recs[:, 1::2] = (kind | (nv << (8 + 5 * np.arange(STEP_GROUPS))).sum(axis=1))[:, None]
         rec_blk = b_unit[first][rec_g] * 2 + blk[first][rec_g]
         blk_begin = np.searchsorted(rec_blk, np.arange(n_blocks + 1)).astype(np.int64)
     blk_n = np.diff(blk_begin)
@@ -672,6 +684,20 @@ def decode_stream(ps: PanelStream) -> np.ndarray:
     return _to_original_order(ps, Wp)
 
 
+def record_kind(key: int) -> int:
+    """Kind field of a step record, log2 S | P << 3, from a bucket key, log2 S | P << 8."""
+    return (key & 0xFF) | ((key >> 8) << 3)
+
+
+def record_slots(rec) -> Tuple[int, int, List[Tuple[int, int, int]]]:
+    """(S, P, slots) of one step record; slot g is (payload dword, first leaf word, chunks) of
+    the step in column group g of its block, offsets relative to the unit."""
+    rec = [int(x) for x in rec]
+    kc = rec[1]
+    slots = [(4 * (w & 0xFFFF), w >> 16, (kc >> (8 + 5 * g)) & 31) for g, w in enumerate(rec[0::2])]
+    return 1 << (kc & 7), (kc >> 3) & 31, slots
+
+
 def step_record_index(ps: PanelStream, u: int, blk: int, r: int) -> int:
     """Table index of record r of decode block (unit u, column-group block blk): the first
     `fixed_steps` records of a block sit at block-computable positions, the rest follow
@@ -685,18 +711,16 @@ def step_record_index(ps: PanelStream, u: int, blk: int, r: int) -> int:
 def decode_steps(ps: PanelStream) -> np.ndarray:
     """Host decoder that walks the step records the way the decode kernel does: block
     (unit u, column-group block b) has unit_hdr[u, 28 + 2b] records, located by
-    step_record_index; slot g of a record is words 4g .. 4g+3 (absolute payload offset,
-    absolute first leaf, valid chunks, kind | j << 16), and lane li of the slot takes
-    chunk 16 * j + li of that bucket when li is below the valid-chunk count. A debugging
-    aid; the GPU path never calls it."""
+    step_record_index; slot g of a record (record_slots) names where the step starts in
+    column group 4b + g (unit payload start + dwords, unit leaf start + leaves) and how many
+    chunks it has, and lane li of the slot takes the step's chunk li when li is below that
+    count. A debugging aid; the GPU path never calls it."""
     Wp = np.zeros((ps.K, ps.N), dtype=np.float32)
     for u in range(ps.n_units):
+        pay0, leaf0 = int(ps.unit_hdr[u, 0]), int(ps.unit_hdr[u, 2])
         for blk in range(BLOCKS_PER_UNIT):
             for r in range(int(ps.unit_hdr[u, 28 + 2 * blk])):
-                e = ps.steps[step_record_index(ps, u, blk, r)]
-                for g in range(STEP_GROUPS):
-                    pay, leaf, nv, kj = (int(x) for x in e[4 * g: 4 * g + 4])
-                    key, j = kj & 0xFFFF, kj >> 16
-                    _place_chunks(ps, Wp, u, blk * STEP_GROUPS + g, 1 << (key & 0xFF), key >> 8,
-                                  pay, leaf, STEP_LANES * j + np.arange(nv))
+                S, P, slots = record_slots(ps.steps[step_record_index(ps, u, blk, r)])
+                for g, (pay, leaf, nv) in enumerate(slots):
+                    _place_chunks(ps, Wp, u, blk * STEP_GROUPS + g, S, P, pay0 + pay, leaf0 + leaf, np.arange(nv))
     return _to_original_order(ps, Wp)

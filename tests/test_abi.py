@@ -95,7 +95,8 @@ def test_descriptor_validation(hip):
     assert hip.mtc_check_desc(ctypes.byref(_desc(payload_dwords=lim // 4))) == 0
     assert hip.mtc_check_desc(ctypes.byref(_desc(payload_dwords=lim // 4 + 1))) == -2
     assert hip.mtc_check_desc(ctypes.byref(_desc(n_leaves=lim // 4 + 1))) == -2
-    assert hip.mtc_check_desc(ctypes.byref(_desc(n_steps=lim // 64 + 1))) == -2
+    assert hip.mtc_check_desc(ctypes.byref(_desc(n_steps=lim // 32))) == 0          # 8-word records
+    assert hip.mtc_check_desc(ctypes.byref(_desc(n_steps=lim // 32 + 1))) == -2
 
 
 def test_entry_points_reject_bad_arguments_before_any_gpu_call(hip):

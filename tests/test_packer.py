@@ -12,8 +12,8 @@ from tensorpack_amd.core.permutation import PermutedQuadtreeRD
 from tensorpack_amd.core.quadtree import QuadtreeRD
 from tensorpack_amd.kernels.gemm import MTCMatrix, arena_decode, arena_encode
 from tensorpack_amd.packer import (BLOCKS_PER_UNIT, LEAF_PAD, MAX_FIXED_STEPS, N_GROUPS, STEP_GROUPS, STEP_LANES,
-                                   decode_stream, decode_steps, pack_codes, pack_levels, step_record_index,
-                                   storage_widths, unpack_codes)
+                                   STEP_WORDS, decode_stream, decode_steps, pack_codes, pack_levels, record_slots,
+                                   step_record_index, storage_widths, unpack_codes)
 
 from conftest import kind_mix_stream, outlier_matrix
 
@@ -204,36 +204,40 @@ def test_step_records_cover_every_chunk_once():
     n = np.concatenate([h[:, 28:29], h[:, 30:31]], axis=1).reshape(-1)          # records per block
     assert F % STEP_LANES == 0 and F <= MAX_FIXED_STEPS and F >= min(n.max(), MAX_FIXED_STEPS)
     # table = fixed area, one null record, then the blocks' overflow records in block order
-    assert st.shape[0] == nb * F + 1 + int(np.maximum(n - F, 0).sum())
-    sl = st.reshape(-1, STEP_GROUPS, 4)
-    assert np.all(sl[nb * F, :, 2] == 0)
-    nv = sl[:, :, 2]
-    assert nv.min() >= 0 and nv.max() <= STEP_LANES
-    assert np.all(sl[:, :, 3] == sl[:, :1, 3])            # one kind and step index per record
+    assert st.shape == (nb * F + 1 + int(np.maximum(n - F, 0).sum()), STEP_WORDS)
+    assert record_slots(st[nb * F])[2] == [(0, 0, 0)] * STEP_GROUPS
     used = np.zeros(st.shape[0], bool)
     seen = {}
     for u in range(ps.n_units):
         for blk in range(BLOCKS_PER_UNIT):
+            steps_of = {}                                 # kind -> steps seen so far in this block
             for r in range(int(h[u, 28 + 2 * blk])):
                 i = step_record_index(ps, u, blk, r)
                 assert not used[i]
                 used[i] = True
-                e = sl[i]
-                assert e[:, 2].max() > 0
-                key, j = int(e[0, 3] & 0xFFFF), int(e[0, 3] >> 16)
-                for g in range(STEP_GROUPS):
+                S, P, slots = record_slots(st[i])
+                assert max(nv for _, _, nv in slots) > 0 and max(nv for _, _, nv in slots) <= STEP_LANES
+                key = (S.bit_length() - 1) | (P << 8)
+                j = steps_of.get(key, 0)                  # a block's records of a kind are its steps in order
+                steps_of[key] = j + 1
+                for g, (pay, leaf, nv) in enumerate(slots):
                     cg = blk * STEP_GROUPS + g
-                    # the slot's (absolute) offsets name one of this column group's buckets of the kind
-                    b = [k for k in range(h[u, 4] + h[u, 8 + cg], h[u, 4] + h[u, 9 + cg])
-                         if h[u, 0] + ps.buckets[k, 0] == e[g, 0] and h[u, 2] + ps.buckets[k, 1] == e[g, 1]]
-                    if e[g, 2] == 0:
+                    if nv == 0:
+                        assert (pay, leaf) == (0, 0)
                         continue
-                    assert len(b) == 1 and int(ps.buckets[b[0], 3]) == key
-                    for t in range(STEP_LANES * j, STEP_LANES * j + int(e[g, 2])):
+                    # the slot names chunk 16 j of this column group's bucket of the kind
+                    b = [k for k in range(h[u, 4] + h[u, 8 + cg], h[u, 4] + h[u, 9 + cg]) if int(ps.buckets[k, 3]) == key]
+                    assert len(b) == 1
+                    pb, lb = int(ps.buckets[b[0], 0]), int(ps.buckets[b[0], 1])
+                    assert pay == pb + STEP_LANES * j * P
+                    assert leaf == lb + (2 * STEP_LANES * j if S == 4 else STEP_LANES * j // (S // 8))
+                    assert nv == min(max(int(ps.buckets[b[0], 2] & 0xFFFF) - STEP_LANES * j, 0), STEP_LANES)
+                    for t in range(STEP_LANES * j, STEP_LANES * j + nv):
                         assert (b[0], t) not in seen
                         seen[(b[0], t)] = 1
     # every record the blocks do not own is a null record
-    assert np.all(sl[~used][:, :, 2] == 0)
+    assert np.all(st[~used][:, 0::2] == 0) and np.all(st[~used][:, 1::2] >> 8 == 0)
+    assert np.all(st[:, 1::2] == st[:, 1:2])             # every slot carries the same kind-and-counts word
     expect = {(k, t) for k in range(ps.n_buckets) for t in range(int(ps.buckets[k, 2] & 0xFFFF))}
     assert set(seen) == expect
 
@@ -247,8 +251,7 @@ def test_step_records_overflow_past_the_fixed_area():
 
 
 def _records(ps):
-    st = ps.steps.reshape(-1, STEP_GROUPS, 4)
-    return int((st[:, :, 2].sum(axis=1) > 0).sum())
+    return int((ps.steps[:, 1] >> 8 > 0).sum())
 
 
 def test_storage_widths_merge_rare_kinds_within_the_byte_limit():
