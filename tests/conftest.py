@@ -84,6 +84,22 @@ def signed_scale_levels(seed=7, K=256, N=128, sizes=(32, 16, 8, 4)):
     return ((K, N), sizes, leaf, modes, scales, codes), W_hat
 
 
+def largest_unit_stream(seed=5):
+    """The largest unit the panel stream allows: 4096 rows x 32 columns of 4x4 leaves, every
+    one at P16 (65536 payload dwords and 8192 leaf words in one unit), random codes and
+    power-of-two scales. Returns the stream and W_hat computed from the codes directly."""
+    from tensorpack_amd.packer import pack_levels
+    K, N = 4096, 32
+    rng = np.random.RandomState(seed)
+    g = (K // 4, N // 4)
+    codes4 = rng.randint(-(1 << 15), 1 << 15, size=g + (4, 4))
+    scales4 = (2.0 ** rng.randint(-24, -14, size=g)).astype(np.float32)
+    W_hat = (codes4.astype(np.float32) * scales4[:, :, None, None]).transpose(0, 2, 1, 3).reshape(K, N)
+    ps = pack_levels((K, N), (4,), {4: np.ones(g, bool)}, {4: np.full(g, 16)}, {4: scales4},
+                     lambda S, P, ii, jj, sc: codes4[ii, jj], chunk_rows=K)
+    return ps, W_hat + np.float32(0.0)
+
+
 def kind_mix_stream(K=4096, N=32, seed=24):
     """Panel stream of 4x4 leaves whose code width changes with the column group (random
     codes, power-of-two scales, 30 % P0): the 4 column groups of a decode block step

@@ -17,7 +17,7 @@ from tensorpack_amd.core.permutation import PermutedQuadtreeRD
 from tensorpack_amd.core.quadtree import QuadtreeRD
 from tensorpack_amd.kernels.gemm import MTCMatrix, mtc_gemm
 
-from conftest import kind_grid_stream, kind_mix_stream, outlier_matrix, signed_scale_levels
+from conftest import kind_grid_stream, kind_mix_stream, largest_unit_stream, outlier_matrix, signed_scale_levels
 
 pytestmark = pytest.mark.gpu
 
@@ -162,6 +162,24 @@ def test_gemv_step_records_past_the_fixed_area(gpu, M):
     Y = DeviceStream(ps, gpu).gemv_f32(torch.from_numpy(X).to(gpu)).cpu().numpy()
     err = O.relative_frobenius_error(O.qt_gemm_f64(X, decode_stream(ps)), Y)
     assert err <= TOL_F32, err
+
+
+def test_largest_unit(gpu):
+    """One 4096-row unit of P16 4x4 leaves (65536 payload dwords, 8192 leaf words: the step
+    records' unit-relative offsets at their largest): dequant bit-exact, Y within the fp32 bar
+    for M = 1, 2, 4 (vector path) and 8 (matrix core)."""
+    import torch
+    from tensorpack_amd.device import DeviceStream
+    ps, W_hat = largest_unit_stream()
+    ds = DeviceStream(ps, gpu)
+    _say("largest unit")
+    got = ds.dequant().cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), W_hat.view(np.uint32))
+    for M in (1, 2, 4, 8):
+        X = np.random.RandomState(M + 90).randn(M, ps.K).astype(np.float32)
+        Y = ds.gemv_f32(torch.from_numpy(X).to(gpu)).cpu().numpy()
+        err = O.relative_frobenius_error(O.qt_gemm_f64(X, W_hat), Y)
+        assert err <= TOL_F32, (M, err)
 
 
 @pytest.mark.parametrize("S", [8, 16, 32])

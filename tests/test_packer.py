@@ -15,7 +15,7 @@ from tensorpack_amd.packer import (BLOCKS_PER_UNIT, LEAF_PAD, MAX_FIXED_STEPS, N
                                    STEP_WORDS, decode_stream, decode_steps, pack_codes, pack_levels, record_slots,
                                    step_record_index, storage_widths, unpack_codes)
 
-from conftest import kind_mix_stream, outlier_matrix
+from conftest import kind_mix_stream, largest_unit_stream, outlier_matrix
 
 
 def _bits(a):
@@ -240,6 +240,19 @@ def test_step_records_cover_every_chunk_once():
     assert np.all(st[:, 1::2] == st[:, 1:2])             # every slot carries the same kind-and-counts word
     expect = {(k, t) for k in range(ps.n_buckets) for t in range(int(ps.buckets[k, 2] & 0xFFFF))}
     assert set(seen) == expect
+
+
+def test_step_records_address_the_largest_unit():
+    """A 4096-row unit of P16 4x4 leaves only: the step records' 16-bit unit-relative offsets
+    reach their largest values (payload dword 65536 - 256 of the last step, leaf 8192 - 32)
+    and still decode to W_hat bit for bit."""
+    ps, W_hat = largest_unit_stream()
+    assert ps.n_units == 1 and ps.payload.size >= 65536 and ps.n_real_leaves == 8192
+    seen = [record_slots(r)[2] for r in ps.steps]
+    assert max(pay for sl in seen for pay, _, nv in sl if nv) == 65536 - STEP_LANES * 16
+    assert max(leaf for sl in seen for _, leaf, nv in sl if nv) == 8192 - 2 * STEP_LANES
+    assert np.array_equal(_bits(decode_steps(ps)), _bits(W_hat))
+    assert np.array_equal(_bits(decode_stream(ps)), _bits(W_hat))
 
 
 def test_step_records_overflow_past_the_fixed_area():
