@@ -206,6 +206,12 @@ class PanelStream:
             if self.steps.ndim != 2 or self.steps.shape[1] != STEP_WORDS or \
                     self.steps.shape[0] < blocks * int(self.fixed_steps) + 1 or self.steps.size * 4 > MAX_DEVICE_ARRAY_BYTES:
                 bad("step records shape")
+            kc = self.steps[:, 1::2].astype(np.int64)
+            ls, P = kc[:, 0] & 7, (kc[:, 0] >> 3) & 31
+            counts = (kc[:, :1] >> (8 + 5 * np.arange(4))) & 31
+            if np.any(kc != kc[:, :1]) or np.any((ls < 2) | (ls > 5)) or \
+                    np.any(~np.isin(P, CODE_WIDTHS)) or np.any(counts > STEP_LANES):
+                bad("step record kind or chunk counts")
         elif nb:
             bad("step records missing")
         if self.fixed_steps not in (0, 16, 32, 48):

@@ -166,9 +166,16 @@ def test_panel_stream_load_rejects_corrupt_stream(saved_qtp, tmp_path):
     bk2[0, 3] = 7 | (2 << 8)                          # no leaf size 128
     lw = ps.leaf_word.copy()
     lw[:] |= 1023                                     # leaf rows past the unit's rows
+    st1 = ps.steps.copy()
+    st1[0, 3] ^= 1 << 8                               # slots of one record disagree on the kind word
+    st2 = ps.steps.copy()
+    st2[0, 1::2] = (st2[0, 1::2] & ~np.uint32(0xF8)) | np.uint32(7 << 3)   # code width 7
+    st3 = ps.steps.copy()
+    st3[0, 1::2] |= np.uint32(17 << 8)                # 17+ chunks in a 16-chunk step
     bad = {"hdr": {"unit_hdr": hdr}, "bucket payload": {"buckets": bk}, "bucket kind": {"buckets": bk2},
            "leaf rows": {"leaf_word": lw}, "row_perm": {"row_perm": np.zeros_like(ps.row_perm)},
-           "col_perm": {"col_perm": ps.col_perm + 1}}
+           "col_perm": {"col_perm": ps.col_perm + 1}, "record kind words": {"steps": st1},
+           "record width": {"steps": st2}, "record count": {"steps": st3}}
     for name, change in bad.items():
         dst = tmp_path / (name.replace(" ", "_") + ".npz")
         _resave(src, dst, **change)
