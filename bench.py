@@ -336,7 +336,7 @@ def leaf_arena(alloc, W):
 # ----------------------------------------------------------------------------------------------
 # c2: the headline decode (M = 1), and M = 16
 # ----------------------------------------------------------------------------------------------
-def bench_c2(args, wl, alloc, traffic, dev):
+def bench_c2(args, wl, alloc, traffic, dev, traffic16=None):
     import torch
     from tensorpack_amd.kernels.gemm import MTCMatrix
     m = MTCMatrix.from_quadtree(alloc, wl.W)
@@ -381,8 +381,13 @@ def bench_c2(args, wl, alloc, traffic, dev):
         res["m16"] = {"us_per_call": ms16 * 1e3, "packed_GBps": packed / (ms16 * 1e-3) / 1e9, "TFLOPs": tf,
                       "frac_fp32_peak": tf / FP32_PEAK_TFLOPS, "chunk_rows": d16.host.chunk_rows,
                       "rel_frobenius_vs_fp64": rel16,
-                      "roofline": {"bound": "fp32", "achieved": tf, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                   "frac": tf / FP32_PEAK_TFLOPS, "traffic": None}}
+                      "roofline": {"bound": "mfma", "achieved": tf, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                   "frac": tf / FP32_PEAK_TFLOPS,
+                                   "traffic": None if traffic16 is None else traffic16["bytes"],
+                                   "kernel": "k_gemv<16>"}}
+        if traffic16 is not None:
+            res["m16"]["roofline"]["traffic_detail"] = dict(traffic16, traffic_over_packed=traffic16["bytes"] / packed)
+            log(f"c2 M=16 traffic {traffic16['bytes'] / 1e6:.2f} MB per launch = {traffic16['bytes'] / packed:.3f}x packed")
         log(f"c2 M=16: {ms16 * 1e3:.2f} us/call, {tf:.2f} TFLOP/s; vs fp64 rel {rel16:.2e}")
         del c16
     return res
@@ -615,7 +620,9 @@ def cpu_baseline_c3(args, mats, allocs):
 # ----------------------------------------------------------------------------------------------
 # c5: the adversarial leaf mix
 # ----------------------------------------------------------------------------------------------
-def bench_c5(args, wl, a, dev):
+def bench_c5(args, wl, a, dev, traffic=None):
+    """c5 at M = 1 (decode over rotating copies) and M = 256 (prefill). `traffic`: counter bytes
+    of one M = 1 launch (traffic_passes), if measured."""
     import torch
     from tensorpack_amd.kernels.gemm import MTCMatrix
     m = MTCMatrix.from_quadtree(a, wl.W)
@@ -647,10 +654,15 @@ def bench_c5(args, wl, a, dev):
     log(f"c5 M=256: {ms2 * 1e3:.1f} us/call, {tf:.1f} TFLOP/s; vs fp64 rel {rel2:.2e}")
     if not rel2 < 2e-3:
         raise SystemExit(f"c5 prefill output differs from the fp64 product: rel {rel2:.3e}")
+    m1 = {"us_per_call": ms * 1e3, "GBps_packed": gbs, "rotating_copies": len(copies), "rel_vs_fp64": rel1,
+          "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": gbs / HBM_PEAK_GBS, "traffic": None if traffic is None else traffic["bytes"],
+                       "kernel": "k_gemv<1>"}}
+    if traffic is not None:
+        m1["roofline"]["traffic_detail"] = dict(traffic, traffic_over_packed=traffic["bytes"] / m.packed_bytes)
+        log(f"c5 M=1 traffic {traffic['bytes'] / 1e6:.2f} MB per launch = {traffic['bytes'] / m.packed_bytes:.3f}x packed")
     return {"workload": wl.name, "packed_bytes": m.packed_bytes, "stream_bytes": ds.device_bytes(),
-            "m1": {"us_per_call": ms * 1e3, "GBps_packed": gbs, "rotating_copies": len(copies), "rel_vs_fp64": rel1,
-                   "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                "frac": gbs / HBM_PEAK_GBS, "traffic": None, "kernel": "k_gemv<1>"}},
+            "m1": m1,
             "m256": {"us_per_call": ms2 * 1e3, "TFLOPs": tf, "x_dtype": "f32 (staged to bf16 by k_stage_x)",
                      "rel_vs_fp64": rel2,
                      "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
@@ -696,11 +708,17 @@ def main():
         if not args.no_traffic:
             c3_traffic = traffic_passes_batch([m.panel_stream(m.decode_chunk_rows(1)) for m in c3_ms],
                                               {w.W.shape[0]: c3_x(w.W.shape[0], 1) for w in mats})
-    traffic = None
+    traffic, traffic16, traffic5 = None, None, None
     if "c2" in want and not args.no_traffic:
         wl, alloc = A["c2"]
         m = MTCMatrix.from_quadtree(alloc, wl.W)
         traffic = traffic_passes(m.panel_stream(m.decode_chunk_rows(1)), wl.activations(1))
+        if not args.no_m16:
+            traffic16 = traffic_passes(m.panel_stream(m.decode_chunk_rows(16)), wl.activations(16), kernel="k_gemv<16")
+    if "c5" in want and not args.no_traffic:
+        wl5, a5 = A["c5"]
+        m5 = MTCMatrix.from_quadtree(a5, wl5.W)
+        traffic5 = traffic_passes(m5.panel_stream(m5.decode_chunk_rows(1)), wl5.activations(1))
 
     import torch
     from tensorpack_amd.device import require_gpu
@@ -712,7 +730,7 @@ def main():
             if not args.no_cpu_baseline:
                 r["cpu_baseline"] = cpu_baseline_c3(args, *A["c3"])
         else:
-            r = bench_c5(args, *A["c5"], dev)
+            r = bench_c5(args, *A["c5"], dev, traffic=traffic5)
             if not args.no_cpu_baseline:
                 wl, a = A["c5"]
                 r["cpu_baseline"] = cpu_port_gbs([leaf_arena(a, wl.W)], [wl.activations(1)], a.total_bits / 8.0,
@@ -722,7 +740,7 @@ def main():
 
     extra = {}
     wl, alloc = A["c2"]
-    c2 = bench_c2(args, wl, alloc, traffic, dev)
+    c2 = bench_c2(args, wl, alloc, traffic, dev, traffic16=traffic16)
     if "m16" in c2:
         extra["c2_m16"] = c2.pop("m16")
     copy_gbs, copy_small_us = device_copy_rates(dev, c2["packed"])
@@ -731,7 +749,7 @@ def main():
     if "c3" in want:
         extra["c3"] = bench_c3(args, *A["c3"], dev, ms_=c3_ms, traffic=c3_traffic)
     if "c5" in want:
-        extra["c5"] = bench_c5(args, *A["c5"], dev)
+        extra["c5"] = bench_c5(args, *A["c5"], dev, traffic=traffic5)
 
     # ---- CPU baselines (bounded samples on this host's cores) ----
     cpu = None
