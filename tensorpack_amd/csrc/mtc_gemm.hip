@@ -22,6 +22,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <vector>
 
 #include "mtc_hip.h"
@@ -47,7 +48,6 @@ constexpr int kTileBytes = kTM * kTK * 2;   // one bf16 operand tile (A and B ar
 constexpr int kABufs = 3;                   // A (X) buffers: copied two steps ahead
 constexpr int kBBufs = 2;                   // B (decoded weight) buffers
 constexpr int kLdsBytes = (kABufs + kBBufs) * kTileBytes;   // 160 KiB, all of a CU's LDS
-constexpr int kDmaPerWave = kTM / 8 / kConsumerWaves;       // 1 KiB (8-row) A copies per consumer wave
 constexpr uint32_t kOutOfRange = 0xFFFFFF00u;               // byte offset past any buffer's end
 constexpr int kRowGroup = 8;                // row tiles per launch-order group (L2 reuse of B)
 constexpr int kXcds = 8;
@@ -186,16 +186,21 @@ __device__ __forceinline__ bool tile_of_block(int bx, int n_row_tiles, int n_ct,
 }
 
 // One output tile block of matrix `d`: output tile (rt, ct), K split by.
-template <bool kFS, int kYDT>
+// TM: output rows of the block (256, or 128 / 64 for short X, whose full-height tiles are too
+// few to fill the chip). The 8 consumer waves are 2 x 4: TM / 2 rows x 64 columns each.
+template <bool kFS, int kYDT, int TM = kTM>
 __device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const int rt, const int ct, const int by,
                                                 const __bf16* __restrict__ X, int64_t ldx, void* __restrict__ Y,
                                                 int64_t ldy, int M, int steps_per_split, float* __restrict__ part) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   constexpr int CW = kFS ? 4 : 2;
+  static_assert(TM == 256 || TM == 128 || TM == 64, "row tiles of 256, 128 or 64 rows");
+  constexpr int DMA = TM / 8 / kConsumerWaves;             // 1 KiB (8-row) A copies per consumer wave
+  constexpr int RW = TM / 2, RI = RW / 32;                 // rows per consumer wave, 32-row MFMA blocks
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: keeps per-wave control scalar
-  const int m0 = rt * kTM, n0 = ct * kTN;
+  const int m0 = rt * TM, n0 = ct * kTN;
   // split K: this block runs steps kb0 .. kb0 + nks - 1 (split by) and, with `part`,
   // writes its partial tile to part[by] instead of Y
   const int kb0 = by * steps_per_split;
@@ -203,17 +208,17 @@ __device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const in
 
   if (wave < kConsumerWaves) {
     // ---------------- consumers: copy X tiles into LDS, bf16 MFMA over the staged tiles ----------------
-    // A copies: step s's 256 x 64 bf16 X tile is 32 copies of 8 rows; this wave does
-    // copies kDmaPerWave * wave + i. Lane l of a copy fills physical 16-byte slot l of the
+    // A copies: step s's TM x 64 bf16 X tile is TM / 8 copies of 8 rows; this wave does
+    // copies DMA * wave + i. Lane l of a copy fills physical 16-byte slot l of the
     // 8 rows, so it reads the logical segment that swz() maps there. Rows past M and
     // segments past K read zeros (out-of-range offsets).
     const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds;
-    const u32x4_t x_r = buffer_rsrc(X + (int64_t)m0 * ldx, (uint32_t)(kTM * ldx * 2));
-    uint32_t a_off[kDmaPerWave];
-    int a_k[kDmaPerWave];                                  // first K element of the lane's segment
+    const u32x4_t x_r = buffer_rsrc(X + (int64_t)m0 * ldx, (uint32_t)(TM * ldx * 2));
+    uint32_t a_off[DMA];
+    int a_k[DMA];                                          // first K element of the lane's segment
 #pragma unroll
-    for (int i = 0; i < kDmaPerWave; ++i) {
-      const int row = 8 * (kDmaPerWave * wave + i) + (lane >> 3);
+    for (int i = 0; i < DMA; ++i) {
+      const int row = 8 * (DMA * wave + i) + (lane >> 3);
       const int lseg = (lane & 7) ^ (row & 7) ^ ((row >> 3) & 1);
       a_k[i] = lseg * 8;
       a_off[i] = m0 + row < M ? (uint32_t)(row * ldx + lseg * 8) * 2 : kOutOfRange;
@@ -222,24 +227,24 @@ __device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const in
       const uint32_t buf = lds0 + (uint32_t)(s % kABufs) * kTileBytes;
       const uint32_t kb = (uint32_t)((kb0 + s) * kTK) * 2;
 #pragma unroll
-      for (int i = 0; i < kDmaPerWave; ++i) {
+      for (int i = 0; i < DMA; ++i) {
         // K % 8 == 0, so a segment is wholly inside or outside K
         const bool in = a_off[i] != kOutOfRange && (kb0 + s) * kTK + a_k[i] < d.K;
         dma16(x_r, in ? a_off[i] + kb : kOutOfRange,
-              __builtin_amdgcn_readfirstlane(buf + (uint32_t)(kDmaPerWave * wave + i) * 1024u));
+              __builtin_amdgcn_readfirstlane(buf + (uint32_t)(DMA * wave + i) * 1024u));
       }
     };
 
     const int wm = wave >> 2, wn = wave & 3;
-    f32x16_t acc[4][2];
+    f32x16_t acc[RI][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < RI; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[i][j] = f32x16_t{};
     copy_a(0);
     if (nks > 1) {
       copy_a(1);
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerWave) : "memory");   // step 0's copies done
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA) : "memory");   // step 0's copies done
     } else {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
@@ -252,22 +257,22 @@ __device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const in
 #pragma unroll
       for (int kk = 0; kk < kTK / 16; ++kk) {
         const int seg = kk * 2 + (lane >> 5);
-        bf16x8_t a[4], b[2];
+        bf16x8_t a[RI], b[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j)
           b[j] = *reinterpret_cast<const bf16x8_t*>(bs + swz(wn * 64 + j * 32 + (lane & 31), seg));
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          a[i] = *reinterpret_cast<const bf16x8_t*>(as + swz(wm * 128 + i * 32 + (lane & 31), seg));
+        for (int i = 0; i < RI; ++i)
+          a[i] = *reinterpret_cast<const bf16x8_t*>(as + swz(wm * RW + i * 32 + (lane & 31), seg));
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < RI; ++i)
 #pragma unroll
           for (int j = 0; j < 2; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
       }
       // step ks+1's copies (issued a step ago) must have landed before the barrier
       if (ahead) {
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerWave) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA) : "memory");
       } else {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }
@@ -285,10 +290,10 @@ __device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const in
       const bool cok = col < d.N;
       const int ycol = (d.col_perm && !part) ? d.col_perm[cok ? col : 0] : col;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < RI; ++i) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const int row = m0 + wm * 128 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+          const int row = m0 + wm * RW + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
           if (cok && row < M) {
             if (fp32_out)
               yf[(int64_t)row * ld + ycol] = acc[i][j][e];
@@ -400,14 +405,15 @@ __device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const in
   }
 }
 
-template <bool kFS, int kYDT>
+// One output tile block of matrix `d`: output tile (rt, ct) of TM rows, K split by.
+template <bool kFS, int kYDT, int TM>
 __global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, const __bf16* __restrict__ X,
                                                         int64_t ldx, void* __restrict__ Y, int64_t ldy, int M,
                                                         int n_row_tiles, int tiles_per_xcd, int steps_per_split,
                                                         float* __restrict__ part) {
   int rt, ct;
   if (!tile_of_block((int)blockIdx.x, n_row_tiles, d.n_col_tiles, tiles_per_xcd, d.col_perm && !part, rt, ct)) return;
-  gemm_tile_block<kFS, kYDT>(d, rt, ct, (int)blockIdx.y, X, ldx, Y, ldy, M, steps_per_split, part);
+  gemm_tile_block<kFS, kYDT, TM>(d, rt, ct, (int)blockIdx.y, X, ldx, Y, ldy, M, steps_per_split, part);
 }
 
 // Up to kMaxGroup matrices that read the same X, in one launch of each kernel: member i owns
@@ -675,35 +681,60 @@ int check_tile_desc(const mtc_tile_desc* d) {
 
 bool needs_staging(const mtc_tile_desc* d, int x_dtype) { return d->row_perm || x_dtype == MTC_DTYPE_F32; }
 
-constexpr int kFillCUs = 256;             // blocks that fill the chip (one 256 x 256 tile block per CU)
+constexpr int kFillCUs = 256;             // blocks that fill the chip (one tile block per CU)
 constexpr int kMinStepsPerSplit = 2;
-constexpr double kStepUs = 2.0;           // time of one K-step of a tile block (measured: 1.9-2.4 us)
 constexpr double kReduceBytesPerUs = 4.0e6;   // split-K partials written + read, bytes per microsecond
 constexpr double kReduceLaunchUs = 3.0;   // the reduction pass's own launch
 
-// K splits for M rows when the output has fewer tiles than the chip has CUs: the split
-// count (at most enough blocks to fill the chip, at least kMinStepsPerSplit K-steps per
-// split) that minimises the estimated time, K-steps per block plus the split-K partial
-// traffic (written by the tile blocks, read by the reduction). Returns the steps per split.
-int split_steps(const mtc_tile_desc* d, int M, int* splits) {
-  const int64_t n_tiles = (int64_t)((M + kTM - 1) / kTM) * d->n_col_tiles;
-  int max_s = n_tiles >= kFillCUs ? 1 : (int)((kFillCUs + n_tiles - 1) / n_tiles);
-  max_s = std::max(1, std::min(max_s, d->n_ksteps / kMinStepsPerSplit));
+// Time of one K-step of a tile block by its row-tile height: 256 rows 1.9-2.4 us. Shorter
+// tiles read less X from LDS per step but decode the same 64 x 256 weight cells and keep
+// the block's fixed costs; timed at 4096 x 4096, M = 256 with forced plans, relative to 256
+// rows: 128 rows 0.79, 64 rows 0.68 (with their fixed costs) of the step time.
+inline double step_us(int tm) { return tm == 256 ? 2.0 : tm == 128 ? 1.58 : 1.36; }
+
+struct TilePlan {
+  int tm;        // output rows per tile block
+  int splits;    // K splits
+  int per;       // K-steps per split
+};
+
+// Tile height and K split of one call: with M rows in tiles of 256 when those fill the chip;
+// otherwise the height (256, or for M <= 256 also 128 or 64) and split count (at most enough
+// blocks to fill the chip, at least kMinStepsPerSplit K-steps per split) that minimise the
+// estimated time: K-steps per block, rounds of blocks past one per CU, and the split-K
+// partial traffic (written by the tile blocks, read by the reduction).
+TilePlan tile_plan(const mtc_tile_desc* d, int M) {
+  const int64_t full = (int64_t)((M + kTM - 1) / kTM) * d->n_col_tiles;
+  if (full >= kFillCUs) return {kTM, 1, d->n_ksteps};
   const double split_bytes = 2.0 * 4.0 * (double)M * d->N;     // one partial, written and read
-  int best_per = d->n_ksteps, best_s = 1;
-  double best = (double)d->n_ksteps * kStepUs;
-  for (int s = 2; s <= max_s; ++s) {
-    const int per = (d->n_ksteps + s - 1) / s;
-    const int s_eff = (d->n_ksteps + per - 1) / per;
-    const double t = per * kStepUs + s_eff * split_bytes / kReduceBytesPerUs + kReduceLaunchUs;
-    if (t < best) {
-      best = t;
-      best_per = per;
-      best_s = s_eff;
+  TilePlan best{kTM, 1, d->n_ksteps};
+  double best_t = 1e300;
+  for (int tm : {256, 128, 64}) {
+    if (tm < kTM && M > kTM) break;                         // shorter tiles timed for M <= 256 only
+    const int64_t n_tiles = (int64_t)((M + tm - 1) / tm) * d->n_col_tiles;
+    int max_s = n_tiles >= kFillCUs ? 1 : (int)((kFillCUs + n_tiles - 1) / n_tiles);
+    max_s = std::max(1, std::min(max_s, d->n_ksteps / kMinStepsPerSplit));
+    for (int s = 1; s <= max_s; ++s) {
+      const int per = (d->n_ksteps + s - 1) / s;
+      const int s_eff = (d->n_ksteps + per - 1) / per;
+      const double rounds = std::ceil((double)(n_tiles * s_eff) / kFillCUs);
+      const double t = rounds * per * step_us(tm) +
+                       (s_eff > 1 ? s_eff * split_bytes / kReduceBytesPerUs + kReduceLaunchUs : 0.0);
+      if (t < best_t) {
+        best_t = t;
+        best = {tm, s_eff, per};
+      }
     }
   }
-  *splits = best_s;
-  return best_per;
+  return best;
+}
+
+// K splits of one call (tile_plan): a group or batch member splits K the same way, so that
+// its Y is the single call's bit for bit. Returns the steps per split.
+int split_steps(const mtc_tile_desc* d, int M, int* splits) {
+  const TilePlan p = tile_plan(d, M);
+  *splits = p.splits;
+  return p.per;
 }
 
 size_t staging_bytes(const mtc_tile_desc* d, int M, int x_dtype) {
@@ -724,17 +755,28 @@ int launch_tile(const mtc_tile_desc* d, const __bf16* X, int64_t ldx, void* Y, i
                 mtc::host::device_lds_limit());
   if (ldx >= ((int64_t)1 << 31) / (2 * kTM))
     return fail(MTC_E_SHAPE, "ldx=%lld too large for 32-bit X tile offsets", (long long)ldx);
-  const void* fn = reinterpret_cast<const void*>(&k_gemm_tile<kFS, kYDT>);
+  const TilePlan p = tile_plan(d, M);
+  const void* fn = p.tm == 256 ? reinterpret_cast<const void*>(&k_gemm_tile<kFS, kYDT, 256>)
+                   : p.tm == 128 ? reinterpret_cast<const void*>(&k_gemm_tile<kFS, kYDT, 128>)
+                                 : reinterpret_cast<const void*>(&k_gemm_tile<kFS, kYDT, 64>);
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
   if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-  const int n_row_tiles = (M + kTM - 1) / kTM;
+  const int n_row_tiles = (M + p.tm - 1) / p.tm;
   const int64_t n_tiles = (int64_t)n_row_tiles * d->n_col_tiles;
   if (n_tiles > (int64_t)1 << 30) return fail(MTC_E_SHAPE, "M=%d gives too many tiles", M);
   const int tiles_per_xcd = (int)((n_tiles + kXcds - 1) / kXcds);
-  int splits = 1;
-  const int per = split_steps(d, M, &splits);
-  hipLaunchKernelGGL((k_gemm_tile<kFS, kYDT>), dim3(tiles_per_xcd * kXcds, splits), dim3(kThreads), kLdsBytes, st,
-                     *d, X, ldx, Y, ldy, M, n_row_tiles, tiles_per_xcd, per, splits > 1 ? part : nullptr);
+  const int splits = p.splits, per = p.per;
+  float* const pt = splits > 1 ? part : nullptr;
+  const dim3 grid(tiles_per_xcd * kXcds, splits);
+  if (p.tm == 256)
+    hipLaunchKernelGGL((k_gemm_tile<kFS, kYDT, 256>), grid, dim3(kThreads), kLdsBytes, st, *d, X, ldx, Y, ldy, M,
+                       n_row_tiles, tiles_per_xcd, per, pt);
+  else if (p.tm == 128)
+    hipLaunchKernelGGL((k_gemm_tile<kFS, kYDT, 128>), grid, dim3(kThreads), kLdsBytes, st, *d, X, ldx, Y, ldy, M,
+                       n_row_tiles, tiles_per_xcd, per, pt);
+  else
+    hipLaunchKernelGGL((k_gemm_tile<kFS, kYDT, 64>), grid, dim3(kThreads), kLdsBytes, st, *d, X, ldx, Y, ldy, M,
+                       n_row_tiles, tiles_per_xcd, per, pt);
   int rc = check_launch("k_gemm_tile");
   if (rc || splits == 1) return rc;
   hipLaunchKernelGGL(k_splitk_reduce<kYDT>, dim3((unsigned)reduce_blocks(M, d->N, d->col_perm != nullptr)),
