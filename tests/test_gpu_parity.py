@@ -124,6 +124,31 @@ def test_gemv_matrix_core_tile_heights_agree(gpu, allocs, name):
         assert np.array_equal(_bits(Y), _bits(Y16[:M])), (name, M)
 
 
+def test_gemm_short_row_tiles(gpu):
+    """Single prefill calls with M <= 256 and few output tiles run blocks of fewer output rows
+    (the tile plan prices 64- and 128-row blocks against 256-row ones; at this shape it takes
+    64 rows, and the c5 configuration test at M = 256 runs 128-row blocks): Y is within the
+    bf16 bar at every M around the tile heights, and a group call, which runs the same K split
+    with 256-row tiles, gives the same Y bit for bit."""
+    import torch
+    from tensorpack_amd.device import gemm_bf16_group
+    K, N = 2048, 512
+    W = outlier_matrix(41, K, N)
+    a = PermutedQuadtreeRD(W, np.exp(np.random.RandomState(42).randn(K)), (32, 16, 8, 4)).select(3.5)
+    m = MTCMatrix.from_quadtree(a, W)
+    g = m.device_tiles(gpu)
+    ref_w = _oracle_what(a, W)
+    for M in (1, 40, 64, 65, 100, 128, 129, 200, 256):
+        _say("gemm short row tiles", M)
+        X = np.random.RandomState(M + 3).randn(M, K).astype(np.float32)
+        Xb = torch.from_numpy(X).to(gpu).to(torch.bfloat16)
+        Y = g.gemm_bf16(Xb).cpu().numpy()
+        err = O.relative_frobenius_error(O.qt_gemm_f64(Xb.float().cpu().numpy(), ref_w), Y)
+        assert err <= TOL_BF16, (M, err)
+        Yg = gemm_bf16_group([g], Xb)[0].cpu().numpy()
+        assert np.array_equal(_bits(Yg), _bits(Y)), M
+
+
 @pytest.mark.parametrize("M,permuted,ydt", [(100, False, "f32"), (300, True, "f32"), (37, True, "bf16")])
 def test_gemm_split_k(gpu, M, permuted, ydt):
     # few output tiles and 32 K-steps: the K steps are split over blocks and the fp32
