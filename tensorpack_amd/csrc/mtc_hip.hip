@@ -770,14 +770,15 @@ __device__ __forceinline__ int mfma_slot(int m, int MT) { return (m & 3) * (MT /
 constexpr int kStageThreads = 64;
 
 template <int MT>
-__device__ __forceinline__ void stage_xt_block(int K, const float* __restrict__ X, int64_t ldx, int M,
-                                               float* __restrict__ xt) {
+__device__ __forceinline__ void stage_xt_block(int K, const float* __restrict__ X, int64_t ldx,
+                                               const int32_t* __restrict__ row_perm, int M, float* __restrict__ xt) {
   const int k = (int)blockIdx.x * kStageThreads + (int)threadIdx.x;
   if (k >= K) return;
   const int m0 = (int)blockIdx.y * MT;
+  const int src = row_perm ? row_perm[k] : k;         // xt row k holds X[:, row_perm[k]]
   float v[MT];
 #pragma unroll
-  for (int m = 0; m < MT; ++m) v[mfma_slot(m, MT)] = m0 + m < M ? X[(int64_t)(m0 + m) * ldx + k] : 0.0f;
+  for (int m = 0; m < MT; ++m) v[mfma_slot(m, MT)] = m0 + m < M ? X[(int64_t)(m0 + m) * ldx + src] : 0.0f;
   float4* o = reinterpret_cast<float4*>(xt + ((size_t)blockIdx.y * K + k) * MT);
 #pragma unroll
   for (int i = 0; i < MT / 4; ++i) o[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
@@ -785,8 +786,9 @@ __device__ __forceinline__ void stage_xt_block(int K, const float* __restrict__ 
 
 template <int MT>
 __global__ __launch_bounds__(kStageThreads) void k_gemv_stage_x(int K, const float* __restrict__ X, int64_t ldx,
-                                                                int M, float* __restrict__ xt) {
-  stage_xt_block<MT>(K, X, ldx, M, xt);
+                                                                const int32_t* __restrict__ row_perm, int M,
+                                                                float* __restrict__ xt) {
+  stage_xt_block<MT>(K, X, ldx, row_perm, M, xt);
 }
 
 // A lane's loads of one pass: the 64-bit window(s) holding its column's codes (two loads for
@@ -995,17 +997,18 @@ __device__ __forceinline__ void gemv_block_mfma(const mtc_stream_desc& d, const 
   };
 
   // ---- X rows of the unit into LDS, overlapped with the first records' loads. The compiler
-  //      waits for loads in issue order, so the order is: row indices, record slots, X pieces,
-  //      then the first record's payload; the LDS stores wait for the X pieces only and the
-  //      payload stays in flight. With xt, each row is one MT-float piece (16 bytes per
-  //      thread); kc * MT fits the LDS, so a thread has at most kMfmaStageIters pieces. ----
+  //      waits for loads in issue order, so the order is: record slots, X pieces, then the
+  //      first record's payload; the LDS stores wait for the X pieces only and the payload
+  //      stays in flight. xt holds X[:, row_perm] (the staging launch gathered it), so the
+  //      unit's rows are one contiguous slab of MT-float pieces (16 bytes per thread); kc * MT
+  //      fits the LDS, so a thread has at most kMfmaStageIters pieces. ----
   constexpr int L = MT / 4;                           // threads per row
   int kr[kMfmaStageIters];
   if (xt) {
 #pragma unroll
     for (int it = 0; it < kMfmaStageIters; ++it) {
       const int r = (it * T + tid) / L;
-      kr[it] = r < rows ? (d.row_perm ? d.row_perm[kb + r] : kb + r) : -1;
+      kr[it] = r < rows ? kb + r : -1;
     }
   }
   const u32x2_t f0 = slot_of(rec_of(wl));
@@ -1233,7 +1236,7 @@ __global__ __launch_bounds__(64 * NW, 4) void k_gemv_batch(const BatchItem* __re
 template <int MT>
 __global__ __launch_bounds__(kStageThreads) void k_gemv_stage_x_batch(const BatchItem* __restrict__ items, int M) {
   const BatchItem& it = items[blockIdx.z];
-  stage_xt_block<MT>(it.d.K, it.X, it.ldx, M, it.xt);
+  stage_xt_block<MT>(it.d.K, it.X, it.ldx, it.d.row_perm, M, it.xt);
 }
 
 // The batch kernel of a shape class (the LDS gather is a per-member flag there).
@@ -1382,7 +1385,7 @@ int launch_gemv(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y,
   if constexpr (MT > 4) {
     xt = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + xt_off);
     hipLaunchKernelGGL(k_gemv_stage_x<MT>, dim3(stage_x_blocks(d), (M + MT - 1) / MT), dim3(kStageThreads), 0, st,
-                       d->K, X, ldx, M, xt);
+                       d->K, X, ldx, d->row_perm, M, xt);
     const int rc = check_launch("k_gemv_stage_x");
     if (rc) return rc;
   }
