@@ -772,16 +772,21 @@ constexpr int kStageThreads = 64;
 template <int MT>
 __device__ __forceinline__ void stage_xt_block(int K, const float* __restrict__ X, int64_t ldx,
                                                const int32_t* __restrict__ row_perm, int M, float* __restrict__ xt) {
-  const int k = (int)blockIdx.x * kStageThreads + (int)threadIdx.x;
-  if (k >= K) return;
+  // one thread per 16-byte piece of xt: row k, slots 4i .. 4i+3 of its MT (consecutive threads
+  // write consecutive pieces); slot s holds M row 4 (s % Q) + s / Q (the inverse of mfma_slot)
+  constexpr int Q = MT / 4;
+  const int64_t t = (int64_t)blockIdx.x * kStageThreads + (int)threadIdx.x;
+  if (t >= (int64_t)K * Q) return;
+  const int k = (int)(t / Q), i = (int)(t - (int64_t)k * Q);
   const int m0 = (int)blockIdx.y * MT;
   const int src = row_perm ? row_perm[k] : k;         // xt row k holds X[:, row_perm[k]]
-  float v[MT];
+  float v[4];
 #pragma unroll
-  for (int m = 0; m < MT; ++m) v[mfma_slot(m, MT)] = m0 + m < M ? X[(int64_t)(m0 + m) * ldx + src] : 0.0f;
-  float4* o = reinterpret_cast<float4*>(xt + ((size_t)blockIdx.y * K + k) * MT);
-#pragma unroll
-  for (int i = 0; i < MT / 4; ++i) o[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+  for (int u = 0; u < 4; ++u) {
+    const int sl = 4 * i + u, m = 4 * (sl % Q) + sl / Q;
+    v[u] = m0 + m < M ? X[(int64_t)(m0 + m) * ldx + src] : 0.0f;
+  }
+  *reinterpret_cast<float4*>(xt + ((size_t)blockIdx.y * K + k) * MT + 4 * i) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
 template <int MT>
@@ -1351,7 +1356,10 @@ bool mfma_rows_fit(int mt, int chunk_rows) {
 }
 
 // Grid x of the X staging of one M tile.
-unsigned stage_x_blocks(const mtc_stream_desc* d) { return (unsigned)((d->K + kStageThreads - 1) / kStageThreads); }
+// Grid x of the matrix-core X staging: one thread per 16-byte piece of xt (K * MT / 4).
+unsigned stage_x_blocks(const mtc_stream_desc* d, int mt) {
+  return (unsigned)(((int64_t)d->K * (mt / 4) + kStageThreads - 1) / kStageThreads);
+}
 
 // Decode blocks of one M tile: one per unit on the matrix core; two per unit on the vector
 // path, with the unit count rounded up to whole XCD rounds.
@@ -1384,7 +1392,7 @@ int launch_gemv(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y,
   float* xt = nullptr;
   if constexpr (MT > 4) {
     xt = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + xt_off);
-    hipLaunchKernelGGL(k_gemv_stage_x<MT>, dim3(stage_x_blocks(d), (M + MT - 1) / MT), dim3(kStageThreads), 0, st,
+    hipLaunchKernelGGL(k_gemv_stage_x<MT>, dim3(stage_x_blocks(d, MT), (M + MT - 1) / MT), dim3(kStageThreads), 0, st,
                        d->K, X, ldx, d->row_perm, M, xt);
     const int rc = check_launch("k_gemv_stage_x");
     if (rc) return rc;
@@ -1530,7 +1538,7 @@ int build_batch_plan(const mtc_gemv_batch_item* items, int n, int M, void* works
       if (mt > 4) it[i].xt = reinterpret_cast<float*>(wsp + xt_off);
       wsp += align_up(wsi, 256);
     }
-    stage_bx = std::max(stage_bx, stage_x_blocks(d));
+    stage_bx = std::max(stage_bx, stage_x_blocks(d, mt));
     const int nb = gemv_blocks(d, mt);
     uint32_t* table = block_item + table_off[cls];
     it[i].start = start[cls];
