@@ -373,6 +373,91 @@ def storage_widths(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int,
     return out
 
 
+def split_leaves(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np.ndarray],
+                 store_w: Dict[int, np.ndarray], chunk_rows: int) -> Dict[int, np.ndarray]:
+    """Per level S in (32, 16), the stored leaves that are packed as (S/8)^2 leaves of size 8
+    (the same scale and storage width, their codes' 8 x 8 sub-blocks: W_hat is unchanged).
+
+    Leaf sizes 8, 16 and 32 share one decode path and differ only in how many chunks share a
+    leaf word, and the chunks of an S x S leaf are exactly those of its 8 x 8 sub-blocks, so a
+    unit's S x S leaves of a storage width can join its 8 x 8 leaves of that width in the same
+    step records. Per unit and storage width, from the largest size down, a size is split when
+    that saves records and its extra leaf words ((S/8)^2 - 1 per leaf, 4 bytes each) add at
+    most MERGE_BYTES_PER_RECORD bytes per record saved."""
+    K, N = (int(x) for x in shape)
+    n_chunks = -(-K // chunk_rows)
+    n_units = (N // PANEL) * n_chunks
+    widths = np.array(CODE_WIDTHS)
+    sizes = {int(x) for x in sizes}
+
+    def stored_at(S):
+        st = store_w[S]
+        ii, jj = np.nonzero(np.asarray(leaf[S], dtype=bool) & np.isin(st, widths))
+        unit = ((jj * S) // PANEL) * n_chunks + (ii * S) // chunk_rows
+        return ii, jj, unit, np.searchsorted(widths, st[ii, jj]), (jj * S % PANEL) // GROUP
+
+    cnt8 = np.zeros((n_units, len(widths), N_GROUPS), dtype=np.int64)   # chunks of (8, P) per column group
+    if 8 in sizes:
+        _, _, unit, p_idx, g0 = stored_at(8)
+        for c in range(2):
+            np.add.at(cnt8, (unit, p_idx, g0 + c), 1)
+    out: Dict[int, np.ndarray] = {}
+    for S in (32, 16):
+        if S not in sizes:
+            continue
+        ii, jj, unit, p_idx, g0 = stored_at(S)
+        out[S] = np.zeros(np.asarray(leaf[S]).shape, dtype=bool)
+        if ii.size == 0:
+            continue
+        cnt = np.zeros_like(cnt8)
+        n_leaf = np.zeros((n_units, len(widths)), dtype=np.int64)
+        for c in range(S // GROUP):
+            np.add.at(cnt, (unit, p_idx, g0 + c), S // 8)
+        np.add.at(n_leaf, (unit, p_idx), 1)
+        split = np.zeros((n_units, len(widths)), dtype=bool)
+        for p in range(len(widths)):
+            saved = _block_records(cnt8[:, p]) + _block_records(cnt[:, p]) - _block_records(cnt8[:, p] + cnt[:, p])
+            extra = n_leaf[:, p] * ((S // 8) ** 2 - 1) * 4
+            split[:, p] = (n_leaf[:, p] > 0) & (saved > 0) & (extra <= MERGE_BYTES_PER_RECORD * saved)
+            cnt8[split[:, p], p] += cnt[split[:, p], p]
+        out[S][ii, jj] = split[unit, p_idx]
+    return out
+
+
+def storage_plan(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np.ndarray],
+                 modes: Dict[int, np.ndarray], chunk_rows: int, merge_kinds: bool = True):
+    """The levels as packed: 16 x 16 and 32 x 32 leaves split into 8 x 8 leaves (split_leaves,
+    decided on the allocated widths), then storage widths chosen over those levels
+    (storage_widths), split leaves counted at level 8 with their parents' modes. Returns
+    (sizes, leaf, modes, storage widths, split): per level the leaf mask, mode grid and
+    storage-width grid as packed, and per level 16 / 32 the leaves that were split. Without
+    `merge_kinds` nothing is split and every leaf is stored at its mode."""
+    K, N = (int(x) for x in shape)
+    sizes = tuple(sorted({int(x) for x in sizes}, reverse=True))
+    split = split_leaves((K, N), sizes, leaf, {S: np.where(np.asarray(leaf[S], bool), np.asarray(modes[S]), 0)
+                                                for S in sizes}, chunk_rows) if merge_kinds else {}
+    leaf_p = {S: np.asarray(leaf[S], dtype=bool) for S in sizes}
+    modes_p = {S: np.asarray(modes[S]) for S in sizes}
+    if any(v.any() for v in split.values()):
+        if 8 not in leaf_p:
+            leaf_p[8] = np.zeros((K // 8, N // 8), dtype=bool)
+            modes_p[8] = np.zeros((K // 8, N // 8), dtype=np.int64)
+        modes_p[8] = modes_p[8].astype(np.int64).copy()
+        leaf_p[8] = leaf_p[8].copy()
+        for S, sp in split.items():
+            r = S // 8
+            up = np.kron(sp, np.ones((r, r), dtype=bool))
+            leaf_p[8] |= up
+            modes_p[8][up] = np.kron(np.asarray(modes[S]).astype(np.int64), np.ones((r, r), dtype=np.int64))[up]
+            leaf_p[S] = leaf_p[S] & ~sp
+    sizes_p = tuple(sorted(leaf_p, reverse=True))
+    if merge_kinds:
+        store_w = storage_widths((K, N), sizes_p, leaf_p, modes_p, chunk_rows)
+    else:
+        store_w = {S: np.where(leaf_p[S] & np.isin(modes_p[S], CODE_WIDTHS), modes_p[S], 0) for S in sizes_p}
+    return sizes_p, leaf_p, modes_p, store_w, split
+
+
 def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np.ndarray],
                 modes: Dict[int, np.ndarray], scales: Dict[int, np.ndarray], codes_of: CodeSource,
                 chunk_rows: int = 512, scale_format: str = "bf16", row_perm: Optional[np.ndarray] = None,
@@ -401,32 +486,57 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
     for S in sizes:
         if int(S) not in LEAF_SIZES:
             raise ValueError(f"leaf size {S} not supported by the panel stream (sizes {LEAF_SIZES})")
-    if merge_kinds:
-        store_w = storage_widths((K, N), sizes, leaf, modes, chunk_rows)
-    else:
-        store_w = {int(S): np.asarray(modes[S]) for S in sizes}
-    for S in sorted((int(s) for s in sizes), reverse=True):
-        lv_leaf = np.asarray(leaf[S], dtype=bool)
-        lv_mode = np.asarray(modes[S])
-        lv_store = store_w[S]
-        lv_scale = np.asarray(scales[S], dtype=np.float32)
+    sizes = tuple(sorted({int(x) for x in sizes}, reverse=True))
+    moved: Dict[int, list] = {}                        # storage width -> 8 x 8 sub-leaves of split leaves
+    sizes_p, leaf_p, modes_p, store_w, split = storage_plan((K, N), sizes, leaf, modes, chunk_rows, merge_kinds)
+    for S, sp in split.items():                        # codes of split leaves, as 8 x 8 sub-leaves
+        ii, jj = np.nonzero(sp)
+        if ii.size == 0:
+            continue
+        r = S // 8
+        sc = np.asarray(scales[S], dtype=np.float32)[ii, jj]
+        qm = np.asarray(modes[S])[ii, jj]
+        q = np.empty((ii.size, S, S), dtype=np.int32)
+        for Pq in np.unique(qm):
+            sel = np.flatnonzero(qm == Pq)
+            q[sel] = np.asarray(codes_of(S, int(Pq), ii[sel], jj[sel], sc[sel])).astype(np.int32)
+        k0, n0 = ii * S, jj * S
+        unit = (n0 // PANEL) * n_chunks + k0 // chunk_rows
+        pw = store_w[8][ii * r, jj * r]                 # every sub-leaf of a leaf: one unit and mode
+        a_, b_ = np.divmod(np.arange(r * r), r)         # sub-block (row a, column b)
+        sub = q.reshape(-1, r, 8, r, 8).transpose(0, 1, 3, 2, 4).reshape(-1, r * r, 8, 8)
+        for P in np.unique(pw):
+            m_ = pw == P
+            moved.setdefault(int(P), []).append((
+                (k0[m_][:, None] + 8 * a_).reshape(-1), (n0[m_] % PANEL)[:, None].repeat(r * r, 1).reshape(-1) +
+                np.tile(8 * b_, int(m_.sum())), np.repeat(unit[m_], r * r), np.repeat(sc[m_], r * r),
+                sub[m_].reshape(-1, 8, 8)))
+    for S in sizes_p:
+        native = S in sizes
         for P in CODE_WIDTHS:                          # storage width: the kind's P
-            ii, jj = np.nonzero(lv_leaf & np.isin(lv_mode, CODE_WIDTHS) & (lv_store == P))
-            if ii.size == 0:
+            k0 = c0 = unit = sc = q = None
+            if native:
+                own = np.asarray(leaf[S], dtype=bool) if S == 8 else leaf_p[S]     # not the split sub-leaves
+                ii, jj = np.nonzero(own & np.isin(modes_p[S], CODE_WIDTHS) & (store_w[S] == P))
+                if ii.size:
+                    sc = np.asarray(scales[S], dtype=np.float32)[ii, jj]
+                    q = np.empty((ii.size, S, S), dtype=np.int32)                 # (n, S, S) row-major
+                    qm = modes_p[S][ii, jj]
+                    for Pq in np.unique(qm):           # codes quantized at each leaf's own width
+                        sel = np.flatnonzero(qm == Pq)
+                        q[sel] = np.asarray(codes_of(S, int(Pq), ii[sel], jj[sel], sc[sel])).astype(np.int32)
+                    k0, n0 = ii * S, jj * S
+                    unit = (n0 // PANEL) * n_chunks + k0 // chunk_rows
+                    c0 = n0 % PANEL
+            if S == 8 and P in moved:
+                parts = ([(k0, c0, unit, sc, q)] if q is not None else []) + moved.pop(P)
+                k0, c0, unit, sc, q = (np.concatenate(x) for x in zip(*parts))
+            if q is None or q.shape[0] == 0:
                 continue
             kr = _kind_rank(S, P)
-            k0, n0 = ii * S, jj * S
-            unit = (n0 // PANEL) * n_chunks + k0 // chunk_rows
-            c0 = n0 % PANEL
             order = np.lexsort((k0, c0, unit))
-            ii, jj, k0, c0, unit = ii[order], jj[order], k0[order], c0[order], unit[order]
-            sc = lv_scale[ii, jj]
-            q = np.empty((ii.size, S, S), dtype=np.int32)                         # (n, S, S) row-major
-            qm = lv_mode[ii, jj]
-            for Pq in np.unique(qm):                   # codes quantized at each leaf's own width
-                sel = np.flatnonzero(qm == Pq)
-                q[sel] = np.asarray(codes_of(S, int(Pq), ii[sel], jj[sel], sc[sel])).astype(np.int32)
-            n_real += ii.size
+            k0, c0, unit, sc, q = k0[order], c0[order], unit[order], sc[order], q[order]
+            n_real += q.shape[0]
             words = ((k0 % chunk_rows) // 4).astype(np.uint32)
             if scale_format == "bf16":
                 words = words | (_bf16_bits(sc) << 16).astype(np.uint32)

@@ -13,7 +13,7 @@ from tensorpack_amd.core.quadtree import QuadtreeRD
 from tensorpack_amd.kernels.gemm import MTCMatrix, arena_decode, arena_encode
 from tensorpack_amd.packer import (BLOCKS_PER_UNIT, LEAF_PAD, MAX_FIXED_STEPS, N_GROUPS, STEP_GROUPS, STEP_LANES,
                                    STEP_WORDS, decode_stream, decode_steps, pack_codes, pack_levels, record_slots,
-                                   step_record_index, storage_widths, unpack_codes)
+                                   split_leaves, step_record_index, storage_plan, storage_widths, unpack_codes)
 
 from conftest import kind_mix_stream, largest_unit_stream, outlier_matrix
 
@@ -103,18 +103,23 @@ def test_stream_layout_invariants():
 @pytest.mark.parametrize("merge", [False, True])
 def test_payload_accounting_matches_allocator_bits(merge):
     """Unmerged, the chunk words hold exactly the allocator's payload bits (plus S = 4 pad
-    leaves); merged, every leaf is stored at its storage width, which is at least its mode."""
+    leaves); merged, every leaf is stored at its storage width, which is at least its mode,
+    and a split 16 x 16 or 32 x 32 leaf as its 8 x 8 sub-leaves (storage_plan)."""
     W = outlier_matrix(12, 256, 256)
     a = QuadtreeRD(W, None, (32, 16, 8, 4)).select(4.0)
     lv = MTCMatrix.from_quadtree(a, W)._levels
     ps = pack_levels(lv.shape, lv.sizes, lv.leaf, lv.modes, lv.scales, lv.codes_of, 256, lv.scale_format,
                      lv.row_perm, lv.col_perm, merge_kinds=merge)
-    widths = storage_widths((256, 256), a.sizes, a.leaf, a.modes, 256) if merge else a.modes
-    for s in a.sizes:
-        stored = a.leaf[s] & (a.modes[s] > 0)
-        assert (widths[s][stored] >= a.modes[s][stored]).all()
-    payload_bits = sum(int((a.leaf[s] & (a.modes[s] > 0) & (widths[s] == m)).sum()) * s * s * m
-                       for s in a.sizes for m in (2, 3, 4, 5, 6, 8, 16))
+    sizes, leaf, modes, widths, split = storage_plan((256, 256), a.sizes, a.leaf, a.modes, 256, merge)
+    assert merge or not split
+    for s in sizes:
+        stored = leaf[s] & (modes[s] > 0)
+        assert (widths[s][stored] >= modes[s][stored]).all()
+    # the split levels hold the allocator's leaves: every weight of a stored leaf once, at its mode
+    assert sum(int((leaf[s] & (modes[s] == m)).sum()) * s * s * m for s in sizes for m in (2, 3, 4, 5, 6, 8, 16)) == \
+        sum(int((a.leaf[s] & (a.modes[s] == m)).sum()) * s * s * m for s in a.sizes for m in (2, 3, 4, 5, 6, 8, 16))
+    payload_bits = sum(int((leaf[s] & (modes[s] > 0) & (widths[s] == m)).sum()) * s * s * m
+                       for s in sizes for m in (2, 3, 4, 5, 6, 8, 16))
     if not merge:
         assert payload_bits == sum(int((a.leaf[s] & (a.modes[s] == m)).sum()) * s * s * m
                                    for s in a.sizes for m in (2, 3, 4, 5, 6, 8, 16))
@@ -292,6 +297,40 @@ def test_storage_widths_merge_rare_kinds_within_the_byte_limit():
     modes[S][0, 2] = 2
     w = storage_widths(shape, (S,), leaf, modes, 256)[S]
     assert (w[:15, 1] == 2).all() and w[15, 1] == 16 and w[0, 2] == 2
+
+
+def test_split_leaves_join_the_8x8_records_within_the_byte_limit():
+    """One unit of 256 rows x 32 columns. Worked by hand: column groups 0-1 hold 30 P3 8x8
+    leaves (rows 0-239, 30 chunks per group: 2 records) and the rows 240-255 hold one P3
+    16 x 16 leaf over column groups 0-3 (2 chunks per group: a record of its own). Split into
+    four 8 x 8 leaves it adds 2 chunks to groups 0-1 (32: still 2 records) and 2 to groups 2-3,
+    so one record is saved for 3 extra leaf words (12 bytes): it is split. A 32 x 32 P16 leaf
+    alone in the other block has no 8 x 8 leaves to join and stays."""
+    shape = (256, 32)
+    leaf = {32: np.zeros((8, 1), bool), 16: np.zeros((16, 2), bool), 8: np.zeros((32, 4), bool)}
+    modes = {S: np.zeros(g.shape, np.int64) for S, g in leaf.items()}
+    leaf[8][:30, 0], modes[8][:30, 0] = True, 3
+    leaf[16][15, 0], modes[16][15, 0] = True, 3
+    sizes = (32, 16, 8)
+    w = storage_widths(shape, sizes, leaf, modes, 256)
+    sp = split_leaves(shape, sizes, leaf, w, 256)
+    assert sp[16][15, 0] and sp[16].sum() == 1 and not sp[32].any()
+    # a lone 32 x 32 leaf: splitting it would add 15 leaf words and save no record
+    leaf[32][0, 0], modes[32][0, 0] = True, 16
+    leaf[8][:4, :] = False
+    sp = split_leaves(shape, sizes, leaf, storage_widths(shape, sizes, leaf, modes, 256), 256)
+    assert not sp[32].any()
+    # the split stream decodes to the same W_hat as the unsplit one
+    rng = np.random.RandomState(3)
+    scales = {S: (2.0 ** rng.randint(-8, -2, size=g.shape)).astype(np.float32) for S, g in leaf.items()}
+    base = {S: rng.randint(0, 1 << 16, size=g.shape + (S, S)) for S, g in leaf.items()}
+    codes = lambda S, P, ii, jj, sc: base[S][ii, jj] % (1 << P) - (1 << (P - 1))
+    p0 = pack_levels(shape, sizes, leaf, modes, scales, codes, 256, merge_kinds=False)
+    p1 = pack_levels(shape, sizes, leaf, modes, scales, codes, 256, merge_kinds=True)
+    assert p1.n_real_leaves == p0.n_real_leaves + 3                # the 16 x 16 leaf as four 8 x 8
+    assert _records(p1) == _records(p0) - 1
+    ref = _bits(decode_stream(p0))
+    assert np.array_equal(_bits(decode_stream(p1)), ref) and np.array_equal(_bits(decode_steps(p1)), ref)
 
 
 @pytest.mark.parametrize("budget,chunk_rows,perm", [(2.5, 128, False), (3.25, 256, True), (4.0, 64, True)])
