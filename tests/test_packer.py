@@ -354,12 +354,13 @@ def test_merged_kinds_decode_to_the_same_w_hat(budget, chunk_rows, perm):
 
 @settings(max_examples=20, deadline=None)
 @given(seed=st.integers(0, 10 ** 6), rows=st.sampled_from([64, 128, 256]), chunk=st.sampled_from([32, 64, 128]),
-       sizes=st.sampled_from([(32, 16, 8, 4), (16, 8, 4), (8, 4), (4,), (32,)]))
+       sizes=st.sampled_from([(32, 16, 8, 4), (16, 8, 4), (8, 4), (4,), (32,), (32, 16, 4), (32, 4)]))
 def test_fuzz_storage_widths(seed, rows, chunk, sizes):
     """Random leaf mixes: a stored width is never narrower than the mode and at most
-    MERGE_MAX_WIDEN bits wider, P0 leaves are never stored, and the merged stream decodes to
-    the unmerged stream's W_hat bit for bit (bucket walk and step-record walk) with no more
-    step records."""
+    MERGE_MAX_WIDEN bits wider, P0 leaves are never stored, and the merged stream (rare kinds
+    widened, large leaves split into 8 x 8 ones, also where the allocation has no 8 x 8 level)
+    decodes to the unmerged stream's W_hat bit for bit (bucket walk and step-record walk) with
+    no more step records."""
     from tensorpack_amd.packer import CODE_WIDTHS, MERGE_MAX_WIDEN
     rng = np.random.RandomState(seed)
     K, N = rows, 64
