@@ -12,6 +12,10 @@ reference's algorithm in plain numpy so GPU results can be checked against it:
   qt_dequant                    mtc/core/quadtree.py:157-171                    element-grid RTN formulation
                                                                                 (baselines/gptq.py:119-138,
                                                                                 tests/test_gptq.py:28-35); pareto KATs
+  uniform_dequant               mtc/core/allocation.py:359-369 (rd_dequant)     uniform-family pareto KATs through
+                                                                                the product allocator + equality (tests)
+  uniform_to_array              mtc/kernels/gemm.py:510-538 (to_array of the    equals uniform_dequant as values; its
+                                uniform arena: integer codes x scale)           zero signs checked by hand (tests)
   permuted_qt_dequant/unpermute mtc/core/permutation.py:70-79                   explicit index loop (tests)
   element_grid / element_rtn    mtc/baselines/gptq.py:119-138                   equality with qt_dequant
   arena_pack / arena_unpack     mtc/kernels/gemm.py:457-478, 29-117,            exhaustive P2 256-combo + round trips
@@ -68,6 +72,39 @@ def qt_dequant(W: np.ndarray, sizes, leaf, modes, scales) -> np.ndarray:
                 lvl[sel] = quantize_blocks(bl[sel], m, sc) * sc[:, None, None]
         out += unblock(lvl)
     return out
+
+
+def uniform_dequant(W: np.ndarray, modes: np.ndarray, scales: np.ndarray, block_size: int) -> np.ndarray:
+    """W_hat of a uniform-block allocation: q * s written per block (so -0.0 where q = 0 and
+    s < 0), +0.0 at P0 blocks. Unlike qt_dequant nothing is summed into a +0.0 buffer."""
+    bs = int(block_size)
+    modes = np.asarray(modes)
+    sc = np.asarray(scales, np.float32)
+    bl = blocks_of(np.asarray(W, np.float32), bs)
+    out = np.zeros_like(bl)
+    for m in QRANGE:
+        sel = modes == m
+        if sel.any():
+            out[sel] = quantize_blocks(bl[sel], m, sc[sel]) * sc[sel][:, None, None]
+    return unblock(out)
+
+
+def uniform_to_array(W: np.ndarray, modes: np.ndarray, scales: np.ndarray, block_size: int) -> np.ndarray:
+    """The uniform-block MTCMatrix rebuilt from its arena: the integer code of each weight (the
+    arena holds integers, so a weight that rounds to zero from below is the code 0) times its
+    block's scale, 0 * scale at P0 blocks. Equal to uniform_dequant as values; where
+    round-half-even gives -0.0 for w / s in (-0.5, 0), rd_dequant keeps -0.0 and this gives
+    0 * s."""
+    bs = int(block_size)
+    modes = np.asarray(modes)
+    sc = np.asarray(scales, np.float32)
+    bl = blocks_of(np.asarray(W, np.float32), bs)
+    q = np.zeros(bl.shape, np.int64)
+    for m in QRANGE:
+        sel = modes == m
+        if sel.any():
+            q[sel] = quantize_blocks(bl[sel], m, sc[sel]).astype(np.int64)
+    return unblock(q.astype(np.float32) * sc[:, :, None, None])
 
 
 def unpermute(Wp: np.ndarray, pr, pc) -> np.ndarray:

@@ -1,6 +1,8 @@
 """Writes tests/golden/pareto_qt_kat.json: the reference's published (bits,
-rel_err) known answers for its quadtree allocators, copied as data from the
-reference's results/pareto.json (the QT / QT-P entries of every scenario).
+rel_err) known answers for its allocators, copied as data from the reference's
+results/pareto.json: the quadtree families (QT, QT-P) and the three uniform-block
+families (16x16 blocks: fixed width, RD without importance, RD with importance)
+of every scenario.
 
 Run in the build container, where the reference checkout is mounted:
     python tests/golden/make_pareto_kat.py /root/reference/results/pareto.json
@@ -10,7 +12,8 @@ import json
 import os
 import sys
 
-FAMILIES = ("MTC-QT quadtree 32-4 (ours)", "MTC-QT-P permuted quadtree (ours)")
+FAMILIES = ("MTC-QT quadtree 32-4 (ours)", "MTC-QT-P permuted quadtree (ours)",
+            "MTC scales, fixed width (ablation)", "MTC-RD, no importance (ablation)", "MTC-RD fixed 16x16 (v1)")
 
 
 def main(src):

@@ -1,8 +1,14 @@
-"""Known answers: the reference's published quadtree results, reproduced exactly.
+"""Known answers: the reference's published allocator results, reproduced exactly.
 
 results/pareto.json of the reference holds, for each synthetic scenario and
 each budget of RD_BUDGETS (mtc/benchmarks/benchmark_pareto.py:33), the total
-bits/element (4 decimals) and the relative output error of MTC-QT and MTC-QT-P.
+bits/element (4 decimals) and the relative output error of MTC-QT and MTC-QT-P,
+and of the three uniform 16x16-block families (benchmark_pareto.py:71-80,
+110-119): every block at one width with the importance-weighted scale search
+(rd_allocate at b + 40/256 with modes=(b,)), and the RD allocation over all
+widths without and with importance (rd_allocate(W, b, None or h, 16)). The
+uniform families pin the fp32-scale search (the default scale format of
+rd_allocate), rd_select's 64-step bisection and greedy fill, and rd_dequant.
 The scenario matrices come from seeded np.random.RandomState streams:
 - llm_like: benchmark_pareto.py:141-153 (make_llm_like) + :156-164 (weight only)
 - gaussian / uniform / outliers / multi_scale: benchmark_runner.py:21-51
@@ -22,12 +28,16 @@ import os
 import numpy as np
 import pytest
 
+from tensorpack_amd.core.allocation import META_BITS_PER_BLOCK, rd_candidates, rd_select
 from tensorpack_amd.core.permutation import PermutedQuadtreeRD
 from tensorpack_amd.core.quadtree import QuadtreeRD
+from oracle import mtc_oracle as O
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 KAT = json.load(open(os.path.join(HERE, "golden", "pareto_qt_kat.json")))["scenarios"]
 QT, QTP = "MTC-QT quadtree 32-4 (ours)", "MTC-QT-P permuted quadtree (ours)"
+FIXED, RD_FLAT, RD_IMP = ("MTC scales, fixed width (ablation)", "MTC-RD, no importance (ablation)",
+                          "MTC-RD fixed 16x16 (v1)")
 SOLVER = {QT: QuadtreeRD, QTP: PermutedQuadtreeRD}
 
 
@@ -104,3 +114,53 @@ def test_both_operand_known_answers(dist, family):
         qa, qb = sa.select(b), sb.select(b)
         got.append(((qa.bits_per_element + qb.bits_per_element) / 2.0, rel_err(C, qa.dequant.T @ qb.dequant)))
     _check(pts, got)
+
+
+def uniform_family(family, labels):
+    """The reference's uniform-block method of `family` at each label, as a function of
+    (W, h) -> (W_hat, bits/element) per label (benchmark_pareto.py:71-80, 110-119). The
+    budget-independent candidate tables are built once per (matrix, importance, widths), as
+    rd_allocate = rd_select(rd_candidates(...)) makes equivalent. Each W_hat is also checked
+    bit for bit against the oracle's uniform_dequant, which the known answers thereby pin."""
+    def keep(out, W, a):
+        assert np.array_equal(O.uniform_dequant(W, a.modes, a.scales, 16).view(np.uint32), a.dequant.view(np.uint32))
+        out.append((a.dequant, a.bits_per_element))
+
+    def run(W, h):
+        out = []
+        if family == FIXED:
+            for lab in labels:
+                b = int(lab[1:])
+                a = rd_select(rd_candidates(W, h, 16, modes=(b,)), b + META_BITS_PER_BLOCK / 256.0)
+                keep(out, W, a)
+        else:
+            c = rd_candidates(W, None if family == RD_FLAT else h, 16)
+            for lab in labels:
+                a = rd_select(c, float(lab[:-1]))
+                keep(out, W, a)
+        return out
+    return run
+
+
+@pytest.mark.parametrize("family", [FIXED, RD_FLAT, RD_IMP])
+def test_llm_like_uniform_known_answers(family):
+    W, X_cal, X_test = llm_like()
+    Y = X_test @ W
+    h = (X_cal.astype(np.float64) ** 2).mean(axis=0)
+    pts = KAT["llm_like (weight-only, calibrated)"][family]
+    res = uniform_family(family, [p["label"] for p in pts])(W, h)
+    _check(pts, [(bits, rel_err(Y, X_test @ wq)) for wq, bits in res])
+
+
+@pytest.mark.parametrize("dist", ["gaussian", "uniform", "outliers", "multi_scale"])
+@pytest.mark.parametrize("family", [FIXED, RD_FLAT, RD_IMP])
+def test_both_operand_uniform_known_answers(dist, family):
+    A = synthetic(dist, 512, 42)
+    B = synthetic(dist, 512, 43)
+    C = A @ B
+    hA = (B.astype(np.float64) ** 2).sum(axis=1)
+    hB = (A.astype(np.float64) ** 2).sum(axis=0)
+    pts = KAT[f"{dist} (A@B, both quantized)"][family]
+    run = uniform_family(family, [p["label"] for p in pts])
+    ra, rb = run(A.T, hA), run(B, hB)
+    _check(pts, [((ba + bb) / 2.0, rel_err(C, at.T @ bq)) for (at, ba), (bq, bb) in zip(ra, rb)])

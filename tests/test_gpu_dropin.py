@@ -39,8 +39,13 @@ def test_packed_kernel_matches_simulation(gpu, budget):
     Bm = MTCMatrix.from_allocation(B, b.modes, b.scales, 16)
     np.testing.assert_allclose(Am.to_array(), a.dequant, rtol=0, atol=0)
     np.testing.assert_allclose(Bm.to_array(), b.dequant, rtol=0, atol=0)
+    # the same W_hat from the oracle, bit for bit, and the product against the oracle's fp64 one
+    A_hat, B_hat = O.uniform_to_array(A, a.modes, a.scales, 16), O.uniform_to_array(B, b.modes, b.scales, 16)
+    assert np.array_equal(Am.to_array().view(np.uint32), A_hat.view(np.uint32))
+    assert np.array_equal(Bm.to_array().view(np.uint32), B_hat.view(np.uint32))
     C_sim = a.dequant @ b.dequant
     assert _rel(C_sim, mtc_gemm(Am, Bm)) < 1e-5
+    assert O.relative_frobenius_error(O.qt_gemm_f64(A_hat, B_hat), mtc_gemm(Am, Bm)) < 1e-5
     assert Am.total_bytes_allocated * 8 == a.payload_bits
     assert Bm.total_bytes_allocated * 8 == b.payload_bits
 

@@ -353,12 +353,13 @@ def test_gemm_uniform_form_fp32_scales(gpu):
     W = rng.randn(256, 128).astype(np.float32)
     al = rd_allocate(W, 4.0, None, 32)
     m = MTCMatrix.from_allocation(W, al.modes, al.scales, 32)
+    W_hat = O.uniform_to_array(W, al.modes, al.scales, 32)
     X = rng.randn(300, 256).astype(np.float32)
     Y = mtc_gemm(torch.from_numpy(X).to(gpu), m, compute="bf16").cpu().numpy()
-    assert O.relative_frobenius_error(O.qt_gemm_f64(O.bf16_round(X), al.dequant), Y) <= TOL_BF16
+    assert O.relative_frobenius_error(O.qt_gemm_f64(O.bf16_round(X), W_hat), Y) <= TOL_BF16
     I = torch.eye(256, device=gpu, dtype=torch.bfloat16)
     Yi = mtc_gemm(I, m, compute="bf16").cpu().numpy()
-    assert np.array_equal(_bits(Yi), _bits(O.bf16_round(al.dequant) + np.float32(0.0)))
+    assert np.array_equal(_bits(Yi), _bits(O.bf16_round(W_hat) + np.float32(0.0)))
 
 
 def test_gemm_bf16_output(gpu, allocs):
@@ -410,9 +411,13 @@ def test_uniform_form_packed_kernel_matches_simulation(gpu):
         a, b = rd_allocate_pair(A, B, budget)
         Am = MTCMatrix.from_allocation(A, a.modes, a.scales, 16)
         Bm = MTCMatrix.from_allocation(B, b.modes, b.scales, 16)
-        np.testing.assert_allclose(Am.to_array(), a.dequant, rtol=0, atol=0)
-        np.testing.assert_allclose(Bm.to_array(), b.dequant, rtol=0, atol=0)
-        C_sim = a.dequant.astype(np.float64) @ b.dequant.astype(np.float64)
+        A_hat = O.uniform_to_array(A, a.modes, a.scales, 16)
+        B_hat = O.uniform_to_array(B, b.modes, b.scales, 16)
+        assert np.array_equal(_bits(Am.to_array()), _bits(A_hat))
+        assert np.array_equal(_bits(Bm.to_array()), _bits(B_hat))
+        # the allocator's W_hat as values (it keeps np.round's -0.0 where the arena holds code 0)
+        assert np.array_equal(Am.to_array(), O.uniform_dequant(A, a.modes, a.scales, 16))
+        C_sim = A_hat.astype(np.float64) @ B_hat.astype(np.float64)
         assert O.relative_frobenius_error(C_sim, mtc_gemm(Am, Bm)) < 1e-5
         assert Am.total_bytes_allocated * 8 == a.payload_bits
         assert Bm.total_bytes_allocated * 8 == b.payload_bits
@@ -425,7 +430,8 @@ def test_uniform_form_dense_x(gpu, M):
     al = rd_allocate(W, 4.0, None, 32)
     m = MTCMatrix.from_allocation(W, al.modes, al.scales, 32)
     X = rng.randn(M, 256).astype(np.float32)
-    assert O.relative_frobenius_error(O.qt_gemm_f64(X, al.dequant), mtc_gemm(X, m)) <= TOL_F32
+    W_hat = O.uniform_to_array(W, al.modes, al.scales, 32)
+    assert O.relative_frobenius_error(O.qt_gemm_f64(X, W_hat), mtc_gemm(X, m)) <= TOL_F32
 
 
 def test_errors_are_clean(gpu, allocs):

@@ -134,3 +134,35 @@ def test_cpu_block_loop_gemm_matches_fp64(cpu_lib, perm):
 def test_bf16_round_ties_to_even():
     x = np.array([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -1.5, 0.0], np.float32)
     assert list(O.bf16_round(x)) == [1.0, 1.0 + 2 ** -6, -1.5, 0.0]
+
+
+def test_uniform_to_array_zero_signs_and_values():
+    """The uniform arena's rebuild (integer codes x scale, gemm.py:510-538) against rd_dequant
+    (allocation.py:359-369): equal as values; worked by hand on one 4x4 block at P2, scale 0.5:
+    w = -0.1 rounds to the code 0, so rd_dequant keeps np.round's -0.0 and the arena gives
+    0 * 0.5 = +0.0; w = 0.2 and -0.3 (codes 0 and -1) and a P0 block (scale 0) give +0.0 / -0.5."""
+    W = np.zeros((4, 8), np.float32)
+    W[0, 0], W[0, 1], W[0, 2] = -0.1, 0.2, -0.3
+    modes = np.array([[2, 0]])
+    scales = np.array([[0.5, 0.0]], np.float32)
+    dq = O.uniform_dequant(W, modes, scales, 4)
+    ta = O.uniform_to_array(W, modes, scales, 4)
+    assert np.signbit(dq[0, 0]) and not np.signbit(ta[0, 0])
+    assert ta[0, 1] == 0.0 and not np.signbit(ta[0, 1]) and ta[0, 2] == -0.5
+    assert not np.signbit(ta[:, 4:]).any() and (ta[:, 4:] == 0).all()
+    assert np.array_equal(dq, ta)
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+def test_uniform_to_array_is_the_stream_decode(layout):
+    """Both panel-stream layouts of a uniform-form matrix decode on the host to the oracle's
+    arena rebuild bit for bit (the GPU dequantizer follows the same streams)."""
+    from tensorpack_amd.core.allocation import rd_allocate
+    from tensorpack_amd.kernels.gemm import MTCMatrix
+    from tensorpack_amd.packer import decode_stream
+    rng = np.random.RandomState(7)
+    W = rng.randn(64, 96).astype(np.float32)
+    al = rd_allocate(W, 3.3, None, 16)
+    m = MTCMatrix.from_allocation(W, al.modes, al.scales, 16)
+    got = decode_stream(m.panel_stream(64, layout))
+    assert np.array_equal(got.view(np.uint32), O.uniform_to_array(W, al.modes, al.scales, 16).view(np.uint32))
