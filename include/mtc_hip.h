@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MTC_ABI_VERSION 9
+#define MTC_ABI_VERSION 10
 
 enum {
   MTC_OK = 0,
@@ -50,6 +50,8 @@ enum { MTC_DTYPE_F32 = 0, MTC_DTYPE_BF16 = 1 };
 
 /* Descriptor flags */
 #define MTC_FLAG_FP32_SCALES 0x1u   /* leaf scales come from `leaf_scale`, not the descriptor word */
+#define MTC_FLAG_MX_LAYOUT 0x2u     /* payload in the matrix-core decode layout (see below); decoded one X
+                                       row per block on v_mfma_f32_4x4x4_16b_f16 */
 
 /*
  * Panel stream. The (permuted) weight Wp is K x N (reduction x output). It is
@@ -105,6 +107,18 @@ enum { MTC_DTYPE_F32 = 0, MTC_DTYPE_BF16 = 1 };
  * at column i/8, row i%8, and chunk t of a bucket is leaf t/(S/8), row block
  * t%(S/8); for S = 4 it is leaves 2t and 2t+1 (16 codes each, column-major; an
  * odd group ends with a pad leaf). A leaf's word is shared by every cg it spans.
+ *
+ * With MTC_FLAG_MX_LAYOUT the buckets hold whole quads of chunks: a bucket of n chunks has
+ * ceil(n / 4) * 4 * P payload dwords (the last quad padded with zero codes; step records and
+ * counts name the real chunks). Quad q's 4P dwords are 4 lanes of P dwords; lane j holds
+ * column j of the quad's chunks 4q .. 4q+3 as 32 offset-binary codes: for o = 0..15, code o of
+ * the "low" string is chunk o/4, chunk row 2(o%4), column j, and code o of the "high" string
+ * is the row after it (chunk rows 0-7 are the leaf's 8 rows for S >= 8; for S = 4 rows 0-3 are
+ * the chunk's first leaf and 4-7 its second). The low string is the concatenation of the low
+ * 16-bit halves of the lane's dwords (dword d holds string bits [16d, 16d+16)), the high string
+ * that of the high halves, and code o sits at bits [o*W, o*W+W) of its string, W = P; for
+ * P = 16 the low bytes of the codes form such strings with W = 8 in dwords 0-7 and the high
+ * bytes in dwords 8-15.
  *
  * Y[:, col_perm[n]] = X[:, row_perm] * Wp[:, n]; NULL perms mean identity.
  * payload and row_perm must be 16-byte aligned.

@@ -68,13 +68,24 @@ __global__ void k_fill_zero(float* __restrict__ p, int64_t n) {
 // ---------------------------------------------------------------------------
 // dequant: one block (8 waves) per unit, wave g decodes column group g
 // ---------------------------------------------------------------------------
+template <int S, int P, int T>
+__device__ __forceinline__ void mx_codes_t(const uint32_t* q, float (&out)[32]);
 template <int S, int P>
-__device__ __forceinline__ void dequant_chunk(const mtc_stream_desc& d, const uint32_t* src, const uint32_t* lw,
-                                              uint32_t lg0, uint32_t t, int kb, int col0, float* __restrict__ W) {
-  uint32_t w[P];
-  load_chunk<P, true>(src, w);
+__device__ __forceinline__ void mx_codes(const uint32_t* q, uint32_t t, float (&out)[32]);
+
+// Chunk t of a bucket into W_hat; src: the chunk's dwords (v1 layout) or its quad's (mx).
+template <int S, int P>
+__device__ __forceinline__ void dequant_chunk(const mtc_stream_desc& d, const uint32_t* src, bool mx,
+                                              const uint32_t* lw, uint32_t lg0, uint32_t t, int kb, int col0,
+                                              float* __restrict__ W) {
   float q[32];
-  decode_chunk<P>(w, q);
+  if (mx) {
+    mx_codes<S, P>(src, t & 3u, q);
+  } else {
+    uint32_t w[P];
+    load_chunk<P, true>(src, w);
+    decode_chunk<P>(w, q);
+  }
   constexpr int R = (S == 4) ? 4 : 8;
 #pragma unroll
   for (int h = 0; h < (S == 4 ? 2 : 1); ++h) {
@@ -117,6 +128,7 @@ __global__ __launch_bounds__(512) void k_dequant(const mtc_stream_desc d, float*
   const int nb = hdr[9 + g] - hdr[8 + g];
   const uint32_t* pay = d.payload + hdr[0];
   const int col0 = panel * kPanel + g * kGroup;
+  const bool mx = (d.flags & MTC_FLAG_MX_LAYOUT) != 0;
   for (int b = 0; b < nb; ++b) {
     const Bucket e = read_bucket(bk + 4 * b);
     const uint32_t* lw = d.leaf_word + hdr[2] + e.leaf;
@@ -124,7 +136,9 @@ __global__ __launch_bounds__(512) void k_dequant(const mtc_stream_desc d, float*
     for (uint32_t t = lane; t < e.n; t += 64) {
       switch (e.key) {
 #define MTC_CASE(S, P) \
-  case MTC_BUCKET_KEY(S, P): dequant_chunk<S, P>(d, pay + e.pay + t * P, lw, lg0, t, kb, col0, W); break;
+  case MTC_BUCKET_KEY(S, P): \
+    dequant_chunk<S, P>(d, mx ? pay + e.pay + (t / 4) * 4 * P : pay + e.pay + t * P, mx, lw, lg0, t, kb, col0, W); \
+    break;
         MTC_FOR_EACH_BUCKET(MTC_CASE)
 #undef MTC_CASE
         default: break;
@@ -200,12 +214,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, in
 constexpr uint32_t kOutOfRange = 0xFFFFFF00u;        // byte offset past any buffer's end
 constexpr int64_t kMaxArrayBytes = 0x7FFFFFFF;       // largest stream array a buffer resource covers
 
-template <bool FS>
-__device__ __forceinline__ void gemv_load(__amdgpu_buffer_rsrc_t pay_r, __amdgpu_buffer_rsrc_t lw_r,
-                                          __amdgpu_buffer_rsrc_t fs_r, uint32_t key, uint32_t pay, uint32_t leaf,
-                                          uint32_t t, u32x16_t& w, uint32_t& ob, uint32_t& lw0, uint32_t& lw1,
-                                          float& fs0, float& fs1) {
-  const uint32_t P = key >> 8, ls = key & 0xFFu;
+// The payload part of a step's loads: P dwords at dword pay + t * P (two load instructions for
+// every width; the tail of a P = 16 chunk comes from gemv_load_p16_tail).
+__device__ __forceinline__ void gemv_load_payload(__amdgpu_buffer_rsrc_t pay_r, uint32_t P, uint32_t pay, uint32_t t,
+                                                  u32x16_t& w, uint32_t& ob) {
   ob = (pay + t * P) << 2;                           // payload byte offset of the chunk
   if (P <= 4) {
     if (P == 2) {
@@ -232,6 +244,15 @@ __device__ __forceinline__ void gemv_load(__amdgpu_buffer_rsrc_t pay_r, __amdgpu
       w[4] = e.x; w[5] = e.y; w[6] = e.z; w[7] = e.w;
     }
   }
+}
+
+template <bool FS>
+__device__ __forceinline__ void gemv_load(__amdgpu_buffer_rsrc_t pay_r, __amdgpu_buffer_rsrc_t lw_r,
+                                          __amdgpu_buffer_rsrc_t fs_r, uint32_t key, uint32_t pay, uint32_t leaf,
+                                          uint32_t t, u32x16_t& w, uint32_t& ob, uint32_t& lw0, uint32_t& lw1,
+                                          float& fs0, float& fs1) {
+  const uint32_t P = key >> 8, ls = key & 0xFFu;
+  gemv_load_payload(pay_r, P, pay, t, w, ob);
   const uint32_t l0 = leaf + (ls == 2 ? 2 * t : t >> (ls - 3));
   const uint32_t b1 = ls == 2 ? (l0 + 1) << 2 : kOutOfRange;   // second 4x4 leaf, if any
   lw0 = __builtin_amdgcn_raw_buffer_load_b32(lw_r, l0 << 2, 0, 0);
@@ -378,14 +399,16 @@ struct GemvShape {
   int kc;        // rows the X staging covers (kSmallRows or kMaxChunkRows)
   bool lg_code;  // the kernel has the LDS-gather code
   bool lg;       // this matrix gathers X in LDS
+  bool mx;       // the stream has the mx payload layout (one X row per block, matrix core)
 };
+inline bool is_mx(const mtc_stream_desc* d) { return (d->flags & MTC_FLAG_MX_LAYOUT) != 0; }
 inline GemvShape gemv_shape(int MT, const mtc_stream_desc* d) {
-  const bool perm = d->row_perm != nullptr;
-  if (MT > 4) return {16, kMaxChunkRows, false, false};   // matrix core
-  if (MT > 2) return {8, kMaxChunkRows, false, false};
-  if (d->chunk_rows <= kSmallRows) return {4, kSmallRows, true, perm && d->K <= kSmallRows};
-  if (d->fixed_steps > kFewSteps) return {16, kMaxChunkRows, true, perm && d->K <= kMaxChunkRows};
-  return {4, kMaxChunkRows, false, false};
+  const bool perm = d->row_perm != nullptr, mx = is_mx(d);
+  if (MT > 4) return {16, kMaxChunkRows, false, false, false};   // matrix core
+  if (MT > 2) return {8, kMaxChunkRows, false, false, false};
+  if (d->chunk_rows <= kSmallRows) return {4, kSmallRows, true, perm && d->K <= kSmallRows, mx};
+  if (d->fixed_steps > kFewSteps) return {16, kMaxChunkRows, true, perm && d->K <= kMaxChunkRows, mx};
+  return {4, kMaxChunkRows, false, false, mx};
 }
 __host__ __device__ constexpr int gemv_prefetch(int NW) { return NW == 4 ? 2 : 3; }
 constexpr int kMaxFixedSteps = 48;          // step records per block at block-computable positions
@@ -1136,14 +1159,20 @@ __device__ __forceinline__ void gemv_block_mfma(const mtc_stream_desc& d, const 
   gemv_store<MT, W, BPU>(d, red, u, 0, Y, ldy, M, part, counters);
 }
 
-// The block code of an M tile: the matrix core for tiles of 8 or 16 rows (X staged transposed
-// in xt, or gathered by the block from X when xt is null), else the vector path.
-template <int MT, bool FS, bool LG, int NW, int KC>
+#include "mtc_gemv_mx.h"
+
+// The block code of an M tile: over an mx stream (MX) one X row on the matrix core with
+// f16 operands; else the matrix core for tiles of 8 or 16 rows (X staged transposed in xt, or
+// gathered by the block from X when xt is null), else the vector path.
+template <int MT, bool FS, bool LG, int NW, int KC, bool MX = false>
 __device__ __forceinline__ void gemv_any(const mtc_stream_desc& d, const int bid, const float* __restrict__ X,
                                          int64_t ldx, float* __restrict__ Y, int64_t ldy, int M,
                                          float* __restrict__ part, uint32_t* __restrict__ counters, const bool lg,
                                          const float* __restrict__ xt) {
-  if constexpr (MT >= 8) {
+  if constexpr (MX) {
+    static_assert(MT == 1, "the mx layout decodes one X row per block");
+    gemv_block_mx<FS, LG, NW, KC>(d, bid, X, ldx, Y, ldy, M, part, counters, lg);
+  } else if constexpr (MT >= 8) {
     static_assert(NW == kMfmaWaves, "matrix-core decode blocks have 16 waves");
     gemv_block_mfma<MT, FS>(d, bid, X, ldx, Y, ldy, M, part, counters, xt);
   } else {
@@ -1152,13 +1181,17 @@ __device__ __forceinline__ void gemv_any(const mtc_stream_desc& d, const int bid
 }
 
 // At least 4 waves per SIMD: a 16-wave block fills a CU's 4 SIMDs; two 8-wave blocks
-// (M tiles of 4 rows) share one only if each wave keeps to 128 VGPRs.
-template <int MT, bool FS, bool LG, int NW, int KC>
-__global__ __launch_bounds__(64 * NW, 4) void k_gemv(const mtc_stream_desc d, const float* __restrict__ X,
+// (M tiles of 4 rows) share one only if each wave keeps to 128 VGPRs. 4-wave blocks over mx
+// streams ask for 7 per CU, as the vector path's 4-wave blocks reach: a decode block's time is
+// mostly memory latency, so the blocks in flight set the throughput.
+__host__ __device__ constexpr int gemv_min_blocks(int NW, bool MX) { return MX && NW == 4 ? 7 : 4; }
+
+template <int MT, bool FS, bool LG, int NW, int KC, bool MX>
+__global__ __launch_bounds__(64 * NW, gemv_min_blocks(NW, MX)) void k_gemv(const mtc_stream_desc d, const float* __restrict__ X,
                                                   int64_t ldx, float* __restrict__ Y, int64_t ldy, int M,
                                                   float* __restrict__ part, uint32_t* __restrict__ counters,
                                                   const float* __restrict__ xt) {
-  gemv_any<MT, FS, LG, NW, KC>(d, blockIdx.x, X, ldx, Y, ldy, M, part, counters, true, xt);
+  gemv_any<MT, FS, LG, NW, KC, MX>(d, blockIdx.x, X, ldx, Y, ldy, M, part, counters, true, xt);
 }
 
 // Up to kMaxGroup single-chunk matrices of one block shape that read the same X, in one launch:
@@ -1172,14 +1205,14 @@ struct GemvGroup {
   int start[kMaxGroup + 1];
 };
 
-template <int MT, bool FS, bool LG, int NW, int KC>
-__global__ __launch_bounds__(64 * NW, 4) void k_gemv_group(const GemvGroup g, const float* __restrict__ X,
+template <int MT, bool FS, bool LG, int NW, int KC, bool MX>
+__global__ __launch_bounds__(64 * NW, gemv_min_blocks(NW, MX)) void k_gemv_group(const GemvGroup g, const float* __restrict__ X,
                                                         int64_t ldx, int M) {
   int i = 0;
 #pragma unroll
   for (int k = 1; k < kMaxGroup; ++k) i += (int)blockIdx.x >= g.start[k];
-  gemv_any<MT, FS, LG, NW, KC>(g.d[i], (int)blockIdx.x - g.start[i], X, ldx, g.Y[i], g.ldy[i], M, nullptr,
-                               nullptr, true, nullptr);
+  gemv_any<MT, FS, LG, NW, KC, MX>(g.d[i], (int)blockIdx.x - g.start[i], X, ldx, g.Y[i], g.ldy[i], M, nullptr,
+                                   nullptr, true, nullptr);
 }
 
 // Any number of matrices, each with its own X and Y. The plan (built on the host by
@@ -1205,9 +1238,13 @@ struct BatchItem {
 // Shape classes of a batch, in the order of their blocks in the plan's block table:
 // 0: 4 waves, X staging of kSmallRows rows (LDS gather per member); 1: 4 waves, kMaxChunkRows
 // rows, no gather; 2: 16 waves, kMaxChunkRows rows (gather per member); 3: 8 waves (M tiles of
-// 4 rows), no gather.
-constexpr int kShapeClasses = 4;
-inline int shape_class(const GemvShape& s) { return s.nw == 8 ? 3 : s.nw == 16 ? 2 : s.kc == kSmallRows ? 0 : 1; }
+// 4 rows), no gather; 4, 5, 6: classes 0, 1, 2 over mx streams.
+constexpr int kShapeClasses = 7;
+inline int shape_class(const GemvShape& s) {
+  const int c = s.nw == 8 ? 3 : s.nw == 16 ? 2 : s.kc == kSmallRows ? 0 : 1;
+  return s.mx ? 4 + c : c;
+}
+inline int class_waves(int cls) { return cls == 3 ? 8 : (cls == 2 || cls == 6) ? 16 : 4; }
 
 struct BatchHeader {
   uint32_t magic;
@@ -1228,13 +1265,13 @@ struct BatchHeader {
 };
 constexpr uint32_t kBatchMagic = 0x4D544342u;   // "BCTM"
 
-template <int MT, bool FS, bool LG, int NW, int KC>
-__global__ __launch_bounds__(64 * NW, 4) void k_gemv_batch(const BatchItem* __restrict__ items,
+template <int MT, bool FS, bool LG, int NW, int KC, bool MX>
+__global__ __launch_bounds__(64 * NW, gemv_min_blocks(NW, MX)) void k_gemv_batch(const BatchItem* __restrict__ items,
                                                         const uint32_t* __restrict__ block_item, int M) {
   const int b = blockIdx.x;
   const BatchItem& it = items[block_item[b]];
-  gemv_any<MT, FS, LG, NW, KC>(it.d, b - it.start, it.X, it.ldx, it.Y, it.ldy, M, it.part, it.counters,
-                               it.lg != 0, it.xt);
+  gemv_any<MT, FS, LG, NW, KC, MX>(it.d, b - it.start, it.X, it.ldx, it.Y, it.ldy, M, it.part, it.counters,
+                                   it.lg != 0, it.xt);
 }
 
 // X of every member staged for the matrix core (grid z: the member).
@@ -1247,17 +1284,22 @@ __global__ __launch_bounds__(kStageThreads) void k_gemv_stage_x_batch(const Batc
 // The batch kernel of a shape class (the LDS gather is a per-member flag there).
 template <int MT>
 const void* gemv_batch_kernel(bool fs, int cls) {
-#define MTC_BATCH_K(LG_, NW_, KC_) \
-  (fs ? reinterpret_cast<const void*>(&k_gemv_batch<MT, true, LG_, NW_, KC_>) \
-      : reinterpret_cast<const void*>(&k_gemv_batch<MT, false, LG_, NW_, KC_>))
+#define MTC_BATCH_K(LG_, NW_, KC_, MX_) \
+  (fs ? reinterpret_cast<const void*>(&k_gemv_batch<MT, true, LG_, NW_, KC_, MX_>) \
+      : reinterpret_cast<const void*>(&k_gemv_batch<MT, false, LG_, NW_, KC_, MX_>))
   if constexpr (MT > 4) {
-    return MTC_BATCH_K(false, 16, kMaxChunkRows);
+    return MTC_BATCH_K(false, 16, kMaxChunkRows, false);
   } else if constexpr (MT > 2) {
-    return MTC_BATCH_K(false, 8, kMaxChunkRows);
+    return MTC_BATCH_K(false, 8, kMaxChunkRows, false);
   } else {
-    if (cls == 0) return MTC_BATCH_K(true, 4, kSmallRows);
-    if (cls == 1) return MTC_BATCH_K(false, 4, kMaxChunkRows);
-    return MTC_BATCH_K(true, 16, kMaxChunkRows);
+    if constexpr (MT == 1) {
+      if (cls == 4) return MTC_BATCH_K(true, 4, kSmallRows, true);
+      if (cls == 5) return MTC_BATCH_K(false, 4, kMaxChunkRows, true);
+      if (cls == 6) return MTC_BATCH_K(true, 16, kMaxChunkRows, true);
+    }
+    if (cls == 0) return MTC_BATCH_K(true, 4, kSmallRows, false);
+    if (cls == 1) return MTC_BATCH_K(false, 4, kMaxChunkRows, false);
+    return MTC_BATCH_K(true, 16, kMaxChunkRows, false);
   }
 #undef MTC_BATCH_K
 }
@@ -1265,19 +1307,26 @@ const void* gemv_batch_kernel(bool fs, int cls) {
 // The single-matrix (Group = false) or group kernel of an M tile, scale format and block shape.
 template <int MT, bool Group>
 const void* gemv_kernel(bool fs, const GemvShape& s) {
-#define MTC_GEMV_K(LG_, NW_, KC_) \
-  (Group ? (fs ? reinterpret_cast<const void*>(&k_gemv_group<MT, true, LG_, NW_, KC_>) \
-               : reinterpret_cast<const void*>(&k_gemv_group<MT, false, LG_, NW_, KC_>)) \
-         : (fs ? reinterpret_cast<const void*>(&k_gemv<MT, true, LG_, NW_, KC_>) \
-               : reinterpret_cast<const void*>(&k_gemv<MT, false, LG_, NW_, KC_>)))
+#define MTC_GEMV_K(LG_, NW_, KC_, MX_) \
+  (Group ? (fs ? reinterpret_cast<const void*>(&k_gemv_group<MT, true, LG_, NW_, KC_, MX_>) \
+               : reinterpret_cast<const void*>(&k_gemv_group<MT, false, LG_, NW_, KC_, MX_>)) \
+         : (fs ? reinterpret_cast<const void*>(&k_gemv<MT, true, LG_, NW_, KC_, MX_>) \
+               : reinterpret_cast<const void*>(&k_gemv<MT, false, LG_, NW_, KC_, MX_>)))
   if constexpr (MT > 4) {
-    return MTC_GEMV_K(false, 16, kMaxChunkRows);
+    return MTC_GEMV_K(false, 16, kMaxChunkRows, false);
   } else if constexpr (MT > 2) {
-    return MTC_GEMV_K(false, 8, kMaxChunkRows);
+    return MTC_GEMV_K(false, 8, kMaxChunkRows, false);
   } else {
-    if (s.nw == 16) return s.lg ? MTC_GEMV_K(true, 16, kMaxChunkRows) : MTC_GEMV_K(false, 16, kMaxChunkRows);
-    if (s.kc == kSmallRows) return s.lg ? MTC_GEMV_K(true, 4, kSmallRows) : MTC_GEMV_K(false, 4, kSmallRows);
-    return MTC_GEMV_K(false, 4, kMaxChunkRows);
+    if constexpr (MT == 1) {
+      if (s.mx) {
+        if (s.nw == 16) return s.lg ? MTC_GEMV_K(true, 16, kMaxChunkRows, true) : MTC_GEMV_K(false, 16, kMaxChunkRows, true);
+        if (s.kc == kSmallRows) return s.lg ? MTC_GEMV_K(true, 4, kSmallRows, true) : MTC_GEMV_K(false, 4, kSmallRows, true);
+        return MTC_GEMV_K(false, 4, kMaxChunkRows, true);
+      }
+    }
+    if (s.nw == 16) return s.lg ? MTC_GEMV_K(true, 16, kMaxChunkRows, false) : MTC_GEMV_K(false, 16, kMaxChunkRows, false);
+    if (s.kc == kSmallRows) return s.lg ? MTC_GEMV_K(true, 4, kSmallRows, false) : MTC_GEMV_K(false, 4, kSmallRows, false);
+    return MTC_GEMV_K(false, 4, kMaxChunkRows, false);
   }
 #undef MTC_GEMV_K
 }
@@ -1301,6 +1350,8 @@ int check_desc(const mtc_stream_desc* d) {
     return fail(MTC_E_DESC, "max_unit_words=%d max_unit_words4=%d", d->max_unit_words, d->max_unit_words4);
   if (d->n_buckets > 0 && (!d->buckets || !d->payload || !d->leaf_word))
     return fail(MTC_E_NULL, "stream arrays missing for %d buckets", d->n_buckets);
+  if (d->flags & ~(MTC_FLAG_FP32_SCALES | MTC_FLAG_MX_LAYOUT))
+    return fail(MTC_E_DESC, "unknown descriptor flags 0x%x", d->flags);
   if ((d->flags & MTC_FLAG_FP32_SCALES) && !d->leaf_scale && d->n_leaves > 0)
     return fail(MTC_E_NULL, "fp32-scale stream without leaf_scale");
   if (!(d->flags & MTC_FLAG_FP32_SCALES) && d->leaf_scale)
@@ -1334,6 +1385,8 @@ constexpr int kMfmaTile16Rows = 2048;
 int gemv_mt(int M, int chunk_rows) {
   return M <= 2 ? M : M <= 4 ? 4 : (M <= 8 || chunk_rows > kMfmaTile16Rows) ? 8 : 16;
 }
+// Rows per M tile for a stream: one for the mx layout (its blocks decode one X row), else gemv_mt.
+int gemv_mt_of(const mtc_stream_desc* d, int M) { return is_mx(d) ? 1 : gemv_mt(M, d->chunk_rows); }
 
 // Workspace of a decode call: split-K counters (counters_bytes, from offset 0) and partials when
 // K is split over row chunks, then, for matrix-core M tiles, X staged per M tile (from xt_off).
@@ -1379,6 +1432,8 @@ size_t gemv_lds_bytes(int K, int chunk_rows, bool perm, int MT) {
           (size_t)gemv_waves(MT) * kStepGroups * MT * kGroup + raw) * 4;
 }
 size_t gemv_lds_bytes(const mtc_stream_desc* d, int MT) {
+  if (is_mx(d))
+    return gemv_mx_lds_bytes(d->chunk_rows, gemv_waves(1), gemv_lds_gather(1, d->row_perm != nullptr, d->K), d->K);
   return gemv_lds_bytes(d->K, d->chunk_rows, d->row_perm != nullptr, MT);
 }
 
@@ -1454,11 +1509,15 @@ int build_batch_plan(const mtc_gemv_batch_item* items, int n, int M, void* works
   int max_rows = 0;
   for (int i = 0; i < n; ++i)
     if (items[i].desc) max_rows = std::max(max_rows, items[i].desc->chunk_rows);
-  const int mt = gemv_mt(M, max_rows);
+  const bool mx = items[0].desc && is_mx(items[0].desc);
+  for (int i = 1; i < n; ++i)
+    if (items[i].desc && is_mx(items[i].desc) != mx)
+      return fail(MTC_E_SHAPE, "batch item %d differs from item 0 in payload layout (MTC_FLAG_MX_LAYOUT)", i);
+  const int mt = mx ? 1 : gemv_mt(M, max_rows);
   if (mt > 4 && n > 65535) return fail(MTC_E_SHAPE, "batch of %d matrices at M=%d (at most 65535 above M=4)", n, M);
   bool fs = false;
   size_t ws = 0, lds = 0;
-  int64_t blocks = 0, class_blocks[kShapeClasses] = {0, 0, 0, 0};
+  int64_t blocks = 0, class_blocks[kShapeClasses] = {};
   for (int i = 0; i < n; ++i) {
     const mtc_stream_desc* d = items[i].desc;
     int rc = check_desc(d);
@@ -1515,8 +1574,8 @@ int build_batch_plan(const mtc_gemv_batch_item* items, int n, int M, void* works
   h->workspace = workspace;
   char* wsp = reinterpret_cast<char*>(workspace);
   unsigned stage_bx = 0;
-  int start[kShapeClasses] = {0, 0, 0, 0};            // next block of each shape's launch
-  int64_t table_off[kShapeClasses] = {0, 0, 0, 0};    // first table entry of each shape's launch
+  int start[kShapeClasses] = {};                      // next block of each shape's launch
+  int64_t table_off[kShapeClasses] = {};              // first table entry of each shape's launch
   for (int c = 1; c < kShapeClasses; ++c) table_off[c] = table_off[c - 1] + class_blocks[c - 1];
   for (int i = 0; i < n; ++i) {
     const mtc_stream_desc* d = items[i].desc;
@@ -1573,7 +1632,7 @@ int launch_gemv_batch(const void* host_plan, const void* device_plan, hipStream_
     const uint32_t* table = block_item + first;
     first += nblk;
     if (nblk == 0) continue;
-    const int nw = cls == 3 ? 8 : cls == 2 ? 16 : 4;
+    const int nw = class_waves(cls);
     const void* kern = h->mt == 1   ? gemv_batch_kernel<1>(h->fs, cls)
                      : h->mt == 2   ? gemv_batch_kernel<2>(h->fs, cls)
                      : h->mt == 4   ? gemv_batch_kernel<4>(h->fs, cls)
@@ -1628,12 +1687,14 @@ MTC_API int mtc_dequant(const mtc_stream_desc* d, float* W_out, void* hip_stream
 
 MTC_API size_t mtc_gemv_lds_bytes(int K, int chunk_rows, int has_row_perm, int M) {
   if (K <= 0 || chunk_rows <= 0 || M <= 0) return 0;
-  return gemv_lds_bytes(K, chunk_rows, has_row_perm != 0, gemv_mt(M, chunk_rows));
+  const size_t v1 = gemv_lds_bytes(K, chunk_rows, has_row_perm != 0, gemv_mt(M, chunk_rows));
+  const size_t mx = gemv_mx_lds_bytes(chunk_rows, gemv_waves(1), gemv_lds_gather(1, has_row_perm != 0, K), K);
+  return std::max(v1, mx);
 }
 
 MTC_API size_t mtc_gemv_workspace_bytes(const mtc_stream_desc* d, int M) {
   if (check_desc(d) || M <= 0) return 0;
-  return gemv_ws_layout(d, M, gemv_mt(M, d->chunk_rows), nullptr);
+  return gemv_ws_layout(d, M, gemv_mt_of(d, M), nullptr);
 }
 
 MTC_API int mtc_gemv_f32(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y, int64_t ldy, int M,
@@ -1644,7 +1705,7 @@ MTC_API int mtc_gemv_f32(const mtc_stream_desc* d, const float* X, int64_t ldx, 
   if (M <= 0) return fail(MTC_E_SHAPE, "M=%d must be positive", M);
   if (ldx < d->K || ldy < d->N) return fail(MTC_E_SHAPE, "ldx=%lld < K or ldy=%lld < N", (long long)ldx, (long long)ldy);
   if ((M - 1) > (INT64_MAX / ldx)) return fail(MTC_E_SHAPE, "M * ldx overflows");
-  const int mt = gemv_mt(M, d->chunk_rows);
+  const int mt = gemv_mt_of(d, M);
   const size_t need = gemv_ws_layout(d, M, mt, nullptr);
   if (need && (!workspace || workspace_bytes < need))
     return fail(MTC_E_WORKSPACE, "GEMV workspace of %zu bytes needed, %zu given", need, workspace ? workspace_bytes : 0);
@@ -1702,7 +1763,7 @@ MTC_API int mtc_gemv_f32_noalloc(const mtc_stream_desc* d, const float* X, int64
   if (ldx < d->K || ldy < d->N) return fail(MTC_E_SHAPE, "ldx=%lld < K or ldy=%lld < N", (long long)ldx, (long long)ldy);
   if ((M - 1) > (INT64_MAX / ldx)) return fail(MTC_E_SHAPE, "M * ldx overflows");
   size_t counter_bytes = 0;
-  const int mt = gemv_mt(M, d->chunk_rows);
+  const int mt = gemv_mt_of(d, M);
   const size_t need = gemv_ws_layout(d, M, mt, &counter_bytes);
   if (need > kScratchBytes)
     return fail(MTC_E_WORKSPACE, "M=%d over %d row chunks needs %zu bytes of split-K scratch; the static scratch "
@@ -1743,8 +1804,9 @@ MTC_API int mtc_gemv_f32_group(const mtc_stream_desc* const* descs, int n, const
       return fail(MTC_E_SHAPE, "group member %d has %d row chunks; groups take single-chunk streams", i, d->n_chunks);
     if (d->K != descs[0]->K) return fail(MTC_E_SHAPE, "group member %d has K=%d, member 0 K=%d", i, d->K, descs[0]->K);
     if ((d->leaf_scale != nullptr) != (descs[0]->leaf_scale != nullptr) ||
-        (d->row_perm != nullptr) != (descs[0]->row_perm != nullptr))
-      return fail(MTC_E_SHAPE, "group member %d differs from member 0 in scale format or row permutation", i);
+        (d->row_perm != nullptr) != (descs[0]->row_perm != nullptr) || is_mx(d) != is_mx(descs[0]))
+      return fail(MTC_E_SHAPE, "group member %d differs from member 0 in scale format, row permutation or "
+                  "payload layout", i);
     if (ldx < d->K || ldy[i] < d->N)
       return fail(MTC_E_SHAPE, "ldx=%lld < K or ldy[%d]=%lld < N", (long long)ldx, i, (long long)ldy[i]);
   }
@@ -1752,7 +1814,7 @@ MTC_API int mtc_gemv_f32_group(const mtc_stream_desc* const* descs, int n, const
   hipStream_t st = as_stream(hip_stream);
   int max_rows = 0;
   for (int i = 0; i < n; ++i) max_rows = std::max(max_rows, descs[i]->chunk_rows);
-  const int mt = gemv_mt(M, max_rows);
+  const int mt = is_mx(descs[0]) ? 1 : gemv_mt(M, max_rows);
   // one launch per block shape among the members (usually one), so that every member's blocks
   // run the code of its own launch
   for (int cls = 0; cls < kShapeClasses; ++cls) {

@@ -11,7 +11,7 @@ from typing import Dict, Optional, Tuple
 import numpy as np
 
 from . import _abi, _native
-from .packer import PanelStream
+from .packer import LAYOUT_MX, PanelStream
 from .tilestream import TileStream
 
 
@@ -69,7 +69,8 @@ class DeviceStream:
 
         d = _abi.MtcStreamDesc()
         d.abi_version = _abi.ABI_VERSION
-        d.flags = _abi.MTC_FLAG_FP32_SCALES if ps.leaf_scale is not None else 0
+        d.flags = (_abi.MTC_FLAG_FP32_SCALES if ps.leaf_scale is not None else 0) | \
+            (_abi.MTC_FLAG_MX_LAYOUT if ps.layout == LAYOUT_MX else 0)
         d.K, d.N, d.chunk_rows = ps.K, ps.N, ps.chunk_rows
         d.n_panels, d.n_chunks = ps.n_panels, ps.n_chunks
         d.n_buckets = ps.n_buckets

@@ -29,7 +29,7 @@ from ..core.precision import (_BlockErrors, block_codes, block_scale, negotiate_
                               select_independent_precision)
 from ..core.quadtree import QTAllocation
 from ..core.types import PrecisionMode
-from ..packer import PanelStream, check_permutation, pack_levels, weight_codes
+from ..packer import LAYOUT_MX, LAYOUT_V1, PanelStream, check_permutation, pack_levels, weight_codes
 from ..tilestream import TileStream, pack_tiles
 
 DECODE_MAX_M = 16             # M at or below this takes the fp32 decode kernel under compute="auto"
@@ -495,35 +495,51 @@ class MTCMatrix:
         leaf = {Bs: np.ones(self.precisions.shape, dtype=bool)}
         return _Levels(self.shape, (Bs,), leaf, {Bs: self.precisions}, {Bs: self.scales}, codes_of, "fp32")
 
-    def panel_stream(self, chunk_rows: int) -> PanelStream:
-        ps = self._host.get(chunk_rows)
+    def panel_stream(self, chunk_rows: int, layout: int = LAYOUT_V1) -> PanelStream:
+        """Host image of the decode layout cut into `chunk_rows`-row units, with the payload in
+        `layout` (LAYOUT_V1: every decode kernel; LAYOUT_MX: the matrix-core decode of one X row)."""
+        key = (int(chunk_rows), int(layout))
+        ps = self._host.get(key)
         if ps is None:
             lv = self._levels if self._levels is not None else self._uniform_levels()
             ps = pack_levels(lv.shape, lv.sizes, lv.leaf, lv.modes, lv.scales, lv.codes_of, chunk_rows,
-                             lv.scale_format, lv.row_perm, lv.col_perm)
-            self._host[chunk_rows] = ps
+                             lv.scale_format, lv.row_perm, lv.col_perm, layout=layout)
+            self._host[key] = ps
         return ps
+
+    @staticmethod
+    def decode_layout(M: int = 1) -> int:
+        """Payload layout of the decode stream for M rows of X: the chunk-contiguous layout
+        (vector decode for M <= 4, 4x4x1 matrix core above). The matrix-core layout for one row
+        (LAYOUT_MX: every multiply-accumulate on the matrix core, the vector units only decode)
+        is available through device_stream(layout=LAYOUT_MX); measured slower at every benchmark
+        shape, whose decode blocks are bound by memory latency rather than by vector issue."""
+        return LAYOUT_V1
 
     def decode_chunk_rows(self, M: int = 1) -> int:
         """Rows per unit of the decode layout for M rows: gemv_chunk_rows, halved
         until the largest unit's on-chip staging fits the LDS budget (host only)."""
         chunk_rows = gemv_chunk_rows(self.shape[0], self.shape[1], M)
         while chunk_rows > 32 and _decode_lds_need(self.panel_stream(chunk_rows), M) > DECODE_LDS_BYTES:
-            self._host.pop(chunk_rows, None)
+            self._host.pop((chunk_rows, LAYOUT_V1), None)
             chunk_rows = max(32, (chunk_rows // 2) // 32 * 32)
         return chunk_rows
 
-    def device_stream(self, chunk_rows: Optional[int] = None, device=None, M: int = 1):
+    def device_stream(self, chunk_rows: Optional[int] = None, device=None, M: int = 1,
+                      layout: Optional[int] = None):
         """Device copy of the stream cut into `chunk_rows`-row units (default: the
-        decode layout for M rows, shrunk until one unit fits on chip)."""
+        decode layout for M rows, shrunk until one unit fits on chip), payload in `layout`
+        (default: decode_layout(M)). Any stream serves any M; the defaults are the fast ones."""
         from ..device import DeviceStream, require_gpu
         dev = require_gpu(device)
         if chunk_rows is None:
             chunk_rows = self.decode_chunk_rows(M)
-        key = (str(dev), int(chunk_rows))
+        if layout is None:
+            layout = self.decode_layout(M)
+        key = (str(dev), int(chunk_rows), int(layout))
         ds = self._dev.get(key)
         if ds is None:
-            ds = DeviceStream(self.panel_stream(int(chunk_rows)), dev)
+            ds = DeviceStream(self.panel_stream(int(chunk_rows), int(layout)), dev)
             self._dev[key] = ds
         return ds
 

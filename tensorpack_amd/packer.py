@@ -35,7 +35,7 @@ LEAF_PAD = 1 << 13
 ROW_BITS = 10                          # leaf word: row/4 in bits 0-9
 MAX_CHUNK_ROWS = 4 << ROW_BITS         # 4096
 UNIT_HDR_WORDS = 32
-STREAM_FORMAT = 9                      # panel stream layout version (matches the C-ABI version)
+STREAM_FORMAT = 10                     # panel stream layout version (matches the C-ABI version)
 PAYLOAD_PAD = 4                        # dwords after the last bucket
 STEP_GROUPS = 4                        # column groups one decode step covers
 STEP_LANES = 16                        # lanes (chunks) per column group in a step
@@ -79,6 +79,7 @@ class PanelStream:
     max_unit_words: int = 0             # decode block of 2 column groups, max staged dwords
     max_unit_words4: int = 0            # decode block of 4 column groups
     stats: Dict[str, float] = field(default_factory=dict)
+    layout: int = 0                     # LAYOUT_V1 or LAYOUT_MX (payload order; see mx_pack)
 
     @property
     def n_panels(self) -> int:
@@ -114,7 +115,7 @@ class PanelStream:
     def save(self, path) -> None:
         arrays = {k: getattr(self, k) for k in self._ARRAYS if getattr(self, k) is not None}
         meta = np.array([STREAM_FORMAT, self.K, self.N, self.chunk_rows, self.n_real_leaves,
-                         self.max_unit_words, self.max_unit_words4, self.fixed_steps], dtype=np.int64)
+                         self.max_unit_words, self.max_unit_words4, self.fixed_steps, self.layout], dtype=np.int64)
         np.savez(path, meta=meta, stats_keys=np.array(sorted(self.stats), dtype=str),
                  stats_vals=np.array([self.stats[k] for k in sorted(self.stats)], dtype=np.float64), **arrays)
 
@@ -131,7 +132,8 @@ class PanelStream:
             ps = cls(K=meta[1], N=meta[2], chunk_rows=meta[3], payload=get("payload"), buckets=get("buckets"),
                      unit_hdr=get("unit_hdr"), leaf_word=get("leaf_word"), leaf_scale=get("leaf_scale"),
                      steps=get("steps"), row_perm=get("row_perm"), col_perm=get("col_perm"), n_real_leaves=meta[4],
-                     max_unit_words=meta[5], max_unit_words4=meta[6], fixed_steps=meta[7], stats=stats)
+                     max_unit_words=meta[5], max_unit_words4=meta[6], fixed_steps=meta[7], stats=stats,
+                     layout=meta[8])
         ps.validate()
         return ps
 
@@ -148,6 +150,9 @@ class PanelStream:
             bad(f"shape ({K}, {N}) (N must be a multiple of {PANEL}, K of 8)")
         if kc % 32 or not 32 <= kc <= MAX_CHUNK_ROWS:
             bad(f"chunk_rows={kc}")
+        if self.layout not in (LAYOUT_V1, LAYOUT_MX):
+            bad(f"layout={self.layout}")
+        mx = self.layout == LAYOUT_MX
         arrays = {"payload": (self.payload, np.uint32), "leaf_word": (self.leaf_word, np.uint32),
                   "unit_hdr": (self.unit_hdr, np.int32), "buckets": (self.buckets, np.uint32)}
         for name, (a, dt) in arrays.items():
@@ -186,7 +191,8 @@ class PanelStream:
                 bad("bucket kind")
             n = b[:, 2] & 0xFFFF
             S = np.left_shift(1, ls)
-            if (b[:, 0] % 4).any() or (h[unit, 0] + b[:, 0] + n * P > h[unit, 1]).any():
+            n_pay = ((n + 3) // 4) * 4 if mx else n                 # mx: whole quads of chunks
+            if (b[:, 0] % 4).any() or (h[unit, 0] + b[:, 0] + n_pay * P > h[unit, 1]).any():
                 bad("bucket payload outside its unit")
             n_leaf = np.where(S == 4, 2 * n, -(-n * 8 // np.maximum(S, 8)))
             first = h[unit, 2] + b[:, 1]
@@ -212,10 +218,52 @@ class PanelStream:
             if np.any(kc != kc[:, :1]) or np.any((ls < 2) | (ls > 5)) or \
                     np.any(~np.isin(P, CODE_WIDTHS)) or np.any(counts > STEP_LANES):
                 bad("step record kind or chunk counts")
+            self._validate_records(h, blocks, ls, P, counts, bad)
         elif nb:
             bad("step records missing")
         if self.fixed_steps not in (0, 16, 32, 48):
             bad(f"fixed_steps={self.fixed_steps}")
+
+    def _validate_records(self, h, blocks, ls, P, counts, bad) -> None:
+        """Step records against the unit headers: each decode block's record count and overflow
+        start (unit header words 27 + 2b, 28 + 2b) stay inside the record array, the null record
+        has no chunks, and every record a block executes (all of its fixed places, which the
+        decode reads whatever the count, and its overflow records) names payload and leaf words
+        inside its own unit for every chunk it counts."""
+        F = int(self.fixed_steps)
+        n_rec = self.steps.shape[0]
+        null = blocks * F
+        if counts[null].any():
+            bad("the null step record has chunks")
+        cb = np.arange(BLOCKS_PER_UNIT)
+        ovf = h[:, 27 + 2 * cb].reshape(-1)                # per block, block = unit * 2 + cb
+        nrec = h[:, 28 + 2 * cb].reshape(-1)
+        extra = np.maximum(nrec - F, 0)
+        if (nrec < 0).any() or ((extra > 0) & ((ovf < null + 1) | (ovf + extra > n_rec))).any():
+            bad("decode block record count or overflow start outside the step records")
+        # every (record, owning unit) pair a block executes
+        fixed_rec = np.arange(null, dtype=np.int64)
+        fixed_unit = fixed_rec // max(F, 1) // BLOCKS_PER_UNIT
+        blk = np.repeat(np.arange(blocks), extra)
+        pos = np.arange(int(extra.sum())) - np.repeat(np.cumsum(extra) - extra, extra)
+        rec = np.concatenate([fixed_rec, ovf[blk] + pos])
+        unit = np.concatenate([fixed_unit, blk // BLOCKS_PER_UNIT])
+        if rec.size == 0:
+            return
+        slot = self.steps[rec][:, 0::2].astype(np.int64)   # (n, 4) slot words
+        n = counts[rec]                                      # (n, 4) chunks per slot
+        Pr, lsr = P[rec][:, None], ls[rec][:, None]
+        n_pay = ((n + 3) // 4) * 4 if self.layout == LAYOUT_MX else n
+        pay_end = (slot & 0xFFFF) * 4 + n_pay * Pr
+        leaves = np.where(lsr == 2, 2 * n, ((np.maximum(n, 1) - 1) >> np.maximum(lsr - 3, 0)) + 1)
+        leaf_end = (slot >> 16) + leaves
+        pay_len = (h[unit, 1] - h[unit, 0])[:, None]
+        leaf_len = (h[unit, 3] - h[unit, 2])[:, None]
+        on = n > 0
+        if (on & (pay_end > pay_len)).any():
+            bad("step record payload outside its unit")
+        if (on & (leaf_end > leaf_len)).any():
+            bad("step record leaf words outside its unit")
 
 
 def _code_bits(P: int, i: int):
@@ -239,6 +287,83 @@ def _code_bits(P: int, i: int):
     if first < P:
         parts.append((j + 1, 0, P - first, first))
     return parts
+
+
+# ---- the matrix-core decode layout ("mx", MTC_FLAG_MX_LAYOUT) ----
+# A bucket's chunks are taken in quads (4 consecutive chunks; the last quad is padded with
+# zero codes) and a quad's 4P dwords are 4 lanes of P dwords: lane j holds column j of the
+# quad's 4 chunks, the 8 codes of each chunk in chunk-row order r = 0..7 (for S = 4 rows 0-3
+# are the chunk's first leaf, rows 4-7 its second). The decode turns a lane's 32 codes into 16
+# dwords o = 0..15 of two f16 operands each: dword o holds chunk t = o / 4, rows r = 2 (o % 4)
+# (low half) and r + 1 (high half). The codes of the low halves form one bit string over the
+# low 16-bit halves of the lane's dwords (dword d holds bits [16 d, 16 d + 16)), those of the
+# high halves the same string over the high halves, so one shift and one masked OR build an
+# operand dword. Code o sits at bits [o W, o W + W) of its string (W = P; P = 16 is two planes
+# of W = 8, the low bytes in dwords 0-7 and the high bytes in dwords 8-15).
+LAYOUT_V1, LAYOUT_MX = 0, 1
+MX_PLANES = {2: (2, 1), 3: (3, 1), 4: (4, 1), 5: (5, 1), 6: (6, 1), 8: (8, 1), 16: (8, 2)}   # P -> (W, planes)
+
+
+def mx_rows(S: int) -> np.ndarray:
+    """(4 columns, 8 chunk rows) -> the chunk's code index (the panel stream's chunk code order)."""
+    j, r = np.meshgrid(np.arange(4), np.arange(8), indexing="ij")
+    return np.where(S == 4, 16 * (r // 4) + 4 * j + r % 4, 8 * j + r)
+
+
+_MX_TABLES: Dict[Tuple[int, int], Tuple[np.ndarray, ...]] = {}
+
+
+def _mx_table(S: int, P: int):
+    """Every code bit of a quad in the mx layout, as flat index arrays: the code (chunk t,
+    chunk code index c), its bit v (8 * plane + k), and where it is stored (lane l, dword d,
+    bit b). Cached per (S == 4, P)."""
+    key = (int(S == 4), int(P))
+    if key not in _MX_TABLES:
+        W, npl = MX_PLANES[P]
+        ci = mx_rows(S)
+        rows = []
+        for j in range(4):
+            for o in range(16):
+                t, r = o // 4, 2 * (o % 4)
+                for half, rr in ((0, r), (1, r + 1)):
+                    for pl in range(npl):
+                        for k in range(W):
+                            b = o * W + k
+                            rows.append((t, ci[j, rr], 8 * pl + k, j, pl * W + b // 16, 16 * half + b % 16))
+        a = np.array(rows, dtype=np.int64)
+        t, c, v, l, d, bb = a.T
+        po = np.lexsort((bb, d, l))                         # grouped by stored dword (pack)
+        uo = np.lexsort((v, c, t))                          # grouped by code (unpack)
+        _MX_TABLES[key] = (t, c, v, l, d, bb, po, uo)
+    return _MX_TABLES[key]
+
+
+def _segment_or(x: np.ndarray, keys: np.ndarray) -> np.ndarray:
+    """OR of the columns of x (n, m) over runs of equal `keys` (sorted; bits are disjoint)."""
+    starts = np.flatnonzero(np.concatenate([[True], keys[1:] != keys[:-1]]))
+    return np.add.reduceat(x, starts, axis=1)
+
+
+def mx_pack(codes: np.ndarray, S: int, P: int) -> np.ndarray:
+    """(n, 4, 32) signed codes of n quads (4 chunks each, panel-stream chunk code order) ->
+    (n, 4, P) uint32: the P dwords of lanes 0..3."""
+    n = codes.shape[0]
+    u = (codes.astype(np.int64) + (1 << (P - 1))).astype(np.uint64)
+    if np.any(u >> np.uint64(P)):
+        raise ValueError(f"codes outside the signed {P}-bit range")
+    t, c, v, l, d, bb, po, _ = _mx_table(S, P)
+    bits = ((u[:, t[po], c[po]] >> v[po].astype(np.uint64)) & np.uint64(1)) << bb[po].astype(np.uint64)
+    return _segment_or(bits, l[po] * 64 + d[po]).reshape(n, 4, P).astype(np.uint32)
+
+
+def mx_unpack(words: np.ndarray, S: int, P: int) -> np.ndarray:
+    """Inverse of mx_pack: (n, 4, P) uint32 -> (n, 4, 32) signed codes."""
+    n = words.shape[0]
+    w = words.astype(np.uint64)
+    t, c, v, l, d, bb, _, uo = _mx_table(S, P)
+    bits = ((w[:, l[uo], d[uo]] >> bb[uo].astype(np.uint64)) & np.uint64(1)) << v[uo].astype(np.uint64)
+    u = _segment_or(bits, t[uo] * 64 + c[uo]).reshape(n, 4, 32).astype(np.int64)
+    return u - (1 << (P - 1))
 
 
 def pack_codes(codes: np.ndarray, P: int) -> np.ndarray:
@@ -461,13 +586,18 @@ def storage_plan(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, n
 def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np.ndarray],
                 modes: Dict[int, np.ndarray], scales: Dict[int, np.ndarray], codes_of: CodeSource,
                 chunk_rows: int = 512, scale_format: str = "bf16", row_perm: Optional[np.ndarray] = None,
-                col_perm: Optional[np.ndarray] = None, merge_kinds: bool = True) -> PanelStream:
+                col_perm: Optional[np.ndarray] = None, merge_kinds: bool = True,
+                layout: int = LAYOUT_V1) -> PanelStream:
     """Pack the leaves given per level s (leaf mask, mode grid, scale grid) of a K x N weight.
 
     `codes_of(S, P, ii, jj, scales)` returns the (n, S, S) integer codes of the
     listed leaves (see weight_codes). With `merge_kinds`, rare kinds are stored at a wider
-    width of the same leaf size (storage_widths); W_hat is the same either way.
+    width of the same leaf size (storage_widths); W_hat is the same either way. `layout`:
+    LAYOUT_V1 (chunk-contiguous payload, every decode kernel) or LAYOUT_MX (quads of chunks
+    stored per lane column for the matrix-core decode of one X row; see mx_pack).
     """
+    if layout not in (LAYOUT_V1, LAYOUT_MX):
+        raise ValueError(f"layout={layout}")
     K, N = (int(x) for x in shape)
     if N % PANEL or K % 8:
         raise ValueError(f"panel stream needs N % {PANEL} == 0 and K % 8 == 0, got {shape}")
@@ -480,7 +610,7 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
 
     # per kind: leaf words (+ unit/kind keys) and chunk records
     lw_words, lw_scales, lw_unit, lw_kind = [], [], [], []
-    ch_unit, ch_cg, ch_kind, ch_row, ch_leaf, ch_words = [], [], [], [], [], []
+    ch_unit, ch_cg, ch_kind, ch_row, ch_leaf, ch_words, ch_codes = [], [], [], [], [], [], []
     n_real = 0
     n_lw = 0
     for S in sizes:
@@ -560,7 +690,10 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
                 ch_kind.append(np.full(n // 2, kr))
                 ch_row.append(k0[0::2])
                 ch_leaf.append(gidx[0::2])
-                ch_words.append(pack_codes(q.transpose(0, 2, 1).reshape(n // 2, 32), P))
+                cq = q.transpose(0, 2, 1).reshape(n // 2, 32)
+                ch_words.append(pack_codes(cq, P))
+                if layout == LAYOUT_MX:
+                    ch_codes.append(cq.astype(np.int16))
             else:
                 n = q.shape[0]
                 nrb, ncg = S // 8, S // GROUP
@@ -574,6 +707,8 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
                 ch_row.append((k0[:, None, None] + 8 * np.arange(nrb)[None, None, :] + 0 * np.arange(ncg)[None, :, None]).reshape(-1))
                 ch_leaf.append(np.broadcast_to(gidx[:, None, None], shp).reshape(-1))
                 ch_words.append(pack_codes(codes, P))
+                if layout == LAYOUT_MX:
+                    ch_codes.append(codes.astype(np.int16))
             lw_words.append(words)
             lw_scales.append(sc)
             lw_unit.append(unit)
@@ -615,15 +750,35 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
         b_cnt = np.diff(np.concatenate([b_start, [n_ch]]))
         b_unit, b_cg, b_kind = cu[b_start], cc[b_start], ck[b_start]
         b_S, b_P = _KIND_S[b_kind], _KIND_P[b_kind]
-        b_dw = (b_cnt * b_P + 3) & ~3
+        if layout == LAYOUT_MX:
+            b_dw = ((b_cnt + 3) // 4) * 4 * b_P                             # whole quads of chunks
+        else:
+            b_dw = (b_cnt * b_P + 3) & ~3
         b_pay = np.concatenate([[0], np.cumsum(b_dw)[:-1]])
         total_dw = int(b_dw.sum())
         payload = np.zeros(total_dw + PAYLOAD_PAD, dtype=np.uint32)   # tail padding: 16-byte loads may run past a chunk
         b_of = np.repeat(np.arange(n_buckets), b_cnt)
-        dst = b_pay[b_of] + (np.arange(n_ch) - b_start[b_of]) * cP
-        for P in np.unique(cP):
-            sel = np.flatnonzero(cP == P)
-            payload[(dst[sel][:, None] + np.arange(P)).reshape(-1)] = src[(src_off[sel][:, None] + np.arange(P)).reshape(-1)]
+        if layout == LAYOUT_MX:
+            codes = np.concatenate(ch_codes)[corder]
+            pos = np.arange(n_ch) - b_start[b_of]                        # chunk index within its bucket
+            for P in np.unique(cP):
+                for four in (True, False):                               # S = 4 chunks order codes by leaf
+                    sel = np.flatnonzero((cP == P) & ((_KIND_S[ck] == 4) == four))
+                    if sel.size == 0:
+                        continue
+                    qkey = b_of[sel] * (1 << 20) + pos[sel] // 4         # one entry per quad
+                    uq, qi = np.unique(qkey, return_inverse=True)
+                    quads = np.zeros((uq.size, 4, 32), dtype=np.int64)
+                    quads[qi, pos[sel] % 4] = codes[sel]
+                    words = mx_pack(quads, 4 if four else 8, int(P))     # (n_quads, 4 lanes, P)
+                    qb = uq >> 20
+                    qdst = b_pay[qb] + (uq & ((1 << 20) - 1)) * 4 * int(P)
+                    payload[(qdst[:, None] + np.arange(4 * int(P))).reshape(-1)] = words.reshape(-1)
+        else:
+            dst = b_pay[b_of] + (np.arange(n_ch) - b_start[b_of]) * cP
+            for P in np.unique(cP):
+                sel = np.flatnonzero(cP == P)
+                payload[(dst[sel][:, None] + np.arange(P)).reshape(-1)] = src[(src_off[sel][:, None] + np.arange(P)).reshape(-1)]
         # first chunk of each bucket within its column group
         gkey = cu * N_GROUPS + cc
         g_start = np.flatnonzero(np.concatenate([[True], gkey[1:] != gkey[:-1]]))
@@ -749,7 +904,7 @@ def pack_levels(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np
                        row_perm=None if row_perm is None else np.ascontiguousarray(row_perm, dtype=np.int32),
                        col_perm=None if col_perm is None else np.ascontiguousarray(col_perm, dtype=np.int32),
                        n_real_leaves=n_real, max_unit_words=max_unit_words,
-                       max_unit_words4=max_unit_words4, stats=stats)
+                       max_unit_words4=max_unit_words4, stats=stats, layout=layout)
 
 
 def _place_chunks(ps: PanelStream, Wp: np.ndarray, u: int, g: int, S: int, P: int, off: int, l0: int,
@@ -757,8 +912,15 @@ def _place_chunks(ps: PanelStream, Wp: np.ndarray, u: int, g: int, S: int, P: in
     """Dequantize chunks `ts` of the bucket whose payload starts at dword `off` and whose
     first leaf word is `l0` (both absolute) into Wp (permuted channel order)."""
     panel, chunk = divmod(u, ps.n_chunks)
+    ts = np.asarray(ts, dtype=np.int64)
+    if ps.layout == LAYOUT_MX and ts.size:
+        nq = int(ts.max()) // 4 + 1                         # every quad up to the last chunk named
+        quads = mx_unpack(ps.payload[off: off + nq * 4 * P].reshape(nq, 4, P), S, P)
     for t in (int(x) for x in ts):
-        cd_all = unpack_codes(ps.payload[off + t * P: off + (t + 1) * P].reshape(1, P), P)[0]
+        if ps.layout == LAYOUT_MX:
+            cd_all = quads[t // 4, t % 4]
+        else:
+            cd_all = unpack_codes(ps.payload[off + t * P: off + (t + 1) * P].reshape(1, P), P)[0]
         if S == 4:
             parts = [(l0 + 2 * t, cd_all[:16], 0, 4), (l0 + 2 * t + 1, cd_all[16:], 0, 4)]
         else:

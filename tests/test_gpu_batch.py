@@ -117,3 +117,29 @@ def test_batch_rejects_mixed_scale_formats(gpu, members):
     qt = members[0][0].device_stream(None, gpu, 1)
     with pytest.raises(MtcError):
         GemvBatch([qt, uni], [torch.randn(1, qt.K, device=gpu), torch.randn(1, uni.K, device=gpu)])
+
+
+@pytest.mark.parametrize("M", [1, 3])
+def test_batch_of_mx_streams_matches_single_calls(gpu, members, M):
+    """Members in the matrix-core payload layout (one X row per block) batch together and give
+    their own calls' Y bit for bit, split-K members included; a batch may not mix layouts."""
+    import torch
+    from tensorpack_amd._abi import MtcError
+    from tensorpack_amd.device import GemvBatch
+    from tensorpack_amd.packer import LAYOUT_MX
+    streams = [m.device_stream(cr, gpu, 1, LAYOUT_MX) for m, _, cr in members]
+    assert any(s.host.n_chunks > 1 for s in streams)
+    rng = np.random.RandomState(30 + M)
+    Xs = [torch.from_numpy(rng.randn(M, s.K).astype(np.float32)).to(gpu) for s in streams]
+    _say(f"mx M={M}: launch")
+    b = GemvBatch(streams, Xs)
+    b.launch()
+    b.launch()
+    torch.cuda.synchronize()
+    for (m, W_hat, _), s, X, y in zip(members, streams, Xs, b.outs):
+        assert torch.equal(y, s.gemv_f32(X)), (s.K, s.N)
+        err = O.relative_frobenius_error(O.qt_gemm_f64(X.cpu().numpy(), W_hat), y.cpu().numpy())
+        assert err < 1e-5, (s.K, s.N, err)
+    v1 = members[0][0].device_stream(None, gpu, M)
+    with pytest.raises(MtcError):
+        GemvBatch([streams[0], v1], [Xs[0], Xs[0]])

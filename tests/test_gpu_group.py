@@ -206,3 +206,23 @@ def test_device_calls_check_their_arguments(gpu, members):
         ds.dequant(out=torch.empty((1, 1), device=gpu))
     from tensorpack_amd.device import require_gpu
     assert require_gpu("cuda").index is not None
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_group_of_mx_streams(gpu, members, M):
+    """A group in the matrix-core payload layout gives each member's own call bit for bit; a
+    group may not mix layouts."""
+    import torch
+    from tensorpack_amd.device import gemv_f32_group
+    from tensorpack_amd.packer import LAYOUT_MX
+    _say("group mx", M)
+    streams = [m.device_stream(None, gpu, 1, LAYOUT_MX) for _, _, _, m in members[:_abi.MAX_GROUP]]
+    X = torch.from_numpy(np.random.RandomState(60 + M).randn(M, 256).astype(np.float32)).to(gpu)
+    ys = gemv_f32_group(streams, X)
+    torch.cuda.synchronize()
+    for (name, W, a, m), s, y in zip(members, streams, ys):
+        assert torch.equal(y, s.gemv_f32(X)), name
+        err = O.relative_frobenius_error(O.qt_gemm_f64(X.cpu().numpy(), _oracle_what(a, W)), y.cpu().numpy())
+        assert err <= TOL_F32, (name, M, err)
+    with pytest.raises(_abi.MtcError):
+        gemv_f32_group([streams[0], members[1][3].device_stream(None, gpu, 1)], X)

@@ -94,6 +94,28 @@ def test_gemv_f32(gpu, allocs, name, M):
     assert err <= TOL_F32, (name, M, err)
 
 
+@pytest.mark.parametrize("name", [c[0] for c in CASES])
+@pytest.mark.parametrize("M", [1, 2, 5, 16])
+def test_gemv_f32_mx_layout(gpu, allocs, name, M):
+    """The matrix-core payload layout (opt-in, one X row per block): W_hat bit-exact and Y
+    within the fp32 bar, at the decode layout's row chunks and at split-K chunkings."""
+    import torch
+    from tensorpack_amd.packer import LAYOUT_MX
+    W, a, m = allocs[name]
+    X = np.random.RandomState(50 + M).randn(M, W.shape[0]).astype(np.float32)
+    Xd = torch.from_numpy(X).to(gpu)
+    ref = O.qt_gemm_f64(X, _oracle_what(a, W))
+    for cr in (None, 64):
+        _say("gemv mx", name, M, cr)
+        ds = m.device_stream(cr, gpu, 1, LAYOUT_MX)
+        if M == 1:
+            got = ds.dequant().cpu().numpy()
+            assert np.array_equal(_bits(got), _bits(_oracle_what(a, W))), (name, cr)
+        Y = ds.gemv_f32(Xd).cpu().numpy()
+        err = O.relative_frobenius_error(ref, Y)
+        assert err <= TOL_F32, (name, M, cr, err)
+
+
 @pytest.mark.parametrize("chunk_rows", [32, 64, 96, 512])
 @pytest.mark.parametrize("M", [4, 12])
 def test_gemv_split_k_chunkings(gpu, allocs, chunk_rows, M):

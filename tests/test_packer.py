@@ -266,6 +266,7 @@ def test_step_records_overflow_past_the_fixed_area():
     assert n.max() > MAX_FIXED_STEPS and ps.fixed_steps == MAX_FIXED_STEPS
     assert ps.steps.shape[0] > ps.n_units * BLOCKS_PER_UNIT * MAX_FIXED_STEPS + 1
     assert np.array_equal(_bits(decode_steps(ps)), _bits(decode_stream(ps)))
+    ps.validate()                         # the overflow records pass the record bounds checks
 
 
 def _records(ps):
@@ -442,3 +443,80 @@ def test_decode_row_chunks_are_even_and_fill_the_chip(K, N, M):
         if n > need:                                    # a split beyond the minimum only to fill the chip
             assert _decode_blocks_per_unit(M) * (N // 32) * (n - 1) < DECODE_FILL_BLOCKS \
                 and c >= DECODE_MIN_SPLIT_ROWS - 32
+
+
+# ---------------- matrix-core (mx) payload layout ----------------
+
+@pytest.mark.parametrize("S", [4, 8])
+@pytest.mark.parametrize("P", [2, 3, 4, 5, 6, 8, 16])
+def test_mx_pack_round_trip_and_bit_order(P, S):
+    """mx_pack stores quad lane j's codes as half-strings: over the W-bit plane pl of every
+    code, dwords pl W .. pl W + W - 1 of lane j read as two 16 W-bit strings (their low
+    16-bit halves, their high halves); code o of a string sits at bits [o W, o W + W) and is
+    chunk o // 4's code at column j, chunk row 2 (o % 4) (low halves) or 2 (o % 4) + 1
+    (high halves), chunk rows indexed into the chunk's code order by mx_rows."""
+    from tensorpack_amd.packer import MX_PLANES, mx_pack, mx_rows, mx_unpack
+    lo, hi = -(1 << (P - 1)), (1 << (P - 1)) - 1
+    q = np.random.RandomState(P + S).randint(lo, hi + 1, size=(3, 4, 32))
+    w = mx_pack(q, S, P)
+    assert w.shape == (3, 4, P) and w.dtype == np.uint32
+    assert np.array_equal(mx_unpack(w, S, P), q)
+    with pytest.raises(ValueError):
+        mx_pack(np.full((1, 4, 32), hi + 1), S, P)
+    # chunk row order: 8x8 leaves keep column-major rows of 8, a 4x4 leaf pair splits at row 4
+    ci = mx_rows(S)
+    assert sorted(ci.reshape(-1)) == list(range(32))
+    assert ci[1, 0] == (4 if S == 4 else 8) and ci[0, 4] == (16 if S == 4 else 4)
+    W, npl = MX_PLANES[P]
+    assert W * npl == P
+    u = q + (1 << (P - 1))
+    for n in range(q.shape[0]):
+        for j in range(4):
+            for pl in range(npl):
+                dw = [int(w[n, j, pl * W + k]) for k in range(W)]
+                for half in (0, 1):
+                    s = sum(((d >> (16 * half)) & 0xFFFF) << (16 * k) for k, d in enumerate(dw))
+                    for o in range(16):
+                        code = int(u[n, o // 4, ci[j, 2 * (o % 4) + half]])
+                        assert (s >> (o * W)) & ((1 << W) - 1) == (code >> (8 * pl)) & ((1 << W) - 1)
+
+
+@pytest.mark.parametrize("cls,budget", [(QuadtreeRD, 2.2), (QuadtreeRD, 9.0), (QuadtreeRD, 15.0),
+                                        (PermutedQuadtreeRD, 4.25)])
+@pytest.mark.parametrize("chunk_rows", [32, 256])
+def test_mx_stream_decodes_to_oracle_w_hat(cls, budget, chunk_rows, tmp_path):
+    """The mx layout carries the same W_hat as the chunk-contiguous one: both host walks
+    (bucket table, step records) decode it bit for bit, its buckets are padded to whole
+    quads, it validates, and the layout survives save/load."""
+    from tensorpack_amd.packer import LAYOUT_MX
+    W = outlier_matrix(int(budget * 10) + 3, 256, 160)
+    a = cls(W, np.exp(np.random.RandomState(5).randn(256)), (32, 16, 8, 4)).select(budget)
+    m = MTCMatrix.from_quadtree(a, W)
+    ps = m.panel_stream(chunk_rows, LAYOUT_MX)
+    v1 = m.panel_stream(chunk_rows)
+    assert ps.layout == LAYOUT_MX and v1.layout == 0
+    ref = _bits(_oracle(a, W))
+    assert np.array_equal(_bits(decode_stream(ps)), ref)
+    assert np.array_equal(_bits(decode_steps(ps)), ref)
+    ps.validate()
+    # same buckets and records; each bucket's payload padded to a multiple of 4 chunks
+    assert np.array_equal(ps.buckets[:, 1:], v1.buckets[:, 1:]) and np.array_equal(ps.leaf_word, v1.leaf_word)
+    P = ps.buckets[:, 3].astype(np.int64) >> 8
+    n = ps.buckets[:, 2].astype(np.int64) & 0xFFFF
+    assert ps.payload.size >= int((((n + 3) // 4) * 4 * P).sum()) >= v1.payload.size
+    f = tmp_path / "mx.npz"
+    ps.save(str(f))
+    back = type(ps).load(str(f))
+    assert back.layout == LAYOUT_MX
+    assert np.array_equal(_bits(decode_stream(back)), ref)
+
+
+def test_mx_stream_rejects_a_short_payload():
+    from tensorpack_amd.packer import LAYOUT_MX
+    W = outlier_matrix(31, 128, 64)
+    m = MTCMatrix.from_quadtree(QuadtreeRD(W, None, (32, 16, 8, 4)).select(3.0), W)
+    ps = m.panel_stream(64, LAYOUT_MX)
+    ps.validate()
+    ps.payload = ps.payload[:-1]
+    with pytest.raises(ValueError):
+        ps.validate()

@@ -172,10 +172,28 @@ def test_panel_stream_load_rejects_corrupt_stream(saved_qtp, tmp_path):
     st2[0, 1::2] = (st2[0, 1::2] & ~np.uint32(0xF8)) | np.uint32(7 << 3)   # code width 7
     st3 = ps.steps.copy()
     st3[0, 1::2] |= np.uint32(17 << 8)                # 17+ chunks in a 16-chunk step
+    h4 = ps.unit_hdr.copy()
+    h4[0, 28] = 60000                                 # a block with more records than the array holds
+    h4[0, 27] = 100000000
+    h5 = ps.unit_hdr.copy()
+    h5[0, 28] = ps.fixed_steps + 2                    # overflow records starting inside the fixed area
+    h5[0, 27] = 0
+    st4 = ps.steps.copy()
+    st4[:, 0::2] = np.uint32(0xFFFFFFFF)              # every slot word at the end of the 16-bit ranges
+    st5 = ps.steps.copy()
+    on = np.nonzero(((st5[:, 1].astype(np.int64) >> 8) & 31) > 0)[0][0]
+    st5[on, 0] = (st5[on, 0] & np.uint32(0xFFFF)) | np.uint32(0xFFF0 << 16)   # first leaf past the unit
+    st6 = ps.steps.copy()
+    st6[on, 0] = (st6[on, 0] & np.uint32(0xFFFF0000)) | np.uint32(0xFFF0)     # payload past the unit
+    st7 = ps.steps.copy()
+    st7[ps.unit_hdr.shape[0] * 2 * ps.fixed_steps, 1::2] |= np.uint32(1 << 8)  # a chunk in the null record
     bad = {"hdr": {"unit_hdr": hdr}, "bucket payload": {"buckets": bk}, "bucket kind": {"buckets": bk2},
            "leaf rows": {"leaf_word": lw}, "row_perm": {"row_perm": np.zeros_like(ps.row_perm)},
            "col_perm": {"col_perm": ps.col_perm + 1}, "record kind words": {"steps": st1},
-           "record width": {"steps": st2}, "record count": {"steps": st3}}
+           "record width": {"steps": st2}, "record count": {"steps": st3},
+           "block record count": {"unit_hdr": h4}, "overflow start": {"unit_hdr": h5},
+           "slot words": {"steps": st4}, "slot leaf": {"steps": st5}, "slot payload": {"steps": st6},
+           "null record": {"steps": st7}}
     for name, change in bad.items():
         dst = tmp_path / (name.replace(" ", "_") + ".npz")
         _resave(src, dst, **change)
