@@ -42,6 +42,13 @@ def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
+M1_LAYOUT = None              # layout of the M = 1 decode streams (None: MTCMatrix.decode_layout(1))
+
+
+def m1_layout(m):
+    return m.decode_layout(1) if M1_LAYOUT is None else M1_LAYOUT
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -58,10 +65,14 @@ def parse():
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH_SIZE/WRITE_SIZE passes")
     ap.add_argument("--pmc-child", help=argparse.SUPPRESS)
     ap.add_argument("--pmc-child-batch", help=argparse.SUPPRESS)
+    ap.add_argument("--pmc-child-tiles", help=argparse.SUPPRESS)
     ap.add_argument("--workload", default="all", choices=["all", "c2", "c3", "c5"],
                     help="all (default): the headline c2 decode plus c4 prefill, the c3 stack and c5; c2: c2 and "
                          "c4 only; c3: the 24-layer decoder stack (168 matrices) at M=1 and M=512 with per-launch "
                          "comparisons; c5: the adversarial leaf mix at M=1 and M=256")
+    ap.add_argument("--m1-layout", default="auto", choices=["auto", "v1", "mx"],
+                    help="payload layout of the M=1 decode streams: auto (MTCMatrix.decode_layout(1)), v1 "
+                         "(chunk-contiguous, vector decode) or mx (matrix-core decode)")
     ap.add_argument("--c3-layers", type=int, default=24)
     ap.add_argument("--no-c3", action="store_true")
     ap.add_argument("--no-c5", action="store_true")
@@ -126,6 +137,82 @@ def pmc_child_batch(folder):
     print("pmc child done", flush=True)
 
 
+TILE_FIELDS = ("cells", "step_off", "payload")
+
+
+def save_tiles(ts, path):
+    """A tile stream as plain arrays (no pickles): its fields plus the permutations, if any."""
+    arrs = {f: getattr(ts, f) for f in TILE_FIELDS}
+    arrs["shape"] = np.array([ts.K, ts.N, ts.n_ksteps, ts.n_col_tiles], dtype=np.int64)
+    for f in ("row_perm", "col_perm"):
+        if getattr(ts, f) is not None:
+            arrs[f] = getattr(ts, f)
+    np.savez(path, **arrs)
+
+
+def load_tiles(path):
+    from tensorpack_amd.tilestream import TileStream
+    with np.load(path) as z:
+        K, N, nk, nc = (int(v) for v in z["shape"])
+        return TileStream(K, N, nk, nc, *(z[f] for f in TILE_FIELDS),
+                          row_perm=z["row_perm"] if "row_perm" in z.files else None,
+                          col_perm=z["col_perm"] if "col_perm" in z.files else None)
+
+
+def pmc_child_tiles(folder):
+    """Body of one counter pass of the prefill: the calibration copies, then four calls over the
+    tile streams saved in `folder` (tiles_NNN.npz; inputs x.npz, one per K, fp32 or bf16 bits):
+    one matrix runs gemm_bf16, several one batched prefill (GemmBatch)."""
+    import torch
+    from tensorpack_amd.device import DeviceTiles, GemmBatch
+    n = len([f for f in os.listdir(folder) if f.startswith("tiles_")])
+    tss = [load_tiles(os.path.join(folder, f"tiles_{i:03d}.npz")) for i in range(n)]
+    with np.load(os.path.join(folder, "x.npz")) as z:
+        xs = {int(k[1:]): z[k] for k in z.files}
+    pmc_copies(torch)
+    tiles = [DeviceTiles(ts) for ts in tss]
+
+    def dev_x(x):
+        if x.dtype == np.uint16:
+            return torch.from_numpy(x.view(np.int16)).cuda().view(torch.bfloat16)
+        return torch.from_numpy(x).cuda()
+    X = {K: dev_x(x) for K, x in xs.items()}
+    M = next(iter(X.values())).shape[0]
+    Ys = [torch.empty((M, t.N), dtype=torch.float32, device="cuda") for t in tiles]
+    if n == 1:
+        launch = lambda: tiles[0].gemm_bf16(X[tiles[0].K], out=Ys[0])
+    else:
+        batch = GemmBatch(tiles, [X[t.K] for t in tiles], Ys)
+        launch = batch.launch
+    launch()
+    torch.cuda.synchronize()
+    for _ in range(4):
+        launch()
+    torch.cuda.synchronize()
+    print("pmc child done", flush=True)
+
+
+PREFILL_KERNELS = ("k_stage_x", "k_gemm_tile", "k_splitk_reduce")
+
+
+def traffic_passes_tiles(tss, xs):
+    """HBM bytes per prefill call over the tile streams `tss` (one: gemm_bf16; several: one batched
+    prefill), summed over the call's launches (X staging, tiles, split-K reduction); `xs`: one
+    input per K, fp32 or bf16 (as uint16 bits). See counter_passes."""
+    import tempfile
+    tmp = tempfile.mkdtemp(prefix="mtc_pmc_")
+    for i, ts in enumerate(tss):
+        save_tiles(ts, os.path.join(tmp, f"tiles_{i:03d}.npz"))
+    np.savez(os.path.join(tmp, "x.npz"), **{f"k{K}": x for K, x in xs.items()})
+    return counter_passes(tmp, ["--pmc-child-tiles", tmp], PREFILL_KERNELS, launches=5)
+
+
+def bf16_bits(x):
+    """fp32 array -> bf16 bits (uint16, round to nearest even), the input of a bf16 prefill call."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
 def traffic_passes(ps, x, kernel="k_gemv"):
     """HBM bytes per decode launch of one stream (`ps`, input `x`); see counter_passes."""
     import tempfile
@@ -183,7 +270,7 @@ def _counter_passes(exe, tmp, child_args, kernel, launches):
         if r.returncode != 0 or not os.path.exists(db):
             log(f"traffic pass {counter} failed (rc {r.returncode}): {r.stderr[-400:]}")
             return None
-        kern = dispatch_values(db, counter, kernel)
+        kern = kernel_values(db, counter, kernel)
         # the four COPY_BYTES device copies are the largest copy dispatches of the pass
         # (host-to-device staging copies share the kernel name but are small)
         copy = sorted(dispatch_values(db, counter, "copyBuffer"))[-4:]
@@ -195,8 +282,76 @@ def _counter_passes(exe, tmp, child_args, kernel, launches):
                         "factor": COPY_BYTES / (copy_kib * 1024.0), "copy_spread": max(copy) / min(copy)}
     fetch = res["FETCH_SIZE"]["kernel_kib"] * 1024.0 * res["FETCH_SIZE"]["factor"]
     write = res["WRITE_SIZE"]["kernel_kib"] * 1024.0 * res["WRITE_SIZE"]["factor"]
-    return {"bytes": fetch + write, "fetch_bytes": fetch, "write_bytes": write,
-            "fetch_factor": res["FETCH_SIZE"]["factor"], "write_factor": res["WRITE_SIZE"]["factor"]}
+    out = {"bytes": fetch + write, "fetch_bytes": fetch, "write_bytes": write,
+           "fetch_factor": res["FETCH_SIZE"]["factor"], "write_factor": res["WRITE_SIZE"]["factor"]}
+    issue = _issue_pass(exe, tmp, child_args, kernel, launches)
+    if issue is not None:
+        out["issue"] = issue
+    waves = _issue_pass(exe, tmp, child_args, kernel, launches, WAVE_COUNTERS, "WAVES")
+    if waves is not None:
+        out["waves"] = waves
+    return out
+
+
+# Instruction-issue counters of one pass (SQ block: at most 8 per pass; GRBM: 2).
+ISSUE_COUNTERS = ("SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_INSTS_VMEM_RD", "SQ_ACTIVE_INST_VALU",
+                  "SQ_BUSY_CYCLES", "SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE")
+# Wave-state counters of a second pass: waves, their cycles, cycles waiting on an instruction's
+# operands, cycles issuing, MFMA instructions, LDS bank conflicts, instruction fetches.
+WAVE_COUNTERS = ("SQ_WAVES", "SQ_WAVE_CYCLES", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY", "SQ_ACTIVE_INST_ANY",
+                 "SQ_INSTS_MFMA", "SQ_LDS_BANK_CONFLICT", "SQ_IFETCH", "GRBM_GUI_ACTIVE")
+
+
+def kernel_values(db, counter, kernel):
+    """Per-dispatch values of `counter` for the kernels named by `kernel` (a substring, or a tuple
+    of substrings whose dispatches are pooled)."""
+    from tensorpack_amd.profiling import dispatch_values
+    names = (kernel,) if isinstance(kernel, str) else tuple(kernel)
+    return [v for k in names for v in dispatch_values(db, counter, k)]
+
+
+def _issue_pass(exe, tmp, child_args, kernel, launches, counters=ISSUE_COUNTERS, name="ISSUE"):
+    """Per-launch values of `counters` for `kernel` from one rocprofv3 --pmc pass over the same
+    child run. ISSUE_COUNTERS: VALU / SALU / LDS / vector-memory-read wave-instructions, the
+    waves' VALU issue cycles, SQ busy cycles, MFMA busy cycles and the GPU's active cycles."""
+    import subprocess
+    cmd = ["timeout", "-s", "KILL", "120", exe, "--pmc", *counters, "-d", tmp, "-o", name, "--",
+           sys.executable, os.path.abspath(__file__)] + child_args
+    log(f"{name.lower()} pass: " + " ".join(cmd[3:]))
+    r = subprocess.run(cmd, capture_output=True, text=True, env=dict(os.environ, TMPDIR="/tmp"))
+    db = os.path.join(tmp, f"{name}_results.db")
+    if r.returncode != 0 or not os.path.exists(db):
+        log(f"{name.lower()} pass failed (rc {r.returncode}): {r.stderr[-400:]}")
+        return None
+    out = {}
+    for c in counters:
+        v = kernel_values(db, c, kernel)
+        if not v:
+            log(f"{name.lower()} pass: no {c} values for {kernel}")
+            return None
+        out[c] = sum(v) / (launches or len(v))
+    return out
+
+
+def issue_ratios(traffic, weights):
+    """Per-weight issue figures of a decode launch from its counter pass (`traffic["issue"]`):
+    VALU lane-instructions per weight (64 lanes per wave-instruction; weights = K * N summed
+    over the matrices, P0 leaves included) and the fraction of the SIMDs' VALU issue slots the
+    launch used (a wave-instruction occupies a 16-lane SIMD for 4 cycles; 1024 SIMDs). The
+    reader sums GRBM_GUI_ACTIVE over the 8 XCD instances, so the launch's cycles are an eighth."""
+    if not traffic or "issue" not in traffic:
+        return None
+    c = traffic["issue"]
+    gpu = (c.get("GRBM_GUI_ACTIVE") or 0.0) / 8.0
+    return {"valu_lane_insts_per_weight": 64.0 * c["SQ_INSTS_VALU"] / weights,
+            "salu_insts_per_weight_x64": 64.0 * c["SQ_INSTS_SALU"] / weights,
+            "valu_issue_fraction": (4.0 * c["SQ_INSTS_VALU"] / (1024.0 * gpu)) if gpu else None,
+            "mfma_busy_fraction": (c["SQ_VALU_MFMA_BUSY_CYCLES"] / (1024.0 * gpu)) if gpu else None,
+            "gpu_cycles": gpu, "weights": weights,
+            "wave_wait_fraction": (traffic["waves"]["SQ_WAIT_INST_ANY"] / traffic["waves"]["SQ_WAVE_CYCLES"])
+            if traffic.get("waves") and traffic["waves"]["SQ_WAVE_CYCLES"] else None,
+            "wave_issue_fraction": (traffic["waves"]["SQ_ACTIVE_INST_ANY"] / traffic["waves"]["SQ_WAVE_CYCLES"])
+            if traffic.get("waves") and traffic["waves"]["SQ_WAVE_CYCLES"] else None}
 
 
 def timed_calls(torch, launch_list, steps, warmup, use_graph):
@@ -341,7 +496,7 @@ def bench_c2(args, wl, alloc, traffic, dev, traffic16=None):
     from tensorpack_amd.kernels.gemm import MTCMatrix
     m = MTCMatrix.from_quadtree(alloc, wl.W)
     t0 = time.time()
-    ds = m.device_stream()
+    ds = m.device_stream(None, dev, 1, M1_LAYOUT)
     log(f"c2 packed in {time.time() - t0:.1f}s: chunk_rows={ds.host.chunk_rows} stream {ds.device_bytes()} B, "
         f"accounted {m.packed_bytes:.0f} B")
     packed = m.packed_bytes
@@ -386,7 +541,8 @@ def bench_c2(args, wl, alloc, traffic, dev, traffic16=None):
                                    "traffic": None if traffic16 is None else traffic16["bytes"],
                                    "kernel": "k_gemv<16>"}}
         if traffic16 is not None:
-            res["m16"]["roofline"]["traffic_detail"] = dict(traffic16, traffic_over_packed=traffic16["bytes"] / packed)
+            res["m16"]["roofline"]["traffic_detail"] = dict(traffic16, traffic_over_packed=traffic16["bytes"] / packed,
+                                                            issue_ratios=issue_ratios(traffic16, wl.W.size))
             log(f"c2 M=16 traffic {traffic16['bytes'] / 1e6:.2f} MB per launch = {traffic16['bytes'] / packed:.3f}x packed")
         log(f"c2 M=16: {ms16 * 1e3:.2f} us/call, {tf:.2f} TFLOP/s; vs fp64 rel {rel16:.2e}")
         del c16
@@ -430,10 +586,13 @@ def p0_area_fraction(a):
     return area / float(q.shape[0] * q.shape[1])
 
 
-def bench_c4(args, wl4, a4, dev):
+def bench_c4(args, wl4, a4, dev, m4=None, traffic=None):
+    """c4 prefill at M = 4096; `m4`: the MTCMatrix, if already built; `traffic`: counter bytes of
+    one call (traffic_passes_tiles)."""
     import torch
     from tensorpack_amd.kernels.gemm import MTCMatrix
-    m4 = MTCMatrix.from_quadtree(a4, wl4.W)
+    if m4 is None:
+        m4 = MTCMatrix.from_quadtree(a4, wl4.W)
     g4 = m4.device_tiles(dev)
     M4 = 4096
     X4 = torch.from_numpy(wl4.activations(M4)).to(dev).to(torch.bfloat16)
@@ -456,11 +615,23 @@ def bench_c4(args, wl4, a4, dev):
         f"{rows.size} sampled rows vs fp64: rel {rel:.2e}")
     if not rel < 2e-3:
         raise SystemExit(f"c4 prefill output differs from the fp64 product: rel {rel:.3e} >= 2e-3")
-    return {"M": M4, "ms_per_call": ms4, "TFLOPs": tf, "frac_bf16_peak": tf / BF16_PEAK_TFLOPS,
-            "packed_bytes": m4.packed_bytes, "p0_area_fraction": p0_area_fraction(a4),
-            "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": tf / BF16_PEAK_TFLOPS, "traffic": None, "kernel": "k_gemm_tile"},
-            "parity": {"rows": int(rows.size), "rel_frobenius_vs_fp64": rel, "tolerance": 2e-3}}
+    res = {"M": M4, "ms_per_call": ms4, "TFLOPs": tf, "frac_bf16_peak": tf / BF16_PEAK_TFLOPS,
+           "packed_bytes": m4.packed_bytes, "p0_area_fraction": p0_area_fraction(a4),
+           "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": tf / BF16_PEAK_TFLOPS, "traffic": None if traffic is None else traffic["bytes"],
+                        "kernel": "k_gemm_tile"},
+           "parity": {"rows": int(rows.size), "rel_frobenius_vs_fp64": rel, "tolerance": 2e-3}}
+    if traffic is not None:
+        res["roofline"]["traffic_detail"] = prefill_traffic_detail(traffic, M4, wl4.W.shape, m4.packed_bytes, 2)
+    return res
+
+
+def prefill_traffic_detail(traffic, M, shape, packed, x_bytes):
+    """The counter bytes of one prefill call beside its algorithmic bytes: the packed weight,
+    X read once (x_bytes per element) and fp32 Y written once."""
+    K, N = shape
+    alg = packed + M * K * x_bytes + 4.0 * M * N
+    return dict(traffic, algorithmic_bytes=alg, traffic_over_algorithmic=traffic["bytes"] / alg)
 
 
 # ----------------------------------------------------------------------------------------------
@@ -471,7 +642,7 @@ def c3_x(K, M):
     return np.random.RandomState(3000 + K + M).randn(M, K).astype(np.float32)
 
 
-def bench_c3(args, mats, allocs, dev, detail=False, ms_=None, traffic=None):
+def bench_c3(args, mats, allocs, dev, detail=False, ms_=None, traffic=None, traffic512=None):
     """M = 1: all 168 matrices (each its own X and Y) in one batched launch per pass, over rotating
     copies of the stack; M = 512: the prefill of every matrix, the q/k/v and gate/up groups sharing
     their input (12 launches per layer), one HIP graph per pass. With `detail`, also the M = 1 pass
@@ -493,7 +664,7 @@ def bench_c3(args, mats, allocs, dev, detail=False, ms_=None, traffic=None):
             xs[key] = torch.from_numpy(c3_x(K, M)).to(dev).to(dtype)
         return xs[key]
 
-    streams = [m.device_stream(None, dev, 1) for m in ms_]
+    streams = [m.device_stream(None, dev, 1, M1_LAYOUT) for m in ms_]
     stack_bytes = sum(s_.device_bytes() for s_ in streams)
     n_rot = max(1, int(np.ceil(args.rotate_gib * (1 << 30) / stack_bytes)))
     sets = [streams] + [[s_.clone() for s_ in streams] for _ in range(n_rot - 1)]
@@ -526,7 +697,8 @@ def bench_c3(args, mats, allocs, dev, detail=False, ms_=None, traffic=None):
                                "frac": gbs / HBM_PEAK_GBS, "traffic": None if traffic is None else traffic["bytes"],
                                "kernel": "k_gemv_batch"}}}
     if traffic is not None:
-        out["m1"]["roofline"]["traffic_detail"] = dict(traffic, traffic_over_packed=traffic["bytes"] / packed)
+        out["m1"]["roofline"]["traffic_detail"] = dict(traffic, traffic_over_packed=traffic["bytes"] / packed,
+                                                       issue_ratios=issue_ratios(traffic, weights))
         log(f"c3 M=1 traffic {traffic['bytes'] / 1e6:.2f} MB per launch = {traffic['bytes'] / packed:.3f}x packed")
     n_per = len(workloads.QWEN_LAYER)
     layer_groups = [[0, 1, 2], [3], [4, 5], [6]]
@@ -600,7 +772,13 @@ def bench_c3(args, mats, allocs, dev, detail=False, ms_=None, traffic=None):
         raise SystemExit(f"c3 prefill output differs from the fp64 product: rel {worst:.3e} >= 2e-3")
     out["m512"] = {"ms_per_pass": msp, "TFLOPs": tf, "launches": pb.launches, "rel_frobenius_layer0_vs_fp64": worst,
                    "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                "frac": tf / BF16_PEAK_TFLOPS, "traffic": None, "kernel": "k_gemm_tile_batch"}}
+                                "frac": tf / BF16_PEAK_TFLOPS,
+                                "traffic": None if traffic512 is None else traffic512["bytes"],
+                                "kernel": "k_gemm_tile_batch"}}
+    if traffic512 is not None:
+        alg = packed + sum(M * w.W.shape[0] * 2 + 4.0 * M * w.W.shape[1] for w in mats)
+        out["m512"]["roofline"]["traffic_detail"] = dict(traffic512, algorithmic_bytes=alg,
+                                                         traffic_over_algorithmic=traffic512["bytes"] / alg)
     if detail:
         out["m512"]["ms_per_pass_grouped_launches"] = ms_grouped
     return out
@@ -620,13 +798,13 @@ def cpu_baseline_c3(args, mats, allocs):
 # ----------------------------------------------------------------------------------------------
 # c5: the adversarial leaf mix
 # ----------------------------------------------------------------------------------------------
-def bench_c5(args, wl, a, dev, traffic=None):
+def bench_c5(args, wl, a, dev, traffic=None, traffic256=None):
     """c5 at M = 1 (decode over rotating copies) and M = 256 (prefill). `traffic`: counter bytes
     of one M = 1 launch (traffic_passes), if measured."""
     import torch
     from tensorpack_amd.kernels.gemm import MTCMatrix
     m = MTCMatrix.from_quadtree(a, wl.W)
-    ds = m.device_stream(None, dev, 1)
+    ds = m.device_stream(None, dev, 1, M1_LAYOUT)
     copies = rotating(ds, args.rotate_gib * (1 << 30))
     X1 = torch.from_numpy(wl.activations(1)).to(dev)
     Y1 = torch.empty((1, wl.W.shape[1]), dtype=torch.float32, device=dev)
@@ -659,14 +837,18 @@ def bench_c5(args, wl, a, dev, traffic=None):
                        "frac": gbs / HBM_PEAK_GBS, "traffic": None if traffic is None else traffic["bytes"],
                        "kernel": "k_gemv<1>"}}
     if traffic is not None:
-        m1["roofline"]["traffic_detail"] = dict(traffic, traffic_over_packed=traffic["bytes"] / m.packed_bytes)
+        m1["roofline"]["traffic_detail"] = dict(traffic, traffic_over_packed=traffic["bytes"] / m.packed_bytes,
+                                                issue_ratios=issue_ratios(traffic, wl.W.size))
         log(f"c5 M=1 traffic {traffic['bytes'] / 1e6:.2f} MB per launch = {traffic['bytes'] / m.packed_bytes:.3f}x packed")
     return {"workload": wl.name, "packed_bytes": m.packed_bytes, "stream_bytes": ds.device_bytes(),
             "m1": m1,
             "m256": {"us_per_call": ms2 * 1e3, "TFLOPs": tf, "x_dtype": "f32 (staged to bf16 by k_stage_x)",
                      "rel_vs_fp64": rel2,
                      "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                  "frac": tf / BF16_PEAK_TFLOPS, "traffic": None}}}
+                                  "frac": tf / BF16_PEAK_TFLOPS,
+                                  "traffic": None if traffic256 is None else traffic256["bytes"],
+                                  "traffic_detail": None if traffic256 is None else
+                                  prefill_traffic_detail(traffic256, M, wl.W.shape, m.packed_bytes, 4)}}}
 
 
 # ----------------------------------------------------------------------------------------------
@@ -678,6 +860,13 @@ def main():
     if args.pmc_child_batch:
         pmc_child_batch(args.pmc_child_batch)
         return
+    if args.pmc_child_tiles:
+        pmc_child_tiles(args.pmc_child_tiles)
+        return
+    global M1_LAYOUT
+    if args.m1_layout != "auto":
+        from tensorpack_amd.packer import LAYOUT_MX, LAYOUT_V1
+        M1_LAYOUT = {"v1": LAYOUT_V1, "mx": LAYOUT_MX}[args.m1_layout]
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
@@ -701,24 +890,35 @@ def main():
             t0 = time.time()
             A[name] = (wl, wl.allocate())
             log(f"{name} allocation {time.time() - t0:.1f}s, {A[name][1].bits_per_element:.4f} b/w")
-    c3_ms, c3_traffic = None, None
+    c3_ms, c3_traffic, c3_traffic512 = None, None, None
     if "c3" in want:
         mats, allocs = A["c3"]
         c3_ms = [MTCMatrix.from_quadtree(a, w.W) for a, w in zip(allocs, mats)]
         if not args.no_traffic:
-            c3_traffic = traffic_passes_batch([m.panel_stream(m.decode_chunk_rows(1)) for m in c3_ms],
+            c3_traffic = traffic_passes_batch([m.panel_stream(m.decode_chunk_rows(1), m1_layout(m)) for m in c3_ms],
                                               {w.W.shape[0]: c3_x(w.W.shape[0], 1) for w in mats})
+            c3_traffic512 = traffic_passes_tiles([m.tile_stream() for m in c3_ms],
+                                                 {w.W.shape[0]: bf16_bits(c3_x(w.W.shape[0], 512)) for w in mats})
+    m4, traffic4 = None, None
+    if "c4" in want:
+        wl4, a4 = A["c4"]
+        m4 = MTCMatrix.from_quadtree(a4, wl4.W)
+        if not args.no_traffic:
+            traffic4 = traffic_passes_tiles([m4.tile_stream()], {wl4.W.shape[0]: bf16_bits(wl4.activations(4096))})
     traffic, traffic16, traffic5 = None, None, None
     if "c2" in want and not args.no_traffic:
         wl, alloc = A["c2"]
         m = MTCMatrix.from_quadtree(alloc, wl.W)
-        traffic = traffic_passes(m.panel_stream(m.decode_chunk_rows(1)), wl.activations(1))
+        traffic = traffic_passes(m.panel_stream(m.decode_chunk_rows(1), m1_layout(m)), wl.activations(1))
         if not args.no_m16:
-            traffic16 = traffic_passes(m.panel_stream(m.decode_chunk_rows(16)), wl.activations(16), kernel="k_gemv<16")
+            traffic16 = traffic_passes(m.panel_stream(m.decode_chunk_rows(16), m.decode_layout(16)), wl.activations(16),
+                                       kernel="k_gemv<16")
+    traffic5_256 = None
     if "c5" in want and not args.no_traffic:
         wl5, a5 = A["c5"]
         m5 = MTCMatrix.from_quadtree(a5, wl5.W)
-        traffic5 = traffic_passes(m5.panel_stream(m5.decode_chunk_rows(1)), wl5.activations(1))
+        traffic5 = traffic_passes(m5.panel_stream(m5.decode_chunk_rows(1), m1_layout(m5)), wl5.activations(1))
+        traffic5_256 = traffic_passes_tiles([m5.tile_stream()], {wl5.W.shape[0]: wl5.activations(256)})
 
     import torch
     from tensorpack_amd.device import require_gpu
@@ -726,11 +926,11 @@ def main():
     torch.cuda.set_device(dev)
     if "c2" not in want:                                  # a single detail workload
         if "c3" in want:
-            r = bench_c3(args, *A["c3"], dev, detail=True, ms_=c3_ms, traffic=c3_traffic)
+            r = bench_c3(args, *A["c3"], dev, detail=True, ms_=c3_ms, traffic=c3_traffic, traffic512=c3_traffic512)
             if not args.no_cpu_baseline:
                 r["cpu_baseline"] = cpu_baseline_c3(args, *A["c3"])
         else:
-            r = bench_c5(args, *A["c5"], dev, traffic=traffic5)
+            r = bench_c5(args, *A["c5"], dev, traffic=traffic5, traffic256=traffic5_256)
             if not args.no_cpu_baseline:
                 wl, a = A["c5"]
                 r["cpu_baseline"] = cpu_port_gbs([leaf_arena(a, wl.W)], [wl.activations(1)], a.total_bits / 8.0,
@@ -745,11 +945,11 @@ def main():
         extra["c2_m16"] = c2.pop("m16")
     copy_gbs, copy_small_us = device_copy_rates(dev, c2["packed"])
     if "c4" in want:
-        extra["c4_prefill"] = bench_c4(args, *A["c4"], dev)
+        extra["c4_prefill"] = bench_c4(args, *A["c4"], dev, m4=m4, traffic=traffic4)
     if "c3" in want:
-        extra["c3"] = bench_c3(args, *A["c3"], dev, ms_=c3_ms, traffic=c3_traffic)
+        extra["c3"] = bench_c3(args, *A["c3"], dev, ms_=c3_ms, traffic=c3_traffic, traffic512=c3_traffic512)
     if "c5" in want:
-        extra["c5"] = bench_c5(args, *A["c5"], dev, traffic=traffic5)
+        extra["c5"] = bench_c5(args, *A["c5"], dev, traffic=traffic5, traffic256=traffic5_256)
 
     # ---- CPU baselines (bounded samples on this host's cores) ----
     cpu = None
@@ -811,7 +1011,8 @@ def main():
                      "us_per_call_median_of_10": None if c2["ms_median"] is None else c2["ms_median"] * 1e3,
                      "kernel": "k_gemv<1>", "stream_GBps": ds.device_bytes() / (ms * 1e-3) / 1e9,
                      "algorithmic_GBps": (c2["packed"] + 4.0 * (K + N)) / (ms * 1e-3) / 1e9,
-                     "traffic_detail": traffic},
+                     "traffic_detail": None if traffic is None else
+                     dict(traffic, issue_ratios=issue_ratios(traffic, K * N))},
         "cpu_baseline": cpu,
         "extra": extra,
     }
