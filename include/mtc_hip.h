@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MTC_ABI_VERSION 10
+#define MTC_ABI_VERSION 11
 
 enum {
   MTC_OK = 0,
@@ -52,6 +52,8 @@ enum { MTC_DTYPE_F32 = 0, MTC_DTYPE_BF16 = 1 };
 #define MTC_FLAG_FP32_SCALES 0x1u   /* leaf scales come from `leaf_scale`, not the descriptor word */
 #define MTC_FLAG_MX_LAYOUT 0x2u     /* payload in the matrix-core decode layout (see below); decoded one X
                                        row per block on v_mfma_f32_4x4x4_16b_f16 */
+#define MTC_FLAG_COLS_GATHERED 0x4u /* tile stream: columns in the original order, 8-word cells with a bf16
+                                       scale pair per column, no col_perm (see mtc_tile_desc) */
 
 /*
  * Panel stream. The (permuted) weight Wp is K x N (reduction x output). It is
@@ -258,7 +260,11 @@ int mtc_gemv_f32_batch(const void* host_plan, const void* device_plan, void* hip
  */
 typedef struct mtc_tile_desc {
   uint32_t abi_version;
-  uint32_t flags;          /* MTC_FLAG_FP32_SCALES: 4-word cells with fp32 scales */
+  uint32_t flags;          /* MTC_FLAG_FP32_SCALES: 4-word cells with fp32 scales;
+                              MTC_FLAG_COLS_GATHERED: 8-word cells (word 0, then per column j a
+                              bf16 top scale | bf16 bottom scale << 16, 3 zero words) whose
+                              columns are Y's own (a QT-P matrix packed with its columns back in
+                              the original order), so col_perm must be NULL */
   int32_t K;
   int32_t N;
   int32_t n_ksteps;        /* ceil(K / 64) */

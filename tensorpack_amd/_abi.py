@@ -2,13 +2,14 @@
 
 import ctypes
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 MTC_OK = 0
 MTC_DTYPE_F32 = 0
 MTC_DTYPE_BF16 = 1
 MTC_FLAG_FP32_SCALES = 0x1
 MTC_FLAG_MX_LAYOUT = 0x2                 # payload in the matrix-core decode layout (packer.LAYOUT_MX)
+MTC_FLAG_COLS_GATHERED = 0x4             # tile stream with columns in the original order (8-word cells)
 
 ERROR_NAMES = {
     -1: "MTC_E_NULL", -2: "MTC_E_DESC", -3: "MTC_E_SHAPE", -4: "MTC_E_DTYPE",

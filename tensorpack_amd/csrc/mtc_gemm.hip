@@ -52,6 +52,20 @@ constexpr uint32_t kOutOfRange = 0xFFFFFF00u;               // byte offset past 
 constexpr int kRowGroup = 8;                // row tiles per launch-order group (L2 reuse of B)
 constexpr int kXcds = 8;
 constexpr int kStageThreads = 256;
+// Cell formats of a tile stream (its descriptor flags): bf16 scale pair (2 words), fp32 scales
+// (4 words), gathered columns with a bf16 scale pair per column (8 words).
+constexpr int kCellBf16 = 0, kCellFp32 = 1, kCellCols = 2;
+__host__ __device__ constexpr int cell_words(int cf) { return cf == kCellFp32 ? 4 : cf == kCellCols ? 8 : 2; }
+inline int cell_format(const mtc_tile_desc* d) {
+  return (d->flags & MTC_FLAG_FP32_SCALES) ? kCellFp32 : (d->flags & MTC_FLAG_COLS_GATHERED) ? kCellCols : kCellBf16;
+}
+// The kernel of a group or batch whose members have cell formats a and b: bf16-pair and
+// gathered-column streams share the kCellCols kernel; fp32-scale streams mix with neither (-1).
+inline int joint_cell_format(int a, int b) {
+  if (a == b) return a;
+  if (a == kCellFp32 || b == kCellFp32) return -1;
+  return kCellCols;
+}
 
 static_assert(kTN / 4 * (kTK / 8) == kCells, "one cell per (column group, row block)");
 static_assert(2 * kProducers == kCells, "two cells per producer thread");
@@ -130,28 +144,31 @@ __device__ __forceinline__ uint32_t dec_shorts(uint32_t v, float s, float c) {
   return pk_bf16(__builtin_fmaf((float)(v & 0xFFFFu), s, c), __builtin_fmaf((float)(v >> 16), s, c));
 }
 
-// The 4 columns (8 rows each, bf16) of one cell from its payload words.
+// The 4 columns (8 rows each, bf16) of one cell from its payload words; column j's top rows
+// (0-3) scaled by st[j], its bottom rows by sb[j] (all four equal unless the columns are gathered).
 // value = (u - offset) * s evaluated as fma(u, s, -offset * s): exact in fp32.
-__device__ __forceinline__ void decode_cell(uint32_t cls, const u32x4_t* pw, float st, float sb, u32x4_t* out) {
+__device__ __forceinline__ void decode_cell(uint32_t cls, const u32x4_t* pw, const float (&st)[4],
+                                            const float (&sb)[4], u32x4_t* out) {
   if (cls == 0) {
-    const float ct = -8.0f * st, cb = -8.0f * sb;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t x = pw[0][j];
-      out[j] = dec_bytes(opaque(x & 0x0F0F0F0Fu), opaque((x >> 4) & 0x0F0F0F0Fu), st, ct, sb, cb);
+      out[j] = dec_bytes(opaque(x & 0x0F0F0F0Fu), opaque((x >> 4) & 0x0F0F0F0Fu), st[j], -8.0f * st[j], sb[j],
+                         -8.0f * sb[j]);
     }
   } else if (cls == 1) {
-    const float ct = -128.0f * st, cb = -128.0f * sb;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) out[j] = dec_bytes(pw[j >> 1][(2 * j) & 3], pw[j >> 1][(2 * j + 1) & 3], st, ct, sb, cb);
+    for (int j = 0; j < 4; ++j)
+      out[j] = dec_bytes(pw[j >> 1][(2 * j) & 3], pw[j >> 1][(2 * j + 1) & 3], st[j], -128.0f * st[j], sb[j],
+                         -128.0f * sb[j]);
   } else if (cls == 2) {
-    const float ct = -32768.0f * st, cb = -32768.0f * sb;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      out[j].x = dec_shorts(pw[j].x, st, ct);
-      out[j].y = dec_shorts(pw[j].y, st, ct);
-      out[j].z = dec_shorts(pw[j].z, sb, cb);
-      out[j].w = dec_shorts(pw[j].w, sb, cb);
+      const float ct = -32768.0f * st[j], cb = -32768.0f * sb[j];
+      out[j].x = dec_shorts(pw[j].x, st[j], ct);
+      out[j].y = dec_shorts(pw[j].y, st[j], ct);
+      out[j].z = dec_shorts(pw[j].z, sb[j], cb);
+      out[j].w = dec_shorts(pw[j].w, sb[j], cb);
     }
   } else {
 #pragma unroll
@@ -188,12 +205,17 @@ __device__ __forceinline__ bool tile_of_block(int bx, int n_row_tiles, int n_ct,
 // One output tile block of matrix `d`: output tile (rt, ct), K split by.
 // TM: output rows of the block (256, or 128 / 64 for short X, whose full-height tiles are too
 // few to fill the chip). The 8 consumer waves are 2 x 4: TM / 2 rows x 64 columns each.
-template <bool kFS, int kYDT, int TM = kTM>
+template <int kCF, int kYDT, int TM = kTM>
 __device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const int rt, const int ct, const int by,
                                                 const __bf16* __restrict__ X, int64_t ldx, void* __restrict__ Y,
                                                 int64_t ldy, int M, int steps_per_split, float* __restrict__ part) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-  constexpr int CW = kFS ? 4 : 2;
+  constexpr int CW = cell_words(kCF);                     // words loaded per cell
+  // words per cell of this stream: the kCellCols kernel also runs bf16-pair streams (a group or
+  // batch that mixes them with gathered-column ones); their cells are 2 words, and the words a
+  // load reads past a cell are not used
+  const bool gcols = kCF == kCellCols && (d.flags & MTC_FLAG_COLS_GATHERED) != 0;
+  const int cw = kCF == kCellCols && !gcols ? 2 : CW;
   static_assert(TM == 256 || TM == 128 || TM == 64, "row tiles of 256, 128 or 64 rows");
   constexpr int DMA = TM / 8 / kConsumerWaves;             // 1 KiB (8-row) A copies per consumer wave
   constexpr int RW = TM / 2, RI = RW / 32;                 // rows per consumer wave, 32-row MFMA blocks
@@ -316,8 +338,8 @@ __device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const in
   // read past the buffer's end and return zeros): with no per-lane branches around
   // loads, the compiler's waits count exactly, so a step waits only for the loads
   // issued a step earlier, never for the ones it has just issued.
-  const __amdgpu_buffer_rsrc_t cell_r = buffer_of(d.cells + ((size_t)ct * d.n_ksteps + kb0) * kCells * CW,
-                                                  (int64_t)nks * kCells * CW * 4);
+  const __amdgpu_buffer_rsrc_t cell_r = buffer_of(d.cells + ((size_t)ct * d.n_ksteps + kb0) * kCells * cw,
+                                                  (int64_t)nks * kCells * cw * 4);
   const __amdgpu_buffer_rsrc_t pay_r = buffer_of(d.payload, d.payload_dwords * 4);
   uint32_t sa0[CW], sa1[CW], sb0[CW], sb1[CW];
   uint32_t base_a = 0, base_b = 0;
@@ -328,16 +350,19 @@ __device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const in
       w[0] = v.x;
       w[1] = v.y;
     } else {
-      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(cell_r, off, 0, 0);
-      w[0] = v.x;
-      w[1] = v.y;
-      w[2] = v.z;
-      w[3] = v.w;
+#pragma unroll
+      for (int h = 0; h < CW / 4; ++h) {
+        const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(cell_r, off + 16u * h, 0, 0);
+        w[4 * h + 0] = v.x;
+        w[4 * h + 1] = v.y;
+        w[4 * h + 2] = v.z;
+        w[4 * h + 3] = v.w;
+      }
     }
   };
   auto load_desc = [&](int ks, uint32_t (&w0)[CW], uint32_t (&w1)[CW], uint32_t& base) {
-    load_words((uint32_t)((ks * kCells + p) * CW) * 4u, w0);
-    load_words((uint32_t)((ks * kCells + p + kProducers) * CW) * 4u, w1);
+    load_words((uint32_t)((ks * kCells + p) * cw) * 4u, w0);
+    load_words((uint32_t)((ks * kCells + p + kProducers) * cw) * 4u, w1);
     base = step_off[ks];
   };
   auto load_cell = [&](const uint32_t (&w)[CW], uint32_t base, u32x4_t (&q)[4]) {
@@ -353,13 +378,17 @@ __device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const in
     load_cell(w1, base, q1);
   };
   auto stage_cell = [&](unsigned char* bs, const uint32_t (&w)[CW], const u32x4_t (&q)[4]) {
-    float st, sb;
-    if constexpr (kFS) {
-      st = __uint_as_float(w[1]);
-      sb = __uint_as_float(w[2]);
-    } else {
-      st = __uint_as_float(w[1] << 16);
-      sb = __uint_as_float(w[1] & 0xFFFF0000u);
+    float st[4], sb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (kCF == kCellFp32) {
+        st[j] = __uint_as_float(w[1]);
+        sb[j] = __uint_as_float(w[2]);
+      } else {
+        const uint32_t sw = gcols ? w[1 + j] : w[1];          // column j's scales, or the cell's
+        st[j] = __uint_as_float(sw << 16);
+        sb[j] = __uint_as_float(sw & 0xFFFF0000u);
+      }
     }
     const uint32_t pos = w[0] >> 16;
     const int col = (int)(pos >> 3) * 4, seg = (int)(pos & 7u);
@@ -406,14 +435,14 @@ __device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const in
 }
 
 // One output tile block of matrix `d`: output tile (rt, ct) of TM rows, K split by.
-template <bool kFS, int kYDT, int TM>
+template <int kCF, int kYDT, int TM>
 __global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, const __bf16* __restrict__ X,
                                                         int64_t ldx, void* __restrict__ Y, int64_t ldy, int M,
                                                         int n_row_tiles, int tiles_per_xcd, int steps_per_split,
                                                         float* __restrict__ part) {
   int rt, ct;
   if (!tile_of_block((int)blockIdx.x, n_row_tiles, d.n_col_tiles, tiles_per_xcd, d.col_perm && !part, rt, ct)) return;
-  gemm_tile_block<kFS, kYDT, TM>(d, rt, ct, (int)blockIdx.y, X, ldx, Y, ldy, M, steps_per_split, part);
+  gemm_tile_block<kCF, kYDT, TM>(d, rt, ct, (int)blockIdx.y, X, ldx, Y, ldy, M, steps_per_split, part);
 }
 
 // Up to kMaxGroup matrices that read the same X, in one launch of each kernel: member i owns
@@ -433,7 +462,7 @@ struct GemmGroup {
   int start[kMaxGroup + 1];
 };
 
-template <bool kFS, int kYDT>
+template <int kCF, int kYDT>
 __global__ __launch_bounds__(kThreads) void k_gemm_tile_group(const GemmGroup g, int M, int n_row_tiles) {
   int i = 0;
 #pragma unroll
@@ -443,7 +472,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile_group(const GemmGroup g,
   if (!tile_of_block((int)blockIdx.x - g.start[i], n_row_tiles, g.d[i].n_col_tiles, g.tiles_per_xcd[i],
                      g.d[i].col_perm && !g.part[i], rt, ct))
     return;
-  gemm_tile_block<kFS, kYDT>(g.d[i], rt, ct, (int)blockIdx.y, g.X[i], g.ldx[i], g.Y[i], g.ldy[i], M,
+  gemm_tile_block<kCF, kYDT>(g.d[i], rt, ct, (int)blockIdx.y, g.X[i], g.ldx[i], g.Y[i], g.ldy[i], M,
                              g.steps_per_split[i], g.part[i]);
 }
 
@@ -627,13 +656,13 @@ struct GemmBatchItem {
 
 constexpr uint32_t kNoItem = 0xFFFFFFFFu;   // a block table entry with no work
 
-template <bool kFS, int kYDT>
+template <int kCF, int kYDT>
 __global__ __launch_bounds__(kThreads) void k_gemm_tile_batch(const GemmBatchItem* __restrict__ items,
                                                               const uint2* __restrict__ blocks, int M) {
   const uint2 e = blocks[blockIdx.x];
   if (e.x == kNoItem) return;                               // padding of an XCD's block list
   const GemmBatchItem& it = items[e.x];
-  gemm_tile_block<kFS, kYDT>(it.d, (int)(e.y & 0xFFFu), (int)((e.y >> 12) & 0xFFFu), (int)(e.y >> 24), it.X, it.ldx,
+  gemm_tile_block<kCF, kYDT>(it.d, (int)(e.y & 0xFFFu), (int)((e.y >> 12) & 0xFFFu), (int)(e.y >> 24), it.X, it.ldx,
                              it.Y, it.ldy, M, it.steps_per_split, it.splits > 1 ? it.part : nullptr);
 }
 
@@ -668,11 +697,14 @@ int check_tile_desc(const mtc_tile_desc* d) {
   if (d->n_ksteps != (d->K + kTK - 1) / kTK || d->n_col_tiles != (d->N + kTN - 1) / kTN)
     return fail(MTC_E_DESC, "n_ksteps=%d n_col_tiles=%d inconsistent with K=%d N=%d", d->n_ksteps, d->n_col_tiles,
                 d->K, d->N);
-  if (d->flags & ~MTC_FLAG_FP32_SCALES) return fail(MTC_E_DESC, "unknown flags 0x%x", d->flags);
+  if (d->flags & ~(MTC_FLAG_FP32_SCALES | MTC_FLAG_COLS_GATHERED)) return fail(MTC_E_DESC, "unknown flags 0x%x", d->flags);
+  if ((d->flags & MTC_FLAG_COLS_GATHERED) && ((d->flags & MTC_FLAG_FP32_SCALES) || d->col_perm))
+    return fail(MTC_E_DESC, "a gathered-column tile stream has bf16 scales and no col_perm (its columns are in "
+                "the original order)");
   if (!d->cells || !d->step_off || !d->payload) return fail(MTC_E_NULL, "tile stream arrays missing");
   if (d->payload_dwords < 4) return fail(MTC_E_DESC, "payload_dwords=%lld", (long long)d->payload_dwords);
   // payload and cells are addressed with 32-bit byte offsets (buffer resources of at most 2 GiB)
-  const int64_t cell_bytes = (int64_t)d->n_ksteps * d->n_col_tiles * kCells * ((d->flags & MTC_FLAG_FP32_SCALES) ? 16 : 8);
+  const int64_t cell_bytes = (int64_t)d->n_ksteps * d->n_col_tiles * kCells * 4 * cell_words(cell_format(d));
   if (d->payload_dwords > 0x7FFFFFFF / 4 || cell_bytes > 0x7FFFFFFF)
     return fail(MTC_E_DESC, "tile stream arrays exceed 2 GiB (payload_dwords=%lld, %lld bytes of cells)",
                 (long long)d->payload_dwords, (long long)cell_bytes);
@@ -747,7 +779,7 @@ size_t partial_bytes(const mtc_tile_desc* d, int M) {
   return splits > 1 ? (size_t)splits * M * d->N * 4 : 0;
 }
 
-template <bool kFS, int kYDT>
+template <int kCF, int kYDT>
 int launch_tile(const mtc_tile_desc* d, const __bf16* X, int64_t ldx, void* Y, int64_t ldy, int M, float* part,
                 hipStream_t st) {
   if ((size_t)kLdsBytes > mtc::host::device_lds_limit())
@@ -756,9 +788,9 @@ int launch_tile(const mtc_tile_desc* d, const __bf16* X, int64_t ldx, void* Y, i
   if (ldx >= ((int64_t)1 << 31) / (2 * kTM))
     return fail(MTC_E_SHAPE, "ldx=%lld too large for 32-bit X tile offsets", (long long)ldx);
   const TilePlan p = tile_plan(d, M);
-  const void* fn = p.tm == 256 ? reinterpret_cast<const void*>(&k_gemm_tile<kFS, kYDT, 256>)
-                   : p.tm == 128 ? reinterpret_cast<const void*>(&k_gemm_tile<kFS, kYDT, 128>)
-                                 : reinterpret_cast<const void*>(&k_gemm_tile<kFS, kYDT, 64>);
+  const void* fn = p.tm == 256 ? reinterpret_cast<const void*>(&k_gemm_tile<kCF, kYDT, 256>)
+                   : p.tm == 128 ? reinterpret_cast<const void*>(&k_gemm_tile<kCF, kYDT, 128>)
+                                 : reinterpret_cast<const void*>(&k_gemm_tile<kCF, kYDT, 64>);
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
   if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
   const int n_row_tiles = (M + p.tm - 1) / p.tm;
@@ -769,13 +801,13 @@ int launch_tile(const mtc_tile_desc* d, const __bf16* X, int64_t ldx, void* Y, i
   float* const pt = splits > 1 ? part : nullptr;
   const dim3 grid(tiles_per_xcd * kXcds, splits);
   if (p.tm == 256)
-    hipLaunchKernelGGL((k_gemm_tile<kFS, kYDT, 256>), grid, dim3(kThreads), kLdsBytes, st, *d, X, ldx, Y, ldy, M,
+    hipLaunchKernelGGL((k_gemm_tile<kCF, kYDT, 256>), grid, dim3(kThreads), kLdsBytes, st, *d, X, ldx, Y, ldy, M,
                        n_row_tiles, tiles_per_xcd, per, pt);
   else if (p.tm == 128)
-    hipLaunchKernelGGL((k_gemm_tile<kFS, kYDT, 128>), grid, dim3(kThreads), kLdsBytes, st, *d, X, ldx, Y, ldy, M,
+    hipLaunchKernelGGL((k_gemm_tile<kCF, kYDT, 128>), grid, dim3(kThreads), kLdsBytes, st, *d, X, ldx, Y, ldy, M,
                        n_row_tiles, tiles_per_xcd, per, pt);
   else
-    hipLaunchKernelGGL((k_gemm_tile<kFS, kYDT, 64>), grid, dim3(kThreads), kLdsBytes, st, *d, X, ldx, Y, ldy, M,
+    hipLaunchKernelGGL((k_gemm_tile<kCF, kYDT, 64>), grid, dim3(kThreads), kLdsBytes, st, *d, X, ldx, Y, ldy, M,
                        n_row_tiles, tiles_per_xcd, per, pt);
   int rc = check_launch("k_gemm_tile");
   if (rc || splits == 1) return rc;
@@ -793,18 +825,18 @@ size_t group_ws_bytes(const mtc_tile_desc* const* descs, int n, int M, int x_dty
   return b;
 }
 
-template <bool kFS, int kYDT>
+template <int kCF, int kYDT>
 int launch_tile_group(GemmGroup& g, int n, int M, const ReduceGroup& rg, int n_red, hipStream_t st) {
   if ((size_t)kLdsBytes > mtc::host::device_lds_limit())
     return fail(MTC_E_SHAPE, "prefill kernel needs %d B of LDS per block, device has %zu", kLdsBytes,
                 mtc::host::device_lds_limit());
-  const void* fn = reinterpret_cast<const void*>(&k_gemm_tile_group<kFS, kYDT>);
+  const void* fn = reinterpret_cast<const void*>(&k_gemm_tile_group<kCF, kYDT>);
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
   if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
   const int n_row_tiles = (M + kTM - 1) / kTM;
   int max_splits = 1;
   for (int i = 0; i < n; ++i) max_splits = std::max(max_splits, g.splits[i]);
-  hipLaunchKernelGGL((k_gemm_tile_group<kFS, kYDT>), dim3(g.start[n], max_splits), dim3(kThreads), kLdsBytes, st, g, M,
+  hipLaunchKernelGGL((k_gemm_tile_group<kCF, kYDT>), dim3(g.start[n], max_splits), dim3(kThreads), kLdsBytes, st, g, M,
                      n_row_tiles);
   int rc = check_launch("k_gemm_tile_group");
   if (rc || n_red == 0) return rc;
@@ -823,7 +855,7 @@ struct GemmBatchHeader {
   int32_t M;
   int32_t x_dtype;
   int32_t y_dtype;
-  int32_t fs;
+  int32_t cf;             // cell format of every item (kCellBf16, kCellFp32, kCellCols)
   int32_t n_stage;
   int32_t n_reduce;
   int32_t stage_blocks_x;
@@ -851,7 +883,7 @@ int build_gemm_batch_plan(const mtc_gemm_batch_item* items, int n, int M, int x_
   if (y_dtype != MTC_DTYPE_F32 && y_dtype != MTC_DTYPE_BF16) return fail(MTC_E_DTYPE, "y_dtype=%d", y_dtype);
   const int n_row_tiles = (M + kTM - 1) / kTM;
   int64_t total_tiles = 0;
-  bool fs = false;
+  int cf = kCellBf16;
   for (int i = 0; i < n; ++i) {
     const mtc_tile_desc* d = items[i].desc;
     int rc = check_tile_desc(d);
@@ -864,9 +896,8 @@ int build_gemm_batch_plan(const mtc_gemm_batch_item* items, int n, int M, int x_
     if (items[i].ldx < d->K || items[i].ldy < d->N)
       return fail(MTC_E_SHAPE, "batch item %d: ldx=%lld < K or ldy=%lld < N", i, (long long)items[i].ldx,
                   (long long)items[i].ldy);
-    const bool fsi = (d->flags & MTC_FLAG_FP32_SCALES) != 0;
-    if (i == 0) fs = fsi;
-    if (fsi != fs) return fail(MTC_E_SHAPE, "batch item %d differs from item 0 in scale format", i);
+    cf = i == 0 ? cell_format(d) : joint_cell_format(cf, cell_format(d));
+    if (cf < 0) return fail(MTC_E_SHAPE, "batch item %d differs from the items before it in scale format", i);
     if (!needs_staging(d, x_dtype) && (items[i].ldx % 8 || (reinterpret_cast<uintptr_t>(items[i].X) & 15)))
       return fail(MTC_E_SHAPE, "batch item %d: bf16 X read in place needs 16-byte aligned rows", i);
     const int64_t ldx_used = needs_staging(d, x_dtype) ? d->K : items[i].ldx;
@@ -973,7 +1004,7 @@ int build_gemm_batch_plan(const mtc_gemm_batch_item* items, int n, int M, int x_
   h->M = M;
   h->x_dtype = x_dtype;
   h->y_dtype = y_dtype;
-  h->fs = fs;
+  h->cf = cf;
   h->n_stage = n_stage;
   h->n_reduce = n_reduce;
   h->stage_blocks_x = stage_bx;
@@ -1024,16 +1055,16 @@ int build_gemm_batch_plan(const mtc_gemm_batch_item* items, int n, int M, int x_
   return ok();
 }
 
-template <bool kFS, int kYDT>
+template <int kCF, int kYDT>
 int launch_tile_batch(const GemmBatchHeader* h, const GemmBatchItem* items, const uint2* blocks,
                       const uint32_t* reduce_list, hipStream_t st) {
   if ((size_t)kLdsBytes > mtc::host::device_lds_limit())
     return fail(MTC_E_SHAPE, "prefill kernel needs %d B of LDS per block, device has %zu", kLdsBytes,
                 mtc::host::device_lds_limit());
-  const void* fn = reinterpret_cast<const void*>(&k_gemm_tile_batch<kFS, kYDT>);
+  const void* fn = reinterpret_cast<const void*>(&k_gemm_tile_batch<kCF, kYDT>);
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
   if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-  hipLaunchKernelGGL((k_gemm_tile_batch<kFS, kYDT>), dim3((unsigned)h->n_blocks), dim3(kThreads), kLdsBytes, st, items,
+  hipLaunchKernelGGL((k_gemm_tile_batch<kCF, kYDT>), dim3((unsigned)h->n_blocks), dim3(kThreads), kLdsBytes, st, items,
                      blocks, h->M);
   int rc = check_launch("k_gemm_tile_batch");
   if (rc || h->n_reduce == 0) return rc;
@@ -1067,11 +1098,18 @@ int launch_gemm_batch(const void* host_plan, const void* device_plan, hipStream_
     const int rc = check_launch("k_stage_x_batch");
     if (rc) return rc;
   }
-  if (h->fs)
-    return h->y_dtype == MTC_DTYPE_F32 ? launch_tile_batch<true, MTC_DTYPE_F32>(h, items, blocks, reduce_list, st)
-                                       : launch_tile_batch<true, MTC_DTYPE_BF16>(h, items, blocks, reduce_list, st);
-  return h->y_dtype == MTC_DTYPE_F32 ? launch_tile_batch<false, MTC_DTYPE_F32>(h, items, blocks, reduce_list, st)
-                                     : launch_tile_batch<false, MTC_DTYPE_BF16>(h, items, blocks, reduce_list, st);
+  const bool f32 = h->y_dtype == MTC_DTYPE_F32;
+  switch (h->cf) {
+    case kCellFp32:
+      return f32 ? launch_tile_batch<kCellFp32, MTC_DTYPE_F32>(h, items, blocks, reduce_list, st)
+                 : launch_tile_batch<kCellFp32, MTC_DTYPE_BF16>(h, items, blocks, reduce_list, st);
+    case kCellCols:
+      return f32 ? launch_tile_batch<kCellCols, MTC_DTYPE_F32>(h, items, blocks, reduce_list, st)
+                 : launch_tile_batch<kCellCols, MTC_DTYPE_BF16>(h, items, blocks, reduce_list, st);
+    default:
+      return f32 ? launch_tile_batch<kCellBf16, MTC_DTYPE_F32>(h, items, blocks, reduce_list, st)
+                 : launch_tile_batch<kCellBf16, MTC_DTYPE_BF16>(h, items, blocks, reduce_list, st);
+  }
 }
 
 }  // namespace
@@ -1130,13 +1168,18 @@ MTC_API int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, in
     xb = reinterpret_cast<const __bf16*>(workspace);
     ldb = d->K;
   }
-  const bool fs = d->flags & MTC_FLAG_FP32_SCALES;
-  if (fs) {
-    return y_dtype == MTC_DTYPE_F32 ? launch_tile<true, MTC_DTYPE_F32>(d, xb, ldb, Y, ldy, M, part, st)
-                                    : launch_tile<true, MTC_DTYPE_BF16>(d, xb, ldb, Y, ldy, M, part, st);
+  const bool f32 = y_dtype == MTC_DTYPE_F32;
+  switch (cell_format(d)) {
+    case kCellFp32:
+      return f32 ? launch_tile<kCellFp32, MTC_DTYPE_F32>(d, xb, ldb, Y, ldy, M, part, st)
+                 : launch_tile<kCellFp32, MTC_DTYPE_BF16>(d, xb, ldb, Y, ldy, M, part, st);
+    case kCellCols:
+      return f32 ? launch_tile<kCellCols, MTC_DTYPE_F32>(d, xb, ldb, Y, ldy, M, part, st)
+                 : launch_tile<kCellCols, MTC_DTYPE_BF16>(d, xb, ldb, Y, ldy, M, part, st);
+    default:
+      return f32 ? launch_tile<kCellBf16, MTC_DTYPE_F32>(d, xb, ldb, Y, ldy, M, part, st)
+                 : launch_tile<kCellBf16, MTC_DTYPE_BF16>(d, xb, ldb, Y, ldy, M, part, st);
   }
-  return y_dtype == MTC_DTYPE_F32 ? launch_tile<false, MTC_DTYPE_F32>(d, xb, ldb, Y, ldy, M, part, st)
-                                  : launch_tile<false, MTC_DTYPE_BF16>(d, xb, ldb, Y, ldy, M, part, st);
 }
 
 MTC_API size_t mtc_gemm_group_workspace_bytes(const mtc_tile_desc* const* descs, int n, int M, int x_dtype) {
@@ -1228,11 +1271,18 @@ MTC_API int mtc_gemm_bf16_group(const mtc_tile_desc* const* descs, int n, const 
     int rc = check_launch("k_stage_x_group");
     if (rc) return rc;
   }
-  const bool fs = descs[0]->flags & MTC_FLAG_FP32_SCALES;
-  if (fs) {
-    return y_dtype == MTC_DTYPE_F32 ? launch_tile_group<true, MTC_DTYPE_F32>(g, n, M, rg, n_red, st)
-                                    : launch_tile_group<true, MTC_DTYPE_BF16>(g, n, M, rg, n_red, st);
+  const bool f32 = y_dtype == MTC_DTYPE_F32;
+  int cf = cell_format(descs[0]);
+  for (int i = 1; i < n; ++i) cf = joint_cell_format(cf, cell_format(descs[i]));
+  switch (cf) {
+    case kCellFp32:
+      return f32 ? launch_tile_group<kCellFp32, MTC_DTYPE_F32>(g, n, M, rg, n_red, st)
+                 : launch_tile_group<kCellFp32, MTC_DTYPE_BF16>(g, n, M, rg, n_red, st);
+    case kCellCols:
+      return f32 ? launch_tile_group<kCellCols, MTC_DTYPE_F32>(g, n, M, rg, n_red, st)
+                 : launch_tile_group<kCellCols, MTC_DTYPE_BF16>(g, n, M, rg, n_red, st);
+    default:
+      return f32 ? launch_tile_group<kCellBf16, MTC_DTYPE_F32>(g, n, M, rg, n_red, st)
+                 : launch_tile_group<kCellBf16, MTC_DTYPE_BF16>(g, n, M, rg, n_red, st);
   }
-  return y_dtype == MTC_DTYPE_F32 ? launch_tile_group<false, MTC_DTYPE_F32>(g, n, M, rg, n_red, st)
-                                  : launch_tile_group<false, MTC_DTYPE_BF16>(g, n, M, rg, n_red, st);
 }

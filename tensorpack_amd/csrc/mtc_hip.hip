@@ -1437,9 +1437,21 @@ size_t gemv_lds_bytes(const mtc_stream_desc* d, int MT) {
   return gemv_lds_bytes(d->K, d->chunk_rows, d->row_perm != nullptr, MT);
 }
 
+// The decode block of an M tile of MT rows fits the device (LDS, matrix-core X staging).
+int check_gemv_fits(const mtc_stream_desc* d, int MT) {
+  const size_t shmem = gemv_lds_bytes(d, MT);
+  const size_t limit = device_lds_limit();
+  if (shmem > limit || !mfma_rows_fit(MT, d->chunk_rows))
+    return fail(MTC_E_SHAPE, "fp32 path: %d rows x chunk_rows=%d needs %zu B of LDS (limit %zu); "
+                "use a stream with smaller chunk_rows", MT, d->chunk_rows, shmem, limit);
+  return MTC_OK;
+}
+
 template <int MT>
 int launch_gemv(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y, int64_t ldy, int M, void* ws,
                 hipStream_t st) {
+  const int fits = check_gemv_fits(d, MT);          // before any launch
+  if (fits) return fits;
   size_t cb = 0, xt_off = 0;
   gemv_ws_layout(d, M, MT, &cb, &xt_off);
   uint32_t* counters = reinterpret_cast<uint32_t*>(ws);
@@ -1453,10 +1465,6 @@ int launch_gemv(const mtc_stream_desc* d, const float* X, int64_t ldx, float* Y,
     if (rc) return rc;
   }
   const size_t shmem = gemv_lds_bytes(d, MT);
-  const size_t limit = device_lds_limit();
-  if (shmem > limit || !mfma_rows_fit(MT, d->chunk_rows))
-    return fail(MTC_E_SHAPE, "fp32 path: %d rows x chunk_rows=%d needs %zu B of LDS (limit %zu); "
-                "use a stream with smaller chunk_rows", MT, d->chunk_rows, shmem, limit);
   const bool fs = d->leaf_scale != nullptr;
   const GemvShape shape = gemv_shape(MT, d);
   const void* kern = gemv_kernel<MT, false>(fs, shape);
@@ -1768,12 +1776,17 @@ MTC_API int mtc_gemv_f32_noalloc(const mtc_stream_desc* d, const float* X, int64
   if (need > kScratchBytes)
     return fail(MTC_E_WORKSPACE, "M=%d over %d row chunks needs %zu bytes of split-K scratch; the static scratch "
                 "holds %zu (use mtc_gemv_f32 with a workspace)", M, d->n_chunks, need, kScratchBytes);
+  rc = check_gemv_fits(d, mt);                       // fails before any launch
+  if (rc) return rc;
   hipStream_t st = as_stream(hip_stream);
   void* ws = nullptr;
   if (need) {
     rc = scratch_address(&ws);
     if (rc) return rc;
-    // the counters start at zero (a fill kernel: no memset node if the caller captures this)
+  }
+  if (d->n_chunks > 1) {
+    // the split-K counters start at zero (a fill kernel: no memset node if the caller captures
+    // this); single-chunk streams have none (their scratch holds only the staged X, if any)
     const int64_t words = (int64_t)(counter_bytes / sizeof(float));
     hipLaunchKernelGGL(k_fill_zero, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st,
                        reinterpret_cast<float*>(ws), words);

@@ -278,7 +278,8 @@ class DeviceTiles:
         self.row_perm, self.col_perm = up(ts.row_perm), up(ts.col_perm)
         d = _abi.MtcTileDesc()
         d.abi_version = _abi.ABI_VERSION
-        d.flags = _abi.MTC_FLAG_FP32_SCALES if ts.fp32_scales else 0
+        d.flags = (_abi.MTC_FLAG_FP32_SCALES if ts.fp32_scales else 0) | \
+                  (_abi.MTC_FLAG_COLS_GATHERED if ts.cols_gathered else 0)
         d.K, d.N, d.n_ksteps, d.n_col_tiles = ts.K, ts.N, ts.n_ksteps, ts.n_col_tiles
         d.payload_dwords = int(ts.payload.size)
         ptr = lambda t: None if t is None else t.data_ptr()

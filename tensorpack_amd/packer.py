@@ -35,7 +35,7 @@ LEAF_PAD = 1 << 13
 ROW_BITS = 10                          # leaf word: row/4 in bits 0-9
 MAX_CHUNK_ROWS = 4 << ROW_BITS         # 4096
 UNIT_HDR_WORDS = 32
-STREAM_FORMAT = 10                     # panel stream layout version (matches the C-ABI version)
+STREAM_FORMAT = 10                     # panel stream layout version (the C-ABI version that introduced it)
 PAYLOAD_PAD = 4                        # dwords after the last bucket
 STEP_GROUPS = 4                        # column groups one decode step covers
 STEP_LANES = 16                        # lanes (chunks) per column group in a step

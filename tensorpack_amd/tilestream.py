@@ -25,6 +25,15 @@ column group in the tile (0-63) * 8 + row block (0-7); word 1 = bf16 scale of
 the top half | bf16 scale of the bottom half << 16. With fp32 scales a cell is
 4 words: word 0, fp32 top scale, fp32 bottom scale, 0.
 
+Matrices with an output column permutation (QT-P) are packed with their columns
+back in the original order ("gathered columns"): column n of the operand is
+column inv[n] of Wp (inv the inverse of col_perm), so a tile's outputs are
+adjacent columns of Y and its stores need no permutation. The four columns of
+a cell then come from four unrelated leaves, so every column carries its own
+(P, scale) halves: an 8-word cell, word 0 as above (the class is the widest of
+its eight halves), word 1 + j = bf16 top scale | bf16 bottom scale << 16 of
+column j, words 5-7 zero. Only bf16 scales take this form.
+
 Steps are ordered column tile major: step = col_tile * n_ksteps + kstep, so a
 block reads its column tile's cells and payload front to back.
 """
@@ -40,7 +49,7 @@ CELLS = 512
 CLS_W4, CLS_W8, CLS_W16, CLS_Z = 0, 1, 2, 3
 CLS_DWORDS = np.array([4, 8, 16, 0], dtype=np.int64)
 CLS_OFFSET = (8, 128, 32768)
-TILE_FORMAT = 1
+TILE_FORMAT = 2                     # 2: gathered-column cells (8 words) for permuted columns
 PAYLOAD_PAD = 8                     # dwords after the last step (see pack_tiles)
 _WIDTHS = (2, 3, 4, 5, 6, 8, 16)
 
@@ -66,6 +75,11 @@ class TileStream:
     def fp32_scales(self) -> bool:
         return self.cells.shape[1] == 4
 
+    @property
+    def cols_gathered(self) -> bool:
+        """Columns in the original order with a scale per column (8-word cells)."""
+        return self.cells.shape[1] == 8
+
     def nbytes(self) -> int:
         n = self.cells.nbytes + self.step_off.nbytes + self.payload.nbytes
         for a in (self.row_perm, self.col_perm):
@@ -86,14 +100,20 @@ def _scale_words(s: np.ndarray, fp32: bool) -> np.ndarray:
 def pack_tiles(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np.ndarray],
                modes: Dict[int, np.ndarray], scales: Dict[int, np.ndarray], codes_of,
                scale_format: str = "bf16", row_perm: Optional[np.ndarray] = None,
-               col_perm: Optional[np.ndarray] = None) -> TileStream:
-    """Tile stream of the leaves given per level s (see packer.pack_levels for the arguments)."""
+               col_perm: Optional[np.ndarray] = None, gather_cols: Optional[bool] = None) -> TileStream:
+    """Tile stream of the leaves given per level s (see packer.pack_levels for the arguments).
+    gather_cols (default: whenever there is a column permutation and the scales are bf16): pack
+    the columns in the original order with a scale per column, so the stream has no col_perm."""
     K, N = (int(x) for x in shape)
     if N % 32 or K % 8:
         raise ValueError(f"tile stream needs N % 32 == 0 and K % 8 == 0, got {shape}")
     if scale_format not in ("bf16", "fp32"):
         raise ValueError(scale_format)
     fp32 = scale_format == "fp32"
+    if gather_cols is None:
+        gather_cols = col_perm is not None and not fp32
+    if gather_cols and (fp32 or col_perm is None):
+        raise ValueError("gathered columns need a column permutation and bf16 scales")
     nks = -(-K // TILE_ROWS)
     nct = -(-N // TILE_COLS)
     R, G = nks * (TILE_ROWS // 8), nct * (TILE_COLS // 4)          # padded cell grid
@@ -134,7 +154,21 @@ def pack_tiles(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np.
                 St[ii[top] // 2, jj[top]] = sc[top]
                 Pb[ii[~top] // 2, jj[~top]] = P
                 Sb[ii[~top] // 2, jj[~top]] = sc[~top]
-    Pm = np.maximum(Pt, Pb)
+    if gather_cols:
+        # per-column halves, then the original column order: operand column n = Wp column inv[n]
+        inv = np.argsort(np.asarray(col_perm, dtype=np.int64), kind="stable")
+        cols = np.zeros(G * 4, dtype=np.int64)
+        cols[:N] = inv
+
+        def gathered(a):
+            out = np.repeat(a, 4, axis=1)[:, cols]
+            out[:, N:] = 0
+            return out
+        Ptc, Pbc, Stc, Sbc = gathered(Pt), gathered(Pb), gathered(St), gathered(Sb)
+        Q = Q[:, inv]
+        Pm = np.maximum(Ptc, Pbc).reshape(R, G, 4).max(axis=2)
+    else:
+        Pm = np.maximum(Pt, Pb)
     cls = np.full((R, G), CLS_Z, dtype=np.int64)
     cls[(Pm >= 1) & (Pm <= 4)] = CLS_W4
     cls[(Pm >= 5) & (Pm <= 8)] = CLS_W8
@@ -154,7 +188,7 @@ def pack_tiles(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np.
     step_tot = per_step.sum(axis=1)
     off_in = (np.cumsum(per_step, axis=1) - per_step).reshape(-1)
     step_off = np.concatenate([[0], np.cumsum(step_tot)]).astype(np.int64)
-    if (step_off[-1] + PAYLOAD_PAD) * 4 > 0x7FFFFFFF or n_steps * CELLS * 4 * 4 > 0x7FFFFFFF:
+    if (step_off[-1] + PAYLOAD_PAD) * 4 > 0x7FFFFFFF or n_steps * CELLS * 4 * (8 if gather_cols else 4) > 0x7FFFFFFF:
         raise ValueError("tile stream payload or cells exceed the kernels' 32-bit byte offsets (2 GiB); "
                          "split the matrix by column tiles")
     # 8 dwords of tail padding: the device reads 32 bytes per cell whatever its class
@@ -182,10 +216,16 @@ def pack_tiles(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np.
         payload[(dst[:, None] + np.arange(ndw)).reshape(-1)] = words.astype(np.uint32).reshape(-1)
 
     w0 = (off_in.astype(np.uint32) | (c_s.astype(np.uint32) << 14) | (pos_s.astype(np.uint32) << 16))
-    st, sb = St[r_s, g_s], Sb[r_s, g_s]
-    if fp32:
+    if gather_cols:
+        j4 = 4 * g_s[:, None] + np.arange(4)                                    # (n, 4) operand columns
+        sw = _scale_words(Stc[r_s[:, None], j4], False) | (_scale_words(Sbc[r_s[:, None], j4], False) << 16)
+        z = np.zeros_like(w0)
+        cells = np.stack([w0, sw[:, 0], sw[:, 1], sw[:, 2], sw[:, 3], z, z, z], axis=1)
+    elif fp32:
+        st, sb = St[r_s, g_s], Sb[r_s, g_s]
         cells = np.stack([w0, _scale_words(st, True), _scale_words(sb, True), np.zeros_like(w0)], axis=1)
     else:
+        st, sb = St[r_s, g_s], Sb[r_s, g_s]
         cells = np.stack([w0, _scale_words(st, False) | (_scale_words(sb, False) << 16)], axis=1)
     counts = np.bincount(c_s, minlength=4)
     stats = {"payload_bytes": float(4 * step_off[-1]), "cell_bytes": float(cells.nbytes), "n_leaves": float(n_leaves),
@@ -194,7 +234,7 @@ def pack_tiles(shape: Tuple[int, int], sizes: Sequence[int], leaf: Dict[int, np.
     return TileStream(K=K, N=N, n_ksteps=nks, n_col_tiles=nct, cells=np.ascontiguousarray(cells.astype(np.uint32)),
                       step_off=step_off.astype(np.uint32), payload=payload,
                       row_perm=None if row_perm is None else np.ascontiguousarray(row_perm, dtype=np.int32),
-                      col_perm=None if col_perm is None else np.ascontiguousarray(col_perm, dtype=np.int32),
+                      col_perm=None if col_perm is None or gather_cols else np.ascontiguousarray(col_perm, dtype=np.int32),
                       stats=stats)
 
 
@@ -213,10 +253,11 @@ def decode_tiles(ts: TileStream) -> np.ndarray:
             w0 = int(cell[0])
             off, c, pos = w0 & 0x3FFF, (w0 >> 14) & 3, w0 >> 16
             if ts.fp32_scales:
-                st, sb = cell[1:3].view(np.float32)
+                st, sb = (np.full(4, v, np.float32) for v in cell[1:3].view(np.float32))
             else:
-                st = np.array([(int(cell[1]) & 0xFFFF) << 16], np.uint32).view(np.float32)[0]
-                sb = np.array([(int(cell[1]) >> 16) << 16], np.uint32).view(np.float32)[0]
+                sw = cell[1:5] if ts.cols_gathered else np.full(4, cell[1], np.uint32)
+                st = ((sw.astype(np.uint32) & 0xFFFF) << 16).view(np.float32)
+                sb = ((sw.astype(np.uint32) >> 16) << 16).view(np.float32)
             r0, c0 = ks * TILE_ROWS + (pos & 7) * 8, ct * TILE_COLS + (pos >> 3) * 4
             if c == CLS_Z:
                 continue
@@ -231,8 +272,8 @@ def decode_tiles(ts: TileStream) -> np.ndarray:
                     else:
                         u[j, r] = (wds[4 * j + r // 2] >> (16 * (r % 2))) & 0xFFFF
             q = (u - CLS_OFFSET[c]).astype(np.float32)
-            s = np.array([st] * 4 + [sb] * 4, np.float32)
-            Wp[r0:r0 + 8, c0:c0 + 4] = (q * s[None, :]).T
+            s = np.concatenate([np.repeat(st[:, None], 4, axis=1), np.repeat(sb[:, None], 4, axis=1)], axis=1)
+            Wp[r0:r0 + 8, c0:c0 + 4] = (q * s).T
     Wp = Wp[:K, :N]
     Wp = _bf16_rne(Wp)
     if ts.row_perm is None and ts.col_perm is None:

@@ -207,10 +207,15 @@ def test_tile_descriptor_layout_and_validation(hip):
     assert out[1:] == [getattr(_abi.MtcTileDesc, f).offset for f in fields]
     assert hip.mtc_check_tile_desc(ctypes.byref(_tdesc())) == 0
     cases = {"abi_version": (4, -7), "N": (100, -2), "K": (252, -2), "n_ksteps": (3, -2), "n_col_tiles": (1, -2),
-             "flags": (4, -2), "cells": (None, -1), "payload": (None, -1), "step_off": (None, -1)}
+             "flags": (8, -2), "cells": (None, -1), "payload": (None, -1), "step_off": (None, -1)}
     for field, (val, code) in cases.items():
         assert hip.mtc_check_tile_desc(ctypes.byref(_tdesc(**{field: val}))) == code, field
     assert hip.mtc_check_tile_desc(None) == -1
+    # gathered columns: bf16 scales and no col_perm only
+    g = _abi.MTC_FLAG_COLS_GATHERED
+    assert hip.mtc_check_tile_desc(ctypes.byref(_tdesc(flags=g))) == 0
+    assert hip.mtc_check_tile_desc(ctypes.byref(_tdesc(flags=g | _abi.MTC_FLAG_FP32_SCALES))) == -2
+    assert hip.mtc_check_tile_desc(ctypes.byref(_tdesc(flags=g, col_perm=0x2000))) == -2
     # payload past 2 GiB (32-bit byte offsets) is rejected
     assert hip.mtc_check_tile_desc(ctypes.byref(_tdesc(payload_dwords=0x7FFFFFFF // 4))) == 0
     assert hip.mtc_check_tile_desc(ctypes.byref(_tdesc(payload_dwords=0x7FFFFFFF // 4 + 1))) == -2

@@ -89,3 +89,48 @@ def test_fuzz_tiles(seed, budget, perm, sizes):
         return
     ts = MTCMatrix.from_quadtree(a, W).tile_stream()
     assert np.array_equal(_bits(decode_tiles(ts)), _bits(_want(a, W)))
+
+
+@pytest.mark.parametrize("K,N,budget", [(256, 288, 3.1), (192, 160, 11.0), (64, 96, 2.0)])
+def test_gathered_columns_for_permuted_matrices(K, N, budget):
+    """A QT-P matrix packs its columns back in the original order: 8-word cells with a scale pair
+    per column, no col_perm, the same bf16 W_hat; column j's scale words name the leaf of the
+    permuted column the original column comes from. gather_cols=False keeps the permuted order."""
+    from tensorpack_amd.tilestream import TILE_COLS, TILE_ROWS, pack_tiles
+    W = outlier_matrix(int(budget * 3), K, N)
+    a = PermutedQuadtreeRD(W, np.exp(np.random.RandomState(6).randn(K)), (32, 16, 8, 4)).select(budget)
+    m = MTCMatrix.from_quadtree(a, W)
+    ts = m.tile_stream()
+    assert ts.cols_gathered and ts.col_perm is None and ts.row_perm is not None and ts.cells.shape[1] == 8
+    assert not ts.cells[:, 5:].any()
+    assert np.array_equal(_bits(decode_tiles(ts)), _bits(_want(a, W)))
+    # scale words against the allocation: original column n is permuted column inv[n]
+    i = a.inner
+    inv = np.argsort(a.col_perm)
+    S_el = np.zeros((K, N), np.float32)
+    for S in i.sizes:
+        L = np.asarray(i.leaf[S], bool)
+        sc = np.where(L, np.asarray(i.scales[S], np.float32), 0.0)
+        S_el += np.kron(sc, np.ones((S, S), np.float32))
+    S_orig = S_el[:, inv]                                     # permuted rows, original columns
+    rng = np.random.RandomState(1)
+    for idx in rng.choice(ts.cells.shape[0], 64, replace=False):
+        step, w0 = idx // CELLS, int(ts.cells[idx, 0])
+        ct, ks = divmod(step, ts.n_ksteps)
+        pos = w0 >> 16
+        r0, c0 = ks * TILE_ROWS + (pos & 7) * 8, ct * TILE_COLS + (pos >> 3) * 4
+        if (w0 >> 14) & 3 == CLS_Z or r0 >= K or c0 >= N:
+            continue
+        for j in range(4):
+            sw = int(ts.cells[idx, 1 + j])
+            top = np.array([(sw & 0xFFFF) << 16], np.uint32).view(np.float32)[0]
+            bot = np.array([(sw >> 16) << 16], np.uint32).view(np.float32)[0]
+            assert top == S_orig[r0, c0 + j] and bot == S_orig[r0 + 4, c0 + j], (idx, j)
+    lv = m._levels
+    ts0 = pack_tiles(lv.shape, lv.sizes, lv.leaf, lv.modes, lv.scales, lv.codes_of, lv.scale_format, lv.row_perm,
+                     lv.col_perm, gather_cols=False)
+    assert not ts0.cols_gathered and ts0.col_perm is not None
+    assert np.array_equal(_bits(decode_tiles(ts0)), _bits(_want(a, W)))
+    with pytest.raises(ValueError):
+        pack_tiles(lv.shape, lv.sizes, lv.leaf, lv.modes, lv.scales, lv.codes_of, lv.scale_format, lv.row_perm,
+                   None, gather_cols=True)
