@@ -145,30 +145,45 @@ __device__ __forceinline__ uint32_t dec_shorts(uint32_t v, float s, float c) {
 }
 
 // The 4 columns (8 rows each, bf16) of one cell from its payload words; column j's top rows
-// (0-3) scaled by st[j], its bottom rows by sb[j] (all four equal unless the columns are gathered).
-// value = (u - offset) * s evaluated as fma(u, s, -offset * s): exact in fp32.
+// (0-3) scaled by st[j], its bottom rows by sb[j] (PC: a scale pair per column; otherwise
+// st[0], sb[0] for all four). value = (u - offset) * s evaluated as fma(u, s, -offset * s):
+// exact in fp32.
+template <bool PC>
 __device__ __forceinline__ void decode_cell(uint32_t cls, const u32x4_t* pw, const float (&st)[4],
                                             const float (&sb)[4], u32x4_t* out) {
+  constexpr int NS = PC ? 4 : 1;
+  float ct[NS], cb[NS];
+  auto offset_terms = [&](float off) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      ct[j] = -off * st[j];
+      cb[j] = -off * sb[j];
+    }
+  };
   if (cls == 0) {
+    offset_terms(8.0f);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      const int k = PC ? j : 0;
       const uint32_t x = pw[0][j];
-      out[j] = dec_bytes(opaque(x & 0x0F0F0F0Fu), opaque((x >> 4) & 0x0F0F0F0Fu), st[j], -8.0f * st[j], sb[j],
-                         -8.0f * sb[j]);
+      out[j] = dec_bytes(opaque(x & 0x0F0F0F0Fu), opaque((x >> 4) & 0x0F0F0F0Fu), st[k], ct[k], sb[k], cb[k]);
     }
   } else if (cls == 1) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      out[j] = dec_bytes(pw[j >> 1][(2 * j) & 3], pw[j >> 1][(2 * j + 1) & 3], st[j], -128.0f * st[j], sb[j],
-                         -128.0f * sb[j]);
-  } else if (cls == 2) {
+    offset_terms(128.0f);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float ct = -32768.0f * st[j], cb = -32768.0f * sb[j];
-      out[j].x = dec_shorts(pw[j].x, st[j], ct);
-      out[j].y = dec_shorts(pw[j].y, st[j], ct);
-      out[j].z = dec_shorts(pw[j].z, sb[j], cb);
-      out[j].w = dec_shorts(pw[j].w, sb[j], cb);
+      const int k = PC ? j : 0;
+      out[j] = dec_bytes(pw[j >> 1][(2 * j) & 3], pw[j >> 1][(2 * j + 1) & 3], st[k], ct[k], sb[k], cb[k]);
+    }
+  } else if (cls == 2) {
+    offset_terms(32768.0f);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = PC ? j : 0;
+      out[j].x = dec_shorts(pw[j].x, st[k], ct[k]);
+      out[j].y = dec_shorts(pw[j].y, st[k], ct[k]);
+      out[j].z = dec_shorts(pw[j].z, sb[k], cb[k]);
+      out[j].w = dec_shorts(pw[j].w, sb[k], cb[k]);
     }
   } else {
 #pragma unroll
@@ -393,7 +408,7 @@ __device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const in
     const uint32_t pos = w[0] >> 16;
     const int col = (int)(pos >> 3) * 4, seg = (int)(pos & 7u);
     u32x4_t o[4];
-    decode_cell((w[0] >> 14) & 3u, q, st, sb, o);
+    decode_cell<kCF == kCellCols>((w[0] >> 14) & 3u, q, st, sb, o);
 #pragma unroll
     for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4_t*>(bs + swz(col + j, seg)) = o[j];
   };
