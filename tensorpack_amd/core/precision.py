@@ -90,6 +90,27 @@ def negotiate_joint_precision(ea: _BlockErrors, eb: _BlockErrors, target_epsilon
     return 16, 16
 
 
+def compute_frobenius_error(orig: np.ndarray, recon: np.ndarray) -> float:
+    """||orig - recon||_F in float32 (precision.py:44-47)."""
+    return _frobenius_error(orig, recon)
+
+
+def compute_relative_error(orig: np.ndarray, recon: np.ndarray) -> float:
+    """||orig - recon||_F / ||orig||_F, 0 for a block of norm < 1e-8 (precision.py:50-55)."""
+    return _relative_error(orig, recon)
+
+
+def negotiate_joint_precision_blocks(block_a: np.ndarray, block_b: np.ndarray, target_epsilon: float = 0.05,
+                                     reduction_tiles: int = 1) -> Tuple[PrecisionMode, PrecisionMode, float, float]:
+    """The reference's form of the negotiation (precision.py:77-140): two blocks in, (pA, pB,
+    scale_a, scale_b) out, with scales 1.0 for a pair whose |A||B| < 1e-7."""
+    ea, eb = _BlockErrors(block_a), _BlockErrors(block_b)
+    if ea.norm * eb.norm < 1e-7:
+        return PrecisionMode.P2, PrecisionMode.P2, 1.0, 1.0
+    pa, pb = negotiate_joint_precision(ea, eb, target_epsilon, reduction_tiles)
+    return PrecisionMode(pa), PrecisionMode(pb), ea.scale[pa], eb.scale[pb]
+
+
 def block_scale(block: np.ndarray, mode: int, scale: Optional[float] = None) -> float:
     """The scale MicroTensor.from_array stores for `block` (microtensor.py:80-92): the given
     one, else max|block| / QMAG[mode], or 1.0 for a block whose max is <= 1e-7."""

@@ -180,3 +180,32 @@ def test_from_numpy_rejects_unsupported():
         MTCMatrix.from_numpy(A, block_size=2)
     with pytest.raises(AssertionError):
         MTCMatrix.from_numpy(np.ones((20, 16), np.float32), block_size=16)
+
+
+def test_precision_module_has_the_reference_names():
+    """mtc.core.precision exposes the reference's helpers with its signatures: the error norms in
+    closed form, and the two-block negotiation returning (pA, pB, scale_a, scale_b)."""
+    from mtc.core.precision import (compute_frobenius_error, compute_relative_error, negotiate_joint_precision,
+                                    quantize_and_dequantize_block)
+    from mtc.core.types import PrecisionMode
+    a = np.array([[3.0, 0.0], [0.0, 4.0]], np.float32)
+    b = np.zeros((2, 2), np.float32)
+    assert compute_frobenius_error(a, b) == 5.0 and compute_relative_error(a, b) == 1.0
+    assert compute_relative_error(b, a) == 0.0                      # a zero block has no relative error
+    assert negotiate_joint_precision(a, b) == (PrecisionMode.P2, PrecisionMode.P2, 1.0, 1.0)
+    rng = np.random.RandomState(3)
+    A, B = rng.randn(16, 16).astype(np.float32), rng.randn(16, 16).astype(np.float32)
+    pa, pb, sa, sb = negotiate_joint_precision(A, B, target_epsilon=0.05)
+    # the bound the rule checks, from the returned modes: ea*|B| + |A|*eb + ea*eb <= eps*|A||B|
+    ea = compute_frobenius_error(A, quantize_and_dequantize_block(A, int(pa))[0])
+    eb = compute_frobenius_error(B, quantize_and_dequantize_block(B, int(pb))[0])
+    nA, nB = np.linalg.norm(A), np.linalg.norm(B)
+    assert ea * nB + nA * eb + ea * eb <= 0.05 * nA * nB
+    assert sa == quantize_and_dequantize_block(A, int(pa))[1] and sb == quantize_and_dequantize_block(B, int(pb))[1]
+    # every cheaper pair (by total bits) violates it
+    for qa in (2, 4, 8, 16):
+        for qb in (2, 4, 8, 16):
+            if qa + qb < int(pa) + int(pb):
+                fa = compute_frobenius_error(A, quantize_and_dequantize_block(A, qa)[0])
+                fb = compute_frobenius_error(B, quantize_and_dequantize_block(B, qb)[0])
+                assert fa * nB + nA * fb + fa * fb > 0.05 * nA * nB
