@@ -477,7 +477,7 @@ struct GemmGroup {
   int start[kMaxGroup + 1];
 };
 
-template <int kCF, int kYDT>
+template <int kCF, int kYDT, int TM>
 __global__ __launch_bounds__(kThreads) void k_gemm_tile_group(const GemmGroup g, int M, int n_row_tiles) {
   int i = 0;
 #pragma unroll
@@ -487,8 +487,8 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile_group(const GemmGroup g,
   if (!tile_of_block((int)blockIdx.x - g.start[i], n_row_tiles, g.d[i].n_col_tiles, g.tiles_per_xcd[i],
                      g.d[i].col_perm && !g.part[i], rt, ct))
     return;
-  gemm_tile_block<kCF, kYDT>(g.d[i], rt, ct, (int)blockIdx.y, g.X[i], g.ldx[i], g.Y[i], g.ldy[i], M,
-                             g.steps_per_split[i], g.part[i]);
+  gemm_tile_block<kCF, kYDT, TM>(g.d[i], rt, ct, (int)blockIdx.y, g.X[i], g.ldx[i], g.Y[i], g.ldy[i], M,
+                                 g.steps_per_split[i], g.part[i]);
 }
 
 // Xp[m, k] = bf16(X[m, row_perm[k]]) (identity without a permutation); 8 outputs per thread.
@@ -671,14 +671,14 @@ struct GemmBatchItem {
 
 constexpr uint32_t kNoItem = 0xFFFFFFFFu;   // a block table entry with no work
 
-template <int kCF, int kYDT>
+template <int kCF, int kYDT, int TM>
 __global__ __launch_bounds__(kThreads) void k_gemm_tile_batch(const GemmBatchItem* __restrict__ items,
                                                               const uint2* __restrict__ blocks, int M) {
   const uint2 e = blocks[blockIdx.x];
   if (e.x == kNoItem) return;                               // padding of an XCD's block list
   const GemmBatchItem& it = items[e.x];
-  gemm_tile_block<kCF, kYDT>(it.d, (int)(e.y & 0xFFFu), (int)((e.y >> 12) & 0xFFFu), (int)(e.y >> 24), it.X, it.ldx,
-                             it.Y, it.ldy, M, it.steps_per_split, it.splits > 1 ? it.part : nullptr);
+  gemm_tile_block<kCF, kYDT, TM>(it.d, (int)(e.y & 0xFFFu), (int)((e.y >> 12) & 0xFFFu), (int)(e.y >> 24), it.X,
+                                 it.ldx, it.Y, it.ldy, M, it.steps_per_split, it.splits > 1 ? it.part : nullptr);
 }
 
 __global__ __launch_bounds__(kStageThreads) void k_stage_x_batch(const GemmBatchItem* __restrict__ items,
@@ -777,10 +777,12 @@ TilePlan tile_plan(const mtc_tile_desc* d, int M) {
 }
 
 // K splits of one call (tile_plan): a group or batch member splits K the same way, so that
-// its Y is the single call's bit for bit. Returns the steps per split.
-int split_steps(const mtc_tile_desc* d, int M, int* splits) {
+// its Y is the single call's bit for bit (the tile height changes no sum). Returns the steps
+// per split; `tm`, if given, receives the tile height the single call would use.
+int split_steps(const mtc_tile_desc* d, int M, int* splits, int* tm = nullptr) {
   const TilePlan p = tile_plan(d, M);
   *splits = p.splits;
+  if (tm) *tm = p.tm;
   return p.per;
 }
 
@@ -841,18 +843,25 @@ size_t group_ws_bytes(const mtc_tile_desc* const* descs, int n, int M, int x_dty
 }
 
 template <int kCF, int kYDT>
-int launch_tile_group(GemmGroup& g, int n, int M, const ReduceGroup& rg, int n_red, hipStream_t st) {
+int launch_tile_group(GemmGroup& g, int n, int M, int tm, const ReduceGroup& rg, int n_red, hipStream_t st) {
   if ((size_t)kLdsBytes > mtc::host::device_lds_limit())
     return fail(MTC_E_SHAPE, "prefill kernel needs %d B of LDS per block, device has %zu", kLdsBytes,
                 mtc::host::device_lds_limit());
-  const void* fn = reinterpret_cast<const void*>(&k_gemm_tile_group<kCF, kYDT>);
+  const void* fn = tm == 256 ? reinterpret_cast<const void*>(&k_gemm_tile_group<kCF, kYDT, 256>)
+                   : tm == 128 ? reinterpret_cast<const void*>(&k_gemm_tile_group<kCF, kYDT, 128>)
+                               : reinterpret_cast<const void*>(&k_gemm_tile_group<kCF, kYDT, 64>);
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
   if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-  const int n_row_tiles = (M + kTM - 1) / kTM;
+  const int n_row_tiles = (M + tm - 1) / tm;
   int max_splits = 1;
   for (int i = 0; i < n; ++i) max_splits = std::max(max_splits, g.splits[i]);
-  hipLaunchKernelGGL((k_gemm_tile_group<kCF, kYDT>), dim3(g.start[n], max_splits), dim3(kThreads), kLdsBytes, st, g, M,
-                     n_row_tiles);
+  const dim3 grid(g.start[n], max_splits);
+  if (tm == 256)
+    hipLaunchKernelGGL((k_gemm_tile_group<kCF, kYDT, 256>), grid, dim3(kThreads), kLdsBytes, st, g, M, n_row_tiles);
+  else if (tm == 128)
+    hipLaunchKernelGGL((k_gemm_tile_group<kCF, kYDT, 128>), grid, dim3(kThreads), kLdsBytes, st, g, M, n_row_tiles);
+  else
+    hipLaunchKernelGGL((k_gemm_tile_group<kCF, kYDT, 64>), grid, dim3(kThreads), kLdsBytes, st, g, M, n_row_tiles);
   int rc = check_launch("k_gemm_tile_group");
   if (rc || n_red == 0) return rc;
   int grid_x = 1;
@@ -877,6 +886,7 @@ struct GemmBatchHeader {
   int32_t reduce_blocks_x;
   int32_t stage_rows;     // rows per LDS staging block (0: global gather)
   int32_t stage_max_k;
+  int32_t tm;             // output rows per tile block (256, 128 or 64)
   uint64_t items_off;
   uint64_t blocks_off;
   uint64_t stage_off;
@@ -896,7 +906,7 @@ int build_gemm_batch_plan(const mtc_gemm_batch_item* items, int n, int M, int x_
   if (M <= 0 || M > 65535) return fail(MTC_E_SHAPE, "M=%d must be in [1, 65535]", M);
   if (x_dtype != MTC_DTYPE_F32 && x_dtype != MTC_DTYPE_BF16) return fail(MTC_E_DTYPE, "x_dtype=%d", x_dtype);
   if (y_dtype != MTC_DTYPE_F32 && y_dtype != MTC_DTYPE_BF16) return fail(MTC_E_DTYPE, "y_dtype=%d", y_dtype);
-  const int n_row_tiles = (M + kTM - 1) / kTM;
+  const int n_row_tiles256 = (M + kTM - 1) / kTM;
   int64_t total_tiles = 0;
   int cf = kCellBf16;
   for (int i = 0; i < n; ++i) {
@@ -918,10 +928,20 @@ int build_gemm_batch_plan(const mtc_gemm_batch_item* items, int n, int M, int x_
     const int64_t ldx_used = needs_staging(d, x_dtype) ? d->K : items[i].ldx;
     if (ldx_used >= ((int64_t)1 << 31) / (2 * kTM))
       return fail(MTC_E_SHAPE, "batch item %d: ldx=%lld too large for 32-bit X tile offsets", i, (long long)ldx_used);
-    total_tiles += (int64_t)n_row_tiles * d->n_col_tiles;
+    total_tiles += (int64_t)n_row_tiles256 * d->n_col_tiles;
   }
-  // the K split of a single call when the batch alone would leave CUs idle; none when it fills them
+  // the K split of a single call when the batch alone would leave CUs idle; none when it fills them.
+  // Tile height: 256 rows when the batch fills the chip, else the shortest any item's single call
+  // would use (its split is kept, so its Y stays the single call's bit for bit).
   const bool fill = total_tiles >= kFillCUs;
+  int tm = kTM;
+  if (!fill)
+    for (int i = 0; i < n; ++i) {
+      int s_i = 1, tm_i = kTM;
+      split_steps(items[i].desc, M, &s_i, &tm_i);
+      tm = std::min(tm, tm_i);
+    }
+  const int n_row_tiles = (M + tm - 1) / tm;
   std::vector<int> splits(n), per(n);
   size_t ws = 0;
   int n_stage = 0, n_reduce = 0, stage_bx = 1, reduce_bx = 1;
@@ -1020,6 +1040,7 @@ int build_gemm_batch_plan(const mtc_gemm_batch_item* items, int n, int M, int x_
   h->x_dtype = x_dtype;
   h->y_dtype = y_dtype;
   h->cf = cf;
+  h->tm = tm;
   h->n_stage = n_stage;
   h->n_reduce = n_reduce;
   h->stage_blocks_x = stage_bx;
@@ -1076,11 +1097,18 @@ int launch_tile_batch(const GemmBatchHeader* h, const GemmBatchItem* items, cons
   if ((size_t)kLdsBytes > mtc::host::device_lds_limit())
     return fail(MTC_E_SHAPE, "prefill kernel needs %d B of LDS per block, device has %zu", kLdsBytes,
                 mtc::host::device_lds_limit());
-  const void* fn = reinterpret_cast<const void*>(&k_gemm_tile_batch<kCF, kYDT>);
+  const void* fn = h->tm == 256 ? reinterpret_cast<const void*>(&k_gemm_tile_batch<kCF, kYDT, 256>)
+                   : h->tm == 128 ? reinterpret_cast<const void*>(&k_gemm_tile_batch<kCF, kYDT, 128>)
+                                  : reinterpret_cast<const void*>(&k_gemm_tile_batch<kCF, kYDT, 64>);
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
   if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-  hipLaunchKernelGGL((k_gemm_tile_batch<kCF, kYDT>), dim3((unsigned)h->n_blocks), dim3(kThreads), kLdsBytes, st, items,
-                     blocks, h->M);
+  const dim3 grid((unsigned)h->n_blocks);
+  if (h->tm == 256)
+    hipLaunchKernelGGL((k_gemm_tile_batch<kCF, kYDT, 256>), grid, dim3(kThreads), kLdsBytes, st, items, blocks, h->M);
+  else if (h->tm == 128)
+    hipLaunchKernelGGL((k_gemm_tile_batch<kCF, kYDT, 128>), grid, dim3(kThreads), kLdsBytes, st, items, blocks, h->M);
+  else
+    hipLaunchKernelGGL((k_gemm_tile_batch<kCF, kYDT, 64>), grid, dim3(kThreads), kLdsBytes, st, items, blocks, h->M);
   int rc = check_launch("k_gemm_tile_batch");
   if (rc || h->n_reduce == 0) return rc;
   hipLaunchKernelGGL(k_splitk_reduce_batch<kYDT>, dim3((unsigned)h->reduce_blocks_x, (unsigned)h->n_reduce),
@@ -1241,7 +1269,15 @@ MTC_API int mtc_gemm_bf16_group(const mtc_tile_desc* const* descs, int n, const 
   memset(&rg, 0, sizeof(rg));
   int n_stage = 0, n_red = 0, blocks = 0;
   char* ws = reinterpret_cast<char*>(workspace);
-  const int n_row_tiles = (M + kTM - 1) / kTM;
+  // tile height: the shortest any member's single call would use (short X whose 256-row tiles
+  // leave CUs idle); every member keeps its own single-call K split
+  int tm = kTM;
+  for (int i = 0; i < n; ++i) {
+    int s_i = 1, tm_i = kTM;
+    split_steps(descs[i], M, &s_i, &tm_i);
+    tm = std::min(tm, tm_i);
+  }
+  const int n_row_tiles = (M + tm - 1) / tm;
   for (int i = 0; i < n; ++i) {
     const mtc_tile_desc* d = descs[i];
     g.d[i] = *d;
@@ -1291,13 +1327,13 @@ MTC_API int mtc_gemm_bf16_group(const mtc_tile_desc* const* descs, int n, const 
   for (int i = 1; i < n; ++i) cf = joint_cell_format(cf, cell_format(descs[i]));
   switch (cf) {
     case kCellFp32:
-      return f32 ? launch_tile_group<kCellFp32, MTC_DTYPE_F32>(g, n, M, rg, n_red, st)
-                 : launch_tile_group<kCellFp32, MTC_DTYPE_BF16>(g, n, M, rg, n_red, st);
+      return f32 ? launch_tile_group<kCellFp32, MTC_DTYPE_F32>(g, n, M, tm, rg, n_red, st)
+                 : launch_tile_group<kCellFp32, MTC_DTYPE_BF16>(g, n, M, tm, rg, n_red, st);
     case kCellCols:
-      return f32 ? launch_tile_group<kCellCols, MTC_DTYPE_F32>(g, n, M, rg, n_red, st)
-                 : launch_tile_group<kCellCols, MTC_DTYPE_BF16>(g, n, M, rg, n_red, st);
+      return f32 ? launch_tile_group<kCellCols, MTC_DTYPE_F32>(g, n, M, tm, rg, n_red, st)
+                 : launch_tile_group<kCellCols, MTC_DTYPE_BF16>(g, n, M, tm, rg, n_red, st);
     default:
-      return f32 ? launch_tile_group<kCellBf16, MTC_DTYPE_F32>(g, n, M, rg, n_red, st)
-                 : launch_tile_group<kCellBf16, MTC_DTYPE_BF16>(g, n, M, rg, n_red, st);
+      return f32 ? launch_tile_group<kCellBf16, MTC_DTYPE_F32>(g, n, M, tm, rg, n_red, st)
+                 : launch_tile_group<kCellBf16, MTC_DTYPE_BF16>(g, n, M, tm, rg, n_red, st);
   }
 }
