@@ -456,6 +456,25 @@ def test_uniform_form_dense_x(gpu, M):
     assert O.relative_frobenius_error(O.qt_gemm_f64(X, W_hat), mtc_gemm(X, m)) <= TOL_F32
 
 
+@pytest.mark.parametrize("M", [1, 3])
+def test_uniform_form_mx_layout(gpu, M):
+    """The uniform-block form (fp32 scales) in the matrix-core payload layout: dequant bit for bit
+    against the reference's to_array, Y within the fp32 bar."""
+    import torch
+    from tensorpack_amd.packer import LAYOUT_MX
+    rng = np.random.RandomState(18)
+    W = rng.randn(256, 128).astype(np.float32)
+    al = rd_allocate(W, 5.0, None, 16)
+    m = MTCMatrix.from_allocation(W, al.modes, al.scales, 16)
+    W_hat = O.uniform_to_array(W, al.modes, al.scales, 16)
+    ds = m.device_stream(None, gpu, 1, LAYOUT_MX)
+    assert ds.host.leaf_scale is not None                   # the fp32-scale kernels
+    assert np.array_equal(_bits(ds.dequant().cpu().numpy()), _bits(W_hat))
+    X = rng.randn(M, 256).astype(np.float32)
+    Y = ds.gemv_f32(torch.from_numpy(X).to(gpu)).cpu().numpy()
+    assert O.relative_frobenius_error(O.qt_gemm_f64(X, W_hat), Y) <= TOL_F32
+
+
 def test_errors_are_clean(gpu, allocs):
     import ctypes
     import torch
