@@ -410,6 +410,17 @@ inline GemvShape gemv_shape(int MT, const mtc_stream_desc* d) {
   if (d->fixed_steps > kFewSteps) return {16, kMaxChunkRows, true, perm && d->K <= kMaxChunkRows, mx};
   return {4, kMaxChunkRows, false, false, mx};
 }
+// Column halves of its unit per vector-path block. A batched launch of one-row M tiles over small
+// units (4 waves, kSmallRows) gives a block both halves of its unit, two waves per half, so that
+// the unit's X rows are staged once and the blocks' fixed costs are spread over twice the
+// records (the batch's blocks fill the chip anyway); every other launch, and a single or grouped
+// call of any shape, runs a block per half, whose four waves keep each wave's chain of records
+// short. A two-half block's waves each run two accumulator sets that stand for the four waves of
+// a one-half block (records wh, wh + 4, ... and wh + 2, wh + 6, ...), so both give the same Y bit
+// for bit.
+__host__ __device__ constexpr int gemv_batch_halves(int MT, int NW, int KC, bool MX) {
+  return MT == 1 && NW == 4 && KC == kSmallRows && !MX ? 2 : 1;
+}
 __host__ __device__ constexpr int gemv_prefetch(int NW) { return NW == 4 ? 2 : 3; }
 constexpr int kMaxFixedSteps = 48;          // step records per block at block-computable positions
 constexpr int kXcds = 8;
@@ -431,16 +442,16 @@ __device__ __forceinline__ float slot_sum(float v) {
 }
 
 
-// The block's outputs from the cross-wave reduction buffer red[wave][slot][m][c] (all waves'
-// values in place, after a barrier). The block covers H column halves of its unit's panel
-// (16 columns each, from half cb; its waves split evenly over them): Y directly for a
-// single-chunk stream; otherwise the block's partial, and the last block of each (M tile,
-// panel) sums the unit partials into Y.
-template <int MT, int W, int H>
+// The block's outputs from the cross-wave reduction buffer red[partial][slot][m][c] (all
+// partials in place, after a barrier; W threads' waves store them). The block covers H column
+// halves of its unit's panel (16 columns each, from half cb), WH partials per half, summed in
+// order: Y directly for a single-chunk stream; otherwise the block's partial, and the last
+// block of each (M tile, panel) sums the unit partials into Y.
+template <int MT, int W, int H, int WH = W / H>
 __device__ __forceinline__ void gemv_store(const mtc_stream_desc& d, const float* red, const int u, const int cb,
                                            float* __restrict__ Y, int64_t ldy, int M, float* __restrict__ part,
                                            uint32_t* __restrict__ counters) {
-  constexpr int T = 64 * W, WH = W / H, CH = kStepGroups * kGroup;   // waves and columns per half
+  constexpr int T = 64 * W, CH = kStepGroups * kGroup;   // threads; partials (WH) and columns per half
   constexpr int blocks_per_chunk = kGemvBlocksPerUnit / H;
   const int tid = threadIdx.x;
   const int mt = blockIdx.y, m0 = mt * MT;
@@ -516,22 +527,26 @@ __device__ __forceinline__ void gemv_store(const mtc_stream_desc& d, const float
 // KC: rows the X staging covers (chunk_rows <= KC, and K <= KC when X is gathered in LDS).
 // PF (gemv_prefetch): steps whose loads a wave issues before the X staging; a wave executes
 // its records in the same order whatever PF is.
-template <int MT, bool FS, bool LG, int NW, int KC>
+template <int MT, bool FS, bool LG, int NW, int KC, int H>
 __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int bid, const float* __restrict__ X,
                                            int64_t ldx, float* __restrict__ Y, int64_t ldy, int M,
                                            float* __restrict__ part, uint32_t* __restrict__ counters,
                                            const bool lg = true) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
+  static_assert(H == 1 || (H == 2 && NW == 4), "two-half blocks have four waves");
   constexpr int W = NW, T = 64 * W, BPU = kGemvBlocksPerUnit;
+  constexpr int WH = W / H, BPB = BPU / H;           // real waves per half, blocks per unit
   const int kc = d.chunk_rows;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: keeps per-wave control scalar
+  const int wh = wave % WH;                           // the wave's place among its half's waves
   const int n_units = d.n_panels * d.n_chunks;
-  // block -> (unit, block of 4 column groups) with both blocks of a unit on one XCD
+  // block -> (unit, block of 4 column groups) with both blocks of a unit on one XCD; in a block
+  // of both halves, wave w takes half w / WH
   const int xcd = bid % kXcds, slot = bid / kXcds;
-  const int u = (slot / BPU) * kXcds + xcd;
+  const int u = (slot / BPB) * kXcds + xcd;
   if (u >= n_units) return;                           // padding block of the XCD mapping
-  const int cb = slot % BPU;
+  const int cb = H == 2 ? wave / WH : slot % BPU;
   const int mt = blockIdx.y;
   const int panel = u / d.n_chunks, chunk = u - panel * d.n_chunks;
   const int m0 = mt * MT;
@@ -541,8 +556,8 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
   float* xs = smem;                                   // [MT][kc]
   float* xs4 = xs + MT * kc;                          // [MT][kc / 4] (MT <= 2 only)
   float* xs8 = xs4 + (gemv_sum4(MT) ? MT * (kc / 4) : 0);   // [MT][kc / 8]
-  float* red = xs8 + MT * (kc / 8);                   // [waves][4 slots][MT][4]
-  float* xraw = red + W * kStepGroups * MT * kGroup;  // [MT][K] whole X rows (LDS gather only)
+  float* red = xs8 + MT * (kc / 8);                   // [H x W partials][4 slots][MT][4] (H W <= gemv_waves)
+  float* xraw = red + H * W * kStepGroups * MT * kGroup;   // [MT][K] whole X rows (LDS gather only)
 
   const ci32p hdr = (ci32p)(d.unit_hdr + kUnitHdr * u);
 
@@ -581,7 +596,7 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
     }
   }
 
-  // ---- this wave's step records: records wave, wave + W, wave + 2W, ... of the block's list.
+  // ---- this wave's step records: records wh, wh + WH, wh + 2WH, ... of its half's list.
   //      A block's first F records sit at block-computable places, so the first three steps'
   //      records are read while the unit header (whose payload and leaf-word starts the
   //      records' offsets are relative to) is still in flight. ----
@@ -627,7 +642,7 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
   Regs r0, r1, r2;
   {
     auto fixed = [&](int k) __attribute__((always_inline)) {
-      const int i = wave + k * W;
+      const int i = wh + k * WH;
       return slot_of(i < F ? (uint32_t)(blk * F + i) : null_rec);
     };
     static_assert(PF >= 1 && PF <= 3, "one to three prefetched steps");
@@ -701,13 +716,17 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
   lds_barrier();                                      // payload loads stay in flight
   const XStage xt{xs, xs4, xs8, kc};
 
-  // ---- decode: the prefetched steps, then any further steps one at a time ----
-  float acc[MT][kGroup];
+  // ---- decode: the prefetched steps, then any further steps one at a time. The wave's k-th
+  //      record (wh + k WH of its half) accumulates into set k % H: set s holds what wave
+  //      wh + s WH of a one-half block sums (its records wh + s WH + j W). ----
+  float acc[H][MT][kGroup];
 #pragma unroll
-  for (int m = 0; m < MT; ++m)
+  for (int s = 0; s < H; ++s)
 #pragma unroll
-    for (int c = 0; c < kGroup; ++c) acc[m][c] = 0.0f;
-  auto compute = [&](const Regs& cur) __attribute__((always_inline)) {
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int c = 0; c < kGroup; ++c) acc[s][m][c] = 0.0f;
+  auto compute = [&](const Regs& cur, float (&acc)[MT][kGroup]) __attribute__((always_inline)) {
     if (cur.on) {
       const uint32_t key = cur.key;
       const uint32_t ls = key & 0xFFu;
@@ -732,31 +751,51 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
   auto rec = [&](int i) __attribute__((always_inline)) {
     return i < F ? (uint32_t)(blk * F + i) : ovf + (uint32_t)(i - F);
   };
-  int i = wave + PF * W;
-  compute(r0);                                        // null records have no active lanes
+  static_assert(H == 1 || PF == 2, "two accumulator sets alternate from the third record on");
+  int i = wh + PF * WH;
+  compute(r0, acc[0]);                                // null records have no active lanes
   u32x2_t nxt = {};                                   // loaded once r0's registers are free
   if (i < nrec) nxt = slot_of(rec(i));
-  if constexpr (PF >= 2) compute(r1);
-  if constexpr (PF >= 3) compute(r2);
-  for (; i < nrec; i += W) {
-    fetch(nxt, r0);
-    if (i + W < nrec) nxt = slot_of(rec(i + W));
-    compute(r0);
+  if constexpr (PF >= 2) compute(r1, acc[1 % H]);
+  if constexpr (PF >= 3) compute(r2, acc[2 % H]);
+  if constexpr (H == 1) {
+    for (; i < nrec; i += WH) {
+      fetch(nxt, r0);
+      if (i + WH < nrec) nxt = slot_of(rec(i + WH));
+      compute(r0, acc[0]);
+    }
+  } else {
+    for (; i < nrec; i += 2 * WH) {
+      fetch(nxt, r0);
+      if (i + WH < nrec) nxt = slot_of(rec(i + WH));
+      compute(r0, acc[0]);
+      if (i + WH >= nrec) break;
+      fetch(nxt, r0);
+      if (i + 2 * WH < nrec) nxt = slot_of(rec(i + 2 * WH));
+      compute(r0, acc[1]);
+    }
   }
 
-  // ---- reduce: the 16 lanes of each slot, then the block's waves ----
+  // ---- reduce: the 16 lanes of each slot, then the block's partials (set s of wave wh of half
+  //      cb is partial wh + s WH of the half, the place of that wave in a one-half block) ----
 #pragma unroll
-  for (int m = 0; m < MT; ++m)
-#pragma unroll
-    for (int c = 0; c < kGroup; ++c) acc[m][c] = slot_sum(acc[m][c]);
-  if (li == kSlotSumLane) {
+  for (int s = 0; s < H; ++s)
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
-      for (int c = 0; c < kGroup; ++c) red[((wave * kStepGroups + g) * MT + m) * kGroup + c] = acc[m][c];
+      for (int c = 0; c < kGroup; ++c) acc[s][m][c] = slot_sum(acc[s][m][c]);
+  if (li == kSlotSumLane) {
+    const int p0 = (H == 2 ? cb * W : 0) + wh;       // this wave's first partial
+#pragma unroll
+    for (int s = 0; s < H; ++s)
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int c = 0; c < kGroup; ++c)
+          red[(((p0 + s * WH) * kStepGroups + g) * MT + m) * kGroup + c] = acc[s][m][c];
   }
   __syncthreads();
-  gemv_store<MT, W, 1>(d, red, u, cb, Y, ldy, M, part, counters);
+  gemv_store<MT, W, H, W>(d, red, u, H == 2 ? 0 : cb, Y, ldy, M, part, counters);
 }
 
 // ---------------------------------------------------------------------------
@@ -1163,8 +1202,9 @@ __device__ __forceinline__ void gemv_block_mfma(const mtc_stream_desc& d, const 
 
 // The block code of an M tile: over an mx stream (MX) one X row on the matrix core with
 // f16 operands; else the matrix core for tiles of 8 or 16 rows (X staged transposed in xt, or
-// gathered by the block from X when xt is null), else the vector path.
-template <int MT, bool FS, bool LG, int NW, int KC, bool MX = false>
+// gathered by the block from X when xt is null), else the vector path with H column halves per
+// block.
+template <int MT, bool FS, bool LG, int NW, int KC, bool MX = false, int H = 1>
 __device__ __forceinline__ void gemv_any(const mtc_stream_desc& d, const int bid, const float* __restrict__ X,
                                          int64_t ldx, float* __restrict__ Y, int64_t ldy, int M,
                                          float* __restrict__ part, uint32_t* __restrict__ counters, const bool lg,
@@ -1176,7 +1216,7 @@ __device__ __forceinline__ void gemv_any(const mtc_stream_desc& d, const int bid
     static_assert(NW == kMfmaWaves, "matrix-core decode blocks have 16 waves");
     gemv_block_mfma<MT, FS>(d, bid, X, ldx, Y, ldy, M, part, counters, xt);
   } else {
-    gemv_block<MT, FS, LG, NW, KC>(d, bid, X, ldx, Y, ldy, M, part, counters, lg);
+    gemv_block<MT, FS, LG, NW, KC, H>(d, bid, X, ldx, Y, ldy, M, part, counters, lg);
   }
 }
 
@@ -1270,8 +1310,8 @@ __global__ __launch_bounds__(64 * NW, gemv_min_blocks(NW, MX)) void k_gemv_batch
                                                         const uint32_t* __restrict__ block_item, int M) {
   const int b = blockIdx.x;
   const BatchItem& it = items[block_item[b]];
-  gemv_any<MT, FS, LG, NW, KC, MX>(it.d, b - it.start, it.X, it.ldx, it.Y, it.ldy, M, it.part, it.counters,
-                                   it.lg != 0, it.xt);
+  gemv_any<MT, FS, LG, NW, KC, MX, gemv_batch_halves(MT, NW, KC, MX)>(
+      it.d, b - it.start, it.X, it.ldx, it.Y, it.ldy, M, it.part, it.counters, it.lg != 0, it.xt);
 }
 
 // X of every member staged for the matrix core (grid z: the member).
@@ -1414,12 +1454,15 @@ unsigned stage_x_blocks(const mtc_stream_desc* d, int mt) {
   return (unsigned)(((int64_t)d->K * (mt / 4) + kStageThreads - 1) / kStageThreads);
 }
 
-// Decode blocks of one M tile: one per unit on the matrix core; two per unit on the vector
-// path, with the unit count rounded up to whole XCD rounds.
-int gemv_blocks(const mtc_stream_desc* d, int mt) {
+// Decode blocks of one M tile: one per unit on the matrix core; on the vector path one per
+// column half, or in a batched launch one per unit where gemv_batch_halves gives blocks both
+// halves; the unit count rounded up to whole XCD rounds.
+int gemv_blocks(const mtc_stream_desc* d, int mt, bool batch = false) {
   const int n_units = d->n_panels * d->n_chunks;
   if (mt > 4) return n_units;
-  return (n_units + kXcds - 1) / kXcds * kXcds * kGemvBlocksPerUnit;
+  const GemvShape s = gemv_shape(mt, d);
+  const int h = batch ? gemv_batch_halves(mt, s.nw, s.kc, s.mx) : 1;
+  return (n_units + kXcds - 1) / kXcds * kXcds * (kGemvBlocksPerUnit / h);
 }
 
 // LDS of a decode block: X rows, their 4- and 8-row sums, the cross-wave reduction and,
@@ -1544,7 +1587,7 @@ int build_batch_plan(const mtc_gemv_batch_item* items, int n, int M, void* works
     if (fsi != fs) return fail(MTC_E_SHAPE, "batch item %d differs from item 0 in scale format", i);
     lds = std::max(lds, mfma_rows_fit(mt, d->chunk_rows) ? gemv_lds_bytes(d, mt) : SIZE_MAX);
     ws += align_up(gemv_ws_layout(d, M, mt, nullptr), 256);
-    const int64_t nb = gemv_blocks(d, mt);
+    const int64_t nb = gemv_blocks(d, mt, true);
     blocks += nb;
     class_blocks[shape_class(gemv_shape(mt, d))] += nb;
   }
@@ -1606,7 +1649,7 @@ int build_batch_plan(const mtc_gemv_batch_item* items, int n, int M, void* works
       wsp += align_up(wsi, 256);
     }
     stage_bx = std::max(stage_bx, stage_x_blocks(d, mt));
-    const int nb = gemv_blocks(d, mt);
+    const int nb = gemv_blocks(d, mt, true);
     uint32_t* table = block_item + table_off[cls];
     it[i].start = start[cls];
     for (int b = 0; b < nb; ++b) table[start[cls] + b] = (uint32_t)i;

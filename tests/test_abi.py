@@ -259,16 +259,23 @@ def test_batch_plan_sizes_and_errors(hip):
         it.desc = ctypes.pointer(d)
         it.X, it.ldx, it.Y, it.ldy = 0x10000, 256, 0x20000, 64
     plan_n, ws_n = ctypes.c_size_t(), ctypes.c_size_t()
+    # units padded to 8 XCDs; one block per small unit (both column halves) for one-row tiles,
+    # one per column half for two-row tiles
+    for M, per_unit in ((1, 1), (2, 2)):
+        assert hip.mtc_gemv_batch_plan(items, 2, M, None, 0, None, 0, ctypes.byref(plan_n), ctypes.byref(ws_n)) == 0
+        blocks = 2 * 8 * per_unit
+        assert plan_n.value >= blocks * 4 and ws_n.value > 0 and ws_n.value % 256 == 0
+        raw = np.zeros(plan_n.value + 64, np.uint8)
+        off = (-raw.ctypes.data) % 64
+        plan = raw[off:off + plan_n.value]
+        ws = 0x100000
+        assert hip.mtc_gemv_batch_plan(items, 2, M, ws, ws_n.value, plan.ctypes.data, plan_n.value, None, None) == 0
+        block_item = plan[-4 * blocks:].view(np.uint32)
+        assert (block_item[:blocks // 2] == 0).all() and (block_item[blocks // 2:] == 1).all()
     assert hip.mtc_gemv_batch_plan(items, 2, 1, None, 0, None, 0, ctypes.byref(plan_n), ctypes.byref(ws_n)) == 0
-    blocks = 16 + 16                                       # units padded to 8 XCDs x 2 blocks per unit
-    assert plan_n.value >= blocks * 4 and ws_n.value > 0 and ws_n.value % 256 == 0
     raw = np.zeros(plan_n.value + 64, np.uint8)
     off = (-raw.ctypes.data) % 64
     plan = raw[off:off + plan_n.value]
-    ws = 0x100000
-    assert hip.mtc_gemv_batch_plan(items, 2, 1, ws, ws_n.value, plan.ctypes.data, plan_n.value, None, None) == 0
-    block_item = plan[-4 * blocks:].view(np.uint32)
-    assert (block_item[:16] == 0).all() and (block_item[16:] == 1).all()
     # errors: empty batch, M = 0, missing X, mixed scale formats, plan or workspace too small
     assert hip.mtc_gemv_batch_plan(items, 0, 1, None, 0, None, 0, ctypes.byref(plan_n), None) == -3
     assert hip.mtc_gemv_batch_plan(items, 2, 0, None, 0, None, 0, ctypes.byref(plan_n), None) == -3
