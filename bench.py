@@ -846,7 +846,7 @@ def bench_c5(args, wl, a, dev, traffic=None, traffic256=None):
         log(f"c5 M=1 traffic {traffic['bytes'] / 1e6:.2f} MB per launch = {traffic['bytes'] / m.packed_bytes:.3f}x packed")
     return {"workload": wl.name, "packed_bytes": m.packed_bytes, "stream_bytes": ds.device_bytes(),
             "m1": m1,
-            "m256": {"us_per_call": ms2 * 1e3, "TFLOPs": tf, "x_dtype": "f32 (staged to bf16 by k_stage_x)",
+            "m256": {"us_per_call": ms2 * 1e3, "TFLOPs": tf, "x_dtype": "f32 (rounded to bf16 by the tile kernel's consumers)",
                      "rel_vs_fp64": rel2,
                      "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                   "frac": tf / BF16_PEAK_TFLOPS,

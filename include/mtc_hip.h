@@ -280,8 +280,10 @@ typedef struct mtc_tile_desc {
 int mtc_check_tile_desc(const mtc_tile_desc* d);
 
 /* Bytes of prefill workspace for M rows of X of dtype x_dtype (256-byte aligned
- * workspace; contents need no initialisation): M*K*2 (rounded up to 256) when X must
- * be staged as bf16 first (fp32 X, or a row permutation to gather), plus
+ * workspace; contents need no initialisation): M*K*2 (rounded up to 256) when X may
+ * be staged as bf16 first (fp32 X, or a row permutation to gather; fp32 X without a
+ * permutation, with 16-byte aligned rows, in the 64- and 128-row tiles of short X is
+ * rounded to bf16 by the tile kernel itself and leaves that area unused), plus
  * splits*M*N*4 when the output has too few 256 x 256 tiles to fill the chip and the
  * K steps are split over blocks (fp32 partial tiles, summed in a fixed order). */
 size_t mtc_gemm_workspace_bytes(const mtc_tile_desc* d, int M, int x_dtype);

@@ -2,12 +2,15 @@
 // into bf16 LDS tiles and multiplied on v_mfma_f32_32x32x16_bf16 (fp32 accumulate).
 //
 //   k_stage_x_rows / k_stage_x : X -> bf16 Xp = X[:, row_perm] (only for fp32 X or a row
-//                 permutation); 1-4 rows per block gathered through LDS, or, for rows
-//                 wider than the LDS holds, one element per lane from global memory
+//                 permutation, and not for unpermuted fp32 X in the short tiles below);
+//                 1-4 rows per block gathered through LDS, or, for rows wider than the LDS
+//                 holds, one element per lane from global memory
 //   k_gemm_tile : one 256 x 256 output tile per block, K in steps of 64. Warp-specialized:
 //                 8 consumer waves (2 x 4 of 128 x 64 outputs) copy X tiles straight
 //                 into LDS (buffer loads with the LDS destination, two steps ahead into
-//                 three A buffers) and issue the MFMAs; 4 producer waves (one per SIMD)
+//                 three A buffers; unpermuted fp32 X in tiles of 64 or 128 rows goes
+//                 through registers instead, rounded to bf16 on the way) and issue the
+//                 MFMAs; 4 producer waves (one per SIMD)
 //                 decode step k+1's weight cells from registers into the other of two B
 //                 buffers and load step k+2's cell payload. Tiles use an XOR swizzle of
 //                 16-byte segments; one LDS-only barrier per step (global loads stay in
@@ -220,9 +223,12 @@ __device__ __forceinline__ bool tile_of_block(int bx, int n_row_tiles, int n_ct,
 // One output tile block of matrix `d`: output tile (rt, ct), K split by.
 // TM: output rows of the block (256, or 128 / 64 for short X, whose full-height tiles are too
 // few to fill the chip). The 8 consumer waves are 2 x 4: TM / 2 rows x 64 columns each.
-template <int kCF, int kYDT, int TM = kTM>
+// Xv: bf16 X (copied into LDS as is), or with kXF fp32 X in original row order, which the
+// consumers round to bf16 on the way into LDS (tiles of at most 128 rows, whose consumers have
+// the registers to hold two steps of X in flight).
+template <int kCF, int kYDT, int TM = kTM, bool kXF = false>
 __device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const int rt, const int ct, const int by,
-                                                const __bf16* __restrict__ X, int64_t ldx, void* __restrict__ Y,
+                                                const void* __restrict__ Xv, int64_t ldx, void* __restrict__ Y,
                                                 int64_t ldy, int M, int steps_per_split, float* __restrict__ part) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   constexpr int CW = cell_words(kCF);                     // words loaded per cell
@@ -232,6 +238,7 @@ __device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const in
   const bool gcols = kCF == kCellCols && (d.flags & MTC_FLAG_COLS_GATHERED) != 0;
   const int cw = kCF == kCellCols && !gcols ? 2 : CW;
   static_assert(TM == 256 || TM == 128 || TM == 64, "row tiles of 256, 128 or 64 rows");
+  static_assert(!kXF || TM <= 128, "fp32 X is rounded by the consumers of tiles of at most 128 rows");
   constexpr int DMA = TM / 8 / kConsumerWaves;             // 1 KiB (8-row) A copies per consumer wave
   constexpr int RW = TM / 2, RI = RW / 32;                 // rows per consumer wave, 32-row MFMA blocks
 
@@ -250,26 +257,18 @@ __device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const in
     // 8 rows, so it reads the logical segment that swz() maps there. Rows past M and
     // segments past K read zeros (out-of-range offsets).
     const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds;
-    const u32x4_t x_r = buffer_rsrc(X + (int64_t)m0 * ldx, (uint32_t)(TM * ldx * 2));
-    uint32_t a_off[DMA];
+    uint32_t a_off[DMA];                                   // element offset of the lane's segment in the tile
     int a_k[DMA];                                          // first K element of the lane's segment
 #pragma unroll
     for (int i = 0; i < DMA; ++i) {
       const int row = 8 * (DMA * wave + i) + (lane >> 3);
       const int lseg = (lane & 7) ^ (row & 7) ^ ((row >> 3) & 1);
       a_k[i] = lseg * 8;
-      a_off[i] = m0 + row < M ? (uint32_t)(row * ldx + lseg * 8) * 2 : kOutOfRange;
+      a_off[i] = m0 + row < M ? (uint32_t)(row * ldx + lseg * 8) : kOutOfRange;
     }
-    auto copy_a = [&](int s) __attribute__((always_inline)) {
-      const uint32_t buf = lds0 + (uint32_t)(s % kABufs) * kTileBytes;
-      const uint32_t kb = (uint32_t)((kb0 + s) * kTK) * 2;
-#pragma unroll
-      for (int i = 0; i < DMA; ++i) {
-        // K % 8 == 0, so a segment is wholly inside or outside K
-        const bool in = a_off[i] != kOutOfRange && (kb0 + s) * kTK + a_k[i] < d.K;
-        dma16(x_r, in ? a_off[i] + kb : kOutOfRange,
-              __builtin_amdgcn_readfirstlane(buf + (uint32_t)(DMA * wave + i) * 1024u));
-      }
+    // K % 8 == 0, so a segment is wholly inside or outside K
+    auto a_in = [&](int s, int i) __attribute__((always_inline)) {
+      return a_off[i] != kOutOfRange && (kb0 + s) * kTK + a_k[i] < d.K;
     };
 
     const int wm = wave >> 2, wn = wave & 3;
@@ -278,17 +277,8 @@ __device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const in
     for (int i = 0; i < RI; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[i][j] = f32x16_t{};
-    copy_a(0);
-    if (nks > 1) {
-      copy_a(1);
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA) : "memory");   // step 0's copies done
-    } else {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-    lds_barrier();                                         // step 0 staged
-    for (int ks = 0; ks < nks; ++ks) {
-      const bool ahead = ks + 2 < nks;
-      if (ahead) copy_a(ks + 2);                           // into the buffer step ks-1 used
+    // the MFMAs of step ks over its staged A and B tiles
+    auto mfma_step = [&](int ks) __attribute__((always_inline)) {
       const unsigned char* as = lds + (ks % kABufs) * kTileBytes;
       const unsigned char* bs = lds + (kABufs + (ks & 1)) * kTileBytes;
 #pragma unroll
@@ -307,13 +297,84 @@ __device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const in
           for (int j = 0; j < 2; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
       }
-      // step ks+1's copies (issued a step ago) must have landed before the barrier
-      if (ahead) {
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA) : "memory");
+    };
+
+    if constexpr (!kXF) {
+      const __bf16* X = reinterpret_cast<const __bf16*>(Xv);
+      const u32x4_t x_r = buffer_rsrc(X + (int64_t)m0 * ldx, (uint32_t)(TM * ldx * 2));
+      auto copy_a = [&](int s) __attribute__((always_inline)) {
+        const uint32_t buf = lds0 + (uint32_t)(s % kABufs) * kTileBytes;
+        const uint32_t kb = (uint32_t)((kb0 + s) * kTK) * 2;
+#pragma unroll
+        for (int i = 0; i < DMA; ++i)
+          dma16(x_r, a_in(s, i) ? a_off[i] * 2 + kb : kOutOfRange,
+                __builtin_amdgcn_readfirstlane(buf + (uint32_t)(DMA * wave + i) * 1024u));
+      };
+      copy_a(0);
+      if (nks > 1) {
+        copy_a(1);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA) : "memory");   // step 0's copies done
       } else {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }
-      lds_barrier();                                       // buffers of step ks free, step ks+1 staged
+      lds_barrier();                                       // step 0 staged
+      for (int ks = 0; ks < nks; ++ks) {
+        const bool ahead = ks + 2 < nks;
+        if (ahead) copy_a(ks + 2);                         // into the buffer step ks-1 used
+        mfma_step(ks);
+        // step ks+1's copies (issued a step ago) must have landed before the barrier
+        if (ahead) {
+          asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA) : "memory");
+        } else {
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        lds_barrier();                                     // buffers of step ks free, step ks+1 staged
+      }
+    } else {
+      // fp32 X: the lane reads its segment's 8 floats (two 16-byte loads; zeros past M and K),
+      // rounds them to bf16 as the staging kernels do (pk_bf16) and stores its slot. Step s + 2's
+      // loads go out before step s's MFMAs into the registers step s held; step s + 1's values
+      // are stored after them, into the buffer step s - 2 used.
+      const float* Xf = reinterpret_cast<const float*>(Xv);
+      const __amdgpu_buffer_rsrc_t xf_r = buffer_of(Xf + (int64_t)m0 * ldx, (int64_t)TM * ldx * 4);
+      typedef u32x4_t XRegs[DMA][2];
+      auto load_x = [&](int s, XRegs& r) __attribute__((always_inline)) {
+        const uint32_t kb = (uint32_t)((kb0 + s) * kTK) * 4;
+#pragma unroll
+        for (int i = 0; i < DMA; ++i) {
+          const bool in = a_in(s, i);
+          r[i][0] = __builtin_amdgcn_raw_buffer_load_b128(xf_r, in ? a_off[i] * 4 + kb : kOutOfRange, 0, 0);
+          r[i][1] = __builtin_amdgcn_raw_buffer_load_b128(xf_r, in ? a_off[i] * 4 + kb + 16 : kOutOfRange, 0, 0);
+        }
+      };
+      auto store_x = [&](int s, const XRegs& r) __attribute__((always_inline)) {
+        unsigned char* buf = lds + (s % kABufs) * kTileBytes;
+#pragma unroll
+        for (int i = 0; i < DMA; ++i) {
+          const u32x4_t lo = r[i][0], hi = r[i][1];
+          const u32x4_t o{pk_bf16(__uint_as_float(lo.x), __uint_as_float(lo.y)),
+                          pk_bf16(__uint_as_float(lo.z), __uint_as_float(lo.w)),
+                          pk_bf16(__uint_as_float(hi.x), __uint_as_float(hi.y)),
+                          pk_bf16(__uint_as_float(hi.z), __uint_as_float(hi.w))};
+          *reinterpret_cast<u32x4_t*>(buf + (DMA * wave + i) * 1024 + 16 * lane) = o;
+        }
+      };
+      XRegs ra, rb;
+      load_x(0, ra);
+      if (nks > 1) load_x(1, rb);
+      store_x(0, ra);
+      lds_barrier();                                       // step 0 staged
+      // cur: step ks's registers (stored a step ago), nxt: step ks + 1's
+      auto body = [&](int ks, XRegs& cur, const XRegs& nxt) __attribute__((always_inline)) {
+        if (ks + 2 < nks) load_x(ks + 2, cur);
+        mfma_step(ks);
+        if (ks + 1 < nks) store_x(ks + 1, nxt);
+        lds_barrier();                                     // buffers of step ks free, step ks+1 staged
+      };
+      for (int ks = 0; ks < nks; ks += 2) {
+        body(ks, ra, rb);
+        if (ks + 1 < nks) body(ks + 1, rb, ra);
+      }
     }
 
     // epilogue: C element e of lane l is row (e/4)*8 + (l/32)*4 + e%4, column l%32.
@@ -449,15 +510,16 @@ __device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const in
   }
 }
 
-// One output tile block of matrix `d`: output tile (rt, ct) of TM rows, K split by.
-template <int kCF, int kYDT, int TM>
-__global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, const __bf16* __restrict__ X,
+// One output tile block of matrix `d`: output tile (rt, ct) of TM rows, K split by; X is bf16,
+// or fp32 with kXF.
+template <int kCF, int kYDT, int TM, bool kXF = false>
+__global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, const void* __restrict__ X,
                                                         int64_t ldx, void* __restrict__ Y, int64_t ldy, int M,
                                                         int n_row_tiles, int tiles_per_xcd, int steps_per_split,
                                                         float* __restrict__ part) {
   int rt, ct;
   if (!tile_of_block((int)blockIdx.x, n_row_tiles, d.n_col_tiles, tiles_per_xcd, d.col_perm && !part, rt, ct)) return;
-  gemm_tile_block<kCF, kYDT, TM>(d, rt, ct, (int)blockIdx.y, X, ldx, Y, ldy, M, steps_per_split, part);
+  gemm_tile_block<kCF, kYDT, TM, kXF>(d, rt, ct, (int)blockIdx.y, X, ldx, Y, ldy, M, steps_per_split, part);
 }
 
 // Up to kMaxGroup matrices that read the same X, in one launch of each kernel: member i owns
@@ -796,18 +858,34 @@ size_t partial_bytes(const mtc_tile_desc* d, int M) {
   return splits > 1 ? (size_t)splits * M * d->N * 4 : 0;
 }
 
+// fp32 X that the tile kernel's consumers round to bf16 themselves, with no staging launch:
+// no row permutation, tiles of at most 128 rows, 16-byte aligned rows, and tile offsets within
+// 32 bits. The sums are those of the staged call (same bf16 values, same kernel otherwise).
+bool fused_x(const mtc_tile_desc* d, const void* X, int x_dtype, int64_t ldx, int M) {
+  return x_dtype == MTC_DTYPE_F32 && !d->row_perm && cell_format(d) != kCellCols && tile_plan(d, M).tm <= 128 &&
+         ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 && ldx < ((int64_t)1 << 31) / (4 * kTM);
+}
+
 template <int kCF, int kYDT>
-int launch_tile(const mtc_tile_desc* d, const __bf16* X, int64_t ldx, void* Y, int64_t ldy, int M, float* part,
-                hipStream_t st) {
+int launch_tile(const mtc_tile_desc* d, const void* X, int64_t ldx, void* Y, int64_t ldy, int M, float* part,
+                hipStream_t st, bool xf = false) {
   if ((size_t)kLdsBytes > mtc::host::device_lds_limit())
     return fail(MTC_E_SHAPE, "prefill kernel needs %d B of LDS per block, device has %zu", kLdsBytes,
                 mtc::host::device_lds_limit());
-  if (ldx >= ((int64_t)1 << 31) / (2 * kTM))
+  if (ldx >= ((int64_t)1 << 31) / ((xf ? 4 : 2) * kTM))
     return fail(MTC_E_SHAPE, "ldx=%lld too large for 32-bit X tile offsets", (long long)ldx);
   const TilePlan p = tile_plan(d, M);
+  if (xf && p.tm > 128) return fail(MTC_E_SHAPE, "fp32 X is read in place by tiles of at most 128 rows only");
   const void* fn = p.tm == 256 ? reinterpret_cast<const void*>(&k_gemm_tile<kCF, kYDT, 256>)
                    : p.tm == 128 ? reinterpret_cast<const void*>(&k_gemm_tile<kCF, kYDT, 128>)
                                  : reinterpret_cast<const void*>(&k_gemm_tile<kCF, kYDT, 64>);
+  if constexpr (kCF != kCellCols) {
+    if (xf)
+      fn = p.tm == 128 ? reinterpret_cast<const void*>(&k_gemm_tile<kCF, kYDT, 128, true>)
+                       : reinterpret_cast<const void*>(&k_gemm_tile<kCF, kYDT, 64, true>);
+  } else if (xf) {
+    return fail(MTC_E_SHAPE, "fp32 X is not read in place for gathered-column streams");
+  }
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
   if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
   const int n_row_tiles = (M + p.tm - 1) / p.tm;
@@ -815,17 +893,12 @@ int launch_tile(const mtc_tile_desc* d, const __bf16* X, int64_t ldx, void* Y, i
   if (n_tiles > (int64_t)1 << 30) return fail(MTC_E_SHAPE, "M=%d gives too many tiles", M);
   const int tiles_per_xcd = (int)((n_tiles + kXcds - 1) / kXcds);
   const int splits = p.splits, per = p.per;
-  float* const pt = splits > 1 ? part : nullptr;
+  float* pt = splits > 1 ? part : nullptr;
+  int nrt = n_row_tiles, tpx = tiles_per_xcd, spp = per;
   const dim3 grid(tiles_per_xcd * kXcds, splits);
-  if (p.tm == 256)
-    hipLaunchKernelGGL((k_gemm_tile<kCF, kYDT, 256>), grid, dim3(kThreads), kLdsBytes, st, *d, X, ldx, Y, ldy, M,
-                       n_row_tiles, tiles_per_xcd, per, pt);
-  else if (p.tm == 128)
-    hipLaunchKernelGGL((k_gemm_tile<kCF, kYDT, 128>), grid, dim3(kThreads), kLdsBytes, st, *d, X, ldx, Y, ldy, M,
-                       n_row_tiles, tiles_per_xcd, per, pt);
-  else
-    hipLaunchKernelGGL((k_gemm_tile<kCF, kYDT, 64>), grid, dim3(kThreads), kLdsBytes, st, *d, X, ldx, Y, ldy, M,
-                       n_row_tiles, tiles_per_xcd, per, pt);
+  void* args[] = {const_cast<mtc_tile_desc*>(d), &X, &ldx, &Y, &ldy, &M, &nrt, &tpx, &spp, &pt};
+  e = hipLaunchKernel(fn, grid, dim3(kThreads), args, kLdsBytes, st);
+  if (e != hipSuccess) return fail(MTC_E_LAUNCH, "k_gemm_tile launch: %s", hipGetErrorString(e));
   int rc = check_launch("k_gemm_tile");
   if (rc || splits == 1) return rc;
   hipLaunchKernelGGL(k_splitk_reduce<kYDT>, dim3((unsigned)reduce_blocks(M, d->N, d->col_perm != nullptr)),
@@ -1185,7 +1258,6 @@ MTC_API int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, in
   if (M <= 0) return fail(MTC_E_SHAPE, "M=%d must be positive", M);
   if (ldx < d->K || ldy < d->N) return fail(MTC_E_SHAPE, "ldx=%lld < K or ldy=%lld < N", (long long)ldx, (long long)ldy);
   hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);
-  const __bf16* xb = reinterpret_cast<const __bf16*>(X);
   int64_t ldb = ldx;
   const size_t stage = staging_bytes(d, M, x_dtype), need = stage + partial_bytes(d, M);
   if (!stage && (ldx % 8 || (reinterpret_cast<uintptr_t>(X) & 15)))
@@ -1195,7 +1267,9 @@ MTC_API int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, in
   if (need && (reinterpret_cast<uintptr_t>(workspace) & 255))
     return fail(MTC_E_WORKSPACE, "workspace not 256-byte aligned");
   float* part = need > stage ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + stage) : nullptr;
-  if (stage) {
+  const void* xa = X;                                  // what the tile kernel reads: X or the staged copy
+  const bool xf = fused_x(d, X, x_dtype, ldx, M);      // fp32 X rounded by the tile kernel (staging area unused)
+  if (stage && !xf) {
     const int R = stage_rows_for(d->K, M);
     if (R) {
       hipLaunchKernelGGL(k_stage_x_rows, dim3((unsigned)((M + R - 1) / R)), dim3(kStageThreads),
@@ -1208,20 +1282,20 @@ MTC_API int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, in
     }
     rc = check_launch("k_stage_x");
     if (rc) return rc;
-    xb = reinterpret_cast<const __bf16*>(workspace);
+    xa = workspace;
     ldb = d->K;
   }
   const bool f32 = y_dtype == MTC_DTYPE_F32;
   switch (cell_format(d)) {
     case kCellFp32:
-      return f32 ? launch_tile<kCellFp32, MTC_DTYPE_F32>(d, xb, ldb, Y, ldy, M, part, st)
-                 : launch_tile<kCellFp32, MTC_DTYPE_BF16>(d, xb, ldb, Y, ldy, M, part, st);
+      return f32 ? launch_tile<kCellFp32, MTC_DTYPE_F32>(d, xa, ldb, Y, ldy, M, part, st, xf)
+                 : launch_tile<kCellFp32, MTC_DTYPE_BF16>(d, xa, ldb, Y, ldy, M, part, st, xf);
     case kCellCols:
-      return f32 ? launch_tile<kCellCols, MTC_DTYPE_F32>(d, xb, ldb, Y, ldy, M, part, st)
-                 : launch_tile<kCellCols, MTC_DTYPE_BF16>(d, xb, ldb, Y, ldy, M, part, st);
+      return f32 ? launch_tile<kCellCols, MTC_DTYPE_F32>(d, xa, ldb, Y, ldy, M, part, st)
+                 : launch_tile<kCellCols, MTC_DTYPE_BF16>(d, xa, ldb, Y, ldy, M, part, st);
     default:
-      return f32 ? launch_tile<kCellBf16, MTC_DTYPE_F32>(d, xb, ldb, Y, ldy, M, part, st)
-                 : launch_tile<kCellBf16, MTC_DTYPE_BF16>(d, xb, ldb, Y, ldy, M, part, st);
+      return f32 ? launch_tile<kCellBf16, MTC_DTYPE_F32>(d, xa, ldb, Y, ldy, M, part, st, xf)
+                 : launch_tile<kCellBf16, MTC_DTYPE_BF16>(d, xa, ldb, Y, ldy, M, part, st, xf);
   }
 }
 

@@ -325,11 +325,17 @@ class DeviceTiles:
         xdt = _abi.MTC_DTYPE_BF16 if X.dtype == torch.bfloat16 else _abi.MTC_DTYPE_F32
         ydt = _abi.MTC_DTYPE_BF16 if out.dtype == torch.bfloat16 else _abi.MTC_DTYPE_F32
         ws, nbytes = self.workspace(M, xdt)
-        rc = self.lib.mtc_gemm_bf16(ctypes.byref(self.desc), X.data_ptr(), xdt, X.stride(0), out.data_ptr(), ydt,
-                                    out.stride(0), M, None if ws is None else ws.data_ptr(), nbytes,
+        rc = self.lib.mtc_gemm_bf16(ctypes.byref(self.desc), X.data_ptr(), xdt, _row_stride(X), out.data_ptr(), ydt,
+                                    _row_stride(out), M, None if ws is None else ws.data_ptr(), nbytes,
                                     current_stream_handle(self.device))
         _abi.check(self.lib, "mtc_gemm_bf16", rc)
         return out
+
+
+def _row_stride(T) -> int:
+    """Elements between rows of a row-major matrix view; a single row's stride is never used, so
+    it is given as the row length (a one-row slice of a wider matrix keeps the wide stride)."""
+    return T.stride(0) if T.shape[0] > 1 else T.shape[1]
 
 
 class GemmBatch:
@@ -371,7 +377,7 @@ class GemmBatch:
         items = (_abi.MtcGemmBatchItem * n)()
         for it, t, X, o in zip(items, self.tiles, self.Xs, self.outs):
             it.desc = ctypes.pointer(t.desc)
-            it.X, it.ldx, it.Y, it.ldy = X.data_ptr(), X.stride(0), o.data_ptr(), o.stride(0)
+            it.X, it.ldx, it.Y, it.ldy = X.data_ptr(), _row_stride(X), o.data_ptr(), _row_stride(o)
         plan_n, ws_n = ctypes.c_size_t(), ctypes.c_size_t()
         _abi.check(lib, "mtc_gemm_batch_plan", lib.mtc_gemm_batch_plan(items, n, M, xdt, ydt, None, 0, None, 0,
                                                                        ctypes.byref(plan_n), ctypes.byref(ws_n)))
@@ -439,8 +445,8 @@ def gemm_bf16_group(tiles, X, outs=None, out_dtype=None):
     if need and (ws is None or ws.numel() < need):
         ws = _GROUP_WS[key] = torch.empty(need, dtype=torch.uint8, device=dev)
     ys = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
-    lds = (ctypes.c_int64 * n)(*[o.stride(0) for o in outs])
-    rc = lib.mtc_gemm_bf16_group(descs, n, X.data_ptr(), xdt, X.stride(0), ys, ydt, lds, M,
+    lds = (ctypes.c_int64 * n)(*[_row_stride(o) for o in outs])
+    rc = lib.mtc_gemm_bf16_group(descs, n, X.data_ptr(), xdt, _row_stride(X), ys, ydt, lds, M,
                                  ws.data_ptr() if need else None, need, current_stream_handle(dev))
     _abi.check(lib, "mtc_gemm_bf16_group", rc)
     return outs

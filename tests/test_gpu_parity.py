@@ -171,6 +171,32 @@ def test_gemm_short_row_tiles(gpu):
         assert np.array_equal(_bits(Yg), _bits(Y)), M
 
 
+@pytest.mark.parametrize("K,ldx", [(2048, 2048), (992, 992), (992, 995)])
+def test_gemm_fp32_x_read_in_place(gpu, K, ldx):
+    """fp32 X without a row permutation, at M <= 256 (tiles of 64 or 128 rows): the tile
+    kernel's consumers round X to bf16 themselves instead of a staging launch. Y equals the
+    call on bf16(X) bit for bit (one split and split K, a partial last K-step at K = 992), and
+    rows not 16-byte aligned (ldx = 995) take the staging launch with the same Y."""
+    import torch
+    N = 512
+    W = outlier_matrix(61, K, N)
+    a = QuadtreeRD(W, None, (32, 16, 8, 4)).select(3.5)
+    m = MTCMatrix.from_quadtree(a, W)
+    g = m.device_tiles(gpu)
+    ref_w = _oracle_what(a, W)
+    for M in (1, 37, 64, 100, 128, 200, 256):
+        _say("gemm fp32 X in place", K, ldx, M)
+        X = np.random.RandomState(M + 5).randn(M, K).astype(np.float32)
+        big = torch.zeros(M, ldx, device=gpu)
+        big[:, :K] = torch.from_numpy(X).to(gpu)
+        Xf = big[:, :K]
+        Yf = g.gemm_bf16(Xf).cpu().numpy()
+        Yb = g.gemm_bf16(Xf.to(torch.bfloat16).contiguous()).cpu().numpy()
+        assert np.array_equal(_bits(Yf), _bits(Yb)), (K, ldx, M)
+        err = O.relative_frobenius_error(O.qt_gemm_f64(O.bf16_round(X), ref_w), Yf)
+        assert err <= TOL_BF16, (K, ldx, M, err)
+
+
 @pytest.mark.parametrize("M,permuted,ydt", [(100, False, "f32"), (300, True, "f32"), (37, True, "bf16")])
 def test_gemm_split_k(gpu, M, permuted, ydt):
     # few output tiles and 32 K-steps: the K steps are split over blocks and the fp32
