@@ -162,7 +162,8 @@ def load_tiles(path):
 def pmc_child_tiles(folder):
     """Body of one counter pass of the prefill: the calibration copies, then four calls over the
     tile streams saved in `folder` (tiles_NNN.npz; inputs x.npz, one per K, fp32 or bf16 bits):
-    one matrix runs gemm_bf16, several one batched prefill (GemmBatch)."""
+    one matrix runs gemm_bf16 (gemm_f32 when the folder holds a file named f32), several one
+    batched prefill (GemmBatch)."""
     import torch
     from tensorpack_amd.device import DeviceTiles, GemmBatch
     n = len([f for f in os.listdir(folder) if f.startswith("tiles_")])
@@ -179,7 +180,9 @@ def pmc_child_tiles(folder):
     X = {K: dev_x(x) for K, x in xs.items()}
     M = next(iter(X.values())).shape[0]
     Ys = [torch.empty((M, t.N), dtype=torch.float32, device="cuda") for t in tiles]
-    if n == 1:
+    if n == 1 and os.path.exists(os.path.join(folder, "f32")):
+        launch = lambda: tiles[0].gemm_f32(X[tiles[0].K], out=Ys[0])
+    elif n == 1:
         launch = lambda: tiles[0].gemm_bf16(X[tiles[0].K], out=Ys[0])
     else:
         batch = GemmBatch(tiles, [X[t.K] for t in tiles], Ys)
@@ -193,18 +196,21 @@ def pmc_child_tiles(folder):
 
 
 PREFILL_KERNELS = ("k_stage_x", "k_gemm_tile", "k_splitk_reduce")
+F32_TILE_KERNELS = ("k_stage_x_f32", "k_gemm_f32", "k_splitk_reduce")
 
 
-def traffic_passes_tiles(tss, xs):
-    """HBM bytes per prefill call over the tile streams `tss` (one: gemm_bf16; several: one batched
-    prefill), summed over the call's launches (X staging, tiles, split-K reduction); `xs`: one
-    input per K, fp32 or bf16 (as uint16 bits). See counter_passes."""
+def traffic_passes_tiles(tss, xs, f32=False):
+    """HBM bytes per prefill call over the tile streams `tss` (one: gemm_bf16, or gemm_f32 with
+    `f32`; several: one batched prefill), summed over the call's launches (X staging, tiles,
+    split-K reduction); `xs`: one input per K, fp32 or bf16 (as uint16 bits). See counter_passes."""
     import tempfile
     tmp = tempfile.mkdtemp(prefix="mtc_pmc_")
     for i, ts in enumerate(tss):
         save_tiles(ts, os.path.join(tmp, f"tiles_{i:03d}.npz"))
     np.savez(os.path.join(tmp, "x.npz"), **{f"k{K}": x for K, x in xs.items()})
-    return counter_passes(tmp, ["--pmc-child-tiles", tmp], PREFILL_KERNELS, launches=5)
+    if f32:
+        open(os.path.join(tmp, "f32"), "w").close()
+    return counter_passes(tmp, ["--pmc-child-tiles", tmp], F32_TILE_KERNELS if f32 else PREFILL_KERNELS, launches=5)
 
 
 def bf16_bits(x):

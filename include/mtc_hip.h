@@ -295,6 +295,18 @@ size_t mtc_gemm_workspace_bytes(const mtc_tile_desc* d, int M, int x_dtype);
 int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, int64_t ldx, void* Y, int y_dtype,
                   int64_t ldy, int M, void* workspace, size_t workspace_bytes, void* hip_stream);
 
+/* fp32 matrix-core path over the tile stream: Y (M x N fp32, leading dim ldy) = X (M x K
+ * fp32, leading dim ldx) * W_hat with the exact fp32 W_hat and fp32 products and sums
+ * (v_mfma_f32_16x16x4f32), in 16-row tiles with K split over blocks until the chip is full;
+ * within the fp32 tolerance of the reference's float32 block loop (mtc/kernels/gemm.py:124-210,
+ * the same operation as mtc_gemv_f32, for callers at 5..16 rows and beyond). X read in place
+ * must have 16-byte aligned rows (ldx % 4 == 0); a stream with a row permutation gathers X
+ * into the workspace first. Workspace (mtc_gemm_f32_workspace_bytes, 256-byte aligned, no
+ * initialisation): the gathered X (M*K*4) and the split-K partials. */
+size_t mtc_gemm_f32_workspace_bytes(const mtc_tile_desc* d, int M);
+int mtc_gemm_f32(const mtc_tile_desc* d, const float* X, int64_t ldx, float* Y, int64_t ldy, int M,
+                 void* workspace, size_t workspace_bytes, void* hip_stream);
+
 /* Prefill for n (1..MTC_MAX_GROUP) matrices that read the same X, one launch per kernel
  * (X staging, tile GEMM, split-K reduction) instead of one per matrix:
  * Y[i] (M x N_i, leading dim ldy[i]) = X * W_hat_i. Every tile stream must have the same

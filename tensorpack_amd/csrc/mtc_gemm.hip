@@ -76,6 +76,7 @@ static_assert(2 * kProducers == kCells, "two cells per producer thread");
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // Byte offset of 16-byte segment `seg` (0..7) of row `row` in a [rows][64] bf16 tile.
@@ -86,6 +87,14 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 // r + 8 share parity and get different segments.
 __device__ __forceinline__ uint32_t swz(int row, int seg) {
   return (uint32_t)(row * 128 + ((seg ^ (row & 7) ^ ((row >> 3) & 1)) << 4));
+}
+
+// fp32 tiles of the matrix-core fp32 path: [rows][64] floats, 256 bytes (all 64 banks) per row,
+// 16-byte segment `seg` (0..15) of row `row` stored at segment seg ^ (row & 15), so the 16 rows
+// that one MFMA operand read takes at one segment land in 16 different segments.
+constexpr int kTileBytesF32 = kTN * kTK * 4;             // one fp32 B tile (64 KiB)
+__device__ __forceinline__ uint32_t swz_f32(int row, int seg) {
+  return (uint32_t)(row * 256 + ((seg ^ (row & 15)) << 4));
 }
 
 // Hides a value's known bits so byte extraction compiles to v_cvt_f32_ubyteN.
@@ -194,6 +203,60 @@ __device__ __forceinline__ void decode_cell(uint32_t cls, const u32x4_t* pw, con
   }
 }
 
+// decode_cell in fp32: out[j][r] = (u - offset) * s for column j, row r (the exact W_hat value,
+// fma(u, s, -offset * s), before any bf16 rounding).
+template <bool PC>
+__device__ __forceinline__ void decode_cell_f32(uint32_t cls, const u32x4_t* pw, const float (&st)[4],
+                                                const float (&sb)[4], float (&out)[4][8]) {
+  constexpr int NS = PC ? 4 : 1;
+  float ct[NS], cb[NS];
+  auto offset_terms = [&](float off) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      ct[j] = -off * st[j];
+      cb[j] = -off * sb[j];
+    }
+  };
+  // rows 0-3 from the bytes of `top`, rows 4-7 from `bot`
+  auto bytes = [&](int j, uint32_t top, uint32_t bot, int k) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      out[j][r] = __builtin_fmaf((float)((top >> (8 * r)) & 0xFFu), st[k], ct[k]);
+      out[j][4 + r] = __builtin_fmaf((float)((bot >> (8 * r)) & 0xFFu), sb[k], cb[k]);
+    }
+  };
+  if (cls == 0) {
+    offset_terms(8.0f);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t x = pw[0][j];
+      bytes(j, opaque(x & 0x0F0F0F0Fu), opaque((x >> 4) & 0x0F0F0F0Fu), PC ? j : 0);
+    }
+  } else if (cls == 1) {
+    offset_terms(128.0f);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bytes(j, pw[j >> 1][(2 * j) & 3], pw[j >> 1][(2 * j + 1) & 3], PC ? j : 0);
+  } else if (cls == 2) {
+    offset_terms(32768.0f);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = PC ? j : 0;
+      const uint32_t v[4] = {pw[j].x, pw[j].y, pw[j].z, pw[j].w};
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const float s = h < 2 ? st[k] : sb[k], c = h < 2 ? ct[k] : cb[k];
+        out[j][2 * h] = __builtin_fmaf((float)(v[h] & 0xFFFFu), s, c);
+        out[j][2 * h + 1] = __builtin_fmaf((float)(v[h] >> 16), s, c);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 8; ++r) out[j][r] = 0.0f;
+  }
+}
+
 // Output tile (rt, ct) of a launch of one matrix from its block index bx: each XCD (bx % 8)
 // takes a contiguous range of tile ids. Without an output column permutation the ids run
 // over groups of kRowGroup row tiles, row tile fastest, so the blocks in flight on one XCD
@@ -220,6 +283,135 @@ __device__ __forceinline__ bool tile_of_block(int bx, int n_row_tiles, int n_ct,
   return true;
 }
 
+// The producer waves of a tile block (pid: 0 .. kProducers-1): load the step's cell descriptors and
+// payload, decode the cells of step k+1 into B buffer (k+1) & 1 at bbase (bf16 [256][64] tiles, or
+// with F32 fp32 [256][64] tiles in swz_f32 order) while the consumers multiply step k, and
+// meet the consumers at one LDS-only barrier per step.
+template <int kCF, bool F32>
+__device__ __forceinline__ void tile_producers(const mtc_tile_desc& d, const int ct, const int kb0, const int nks,
+                                               unsigned char* bbase, const int pid) {
+  constexpr int CW = cell_words(kCF);                     // words loaded per cell
+  // words per cell of this stream: the kCellCols kernel also runs bf16-pair streams (a group or
+  // batch that mixes them with gathered-column ones); their cells are 2 words, and the words a
+  // load reads past a cell are not used
+  const bool gcols = kCF == kCellCols && (d.flags & MTC_FLAG_COLS_GATHERED) != 0;
+  const int cw = kCF == kCellCols && !gcols ? 2 : CW;
+  const int p = pid;                                       // 0 .. kProducers-1
+  const uint32_t* step_off = d.step_off + (size_t)ct * d.n_ksteps + kb0;
+  // cells p and p + kProducers of a step: descriptor words (two sets that swap roles
+  // every step, so no register copies wait on loads in flight) and payload words.
+  // Every load goes through a buffer resource and every cell issues the same loads
+  // (one descriptor load, four 16-byte payload loads; those its class does not need
+  // read past the buffer's end and return zeros): with no per-lane branches around
+  // loads, the compiler's waits count exactly, so a step waits only for the loads
+  // issued a step earlier, never for the ones it has just issued.
+  const __amdgpu_buffer_rsrc_t cell_r = buffer_of(d.cells + ((size_t)ct * d.n_ksteps + kb0) * kCells * cw,
+                                                  (int64_t)nks * kCells * cw * 4);
+  const __amdgpu_buffer_rsrc_t pay_r = buffer_of(d.payload, d.payload_dwords * 4);
+  uint32_t sa0[CW], sa1[CW], sb0[CW], sb1[CW];
+  uint32_t base_a = 0, base_b = 0;
+  u32x4_t q0[4], q1[4];
+  auto load_words = [&](uint32_t off, uint32_t (&w)[CW]) __attribute__((always_inline)) {
+    if constexpr (CW == 2) {
+      const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(cell_r, off, 0, 0);
+      w[0] = v.x;
+      w[1] = v.y;
+    } else {
+#pragma unroll
+      for (int h = 0; h < CW / 4; ++h) {
+        const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(cell_r, off + 16u * h, 0, 0);
+        w[4 * h + 0] = v.x;
+        w[4 * h + 1] = v.y;
+        w[4 * h + 2] = v.z;
+        w[4 * h + 3] = v.w;
+      }
+    }
+  };
+  auto load_desc = [&](int ks, uint32_t (&w0)[CW], uint32_t (&w1)[CW], uint32_t& base) {
+    load_words((uint32_t)((ks * kCells + p) * cw) * 4u, w0);
+    load_words((uint32_t)((ks * kCells + p + kProducers) * cw) * 4u, w1);
+    base = step_off[ks];
+  };
+  auto load_cell = [&](const uint32_t (&w)[CW], uint32_t base, u32x4_t (&q)[4]) {
+    const uint32_t cls = (w[0] >> 14) & 3u;
+    const uint32_t o = (base + (w[0] & 0x3FFFu)) * 4u;
+    const uint32_t n = cls == 0 ? 1u : cls == 1 ? 2u : cls == 2 ? 4u : 0u;
+#pragma unroll
+    for (uint32_t t = 0; t < 4; ++t)
+      q[t] = __builtin_amdgcn_raw_buffer_load_b128(pay_r, t < n ? o + 16u * t : kOutOfRange, 0, 0);
+  };
+  auto load_payload = [&](const uint32_t (&w0)[CW], const uint32_t (&w1)[CW], uint32_t base) {
+    load_cell(w0, base, q0);
+    load_cell(w1, base, q1);
+  };
+  auto stage_cell = [&](unsigned char* bs, const uint32_t (&w)[CW], const u32x4_t (&q)[4]) {
+    float st[4], sb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (kCF == kCellFp32) {
+        st[j] = __uint_as_float(w[1]);
+        sb[j] = __uint_as_float(w[2]);
+      } else {
+        const uint32_t sw = gcols ? w[1 + j] : w[1];          // column j's scales, or the cell's
+        st[j] = __uint_as_float(sw << 16);
+        sb[j] = __uint_as_float(sw & 0xFFFF0000u);
+      }
+    }
+    const uint32_t pos = w[0] >> 16;
+    const int col = (int)(pos >> 3) * 4, seg = (int)(pos & 7u);
+    if constexpr (F32) {
+      float o[4][8];
+      decode_cell_f32<kCF == kCellCols>((w[0] >> 14) & 3u, q, st, sb, o);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = col + j;
+        *reinterpret_cast<f32x4_t*>(bs + swz_f32(n, 2 * seg)) = f32x4_t{o[j][0], o[j][1], o[j][2], o[j][3]};
+        *reinterpret_cast<f32x4_t*>(bs + swz_f32(n, 2 * seg + 1)) = f32x4_t{o[j][4], o[j][5], o[j][6], o[j][7]};
+      }
+    } else {
+      u32x4_t o[4];
+      decode_cell<kCF == kCellCols>((w[0] >> 14) & 3u, q, st, sb, o);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4_t*>(bs + swz(col + j, seg)) = o[j];
+    }
+  };
+  auto fill = [&](int buf, const uint32_t (&w0)[CW], const uint32_t (&w1)[CW]) {
+    unsigned char* bs = bbase + buf * (F32 ? kTileBytesF32 : kTileBytes);
+    stage_cell(bs, w0, q0);
+    stage_cell(bs, w1, q1);
+  };
+  // One step while the consumers multiply step ks: stage step ks+1's B tile (descriptors
+  // `cur`, payload already in registers), then load step ks+2's payload (its descriptors
+  // `nxt` were loaded a step earlier) and step ks+3's descriptors into `cur`.
+  auto step = [&](int ks, uint32_t (&c0)[CW], uint32_t (&c1)[CW], uint32_t& cbase, const uint32_t (&n0)[CW],
+                  const uint32_t (&n1)[CW], uint32_t nbase) __attribute__((always_inline)) {
+    if (ks + 1 < nks) {
+      fill((ks + 1) & 1, c0, c1);
+      if (ks + 2 < nks) {
+        load_payload(n0, n1, nbase);
+        if (ks + 3 < nks) load_desc(ks + 3, c0, c1, cbase);
+      }
+    }
+    lds_barrier();
+  };
+
+  // prologue: stage step 0's B tile; hold step 1's payload in registers with its
+  // descriptors in set a, and step 2's descriptors in set b
+  load_desc(0, sb0, sb1, base_b);
+  if (nks > 1) load_desc(1, sa0, sa1, base_a);
+  load_payload(sb0, sb1, base_b);
+  fill(0, sb0, sb1);
+  if (nks > 1) {
+    load_payload(sa0, sa1, base_a);
+    if (nks > 2) load_desc(2, sb0, sb1, base_b);
+  }
+  lds_barrier();
+  for (int ks = 0; ks < nks; ks += 2) {
+    step(ks, sa0, sa1, base_a, sb0, sb1, base_b);
+    if (ks + 1 < nks) step(ks + 1, sb0, sb1, base_b, sa0, sa1, base_a);
+  }
+}
+
 // One output tile block of matrix `d`: output tile (rt, ct), K split by.
 // TM: output rows of the block (256, or 128 / 64 for short X, whose full-height tiles are too
 // few to fill the chip). The 8 consumer waves are 2 x 4: TM / 2 rows x 64 columns each.
@@ -231,12 +423,6 @@ __device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const in
                                                 const void* __restrict__ Xv, int64_t ldx, void* __restrict__ Y,
                                                 int64_t ldy, int M, int steps_per_split, float* __restrict__ part) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-  constexpr int CW = cell_words(kCF);                     // words loaded per cell
-  // words per cell of this stream: the kCellCols kernel also runs bf16-pair streams (a group or
-  // batch that mixes them with gathered-column ones); their cells are 2 words, and the words a
-  // load reads past a cell are not used
-  const bool gcols = kCF == kCellCols && (d.flags & MTC_FLAG_COLS_GATHERED) != 0;
-  const int cw = kCF == kCellCols && !gcols ? 2 : CW;
   static_assert(TM == 256 || TM == 128 || TM == 64, "row tiles of 256, 128 or 64 rows");
   static_assert(!kXF || TM <= 128, "fp32 X is rounded by the consumers of tiles of at most 128 rows");
   constexpr int DMA = TM / 8 / kConsumerWaves;             // 1 KiB (8-row) A copies per consumer wave
@@ -404,110 +590,7 @@ __device__ __forceinline__ void gemm_tile_block(const mtc_tile_desc& d, const in
     return;
   }
 
-  // ---------------- producers: load X and cells, decode, stage the next step ----------------
-  const int p = tid - 64 * kConsumerWaves;                 // 0 .. kProducers-1
-  const uint32_t* step_off = d.step_off + (size_t)ct * d.n_ksteps + kb0;
-  // cells p and p + kProducers of a step: descriptor words (two sets that swap roles
-  // every step, so no register copies wait on loads in flight) and payload words.
-  // Every load goes through a buffer resource and every cell issues the same loads
-  // (one descriptor load, four 16-byte payload loads; those its class does not need
-  // read past the buffer's end and return zeros): with no per-lane branches around
-  // loads, the compiler's waits count exactly, so a step waits only for the loads
-  // issued a step earlier, never for the ones it has just issued.
-  const __amdgpu_buffer_rsrc_t cell_r = buffer_of(d.cells + ((size_t)ct * d.n_ksteps + kb0) * kCells * cw,
-                                                  (int64_t)nks * kCells * cw * 4);
-  const __amdgpu_buffer_rsrc_t pay_r = buffer_of(d.payload, d.payload_dwords * 4);
-  uint32_t sa0[CW], sa1[CW], sb0[CW], sb1[CW];
-  uint32_t base_a = 0, base_b = 0;
-  u32x4_t q0[4], q1[4];
-  auto load_words = [&](uint32_t off, uint32_t (&w)[CW]) __attribute__((always_inline)) {
-    if constexpr (CW == 2) {
-      const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(cell_r, off, 0, 0);
-      w[0] = v.x;
-      w[1] = v.y;
-    } else {
-#pragma unroll
-      for (int h = 0; h < CW / 4; ++h) {
-        const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(cell_r, off + 16u * h, 0, 0);
-        w[4 * h + 0] = v.x;
-        w[4 * h + 1] = v.y;
-        w[4 * h + 2] = v.z;
-        w[4 * h + 3] = v.w;
-      }
-    }
-  };
-  auto load_desc = [&](int ks, uint32_t (&w0)[CW], uint32_t (&w1)[CW], uint32_t& base) {
-    load_words((uint32_t)((ks * kCells + p) * cw) * 4u, w0);
-    load_words((uint32_t)((ks * kCells + p + kProducers) * cw) * 4u, w1);
-    base = step_off[ks];
-  };
-  auto load_cell = [&](const uint32_t (&w)[CW], uint32_t base, u32x4_t (&q)[4]) {
-    const uint32_t cls = (w[0] >> 14) & 3u;
-    const uint32_t o = (base + (w[0] & 0x3FFFu)) * 4u;
-    const uint32_t n = cls == 0 ? 1u : cls == 1 ? 2u : cls == 2 ? 4u : 0u;
-#pragma unroll
-    for (uint32_t t = 0; t < 4; ++t)
-      q[t] = __builtin_amdgcn_raw_buffer_load_b128(pay_r, t < n ? o + 16u * t : kOutOfRange, 0, 0);
-  };
-  auto load_payload = [&](const uint32_t (&w0)[CW], const uint32_t (&w1)[CW], uint32_t base) {
-    load_cell(w0, base, q0);
-    load_cell(w1, base, q1);
-  };
-  auto stage_cell = [&](unsigned char* bs, const uint32_t (&w)[CW], const u32x4_t (&q)[4]) {
-    float st[4], sb[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if constexpr (kCF == kCellFp32) {
-        st[j] = __uint_as_float(w[1]);
-        sb[j] = __uint_as_float(w[2]);
-      } else {
-        const uint32_t sw = gcols ? w[1 + j] : w[1];          // column j's scales, or the cell's
-        st[j] = __uint_as_float(sw << 16);
-        sb[j] = __uint_as_float(sw & 0xFFFF0000u);
-      }
-    }
-    const uint32_t pos = w[0] >> 16;
-    const int col = (int)(pos >> 3) * 4, seg = (int)(pos & 7u);
-    u32x4_t o[4];
-    decode_cell<kCF == kCellCols>((w[0] >> 14) & 3u, q, st, sb, o);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4_t*>(bs + swz(col + j, seg)) = o[j];
-  };
-  auto fill = [&](int buf, const uint32_t (&w0)[CW], const uint32_t (&w1)[CW]) {
-    unsigned char* bs = lds + (kABufs + buf) * kTileBytes;
-    stage_cell(bs, w0, q0);
-    stage_cell(bs, w1, q1);
-  };
-  // One step while the consumers multiply step ks: stage step ks+1's B tile (descriptors
-  // `cur`, payload already in registers), then load step ks+2's payload (its descriptors
-  // `nxt` were loaded a step earlier) and step ks+3's descriptors into `cur`.
-  auto step = [&](int ks, uint32_t (&c0)[CW], uint32_t (&c1)[CW], uint32_t& cbase, const uint32_t (&n0)[CW],
-                  const uint32_t (&n1)[CW], uint32_t nbase) __attribute__((always_inline)) {
-    if (ks + 1 < nks) {
-      fill((ks + 1) & 1, c0, c1);
-      if (ks + 2 < nks) {
-        load_payload(n0, n1, nbase);
-        if (ks + 3 < nks) load_desc(ks + 3, c0, c1, cbase);
-      }
-    }
-    lds_barrier();
-  };
-
-  // prologue: stage step 0's B tile; hold step 1's payload in registers with its
-  // descriptors in set a, and step 2's descriptors in set b
-  load_desc(0, sb0, sb1, base_b);
-  if (nks > 1) load_desc(1, sa0, sa1, base_a);
-  load_payload(sb0, sb1, base_b);
-  fill(0, sb0, sb1);
-  if (nks > 1) {
-    load_payload(sa0, sa1, base_a);
-    if (nks > 2) load_desc(2, sb0, sb1, base_b);
-  }
-  lds_barrier();
-  for (int ks = 0; ks < nks; ks += 2) {
-    step(ks, sa0, sa1, base_a, sb0, sb1, base_b);
-    if (ks + 1 < nks) step(ks + 1, sb0, sb1, base_b, sa0, sa1, base_a);
-  }
+  tile_producers<kCF, false>(d, ct, kb0, nks, lds + kABufs * kTileBytes, tid - 64 * kConsumerWaves);
 }
 
 // One output tile block of matrix `d`: output tile (rt, ct) of TM rows, K split by; X is bf16,
@@ -520,6 +603,128 @@ __global__ __launch_bounds__(kThreads) void k_gemm_tile(const mtc_tile_desc d, c
   int rt, ct;
   if (!tile_of_block((int)blockIdx.x, n_row_tiles, d.n_col_tiles, tiles_per_xcd, d.col_perm && !part, rt, ct)) return;
   gemm_tile_block<kCF, kYDT, TM, kXF>(d, rt, ct, (int)blockIdx.y, X, ldx, Y, ldy, M, steps_per_split, part);
+}
+
+// ---------------------------------------------------------------------------
+// fp32 matrix-core path over the tile stream (mtc_gemm_f32): Y = X * W_hat with fp32 X and
+// the exact fp32 W_hat, on v_mfma_f32_16x16x4f32 (fp32 products and sums) - the decode-size
+// counterpart of k_gemm_tile for callers that need the fp32 result (M of a few to 16 rows per
+// tile). Block = one 16 x 256 output tile, K in steps of 64, the same warp split as k_gemm_tile:
+// 4 producer waves decode step k+1's cells into an fp32 B tile ([256][64], swz_f32) while 8
+// consumer waves multiply step k; consumer wave w owns output columns 32w .. 32w+31 (two 16 x 16
+// MFMA tiles). Waves 0-3 copy the step's X tile ([16][64] fp32, swz_f32; 4 KiB, one 1 KiB copy
+// each) straight into LDS two steps ahead. MFMA lane l takes A[l % 16][l / 16] and
+// B[l / 16][l % 16] and holds D[4 (l / 16) + r][l % 16] in register r (checked on the GPU); each
+// 16-row group g of a step is 4 MFMAs in which lane quarter q contributes K rows 16g + 4q + s
+// (s = 0..3), so one 16-byte LDS read gives a lane its operand for all four.
+// ---------------------------------------------------------------------------
+constexpr int kFM = 16;                                   // output rows per fp32 tile
+constexpr int kABytesF32 = kFM * kTK * 4;                 // one fp32 X tile (4 KiB)
+constexpr int kLdsBytesF32 = kABufs * kABytesF32 + kBBufs * kTileBytesF32;   // 140 KiB
+
+template <int kCF>
+__device__ __forceinline__ void gemm_f32_block(const mtc_tile_desc& d, const int rt, const int ct, const int by,
+                                               const float* __restrict__ X, int64_t ldx, float* __restrict__ Y,
+                                               int64_t ldy, int M, int steps_per_split, float* __restrict__ part) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int m0 = rt * kFM, n0 = ct * kTN;
+  const int kb0 = by * steps_per_split;
+  const int nks = min(steps_per_split, d.n_ksteps - kb0);
+  unsigned char* const bbase = lds + kABufs * kABytesF32;
+
+  if (wave < kConsumerWaves) {
+    // X copies: wave w < 4 copies rows 4w .. 4w+3 of each step's tile; lane l fills physical
+    // segment l % 16 of row 4w + l / 16, reading the logical segment swz_f32 maps there.
+    // Rows past M and segments past K read zeros.
+    const bool copies = wave < kFM / 4;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds;
+    const u32x4_t x_r = buffer_rsrc(X + (int64_t)m0 * ldx, (uint32_t)(kFM * ldx * 4));
+    const int xrow = 4 * wave + (lane >> 4);
+    const int xseg = (lane & 15) ^ (xrow & 15);           // logical segment: K elements 4 xseg .. +3
+    const uint32_t x_off = copies && m0 + xrow < M ? (uint32_t)(xrow * ldx + 4 * xseg) * 4 : kOutOfRange;
+    auto copy_x = [&](int s) __attribute__((always_inline)) {
+      if (!copies) return;
+      const bool in = x_off != kOutOfRange && (kb0 + s) * kTK + 4 * xseg < d.K;   // K % 8 == 0
+      dma16(x_r, in ? x_off + (uint32_t)((kb0 + s) * kTK) * 4 : kOutOfRange,
+            __builtin_amdgcn_readfirstlane(lds0 + (uint32_t)(s % kABufs) * kABytesF32 + (uint32_t)wave * 1024u));
+    };
+    f32x4_t acc[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
+    const int r16 = lane & 15, q = lane >> 4;
+    copy_x(0);
+    if (nks > 1) {
+      copy_x(1);
+      asm volatile("s_waitcnt vmcnt(1)" ::: "memory");    // step 0's copy done (waves without copies: none)
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    lds_barrier();                                         // step 0 staged
+    for (int ks = 0; ks < nks; ++ks) {
+      const bool ahead = ks + 2 < nks;
+      if (ahead) copy_x(ks + 2);                           // into the buffer step ks-1 used
+      const unsigned char* as = lds + (ks % kABufs) * kABytesF32;
+      const unsigned char* bs = bbase + (ks & 1) * kTileBytesF32;
+#pragma unroll
+      for (int g = 0; g < kTK / 16; ++g) {
+        const f32x4_t a = *reinterpret_cast<const f32x4_t*>(as + swz_f32(r16, 4 * g + q));
+        f32x4_t b[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) b[t] = *reinterpret_cast<const f32x4_t*>(bs + swz_f32(32 * wave + 16 * t + r16, 4 * g + q));
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+          for (int t = 0; t < 2; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[t][s], acc[t], 0, 0, 0);
+      }
+      if (ahead) {
+        asm volatile("s_waitcnt vmcnt(1)" ::: "memory");  // step ks+1's copy (issued a step ago) landed
+      } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      lds_barrier();                                       // buffers of step ks free, step ks+1 staged
+    }
+    // epilogue: register r of lane l is row 4 (l / 16) + r, column l % 16 of each 16 x 16 tile.
+    // Split K writes a plain fp32 partial tile to part[by] (no column permutation).
+    float* const yf = part ? part + (size_t)by * M * d.N : Y;
+    const int64_t ld = part ? (int64_t)d.N : ldy;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int col = n0 + 32 * wave + 16 * t + r16;
+      if (col >= d.N) continue;
+      const int ycol = (d.col_perm && !part) ? d.col_perm[col] : col;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + 4 * q + r;
+        if (row < M) yf[(int64_t)row * ld + ycol] = acc[t][r];
+      }
+    }
+    return;
+  }
+
+  tile_producers<kCF, true>(d, ct, kb0, nks, bbase, tid - 64 * kConsumerWaves);
+}
+
+template <int kCF>
+__global__ __launch_bounds__(kThreads) void k_gemm_f32(const mtc_tile_desc d, const float* __restrict__ X, int64_t ldx,
+                                                       float* __restrict__ Y, int64_t ldy, int M, int n_row_tiles,
+                                                       int tiles_per_xcd, int steps_per_split,
+                                                       float* __restrict__ part) {
+  int rt, ct;
+  if (!tile_of_block((int)blockIdx.x, n_row_tiles, d.n_col_tiles, tiles_per_xcd, d.col_perm && !part, rt, ct)) return;
+  gemm_f32_block<kCF>(d, rt, ct, (int)blockIdx.y, X, ldx, Y, ldy, M, steps_per_split, part);
+}
+
+// Xp[m, k] = X[m, row_perm[k]] in fp32 (four outputs per thread), for the fp32 tile path over a
+// stream with a row permutation.
+__global__ __launch_bounds__(kStageThreads) void k_stage_x_f32(const float* __restrict__ X, int64_t ldx,
+                                                               const int32_t* __restrict__ row_perm,
+                                                               float* __restrict__ Xp, int K) {
+  const int64_t m = blockIdx.y;
+  const int k0 = ((int)blockIdx.x * kStageThreads + (int)threadIdx.x) * 4;
+  if (k0 >= K) return;
+  const int4 src = *reinterpret_cast<const int4*>(row_perm + k0);   // K % 8 == 0, k0 % 4 == 0
+  const float* x = X + m * ldx;
+  *reinterpret_cast<float4*>(Xp + m * K + k0) = make_float4(x[src.x], x[src.y], x[src.z], x[src.w]);
 }
 
 // Up to kMaxGroup matrices that read the same X, in one launch of each kernel: member i owns
@@ -1242,6 +1447,89 @@ MTC_API int mtc_gemm_bf16_batch(const void* host_plan, const void* device_plan, 
 }
 
 MTC_API int mtc_check_tile_desc(const mtc_tile_desc* d) { return check_tile_desc(d); }
+
+// ---- fp32 tile path (k_gemm_f32) ----
+// K splits of an fp32 call: enough (16-row tile, column tile, split) blocks to fill the chip, at
+// least kMinStepsPerSplit K-steps each.
+struct F32Plan {
+  int splits;
+  int per;       // K-steps per split
+};
+F32Plan f32_plan(const mtc_tile_desc* d, int M) {
+  const int64_t n_tiles = (int64_t)((M + kFM - 1) / kFM) * d->n_col_tiles;
+  int s = n_tiles >= kFillCUs ? 1 : (int)((kFillCUs + n_tiles - 1) / n_tiles);
+  s = std::max(1, std::min(s, d->n_ksteps / kMinStepsPerSplit));
+  const int per = (d->n_ksteps + s - 1) / s;
+  return {(d->n_ksteps + per - 1) / per, per};
+}
+// Workspace of an fp32 call: X gathered through row_perm (M*K*4, rounded up to 256), then the
+// split-K partials (splits*M*N*4).
+size_t f32_stage_bytes(const mtc_tile_desc* d, int M) {
+  return d->row_perm ? ((size_t)M * d->K * 4 + 255) / 256 * 256 : 0;
+}
+size_t f32_ws_bytes(const mtc_tile_desc* d, int M) {
+  const F32Plan p = f32_plan(d, M);
+  return f32_stage_bytes(d, M) + (p.splits > 1 ? (size_t)p.splits * M * d->N * 4 : 0);
+}
+
+MTC_API size_t mtc_gemm_f32_workspace_bytes(const mtc_tile_desc* d, int M) {
+  if (check_tile_desc(d) || M <= 0) return 0;
+  return f32_ws_bytes(d, M);
+}
+
+MTC_API int mtc_gemm_f32(const mtc_tile_desc* d, const float* X, int64_t ldx, float* Y, int64_t ldy, int M,
+                         void* workspace, size_t workspace_bytes, void* hip_stream) {
+  int rc = check_tile_desc(d);
+  if (rc) return rc;
+  if (!X || !Y) return fail(MTC_E_NULL, "X or Y is NULL");
+  if (M <= 0) return fail(MTC_E_SHAPE, "M=%d must be positive", M);
+  if (ldx < d->K || ldy < d->N) return fail(MTC_E_SHAPE, "ldx=%lld < K or ldy=%lld < N", (long long)ldx, (long long)ldy);
+  if (!d->row_perm && (ldx % 4 || (reinterpret_cast<uintptr_t>(X) & 15)))
+    return fail(MTC_E_SHAPE, "fp32 X read in place needs 16-byte aligned rows (ldx=%lld)", (long long)ldx);
+  if (ldx >= ((int64_t)1 << 31) / (4 * kFM))
+    return fail(MTC_E_SHAPE, "ldx=%lld too large for 32-bit X tile offsets", (long long)ldx);
+  if ((size_t)kLdsBytesF32 > mtc::host::device_lds_limit())
+    return fail(MTC_E_SHAPE, "fp32 tile kernel needs %d B of LDS per block, device has %zu", kLdsBytesF32,
+                mtc::host::device_lds_limit());
+  const size_t stage = f32_stage_bytes(d, M), need = f32_ws_bytes(d, M);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(MTC_E_WORKSPACE, "fp32 tile workspace of %zu bytes needed, %zu given", need,
+                workspace ? workspace_bytes : 0);
+  if (need && (reinterpret_cast<uintptr_t>(workspace) & 255))
+    return fail(MTC_E_WORKSPACE, "workspace not 256-byte aligned");
+  hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);
+  const float* xa = X;
+  int64_t lda = ldx;
+  if (stage) {
+    float* xp = reinterpret_cast<float*>(workspace);
+    hipLaunchKernelGGL(k_stage_x_f32, dim3((unsigned)((d->K / 4 + kStageThreads - 1) / kStageThreads), (unsigned)M),
+                       dim3(kStageThreads), 0, st, X, ldx, d->row_perm, xp, d->K);
+    rc = check_launch("k_stage_x_f32");
+    if (rc) return rc;
+    xa = xp;
+    lda = d->K;
+  }
+  const F32Plan p = f32_plan(d, M);
+  float* part = p.splits > 1 ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + stage) : nullptr;
+  const int n_row_tiles = (M + kFM - 1) / kFM;
+  const int64_t n_tiles = (int64_t)n_row_tiles * d->n_col_tiles;
+  if (n_tiles > (int64_t)1 << 30) return fail(MTC_E_SHAPE, "M=%d gives too many tiles", M);
+  const int tiles_per_xcd = (int)((n_tiles + kXcds - 1) / kXcds);
+  const void* fn = cell_format(d) == kCellFp32   ? reinterpret_cast<const void*>(&k_gemm_f32<kCellFp32>)
+                   : cell_format(d) == kCellCols ? reinterpret_cast<const void*>(&k_gemm_f32<kCellCols>)
+                                                 : reinterpret_cast<const void*>(&k_gemm_f32<kCellBf16>);
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytesF32);
+  if (e != hipSuccess) return fail(MTC_E_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+  int nrt = n_row_tiles, tpx = tiles_per_xcd, spp = p.per;
+  void* args[] = {const_cast<mtc_tile_desc*>(d), &xa, &lda, &Y, &ldy, &M, &nrt, &tpx, &spp, &part};
+  e = hipLaunchKernel(fn, dim3(tiles_per_xcd * kXcds, p.splits), dim3(kThreads), args, kLdsBytesF32, st);
+  if (e != hipSuccess) return fail(MTC_E_LAUNCH, "k_gemm_f32 launch: %s", hipGetErrorString(e));
+  rc = check_launch("k_gemm_f32");
+  if (rc || p.splits == 1) return rc;
+  hipLaunchKernelGGL(k_splitk_reduce<MTC_DTYPE_F32>, dim3((unsigned)reduce_blocks(M, d->N, d->col_perm != nullptr)),
+                     dim3(kReduceThreads), 0, st, part, p.splits, M, d->N, d->col_perm, Y, ldy);
+  return check_launch("k_splitk_reduce");
+}
 
 MTC_API size_t mtc_gemm_workspace_bytes(const mtc_tile_desc* d, int M, int x_dtype) {
   if (check_tile_desc(d) || M <= 0) return 0;

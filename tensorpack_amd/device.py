@@ -301,8 +301,24 @@ class DeviceTiles:
         return sum(t.numel() * t.element_size() for t in (self.cells, self.step_off, self.payload, self.row_perm,
                                                            self.col_perm) if t is not None)
 
-    def workspace(self, M: int, x_dtype: int):
-        need = int(self.lib.mtc_gemm_workspace_bytes(ctypes.byref(self.desc), int(M), int(x_dtype)))
+    def clone(self) -> "DeviceTiles":
+        """A second device copy of the same tile stream (distinct buffers, same contents)."""
+        other = object.__new__(DeviceTiles)
+        other.device, other.host, other.lib = self.device, self.host, self.lib
+        for name in ("cells", "step_off", "payload", "row_perm", "col_perm"):
+            t = getattr(self, name)
+            setattr(other, name, None if t is None else t.clone())
+        d = _abi.MtcTileDesc.from_buffer_copy(self.desc)
+        ptr = lambda t: None if t is None else t.data_ptr()
+        d.cells, d.step_off, d.payload = ptr(other.cells), ptr(other.step_off), ptr(other.payload)
+        d.row_perm, d.col_perm = ptr(other.row_perm), ptr(other.col_perm)
+        other.desc = d
+        other._ws = {}
+        return other
+
+    def workspace(self, M: int, x_dtype: int, need: int = None):
+        if need is None:
+            need = int(self.lib.mtc_gemm_workspace_bytes(ctypes.byref(self.desc), int(M), int(x_dtype)))
         if need == 0:
             return None, 0
         key = current_stream_handle(self.device)       # one per stream: calls on two streams may overlap
@@ -329,6 +345,25 @@ class DeviceTiles:
                                     _row_stride(out), M, None if ws is None else ws.data_ptr(), nbytes,
                                     current_stream_handle(self.device))
         _abi.check(self.lib, "mtc_gemm_bf16", rc)
+        return out
+
+    def gemm_f32(self, X, out=None):
+        """Y = X @ W_hat in fp32 on the matrix core (mtc_gemm_f32): the exact W_hat, fp32
+        products and sums, for M from a few rows up."""
+        torch = _torch()
+        _need(X.dim() == 2 and X.stride(1) == 1 and X.dtype == torch.float32 and X.shape[1] == self.K
+              and X.device == self.device, f"X must be (M, {self.K}) fp32 row-major on {self.device}")
+        M = X.shape[0]
+        if out is None:
+            out = torch.empty((M, self.N), dtype=torch.float32, device=self.device)
+        _need(out.dtype == torch.float32 and out.stride(1) == 1 and tuple(out.shape) == (M, self.N)
+              and out.device == self.device, f"out must be ({M}, {self.N}) fp32 row-major on {self.device}")
+        need = int(self.lib.mtc_gemm_f32_workspace_bytes(ctypes.byref(self.desc), int(M)))
+        ws, nbytes = self.workspace(M, _abi.MTC_DTYPE_F32, need)
+        rc = self.lib.mtc_gemm_f32(ctypes.byref(self.desc), X.data_ptr(), _row_stride(X), out.data_ptr(),
+                                   _row_stride(out), M, None if ws is None else ws.data_ptr(), nbytes,
+                                   current_stream_handle(self.device))
+        _abi.check(self.lib, "mtc_gemm_f32", rc)
         return out
 
 

@@ -33,6 +33,7 @@ from ..packer import LAYOUT_MX, LAYOUT_V1, PanelStream, check_permutation, pack_
 from ..tilestream import TileStream, pack_tiles
 
 DECODE_MAX_M = 16             # M at or below this takes the fp32 decode kernel under compute="auto"
+F32_DECODE_MAX_M = 16         # fp32 compute above this many rows runs the fp32 tile path (mtc_gemm_f32)
 DECODE_X_LDS_BYTES = 64 * 1024   # on-chip budget for the gathered X rows of one vector-path decode block
 DECODE_MFMA_X_LDS_BYTES = 128 * 1024   # the same for a matrix-core decode block (M tiles of 8 or 16 rows)
 DECODE_LDS_BYTES = 160 * 1024    # per-block LDS of gfx950
@@ -602,13 +603,26 @@ def _kernel_layout(X):
     return X if ok else X.contiguous()
 
 
+def _gemm_f32(B: "MTCMatrix", Xf, dev):
+    """fp32 Y = Xf @ W_hat: the decode kernels over the panel stream up to F32_DECODE_MAX_M rows,
+    the fp32 matrix-core tile path above. The tile path is faster from 16 rows on (c2: M = 16 23.0
+    against 24.0 µs, M = 64 52 against 73 µs, M = 256 176 against 276 µs) but its cell
+    descriptors and split-K partials move 40 MB per call at c2 M = 16 against 14 MB for the
+    decode path, so the decode path keeps M <= 16."""
+    M = Xf.shape[0]
+    if M > F32_DECODE_MAX_M:
+        return B.device_tiles(dev).gemm_f32(Xf)
+    return B.device_stream(None, dev, M).gemv_f32(Xf)
+
+
 def mtc_gemm(A, B: MTCMatrix, *, compute: str = "auto", out_dtype=None):
     """Y = A @ W_hat.
 
     - A MTCMatrix (reference form): returns np.ndarray fp32 C = A_hat @ B_hat.
     - A dense (M, K) or (K,), numpy or torch: returns the same kind (device
-      tensor for torch input). compute="fp32" runs the fp32 decode kernel
-      (default for M <= 16), compute="bf16" the bf16 MFMA kernel (default above).
+      tensor for torch input). compute="fp32" runs the fp32 path (default for
+      M <= 16: the decode kernel; above 16 rows the fp32 matrix-core tile kernel),
+      compute="bf16" the bf16 MFMA kernel (default above 16 rows).
     """
     if not isinstance(B, MTCMatrix):
         raise TypeError(f"right operand must be an MTCMatrix, got {type(B).__name__}")
@@ -621,7 +635,7 @@ def mtc_gemm(A, B: MTCMatrix, *, compute: str = "auto", out_dtype=None):
         assert K == K2, f"Shape mismatch: {A.shape} vs {B.shape}"
         assert A.block_size == B.block_size, "Block size mismatch"
         a_hat = A.dequant_device(dev)
-        return B.device_stream(None, dev, M).gemv_f32(a_hat).cpu().numpy()
+        return _gemm_f32(B, a_hat, dev).cpu().numpy()
 
     from_numpy = not isinstance(A, torch.Tensor)
     X = _as_device_tensor(A, dev)
@@ -639,7 +653,7 @@ def mtc_gemm(A, B: MTCMatrix, *, compute: str = "auto", out_dtype=None):
         Y = torch.zeros((0, B.shape[1]), dtype=out_dtype or torch.float32, device=dev)
     elif compute == "fp32":
         Xf = _kernel_layout(X.float())
-        Y = B.device_stream(None, dev, M).gemv_f32(Xf)
+        Y = _gemm_f32(B, Xf, dev)
         if out_dtype is not None and out_dtype != torch.float32:
             Y = Y.to(out_dtype)
     elif compute == "bf16":
@@ -659,8 +673,9 @@ def mtc_gemm_group(A, Bs, *, compute: str = "auto"):
     projections of a decoder layer; in the reference each is its own
     LinearMTCAdaptive.forward call, mtc/nn/layers.py:150-151).
 
-    At decode sizes (fp32 path) matrices whose decode streams have a single row chunk run
-    MAX_GROUP at a time in one launch (mtc_gemv_f32_group); at prefill sizes (bf16 path)
+    At decode sizes (fp32 path, up to F32_DECODE_MAX_M rows) matrices whose decode streams have
+    a single row chunk run MAX_GROUP at a time in one launch (mtc_gemv_f32_group); above that the
+    fp32 path runs one mtc_gemm_f32 call per matrix; at prefill sizes (bf16 path)
     MAX_GROUP at a time through one launch per kernel (mtc_gemm_bf16_group). Each result
     is bit-identical to mtc_gemm(A, W_i); other members launch one matrix at a time.
     Returns a list in the order of Bs, each of the kind mtc_gemm returns.
@@ -689,6 +704,14 @@ def mtc_gemm_group(A, Bs, *, compute: str = "auto"):
     if compute == "auto":
         compute = "fp32" if M <= DECODE_MAX_M else "bf16"
     outs = [None] * len(Bs)
+    if compute == "fp32" and M > F32_DECODE_MAX_M:
+        Xf = _kernel_layout(X.float())
+        outs = [_gemm_f32(B, Xf, dev) for B in Bs]
+        if squeeze:
+            outs = [y.squeeze(0) for y in outs]
+        if from_numpy:
+            return [y.cpu().numpy() for y in outs]
+        return outs
     if compute == "fp32" and M > 0:
         Xf = _kernel_layout(X.float())
         streams = [B.device_stream(None, dev, M) for B in Bs]

@@ -105,6 +105,8 @@ def test_c2_decode(gpu, M):
     _check_f32(f"c2 M={M}", X, Y, W_hat)
     Y2 = mtc_gemm(torch.from_numpy(X).to(gpu), m)
     assert torch.equal(Y, Y2)
+    if M == 16:                                     # the fp32 matrix-core tile path at the same rows
+        _check_f32(f"c2 M={M} (fp32 tiles)", X, m.device_tiles(gpu).gemm_f32(torch.from_numpy(X).to(gpu)), W_hat)
     if M == 16:                                     # the M = 1 layout at M = 16: two 8-row M tiles
         _say("c2 M=16 decode, chunk_rows 4096")
         _check_f32("c2 M=16 (4096-row units)", X, m.device_stream(4096, gpu).gemv_f32(torch.from_numpy(X).to(gpu)),

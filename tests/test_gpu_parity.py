@@ -15,7 +15,7 @@ from oracle import mtc_oracle as O
 from tensorpack_amd.core.allocation import rd_allocate, rd_allocate_pair
 from tensorpack_amd.core.permutation import PermutedQuadtreeRD
 from tensorpack_amd.core.quadtree import QuadtreeRD
-from tensorpack_amd.kernels.gemm import MTCMatrix, mtc_gemm
+from tensorpack_amd.kernels.gemm import F32_DECODE_MAX_M, MTCMatrix, mtc_gemm
 
 from conftest import kind_grid_stream, kind_mix_stream, largest_unit_stream, outlier_matrix, signed_scale_levels
 
@@ -352,6 +352,32 @@ def test_gemm_bf16(gpu, allocs, name, M, xdtype):
     ref = O.qt_gemm_f64(O.bf16_round(X), _oracle_what(a, W))
     err = O.relative_frobenius_error(ref, Y)
     assert err <= TOL_BF16, (name, M, err)
+
+
+@pytest.mark.parametrize("name", [c[0] for c in CASES])
+@pytest.mark.parametrize("M", [1, 5, 16, 17, 40])
+def test_gemm_f32_tiles(gpu, allocs, name, M):
+    """The fp32 matrix-core path over the tile stream (mtc_gemm_f32: exact W_hat, fp32 products
+    and sums, 16-row tiles, split K): Y within the fp32 bar, every call the same bits, and X = I
+    returns W_hat itself (one product per output, exact in fp32)."""
+    import torch
+    W, a, m = allocs[name]
+    t = m.device_tiles(gpu)
+    _say("gemm f32 tiles", name, M)
+    X = np.random.RandomState(M + 90).randn(M, W.shape[0]).astype(np.float32)
+    Xd = torch.from_numpy(X).to(gpu)
+    Y = t.gemm_f32(Xd).cpu().numpy()
+    ref = O.qt_gemm_f64(X, _oracle_what(a, W))
+    err = O.relative_frobenius_error(ref, Y)
+    assert err <= TOL_F32, (name, M, err)
+    assert np.array_equal(_bits(t.gemm_f32(Xd).cpu().numpy()), _bits(Y)), (name, M)
+    if M > F32_DECODE_MAX_M:                     # mtc_gemm's fp32 path above 16 rows is this kernel
+        assert np.array_equal(_bits(mtc_gemm(Xd, m, compute="fp32").cpu().numpy()), _bits(Y)), (name, M)
+    if M == 1:
+        K = W.shape[0]
+        Yi = t.gemm_f32(torch.eye(K, device=gpu)).cpu().numpy()
+        want = _oracle_what(a, W) + np.float32(0.0)
+        assert np.array_equal(_bits(Yi), _bits(want)), name
 
 
 @pytest.mark.parametrize("name", [c[0] for c in CASES])
