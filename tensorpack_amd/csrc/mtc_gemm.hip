@@ -90,11 +90,14 @@ __device__ __forceinline__ uint32_t swz(int row, int seg) {
 }
 
 // fp32 tiles of the matrix-core fp32 path: [rows][64] floats, 256 bytes (all 64 banks) per row,
-// 16-byte segment `seg` (0..15) of row `row` stored at segment seg ^ (row & 15), so the 16 rows
-// that one MFMA operand read takes at one segment land in 16 different segments.
+// 16-byte segment `seg` (0..15) of row `row` stored at segment seg ^ f(row), f(row) = (row & 15)
+// ^ bit 2 of row: the 16 rows that one MFMA operand read takes at one segment land in 16
+// different segments (f is a bijection on 0..15), and so do the producers' stores of one column
+// of two neighbouring cells (rows n and n + 4, whose f differ in bit 0, at the 8 even or the 8
+// odd segments).
 constexpr int kTileBytesF32 = kTN * kTK * 4;             // one fp32 B tile (64 KiB)
 __device__ __forceinline__ uint32_t swz_f32(int row, int seg) {
-  return (uint32_t)(row * 256 + ((seg ^ (row & 15)) << 4));
+  return (uint32_t)(row * 256 + ((seg ^ (row & 15) ^ ((row >> 2) & 1)) << 4));
 }
 
 // Hides a value's known bits so byte extraction compiles to v_cvt_f32_ubyteN.
@@ -642,7 +645,7 @@ __device__ __forceinline__ void gemm_f32_block(const mtc_tile_desc& d, const int
     const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds;
     const u32x4_t x_r = buffer_rsrc(X + (int64_t)m0 * ldx, (uint32_t)(kFM * ldx * 4));
     const int xrow = 4 * wave + (lane >> 4);
-    const int xseg = (lane & 15) ^ (xrow & 15);           // logical segment: K elements 4 xseg .. +3
+    const int xseg = (lane & 15) ^ (xrow & 15) ^ ((xrow >> 2) & 1);   // logical segment (swz_f32): K 4 xseg .. +3
     const uint32_t x_off = copies && m0 + xrow < M ? (uint32_t)(xrow * ldx + 4 * xseg) * 4 : kOutOfRange;
     auto copy_x = [&](int s) __attribute__((always_inline)) {
       if (!copies) return;
@@ -665,17 +668,21 @@ __device__ __forceinline__ void gemm_f32_block(const mtc_tile_desc& d, const int
       if (ahead) copy_x(ks + 2);                           // into the buffer step ks-1 used
       const unsigned char* as = lds + (ks % kABufs) * kABytesF32;
       const unsigned char* bs = bbase + (ks & 1) * kTileBytesF32;
+      // the step's operands first (12 reads in flight), then its 32 MFMAs
+      f32x4_t a[kTK / 16], b[kTK / 16][2];
 #pragma unroll
       for (int g = 0; g < kTK / 16; ++g) {
-        const f32x4_t a = *reinterpret_cast<const f32x4_t*>(as + swz_f32(r16, 4 * g + q));
-        f32x4_t b[2];
+        a[g] = *reinterpret_cast<const f32x4_t*>(as + swz_f32(r16, 4 * g + q));
 #pragma unroll
-        for (int t = 0; t < 2; ++t) b[t] = *reinterpret_cast<const f32x4_t*>(bs + swz_f32(32 * wave + 16 * t + r16, 4 * g + q));
+        for (int t = 0; t < 2; ++t)
+          b[g][t] = *reinterpret_cast<const f32x4_t*>(bs + swz_f32(32 * wave + 16 * t + r16, 4 * g + q));
+      }
+#pragma unroll
+      for (int g = 0; g < kTK / 16; ++g)
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
-          for (int t = 0; t < 2; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[t][s], acc[t], 0, 0, 0);
-      }
+          for (int t = 0; t < 2; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[g][s], b[g][t][s], acc[t], 0, 0, 0);
       if (ahead) {
         asm volatile("s_waitcnt vmcnt(1)" ::: "memory");  // step ks+1's copy (issued a step ago) landed
       } else {
