@@ -633,8 +633,8 @@ __device__ __forceinline__ void gemv_block(const mtc_stream_desc& d, const int b
                   r.lw0, r.lw1, r.fs0, r.fs1);
   };
 
-  // The first three steps: block record wave + k*W is a fixed record (or the null record:
-  // a block with records past F has F = 48 >= 3W, so those indices are all fixed; 8-wave
+  // The first three steps: record wh + k*WH of the wave's half is a fixed record (or the null
+  // record: a block with records past F has F = 48 >= 3W, so those indices are all fixed; 8-wave
   // blocks of 1-2 rows run only streams with F <= 16, whose blocks have no records past F). Their
   // records are read together with X; all of them are waited for here, before any payload
   // load, so that no later wait (the compiler counts loads in issue order, and the payload
