@@ -611,6 +611,8 @@ def _gemm_f32(B: "MTCMatrix", Xf, dev):
     decode path, so the decode path keeps M <= 16."""
     M = Xf.shape[0]
     if M > F32_DECODE_MAX_M:
+        if Xf.stride(0) % 4 or Xf.data_ptr() % 16:   # the tile kernel reads rows in 16-byte pieces
+            Xf = Xf.contiguous()
         return B.device_tiles(dev).gemm_f32(Xf)
     return B.device_stream(None, dev, M).gemv_f32(Xf)
 

@@ -373,6 +373,10 @@ def test_gemm_f32_tiles(gpu, allocs, name, M):
     assert np.array_equal(_bits(t.gemm_f32(Xd).cpu().numpy()), _bits(Y)), (name, M)
     if M > F32_DECODE_MAX_M:                     # mtc_gemm's fp32 path above 16 rows is this kernel
         assert np.array_equal(_bits(mtc_gemm(Xd, m, compute="fp32").cpu().numpy()), _bits(Y)), (name, M)
+        # a view whose rows are not 16-byte aligned is copied first, with the same result
+        big = torch.zeros((M, W.shape[0] + 1), device=gpu)
+        big[:, 1:] = Xd
+        assert np.array_equal(_bits(mtc_gemm(big[:, 1:], m, compute="fp32").cpu().numpy()), _bits(Y)), (name, M)
     if M == 1:
         K = W.shape[0]
         Yi = t.gemm_f32(torch.eye(K, device=gpu)).cpu().numpy()
