@@ -195,7 +195,9 @@ def pmc_child_tiles(folder):
     print("pmc child done", flush=True)
 
 
-PREFILL_KERNELS = ("k_stage_x", "k_gemm_tile", "k_splitk_reduce")
+# the prefill's launches: X staging, the tile kernel and its split-K reduction, or, on the
+# decode-once path, the bf16 decode of W_hat and hipBLASLt's GEMM (its kernels' names start Cijk_)
+PREFILL_KERNELS = ("k_stage_x", "k_gemm_tile", "k_splitk_reduce", "k_tile_dequant_bf16", "Cijk_")
 F32_TILE_KERNELS = ("k_stage_x_f32", "k_gemm_f32", "k_splitk_reduce")
 
 
@@ -605,11 +607,27 @@ def bench_c4(args, wl4, a4, dev, m4=None, traffic=None):
     M4 = 4096
     X4 = torch.from_numpy(wl4.activations(M4)).to(dev).to(torch.bfloat16)
     Y4 = torch.empty((M4, wl4.W.shape[1]), dtype=torch.float32, device=dev)
+    from tensorpack_amd.device import set_prefill_decode_once
+    # the library's own choice at this shape: W_hat decoded once into bf16, then hipBLASLt's GEMM
     g4.gemm_bf16(X4, out=Y4)
     torch.cuda.synchronize()
     s4, ms4 = timed_calls(torch, [lambda: g4.gemm_bf16(X4, out=Y4)], args.prefill_steps, args.prefill_warmup, False)
     flop4 = 2.0 * M4 * wl4.W.shape[0] * wl4.W.shape[1]
     tf = flop4 / (ms4 * 1e-3) / 1e12
+    # the fused tile kernel (k_gemm_tile) on the same call, the path switched off
+    Y4t = torch.empty_like(Y4)
+    prev = set_prefill_decode_once(False)
+    try:
+        g4.gemm_bf16(X4, out=Y4t)
+        torch.cuda.synchronize()
+        _, ms4t = timed_calls(torch, [lambda: g4.gemm_bf16(X4, out=Y4t)], args.prefill_steps, args.prefill_warmup, False)
+    finally:
+        set_prefill_decode_once(prev)
+    tf_t = flop4 / (ms4t * 1e-3) / 1e12
+    rel_t = rel_frobenius(Y4t.cpu().numpy().astype(np.float64), Y4.cpu().numpy())
+    del Y4t
+    log(f"c4 M=4096 on the fused tile kernel: {ms4t:.3f} ms/call, {tf_t:.1f} TFLOP/s "
+        f"({100 * tf_t / BF16_PEAK_TFLOPS:.1f}%); decode-once vs tile kernel rel {rel_t:.2e}")
     # the timed output: 4 rows of every 256-row tile, all 8192 columns (every column tile), against
     # the fp64 product of the same bf16 X and the allocator's W_hat
     rng = np.random.RandomState(4242)
@@ -624,10 +642,13 @@ def bench_c4(args, wl4, a4, dev, m4=None, traffic=None):
     if not rel < 2e-3:
         raise SystemExit(f"c4 prefill output differs from the fp64 product: rel {rel:.3e} >= 2e-3")
     res = {"M": M4, "ms_per_call": ms4, "TFLOPs": tf, "frac_bf16_peak": tf / BF16_PEAK_TFLOPS,
+           "path": "decode once (k_tile_dequant_bf16) + hipBLASLt bf16 GEMM",
+           "tile_kernel": {"ms_per_call": ms4t, "TFLOPs": tf_t, "frac_bf16_peak": tf_t / BF16_PEAK_TFLOPS,
+                           "rel_frobenius_vs_decode_once": rel_t},
            "packed_bytes": m4.packed_bytes, "p0_area_fraction": p0_area_fraction(a4),
            "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                         "frac": tf / BF16_PEAK_TFLOPS, "traffic": None if traffic is None else traffic["bytes"],
-                        "kernel": "k_gemm_tile"},
+                        "kernel": "k_tile_dequant_bf16 + hipBLASLt GEMM (whole call)"},
            "parity": {"rows": int(rows.size), "rel_frobenius_vs_fp64": rel, "tolerance": 2e-3}}
     if traffic is not None:
         res["roofline"]["traffic_detail"] = prefill_traffic_detail(traffic, M4, wl4.W.shape, m4.packed_bytes, 2)

@@ -285,15 +285,31 @@ int mtc_check_tile_desc(const mtc_tile_desc* d);
  * permutation, with 16-byte aligned rows, in the 64- and 128-row tiles of short X is
  * rounded to bf16 by the tile kernel itself and leaves that area unused), plus
  * splits*M*N*4 when the output has too few 256 x 256 tiles to fill the chip and the
- * K steps are split over blocks (fp32 partial tiles, summed in a fixed order). */
+ * K steps are split over blocks (fp32 partial tiles, summed in a fixed order).
+ * For a call eligible for the decode-once path (below) at least N*64*ceil(K/64)*2
+ * (W_hat in bf16) + the staged X + 32 MiB (the GEMM's own workspace). */
 size_t mtc_gemm_workspace_bytes(const mtc_tile_desc* d, int M, int x_dtype);
 
 /* bf16 MFMA path (prefill): Y (M x N, fp32 or bf16, leading dim ldy) =
  * X (M x K, fp32 or bf16, leading dim ldx) * W_hat with bf16 operands and
  * fp32 accumulation. bf16 X read in place must have 16-byte aligned rows
- * (ldx % 8 == 0). Any M >= 1. */
+ * (ldx % 8 == 0). Any M >= 1.
+ * Decode-once path: a call with M >= 1024, no col_perm and enough 256 x 256 output tiles
+ * to fill the chip (ceil(M/256) * ceil(N/256) >= 256) decodes W_hat once into bf16 in the
+ * workspace (the values the tile kernel would multiply) and runs hipBLASLt's bf16 GEMM
+ * with fp32 accumulation on it, instead of the tile kernel, which decodes each weight step
+ * once per 256-row tile. The same shape always runs the same GEMM algorithm, so results
+ * are deterministic. Without hipBLASLt, or with no algorithm for the shape, the call runs
+ * the tile kernel. */
 int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, int64_t ldx, void* Y, int y_dtype,
                   int64_t ldy, int M, void* workspace, size_t workspace_bytes, void* hip_stream);
+
+/* Switches the decode-once path of mtc_gemm_bf16 / mtc_gemm_bf16_group on (1, the default)
+ * or off (0: every call runs the tile kernel) for the process; -1 only queries. Returns the
+ * previous setting. No counterpart in the reference: for callers and tests that measure or
+ * check the fused tile kernel at shapes the decode-once path would take. Not synchronised
+ * with calls in flight on other threads. */
+int mtc_set_prefill_decode_once(int enable);
 
 /* fp32 matrix-core path over the tile stream: Y (M x N fp32, leading dim ldy) = X (M x K
  * fp32, leading dim ldx) * W_hat with the exact fp32 W_hat and fp32 products and sums
@@ -311,8 +327,10 @@ int mtc_gemm_f32(const mtc_tile_desc* d, const float* X, int64_t ldx, float* Y, 
  * (X staging, tile GEMM, split-K reduction) instead of one per matrix:
  * Y[i] (M x N_i, leading dim ldy[i]) = X * W_hat_i. Every tile stream must have the same
  * K and scale format. The workspace (mtc_gemm_group_workspace_bytes, 256-byte aligned, no
- * initialisation) holds, per member, its staged X and its split-K partials. Each Y[i]
- * equals, bit for bit, what mtc_gemm_bf16 writes for matrix i alone. */
+ * initialisation) holds, per member, its staged X and its split-K partials, then one area
+ * for the members a single call would run on the decode-once path, which run on it here too,
+ * one after another. Each Y[i] equals, bit for bit, what mtc_gemm_bf16 writes for matrix i
+ * alone. */
 size_t mtc_gemm_group_workspace_bytes(const mtc_tile_desc* const* descs, int n, int M, int x_dtype);
 int mtc_gemm_bf16_group(const mtc_tile_desc* const* descs, int n, const void* X, int x_dtype, int64_t ldx,
                         void* const* Y, int y_dtype, const int64_t* ldy, int M, void* workspace,
@@ -328,7 +346,9 @@ int mtc_gemm_bf16_group(const mtc_tile_desc* const* descs, int n, const void* X,
  * for byte to a 64-byte aligned device buffer, launch with mtc_gemm_bf16_batch. When the
  * members' output tiles together fill the chip no K is split; otherwise each member splits K
  * as mtc_gemm_bf16 would, and its Y then equals that call's bit for bit. Results are
- * deterministic. Launches that share a workspace must not overlap. */
+ * deterministic. Every member runs on the tile kernel (a member that mtc_gemm_bf16 alone
+ * would run on the decode-once path fills the chip by itself, so such a batch splits no K).
+ * Launches that share a workspace must not overlap. */
 typedef struct mtc_gemm_batch_item {
   const mtc_tile_desc* desc;     /* read while the plan is built */
   const void* X;                 /* M x K, x_dtype, leading dim ldx */

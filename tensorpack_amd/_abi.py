@@ -20,7 +20,8 @@ EXPORTED = ("mtc_abi_version", "mtc_last_error", "mtc_check_desc", "mtc_dequant"
             "mtc_gemv_workspace_bytes", "mtc_gemv_f32", "mtc_gemv_f32_group", "mtc_check_tile_desc", "mtc_gemm_workspace_bytes",
             "mtc_gemm_bf16", "mtc_gemm_group_workspace_bytes", "mtc_gemm_bf16_group", "mtc_gemv_batch_plan",
             "mtc_gemv_f32_batch", "mtc_gemv_noalloc_scratch_bytes", "mtc_gemv_f32_noalloc", "mtc_gemm_batch_plan",
-            "mtc_gemm_bf16_batch", "mtc_gemm_f32_workspace_bytes", "mtc_gemm_f32")
+            "mtc_gemm_bf16_batch", "mtc_gemm_f32_workspace_bytes", "mtc_gemm_f32",
+            "mtc_set_prefill_decode_once")
 
 
 class MtcStreamDesc(ctypes.Structure):
@@ -138,6 +139,8 @@ def declare(lib: ctypes.CDLL) -> None:
     lib.mtc_gemm_bf16.argtypes = [TileDescP, vp, i32, i64, vp, i32, i64, i32, vp, sz, vp]
     lib.mtc_gemm_f32_workspace_bytes.restype = sz
     lib.mtc_gemm_f32_workspace_bytes.argtypes = [TileDescP, i32]
+    lib.mtc_set_prefill_decode_once.restype = i32
+    lib.mtc_set_prefill_decode_once.argtypes = [i32]
     lib.mtc_gemm_f32.restype = i32
     lib.mtc_gemm_f32.argtypes = [TileDescP, vp, i64, vp, i64, i32, vp, sz, vp]
     lib.mtc_gemm_group_workspace_bytes.restype = sz

@@ -15,17 +15,27 @@
 //                 buffers and load step k+2's cell payload. Tiles use an XOR swizzle of
 //                 16-byte segments; one LDS-only barrier per step (global loads stay in
 //                 flight across it). Output columns go through col_perm.
+//   k_tile_dequant_bf16 : prefill whose 256-row tiles fill the chip many times over decodes
+//                 W_hat once into bf16 and multiplies it with a plain hipBLASLt GEMM instead
+//                 (the tile kernel would decode each weight step once per row tile).
 //
 // Reference behaviour: mtc/kernels/gemm.py:124-210 (block loop: skip P0 blocks,
 // unpack, scale, multiply-accumulate) with W_hat as in mtc/core/quadtree.py:157-171.
 
+#include <dlfcn.h>
 #include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
+#include <map>
+#include <mutex>
+#include <tuple>
+#include <type_traits>
 #include <vector>
 
 #include "mtc_hip.h"
@@ -734,6 +744,85 @@ __global__ __launch_bounds__(kStageThreads) void k_stage_x_f32(const float* __re
   *reinterpret_cast<float4*>(Xp + m * K + k0) = make_float4(x[src.x], x[src.y], x[src.z], x[src.w]);
 }
 
+// ---- decode once: W_hat in bf16 for a plain GEMM ----
+// One block per (column tile ct, K-step ks), grid n_col_tiles x n_ksteps, 256 threads: thread t
+// decodes cells t and t + 256 of the step as the tile kernel's producers do (decode_cell: the same
+// bf16 values the MFMAs would read), into a swizzled [256][64] LDS tile, then the block writes it
+// out as whole 128-byte row pieces: Wt[n][k] (N rows of ldw bf16, ldw = 64 * n_ksteps) holds
+// W_hat[k][n] for stream row k (row_perm order, as the staged X) and column n; rows k >= K hold
+// the stream's zero padding. (Stores straight from registers, one cell per thread, ran 54 us
+// against 40 us at 8192 x 8192: a step's cells are sorted by class first, so their lines split.)
+template <int kCF>
+__global__ __launch_bounds__(256) void k_tile_dequant_bf16(const mtc_tile_desc d, __bf16* __restrict__ Wt,
+                                                          int64_t ldw) {
+  __shared__ __attribute__((aligned(16))) unsigned char bs[kTN * kTK * 2];
+  constexpr int CW = cell_words(kCF);
+  const int t = threadIdx.x;
+  const size_t step = (size_t)blockIdx.x * d.n_ksteps + blockIdx.y;
+  const __amdgpu_buffer_rsrc_t cell_r = buffer_of(d.cells + step * kCells * CW, (int64_t)kCells * CW * 4);
+  const __amdgpu_buffer_rsrc_t pay_r = buffer_of(d.payload, d.payload_dwords * 4);
+  const uint32_t base = d.step_off[step];
+  uint32_t w[2][CW];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t off = (uint32_t)((t + 256 * h) * CW) * 4u;
+    if constexpr (CW == 2) {
+      const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(cell_r, off, 0, 0);
+      w[h][0] = v.x;
+      w[h][1] = v.y;
+    } else {
+#pragma unroll
+      for (int i = 0; i < CW / 4; ++i) {
+        const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(cell_r, off + 16u * i, 0, 0);
+        w[h][4 * i + 0] = v.x;
+        w[h][4 * i + 1] = v.y;
+        w[h][4 * i + 2] = v.z;
+        w[h][4 * i + 3] = v.w;
+      }
+    }
+  }
+  u32x4_t q[2][4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t cls = (w[h][0] >> 14) & 3u;
+    const uint32_t o = (base + (w[h][0] & 0x3FFFu)) * 4u;
+    const uint32_t n = cls == 0 ? 1u : cls == 1 ? 2u : cls == 2 ? 4u : 0u;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i)
+      q[h][i] = __builtin_amdgcn_raw_buffer_load_b128(pay_r, i < n ? o + 16u * i : kOutOfRange, 0, 0);
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    float st[4], sb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (kCF == kCellFp32) {
+        st[j] = __uint_as_float(w[h][1]);
+        sb[j] = __uint_as_float(w[h][2]);
+      } else {
+        const uint32_t sw = kCF == kCellCols ? w[h][1 + j] : w[h][1];
+        st[j] = __uint_as_float(sw << 16);
+        sb[j] = __uint_as_float(sw & 0xFFFF0000u);
+      }
+    }
+    const uint32_t pos = (w[h][0] >> 16) & (kCells - 1);   // (column group, row block) of the cell
+    const int col = (int)(pos >> 3) * 4, seg = (int)(pos & 7u);
+    u32x4_t o[4];
+    decode_cell<kCF == kCellCols>((w[h][0] >> 14) & 3u, q[h], st, sb, o);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4_t*>(bs + swz(col + j, seg)) = o[j];
+  }
+  __syncthreads();
+  __bf16* const out = Wt + (int64_t)blockIdx.y * kTK;
+#pragma unroll
+  for (int i = 0; i < kTN * 8 / 256; ++i) {
+    const int piece = t + 256 * i, row = piece >> 3, seg = piece & 7;
+    const int n = (int)blockIdx.x * kTN + row;
+    if (n < d.N)
+      *reinterpret_cast<u32x4_t*>(out + (int64_t)n * ldw + seg * 8) = *reinterpret_cast<const u32x4_t*>(bs + swz(row, seg));
+  }
+}
+
 // Up to kMaxGroup matrices that read the same X, in one launch of each kernel: member i owns
 // tile blocks [start[i], start[i + 1]) (whole XCD rounds, so each block runs on the XCD it
 // would in a launch of its own) and K splits 0 .. splits[i] - 1 along the grid's y.
@@ -1118,13 +1207,201 @@ int launch_tile(const mtc_tile_desc* d, const void* X, int64_t ldx, void* Y, int
   return check_launch("k_splitk_reduce");
 }
 
-// Workspace of a group: per member, its staged X (if any) then its split-K partials, each
-// on a 256-byte boundary.
 size_t round256(size_t b) { return (b + 255) / 256 * 256; }
-size_t group_ws_bytes(const mtc_tile_desc* const* descs, int n, int M, int x_dtype) {
-  size_t b = 0;
-  for (int i = 0; i < n; ++i) b += round256(staging_bytes(descs[i], M, x_dtype)) + round256(partial_bytes(descs[i], M));
-  return b;
+
+// X -> bf16 Xp = X[:, row_perm] (M x K, leading dim K) ahead of the tile kernel or the plain GEMM.
+int stage_x(const mtc_tile_desc* d, const void* X, int x_dtype, int64_t ldx, int M, __bf16* Xp, hipStream_t st) {
+  const int R = stage_rows_for(d->K, M);
+  if (R) {
+    hipLaunchKernelGGL(k_stage_x_rows, dim3((unsigned)((M + R - 1) / R)), dim3(kStageThreads), (size_t)R * d->K * 2,
+                       st, X, x_dtype, ldx, d->row_perm, Xp, d->K, M, R);
+  } else {
+    dim3 grid((d->K / 8 + kStageThreads - 1) / kStageThreads, M);
+    hipLaunchKernelGGL(k_stage_x, grid, dim3(kStageThreads), 0, st, X, x_dtype, ldx, d->row_perm, Xp, d->K);
+  }
+  return check_launch("k_stage_x");
+}
+
+// ---- decode once, then a plain GEMM ----
+// A call whose own 256-row output tiles fill the chip, from kDecodeOnceMinRows rows of X on,
+// without an output column permutation: the tile kernel would decode every weight step once per
+// row tile (16 times at 4096 rows), so W_hat is decoded once into bf16 (k_tile_dequant_bf16, the
+// bf16 values the tile kernel's MFMAs read) and multiplied by hipBLASLt's bf16 GEMM with fp32
+// accumulation, X staged as for the tile kernel. The shape alone makes a call eligible, so
+// workspace sizes never depend on the library; an eligible call runs the fused tile kernel when
+// hipBLASLt or an algorithm for its shape is missing, or when the path is switched off
+// (mtc_set_prefill_decode_once).
+constexpr int kDecodeOnceMinRows = 1024;
+constexpr size_t kBlasWsBytes = (size_t)32 << 20;   // the GEMM's own workspace (fixed: one algorithm per shape)
+std::atomic<int> g_decode_once{1};
+
+int64_t decode_once_ldw(const mtc_tile_desc* d) { return (int64_t)d->n_ksteps * kTK; }
+size_t decode_once_wt_bytes(const mtc_tile_desc* d) { return round256((size_t)d->N * decode_once_ldw(d) * 2); }
+
+bool decode_once_shape(const mtc_tile_desc* d, int M) {
+  return !d->col_perm && M >= kDecodeOnceMinRows && (int64_t)((M + kTM - 1) / kTM) * d->n_col_tiles >= kFillCUs;
+}
+
+// Workspace of the path: Wt (N x ldw bf16), the staged X (if any), the GEMM's workspace.
+size_t decode_once_bytes(const mtc_tile_desc* d, int M, int x_dtype) {
+  return decode_once_wt_bytes(d) + round256(staging_bytes(d, M, x_dtype)) + kBlasWsBytes;
+}
+
+namespace lt {
+
+struct Api {
+  decltype(&hipblasLtCreate) create = nullptr;
+  decltype(&hipblasLtMatmulDescCreate) desc_create = nullptr;
+  decltype(&hipblasLtMatmulDescSetAttribute) desc_set = nullptr;
+  decltype(&hipblasLtMatrixLayoutCreate) layout_create = nullptr;
+  decltype(&hipblasLtMatmulPreferenceCreate) pref_create = nullptr;
+  decltype(&hipblasLtMatmulPreferenceSetAttribute) pref_set = nullptr;
+  decltype(&hipblasLtMatmulPreferenceDestroy) pref_destroy = nullptr;
+  decltype(&hipblasLtMatmulAlgoGetHeuristic) heuristic = nullptr;
+  decltype(&hipblasLtMatmul) matmul = nullptr;
+  bool ok = false;
+};
+
+// hipBLASLt, opened on first use: a process that already holds it (a PyTorch process does) shares
+// its copy; without it every call takes the fused tile kernel.
+const Api& api() {
+  static const Api a = [] {
+    Api r;
+    void* h = nullptr;
+    for (const char* name : {"libhipblaslt.so.1", "libhipblaslt.so", "/opt/rocm/lib/libhipblaslt.so.1"})
+      if (!h) h = dlopen(name, RTLD_NOW | RTLD_LOCAL);
+    if (!h) return r;
+    auto sym = [h](auto& f, const char* name) {
+      f = reinterpret_cast<std::remove_reference_t<decltype(f)>>(dlsym(h, name));
+      return f != nullptr;
+    };
+    r.ok = sym(r.create, "hipblasLtCreate") && sym(r.desc_create, "hipblasLtMatmulDescCreate") &&
+           sym(r.desc_set, "hipblasLtMatmulDescSetAttribute") && sym(r.layout_create, "hipblasLtMatrixLayoutCreate") &&
+           sym(r.pref_create, "hipblasLtMatmulPreferenceCreate") &&
+           sym(r.pref_set, "hipblasLtMatmulPreferenceSetAttribute") &&
+           sym(r.pref_destroy, "hipblasLtMatmulPreferenceDestroy") &&
+           sym(r.heuristic, "hipblasLtMatmulAlgoGetHeuristic") && sym(r.matmul, "hipblasLtMatmul");
+    return r;
+  }();
+  return a;
+}
+
+// Column-major view of the row-major product: Y^T (N x M, ld ldy) = Wt^T (op T of the K x N,
+// ld ldw, array Wt) * Xb^T (K x M, ld ldb, array Xb).
+struct Plan {
+  hipblasLtHandle_t handle = nullptr;
+  hipblasLtMatmulDesc_t op = nullptr;
+  hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
+  hipblasLtMatmulAlgo_t algo{};
+  bool ok = false;
+};
+
+std::mutex g_mu;
+std::map<int, hipblasLtHandle_t> g_handles;                                   // per device
+std::map<std::tuple<int, int, int, int, int, int64_t, int64_t, int64_t>, Plan> g_plans;
+
+// The GEMM plan of a shape on the current device, made once (the heuristic's first algorithm
+// within kBlasWsBytes of workspace, so a shape always runs the same algorithm); nullptr when
+// the library or an algorithm is missing.
+const Plan* plan_for(int M, int N, int K, int64_t ldw, int64_t ldb, int64_t ldy, int ydt) {
+  const Api& L = api();
+  if (!L.ok) return nullptr;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lock(g_mu);
+  const auto key = std::make_tuple(dev, M, N, K, ydt, ldw, ldb, ldy);
+  auto it = g_plans.find(key);
+  if (it != g_plans.end()) return it->second.ok ? &it->second : nullptr;
+  Plan& p = g_plans[key];
+  auto hit = g_handles.find(dev);
+  if (hit == g_handles.end()) {
+    hipblasLtHandle_t h = nullptr;
+    if (L.create(&h) != HIPBLAS_STATUS_SUCCESS) h = nullptr;
+    hit = g_handles.emplace(dev, h).first;
+  }
+  if (!hit->second) return nullptr;
+  p.handle = hit->second;
+  const int32_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+  const hipDataType yt = ydt == MTC_DTYPE_F32 ? HIP_R_32F : HIP_R_16BF;
+  if (L.desc_create(&p.op, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS ||
+      L.desc_set(p.op, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) != HIPBLAS_STATUS_SUCCESS ||
+      L.desc_set(p.op, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) != HIPBLAS_STATUS_SUCCESS ||
+      L.layout_create(&p.a, HIP_R_16BF, (uint64_t)K, (uint64_t)N, ldw) != HIPBLAS_STATUS_SUCCESS ||
+      L.layout_create(&p.b, HIP_R_16BF, (uint64_t)K, (uint64_t)M, ldb) != HIPBLAS_STATUS_SUCCESS ||
+      L.layout_create(&p.c, yt, (uint64_t)N, (uint64_t)M, ldy) != HIPBLAS_STATUS_SUCCESS)
+    return nullptr;
+  hipblasLtMatmulPreference_t pref = nullptr;
+  const uint64_t max_ws = kBlasWsBytes;
+  if (L.pref_create(&pref) != HIPBLAS_STATUS_SUCCESS) return nullptr;
+  hipblasLtMatmulHeuristicResult_t res[1];
+  int got = 0;
+  if (L.pref_set(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &max_ws, sizeof(max_ws)) == HIPBLAS_STATUS_SUCCESS &&
+      L.heuristic(p.handle, p.op, p.a, p.b, p.c, p.c, pref, 1, res, &got) == HIPBLAS_STATUS_SUCCESS && got >= 1 &&
+      res[0].state == HIPBLAS_STATUS_SUCCESS && res[0].workspaceSize <= kBlasWsBytes) {
+    p.algo = res[0].algo;
+    p.ok = true;
+  }
+  L.pref_destroy(pref);
+  return p.ok ? &p : nullptr;
+}
+
+int gemm(const Plan* p, const __bf16* Wt, const __bf16* Xb, void* Y, void* ws, hipStream_t st) {
+  const float alpha = 1.0f, beta = 0.0f;
+  const hipblasStatus_t s =
+      api().matmul(p->handle, p->op, &alpha, Wt, p->a, Xb, p->b, &beta, Y, p->c, Y, p->c, &p->algo, ws, kBlasWsBytes, st);
+  if (s != HIPBLAS_STATUS_SUCCESS) return fail(MTC_E_LAUNCH, "hipblasLtMatmul: status %d", (int)s);
+  return ok();
+}
+
+}  // namespace lt
+
+// The plan of an eligible call, or nullptr for the fused tile kernel.
+const lt::Plan* decode_once_plan(const mtc_tile_desc* d, int x_dtype, int64_t ldx, int64_t ldy, int y_dtype, int M) {
+  if (!decode_once_shape(d, M) || !g_decode_once.load(std::memory_order_relaxed)) return nullptr;
+  return lt::plan_for(M, d->N, d->K, decode_once_ldw(d), needs_staging(d, x_dtype) ? d->K : ldx, ldy, y_dtype);
+}
+
+// Stage X (if needed), decode W_hat into Wt, run the GEMM; ws holds decode_once_bytes.
+int decode_once_call(const mtc_tile_desc* d, const void* X, int x_dtype, int64_t ldx, void* Y, int M, void* ws,
+                     const lt::Plan* p, hipStream_t st) {
+  char* w = reinterpret_cast<char*>(ws);
+  __bf16* const Wt = reinterpret_cast<__bf16*>(w);
+  w += decode_once_wt_bytes(d);
+  const __bf16* xb = reinterpret_cast<const __bf16*>(X);
+  if (needs_staging(d, x_dtype)) {
+    const int rc = stage_x(d, X, x_dtype, ldx, M, reinterpret_cast<__bf16*>(w), st);
+    if (rc) return rc;
+    xb = reinterpret_cast<const __bf16*>(w);
+    w += round256(staging_bytes(d, M, x_dtype));
+  }
+  const dim3 grid((unsigned)d->n_col_tiles, (unsigned)d->n_ksteps);
+  const int64_t ldw = decode_once_ldw(d);
+  switch (cell_format(d)) {
+    case kCellFp32:
+      hipLaunchKernelGGL(k_tile_dequant_bf16<kCellFp32>, grid, dim3(256), 0, st, *d, Wt, ldw);
+      break;
+    case kCellCols:
+      hipLaunchKernelGGL(k_tile_dequant_bf16<kCellCols>, grid, dim3(256), 0, st, *d, Wt, ldw);
+      break;
+    default:
+      hipLaunchKernelGGL(k_tile_dequant_bf16<kCellBf16>, grid, dim3(256), 0, st, *d, Wt, ldw);
+  }
+  const int rc = check_launch("k_tile_dequant_bf16");
+  if (rc) return rc;
+  return lt::gemm(p, Wt, xb, Y, w, st);
+}
+
+// Workspace of a group: per member, its staged X (if any) then its split-K partials, each on a
+// 256-byte boundary; then, when a member is eligible for the decode-once path, one area that the
+// eligible members use in turn.
+size_t group_ws_bytes(const mtc_tile_desc* const* descs, int n, int M, int x_dtype, size_t* once_off = nullptr) {
+  size_t b = 0, once = 0;
+  for (int i = 0; i < n; ++i) {
+    b += round256(staging_bytes(descs[i], M, x_dtype)) + round256(partial_bytes(descs[i], M));
+    if (decode_once_shape(descs[i], M)) once = std::max(once, decode_once_bytes(descs[i], M, x_dtype));
+  }
+  if (once_off) *once_off = b;
+  return b + once;
 }
 
 template <int kCF, int kYDT>
@@ -1540,7 +1817,12 @@ MTC_API int mtc_gemm_f32(const mtc_tile_desc* d, const float* X, int64_t ldx, fl
 
 MTC_API size_t mtc_gemm_workspace_bytes(const mtc_tile_desc* d, int M, int x_dtype) {
   if (check_tile_desc(d) || M <= 0) return 0;
-  return staging_bytes(d, M, x_dtype) + partial_bytes(d, M);
+  const size_t fused = staging_bytes(d, M, x_dtype) + partial_bytes(d, M);
+  return decode_once_shape(d, M) ? std::max(fused, decode_once_bytes(d, M, x_dtype)) : fused;
+}
+
+MTC_API int mtc_set_prefill_decode_once(int enable) {
+  return enable < 0 ? g_decode_once.load() : g_decode_once.exchange(enable ? 1 : 0);
 }
 
 MTC_API int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, int64_t ldx, void* Y, int y_dtype,
@@ -1554,28 +1836,21 @@ MTC_API int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, in
   if (ldx < d->K || ldy < d->N) return fail(MTC_E_SHAPE, "ldx=%lld < K or ldy=%lld < N", (long long)ldx, (long long)ldy);
   hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);
   int64_t ldb = ldx;
-  const size_t stage = staging_bytes(d, M, x_dtype), need = stage + partial_bytes(d, M);
+  const size_t stage = staging_bytes(d, M, x_dtype);
   if (!stage && (ldx % 8 || (reinterpret_cast<uintptr_t>(X) & 15)))
     return fail(MTC_E_SHAPE, "bf16 X read in place needs 16-byte aligned rows (ldx=%lld)", (long long)ldx);
+  const lt::Plan* once = decode_once_plan(d, x_dtype, ldx, ldy, y_dtype, M);
+  const size_t need = once ? decode_once_bytes(d, M, x_dtype) : stage + partial_bytes(d, M);
   if (need && (!workspace || workspace_bytes < need))
     return fail(MTC_E_WORKSPACE, "prefill workspace of %zu bytes needed, %zu given", need, workspace ? workspace_bytes : 0);
   if (need && (reinterpret_cast<uintptr_t>(workspace) & 255))
     return fail(MTC_E_WORKSPACE, "workspace not 256-byte aligned");
+  if (once) return decode_once_call(d, X, x_dtype, ldx, Y, M, workspace, once, st);
   float* part = need > stage ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + stage) : nullptr;
   const void* xa = X;                                  // what the tile kernel reads: X or the staged copy
   const bool xf = fused_x(d, X, x_dtype, ldx, M);      // fp32 X rounded by the tile kernel (staging area unused)
   if (stage && !xf) {
-    const int R = stage_rows_for(d->K, M);
-    if (R) {
-      hipLaunchKernelGGL(k_stage_x_rows, dim3((unsigned)((M + R - 1) / R)), dim3(kStageThreads),
-                         (size_t)R * d->K * 2, st, X, x_dtype, ldx, d->row_perm, reinterpret_cast<__bf16*>(workspace),
-                         d->K, M, R);
-    } else {
-      dim3 grid((d->K / 8 + kStageThreads - 1) / kStageThreads, M);
-      hipLaunchKernelGGL(k_stage_x, grid, dim3(kStageThreads), 0, st, X, x_dtype, ldx, d->row_perm,
-                         reinterpret_cast<__bf16*>(workspace), d->K);
-    }
-    rc = check_launch("k_stage_x");
+    rc = stage_x(d, X, x_dtype, ldx, M, reinterpret_cast<__bf16*>(workspace), st);
     if (rc) return rc;
     xa = workspace;
     ldb = d->K;
@@ -1623,25 +1898,31 @@ MTC_API int mtc_gemm_bf16_group(const mtc_tile_desc* const* descs, int n, const 
     if (!needs_staging(d, x_dtype) && (ldx % 8 || (reinterpret_cast<uintptr_t>(X) & 15)))
       return fail(MTC_E_SHAPE, "bf16 X read in place needs 16-byte aligned rows (ldx=%lld)", (long long)ldx);
   }
-  const size_t need = group_ws_bytes(descs, n, M, x_dtype);
+  size_t once_off = 0;
+  const size_t need = group_ws_bytes(descs, n, M, x_dtype, &once_off);
   if (need && (!workspace || workspace_bytes < need))
     return fail(MTC_E_WORKSPACE, "prefill workspace of %zu bytes needed, %zu given", need, workspace ? workspace_bytes : 0);
   if (need && (reinterpret_cast<uintptr_t>(workspace) & 255))
     return fail(MTC_E_WORKSPACE, "workspace not 256-byte aligned");
   if (M > (1 << 30)) return fail(MTC_E_SHAPE, "M=%d too large", M);
   hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);
+  // members that a single call would run on the decode-once path run on it here too, one after
+  // another in the area past the fused members' layout; the rest share the fused launches
+  const lt::Plan* once[kMaxGroup];
+  for (int i = 0; i < n; ++i) once[i] = decode_once_plan(descs[i], x_dtype, ldx, ldy[i], y_dtype, M);
   GemmGroup g;
   StageGroup sg;
   ReduceGroup rg;
   memset(&g, 0, sizeof(g));
   memset(&sg, 0, sizeof(sg));
   memset(&rg, 0, sizeof(rg));
-  int n_stage = 0, n_red = 0, blocks = 0;
+  int n_stage = 0, n_red = 0, blocks = 0, nf = 0, cf = -2;
   char* ws = reinterpret_cast<char*>(workspace);
   // tile height: the shortest any member's single call would use (short X whose 256-row tiles
   // leave CUs idle); every member keeps its own single-call K split
   int tm = kTM;
   for (int i = 0; i < n; ++i) {
+    if (once[i]) continue;
     int s_i = 1, tm_i = kTM;
     split_steps(descs[i], M, &s_i, &tm_i);
     tm = std::min(tm, tm_i);
@@ -1649,28 +1930,34 @@ MTC_API int mtc_gemm_bf16_group(const mtc_tile_desc* const* descs, int n, const 
   const int n_row_tiles = (M + tm - 1) / tm;
   for (int i = 0; i < n; ++i) {
     const mtc_tile_desc* d = descs[i];
-    g.d[i] = *d;
-    g.Y[i] = Y[i];
-    g.ldy[i] = ldy[i];
     const size_t stage = round256(staging_bytes(d, M, x_dtype)), pb = round256(partial_bytes(d, M));
+    if (once[i]) {
+      ws += stage + pb;
+      continue;
+    }
+    const int j = nf++;
+    cf = cf == -2 ? cell_format(d) : joint_cell_format(cf, cell_format(d));
+    g.d[j] = *d;
+    g.Y[j] = Y[i];
+    g.ldy[j] = ldy[i];
     if (stage) {
       sg.row_perm[n_stage] = d->row_perm;
       sg.Xp[n_stage] = reinterpret_cast<__bf16*>(ws);
       ++n_stage;
-      g.X[i] = reinterpret_cast<const __bf16*>(ws);
-      g.ldx[i] = d->K;
+      g.X[j] = reinterpret_cast<const __bf16*>(ws);
+      g.ldx[j] = d->K;
     } else {
-      g.X[i] = reinterpret_cast<const __bf16*>(X);
-      g.ldx[i] = ldx;
+      g.X[j] = reinterpret_cast<const __bf16*>(X);
+      g.ldx[j] = ldx;
     }
-    if (g.ldx[i] >= ((int64_t)1 << 31) / (2 * kTM))
-      return fail(MTC_E_SHAPE, "ldx=%lld too large for 32-bit X tile offsets", (long long)g.ldx[i]);
+    if (g.ldx[j] >= ((int64_t)1 << 31) / (2 * kTM))
+      return fail(MTC_E_SHAPE, "ldx=%lld too large for 32-bit X tile offsets", (long long)g.ldx[j]);
     int splits = 1;
-    g.steps_per_split[i] = split_steps(d, M, &splits);
-    g.splits[i] = splits;
-    g.part[i] = splits > 1 ? reinterpret_cast<float*>(ws + stage) : nullptr;
+    g.steps_per_split[j] = split_steps(d, M, &splits);
+    g.splits[j] = splits;
+    g.part[j] = splits > 1 ? reinterpret_cast<float*>(ws + stage) : nullptr;
     if (splits > 1) {
-      rg.part[n_red] = g.part[i];
+      rg.part[n_red] = g.part[j];
       rg.splits[n_red] = splits;
       rg.N[n_red] = d->N;
       rg.col_perm[n_red] = d->col_perm;
@@ -1680,29 +1967,37 @@ MTC_API int mtc_gemm_bf16_group(const mtc_tile_desc* const* descs, int n, const 
     }
     ws += stage + pb;
     const int64_t n_tiles = (int64_t)n_row_tiles * d->n_col_tiles;
-    g.tiles_per_xcd[i] = (int)((n_tiles + kXcds - 1) / kXcds);
-    g.start[i] = blocks;
-    blocks += g.tiles_per_xcd[i] * kXcds;
+    g.tiles_per_xcd[j] = (int)((n_tiles + kXcds - 1) / kXcds);
+    g.start[j] = blocks;
+    blocks += g.tiles_per_xcd[j] * kXcds;
   }
-  for (int i = n; i <= kMaxGroup; ++i) g.start[i] = blocks;
+  for (int j = nf; j <= kMaxGroup; ++j) g.start[j] = blocks;
+  int rc = 0;
   if (n_stage) {
     dim3 grid((descs[0]->K / 8 + kStageThreads - 1) / kStageThreads, M, n_stage);
     hipLaunchKernelGGL(k_stage_x_group, grid, dim3(kStageThreads), 0, st, sg, X, x_dtype, ldx, descs[0]->K);
-    int rc = check_launch("k_stage_x_group");
+    rc = check_launch("k_stage_x_group");
     if (rc) return rc;
   }
   const bool f32 = y_dtype == MTC_DTYPE_F32;
-  int cf = cell_format(descs[0]);
-  for (int i = 1; i < n; ++i) cf = joint_cell_format(cf, cell_format(descs[i]));
-  switch (cf) {
-    case kCellFp32:
-      return f32 ? launch_tile_group<kCellFp32, MTC_DTYPE_F32>(g, n, M, tm, rg, n_red, st)
-                 : launch_tile_group<kCellFp32, MTC_DTYPE_BF16>(g, n, M, tm, rg, n_red, st);
-    case kCellCols:
-      return f32 ? launch_tile_group<kCellCols, MTC_DTYPE_F32>(g, n, M, tm, rg, n_red, st)
-                 : launch_tile_group<kCellCols, MTC_DTYPE_BF16>(g, n, M, tm, rg, n_red, st);
-    default:
-      return f32 ? launch_tile_group<kCellBf16, MTC_DTYPE_F32>(g, n, M, tm, rg, n_red, st)
-                 : launch_tile_group<kCellBf16, MTC_DTYPE_BF16>(g, n, M, tm, rg, n_red, st);
+  if (nf) {
+    switch (cf) {
+      case kCellFp32:
+        rc = f32 ? launch_tile_group<kCellFp32, MTC_DTYPE_F32>(g, nf, M, tm, rg, n_red, st)
+                 : launch_tile_group<kCellFp32, MTC_DTYPE_BF16>(g, nf, M, tm, rg, n_red, st);
+        break;
+      case kCellCols:
+        rc = f32 ? launch_tile_group<kCellCols, MTC_DTYPE_F32>(g, nf, M, tm, rg, n_red, st)
+                 : launch_tile_group<kCellCols, MTC_DTYPE_BF16>(g, nf, M, tm, rg, n_red, st);
+        break;
+      default:
+        rc = f32 ? launch_tile_group<kCellBf16, MTC_DTYPE_F32>(g, nf, M, tm, rg, n_red, st)
+                 : launch_tile_group<kCellBf16, MTC_DTYPE_BF16>(g, nf, M, tm, rg, n_red, st);
+    }
+    if (rc) return rc;
   }
+  for (int i = 0; i < n && !rc; ++i)
+    if (once[i]) rc = decode_once_call(descs[i], X, x_dtype, ldx, Y[i], M, reinterpret_cast<char*>(workspace) + once_off,
+                                       once[i], st);
+  return rc;
 }

@@ -367,6 +367,12 @@ class DeviceTiles:
         return out
 
 
+def set_prefill_decode_once(enable: bool) -> bool:
+    """Switches the decode-once prefill path of gemm_bf16 / gemm_bf16_group on (the default) or
+    off for the process (mtc_set_prefill_decode_once); returns the previous setting."""
+    return bool(_native.hip_lib().mtc_set_prefill_decode_once(1 if enable else 0))
+
+
 def _row_stride(T) -> int:
     """Elements between rows of a row-major matrix view; a single row's stride is never used, so
     it is given as the row length (a one-row slice of a wider matrix keeps the wide stride)."""

@@ -180,6 +180,34 @@ def test_group_prefill_entry_rejects_bad_arguments_before_any_gpu_call(hip):
     assert hip.mtc_gemm_group_workspace_bytes(None, 2, 4, 1) == 0
 
 
+def test_decode_once_workspace_by_shape(hip):
+    """Prefill whose 256-row output tiles fill the chip, from 1024 rows of X on and without an
+    output column permutation, takes the decode-once path: its workspace holds W_hat in bf16
+    (N x 64 * n_ksteps), the staged X and 32 MiB for the GEMM. The shape alone decides."""
+    blas = 32 << 20
+    big = _tdesc(K=1024, N=4096, n_ksteps=16, n_col_tiles=16)
+    wt = 4096 * 1024 * 2
+    ws = lambda d, M, xdt: hip.mtc_gemm_workspace_bytes(ctypes.byref(d), M, xdt)
+    assert ws(big, 4096, 1) == wt + blas                                  # 16 x 16 tiles, bf16 X read in place
+    assert ws(big, 4096, 0) == wt + 4096 * 1024 * 2 + blas                # fp32 X staged as bf16
+    wide = _tdesc(K=1024, N=16384, n_ksteps=16, n_col_tiles=64)
+    assert ws(wide, 1000, 1) == 0                                         # fills the chip, but under 1024 rows
+    assert ws(wide, 1024, 1) == 16384 * 1024 * 2 + blas
+    rows = _tdesc(K=1024, N=4096, n_ksteps=16, n_col_tiles=16, row_perm=0x2000)
+    assert ws(rows, 4096, 1) == wt + 4096 * 1024 * 2 + blas               # a row permutation: X staged
+    cols = _tdesc(K=1024, N=4096, n_ksteps=16, n_col_tiles=16, row_perm=0x2000, col_perm=0x3000)
+    assert ws(cols, 4096, 1) == 4096 * 1024 * 2                           # a column permutation: tile kernel
+    D = _abi.TileDescP
+    small = _tdesc(K=1024, n_ksteps=16)
+    descs = (D * 2)(ctypes.pointer(small), ctypes.pointer(big))
+    assert hip.mtc_gemm_group_workspace_bytes(descs, 2, 4096, 1) == ws(small, 4096, 1) + wt + blas
+    assert hip.mtc_set_prefill_decode_once(-1) == 1
+    assert hip.mtc_set_prefill_decode_once(0) == 1
+    assert hip.mtc_set_prefill_decode_once(-1) == 0
+    assert ws(big, 4096, 1) == wt + blas                                  # sizes do not follow the switch
+    assert hip.mtc_set_prefill_decode_once(1) == 0
+
+
 def _tdesc(**kw):
     d = _abi.MtcTileDesc()
     d.abi_version = _abi.ABI_VERSION

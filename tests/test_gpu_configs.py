@@ -122,27 +122,34 @@ def test_c4_prefill(gpu):
     t = m.device_tiles(gpu)
     assert t.host.n_col_tiles == 32 and t.host.n_ksteps == 128
     from tensorpack_amd._abi import MTC_DTYPE_BF16
+    from tensorpack_amd.device import set_prefill_decode_once
     ws, nbytes = t.workspace(M, MTC_DTYPE_BF16)
-    assert nbytes == 0                               # 16 x 32 tiles fill the chip: no split, no staging
-    _say("c4 M=4096 prefill")
-    Y = t.gemm_bf16(X)
-    torch.cuda.synchronize()
+    # 16 x 32 tiles fill the chip: the decode-once path (W_hat in bf16 + the GEMM's 32 MiB), no staging
+    assert nbytes == 8192 * 8192 * 2 + (32 << 20)
     rng = np.random.RandomState(4242)
     rows = np.concatenate([rt * 256 + np.r_[0, 255, rng.choice(np.arange(1, 255), 2, replace=False)]
                            for rt in range(16)])
     Xs = X[torch.from_numpy(rows).to(gpu)].float().cpu().numpy()      # exact bf16 values
-    Ys = Y[torch.from_numpy(rows).to(gpu)].cpu().numpy()
     ref = O.qt_gemm_f64(Xs, W_hat)
-    err = O.relative_frobenius_error(ref, Ys)
-    _say(f"c4 M=4096 sampled {rows.size} rows rel {err:.2e}")
-    assert err < TOL_BF16
-    for ct in range(32):                             # each column tile on its own
-        sl = slice(256 * ct, 256 * ct + 256)
-        assert O.relative_frobenius_error(ref[:, sl], Ys[:, sl]) < TOL_BF16, ct
-    for rt in range(16):                             # each row tile on its own
-        sl = slice(4 * rt, 4 * rt + 4)
-        assert O.relative_frobenius_error(ref[sl], Ys[sl]) < TOL_BF16, rt
-    assert torch.isfinite(Y).all()
+    for once in (True, False):                       # the library's choice, then the fused tile kernel
+        _say("c4 M=4096 prefill", "decode once + GEMM" if once else "tile kernel")
+        prev = set_prefill_decode_once(once)
+        try:
+            Y = t.gemm_bf16(X)
+            torch.cuda.synchronize()
+        finally:
+            set_prefill_decode_once(prev)
+        Ys = Y[torch.from_numpy(rows).to(gpu)].cpu().numpy()
+        err = O.relative_frobenius_error(ref, Ys)
+        _say(f"c4 M=4096 sampled {rows.size} rows rel {err:.2e}")
+        assert err < TOL_BF16
+        for ct in range(32):                             # each column tile on its own
+            sl = slice(256 * ct, 256 * ct + 256)
+            assert O.relative_frobenius_error(ref[:, sl], Ys[:, sl]) < TOL_BF16, ct
+        for rt in range(16):                             # each row tile on its own
+            sl = slice(4 * rt, 4 * rt + 4)
+            assert O.relative_frobenius_error(ref[sl], Ys[sl]) < TOL_BF16, rt
+        assert torch.isfinite(Y).all()
 
 
 @pytest.mark.parametrize("M", [1, 256])

@@ -1,0 +1,133 @@
+"""Prefill on the decode-once path (run on an MI355X): calls whose 256-row output tiles fill the
+chip from 1024 rows of X on decode W_hat once into bf16 (k_tile_dequant_bf16) and multiply it
+with hipBLASLt's bf16 GEMM (fp32 accumulation).
+
+Bars: the decoded bf16 W_hat bit-exact against bf16(oracle W_hat) in the stream's row order;
+Y within 2e-3 relative Frobenius of the fp64 product of the same bf16 X (the bf16 path's
+bar) and within 1e-5 of the fused tile kernel's Y (the same bf16 operands, fp32 sums in
+another order); repeated calls and group members bit-identical to single calls.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import mtc_oracle as O
+from tensorpack_amd import _abi
+from tensorpack_amd.core.allocation import rd_allocate
+from tensorpack_amd.core.permutation import PermutedQuadtreeRD
+from tensorpack_amd.core.quadtree import QuadtreeRD
+from tensorpack_amd.kernels.gemm import MTCMatrix
+
+from conftest import outlier_matrix
+
+pytestmark = pytest.mark.gpu
+
+TOL_BF16 = 2e-3
+K, N, M = 1024, 4096, 4096          # 16 x 16 output tiles of 256: eligible from 1024 rows on
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def mats():
+    """QT (bf16 scale pairs), QT-P (gathered columns, row permutation) and the uniform form
+    (fp32 scales): one of each cell format, with the oracle's W_hat in the original order."""
+    W = outlier_matrix(71, K, N)
+    h = np.exp(np.random.RandomState(72).randn(K))
+    out = {}
+    a = QuadtreeRD(W, h, (32, 16, 8, 4)).select(4.5)
+    out["qt"] = (MTCMatrix.from_quadtree(a, W), O.qt_dequant(W, a.sizes, a.leaf, a.modes, a.scales))
+    p = PermutedQuadtreeRD(W, h, (32, 16, 8, 4)).select(3.5)
+    i = p.inner
+    out["qtp"] = (MTCMatrix.from_quadtree(p, W),
+                  O.permuted_qt_dequant(W, p.row_perm, p.col_perm, i.sizes, i.leaf, i.modes, i.scales))
+    al = rd_allocate(W, 4.0, None, 32)
+    out["uniform"] = (MTCMatrix.from_allocation(W, al.modes, al.scales, 32), O.uniform_to_array(W, al.modes, al.scales, 32))
+    return out
+
+
+@pytest.fixture(scope="module")
+def xs(gpu):
+    import torch
+    X = np.random.RandomState(73).randn(M, K).astype(np.float32)
+    Xf = torch.from_numpy(X).to(gpu)
+    return Xf, Xf.to(torch.bfloat16)
+
+
+def _fused(fn):
+    from tensorpack_amd.device import set_prefill_decode_once
+    prev = set_prefill_decode_once(False)
+    try:
+        return fn()
+    finally:
+        set_prefill_decode_once(prev)
+
+
+@pytest.mark.parametrize("name", ["qt", "qtp", "uniform"])
+def test_decode_once_matches_oracle_and_tile_kernel(gpu, mats, xs, name):
+    import torch
+    m, W_hat = mats[name]
+    g = m.device_tiles(gpu)
+    Xf, Xb = xs
+    assert g.lib.mtc_set_prefill_decode_once(-1) == 1
+    fmt = ("gathered columns" if g.desc.flags & _abi.MTC_FLAG_COLS_GATHERED else
+           "fp32 scales" if g.desc.flags & _abi.MTC_FLAG_FP32_SCALES else "bf16 scales")
+    _say("decode-once", name, fmt, "row_perm" if g.host.row_perm is not None else "")
+    Y = g.gemm_bf16(Xb)
+    torch.cuda.synchronize()
+    # the decoded weight sits at the start of the workspace: Wt[n][k] = bf16(W_hat[row_perm[k], n])
+    ws, _ = g.workspace(M, 1)
+    ldw = 64 * g.host.n_ksteps
+    Wt = ws[: N * ldw * 2].view(torch.bfloat16).view(N, ldw)[:, :K].float().cpu().numpy()
+    rows = g.host.row_perm if g.host.row_perm is not None else np.arange(K)
+    want = O.bf16_round(W_hat[rows]).T + np.float32(0.0)
+    assert np.array_equal(_bits(Wt), _bits(want)), name
+    Y = Y.cpu().numpy()
+    err = O.relative_frobenius_error(O.qt_gemm_f64(Xb.float().cpu().numpy(), W_hat), Y)
+    assert err <= TOL_BF16, (name, err)
+    assert np.array_equal(_bits(g.gemm_bf16(Xb).cpu().numpy()), _bits(Y)), "repeat"
+    Yt = _fused(lambda: g.gemm_bf16(Xb)).cpu().numpy()
+    assert O.relative_frobenius_error(Yt, Y) <= 1e-5, name
+    # fp32 X is staged to bf16 first: the same GEMM on the same operands
+    assert np.array_equal(_bits(g.gemm_bf16(Xf).cpu().numpy()), _bits(Y)), "fp32 X"
+
+
+def test_decode_once_bf16_output_and_strided_x(gpu, mats, xs):
+    import torch
+    m, W_hat = mats["qt"]
+    g = m.device_tiles(gpu)
+    _, Xb = xs
+    _say("decode-once bf16 Y, strided X")
+    ref = O.qt_gemm_f64(Xb.float().cpu().numpy(), W_hat)
+    Yb = g.gemm_bf16(Xb, out_dtype=torch.bfloat16).float().cpu().numpy()
+    assert O.relative_frobenius_error(ref, Yb) <= TOL_BF16 + 4e-3
+    big = torch.zeros(M, K + 64, device=gpu, dtype=torch.bfloat16)
+    big[:, :K] = Xb
+    Ys = g.gemm_bf16(big[:, :K]).cpu().numpy()
+    assert O.relative_frobenius_error(ref, Ys) <= TOL_BF16
+
+
+def test_decode_once_group_members_equal_single_calls(gpu, mats, xs):
+    """A group of an eligible member and one that runs the tile kernel with split K (N = 256:
+    16 tiles): each Y equals its single call bit for bit."""
+    from tensorpack_amd.device import gemm_bf16_group
+    m, _ = mats["qt"]
+    Wn = outlier_matrix(74, K, 256)
+    a = QuadtreeRD(Wn, None, (32, 16, 8, 4)).select(4.5)
+    small = MTCMatrix.from_quadtree(a, Wn).device_tiles(gpu)
+    g = m.device_tiles(gpu)
+    assert g.lib.mtc_gemm_workspace_bytes(ctypes.byref(small.desc), M, 1) < (32 << 20)   # not eligible
+    _, Xb = xs
+    for X in (Xb, Xb.float()):
+        _say("decode-once group", X.dtype)
+        Ys = gemm_bf16_group([small, g], X)
+        assert np.array_equal(_bits(Ys[0].cpu().numpy()), _bits(small.gemm_bf16(X).cpu().numpy()))
+        assert np.array_equal(_bits(Ys[1].cpu().numpy()), _bits(g.gemm_bf16(X).cpu().numpy()))
