@@ -294,13 +294,12 @@ size_t mtc_gemm_workspace_bytes(const mtc_tile_desc* d, int M, int x_dtype);
  * X (M x K, fp32 or bf16, leading dim ldx) * W_hat with bf16 operands and
  * fp32 accumulation. bf16 X read in place must have 16-byte aligned rows
  * (ldx % 8 == 0). Any M >= 1.
- * Decode-once path: a call with M >= 1024, no col_perm and enough 256 x 256 output tiles
- * to fill the chip (ceil(M/256) * ceil(N/256) >= 256) decodes W_hat once into bf16 in the
- * workspace (the values the tile kernel would multiply) and runs hipBLASLt's bf16 GEMM
- * with fp32 accumulation on it, instead of the tile kernel, which decodes each weight step
- * once per 256-row tile. The same shape always runs the same GEMM algorithm, so results
- * are deterministic. Without hipBLASLt, or with no algorithm for the shape, the call runs
- * the tile kernel. */
+ * Decode-once path: a call with M >= max(512, K / 8) and no col_perm decodes W_hat once
+ * into bf16 in the workspace (the values the tile kernel would multiply) and runs
+ * hipBLASLt's bf16 GEMM with fp32 accumulation on it, instead of the tile kernel, which
+ * decodes each weight step once per 256-row tile. The same shape always runs the same GEMM
+ * algorithm, so results are deterministic. Without hipBLASLt, or with no algorithm for the
+ * shape, the call runs the tile kernel. */
 int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, int64_t ldx, void* Y, int y_dtype,
                   int64_t ldy, int M, void* workspace, size_t workspace_bytes, void* hip_stream);
 
@@ -346,9 +345,11 @@ int mtc_gemm_bf16_group(const mtc_tile_desc* const* descs, int n, const void* X,
  * for byte to a 64-byte aligned device buffer, launch with mtc_gemm_bf16_batch. When the
  * members' output tiles together fill the chip no K is split; otherwise each member splits K
  * as mtc_gemm_bf16 would, and its Y then equals that call's bit for bit. Results are
- * deterministic. Every member runs on the tile kernel (a member that mtc_gemm_bf16 alone
- * would run on the decode-once path fills the chip by itself, so such a batch splits no K).
- * Launches that share a workspace must not overlap. */
+ * deterministic. In a batch that does not fill the chip, members that mtc_gemm_bf16 alone
+ * would run on the decode-once path run on it here too, one after another after the tile
+ * launches (in one more workspace area), so their Y also equals the single call's; a batch
+ * that fills the chip runs every member on the tile kernel. Launches that share a workspace
+ * must not overlap. */
 typedef struct mtc_gemm_batch_item {
   const mtc_tile_desc* desc;     /* read while the plan is built */
   const void* X;                 /* M x K, x_dtype, leading dim ldx */

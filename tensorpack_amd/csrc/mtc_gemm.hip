@@ -1223,15 +1223,17 @@ int stage_x(const mtc_tile_desc* d, const void* X, int x_dtype, int64_t ldx, int
 }
 
 // ---- decode once, then a plain GEMM ----
-// A call whose own 256-row output tiles fill the chip, from kDecodeOnceMinRows rows of X on,
-// without an output column permutation: the tile kernel would decode every weight step once per
-// row tile (16 times at 4096 rows), so W_hat is decoded once into bf16 (k_tile_dequant_bf16, the
-// bf16 values the tile kernel's MFMAs read) and multiplied by hipBLASLt's bf16 GEMM with fp32
-// accumulation, X staged as for the tile kernel. The shape alone makes a call eligible, so
-// workspace sizes never depend on the library; an eligible call runs the fused tile kernel when
-// hipBLASLt or an algorithm for its shape is missing, or when the path is switched off
-// (mtc_set_prefill_decode_once).
-constexpr int kDecodeOnceMinRows = 1024;
+// A call with at least max(kDecodeOnceMinRows, K / 8) rows of X and no output column
+// permutation: the tile kernel would decode every weight step once per row tile (16 times at 4096
+// rows), so W_hat is decoded once into bf16 (k_tile_dequant_bf16, the bf16 values the tile
+// kernel's MFMAs read) and multiplied by hipBLASLt's bf16 GEMM with fp32 accumulation, X staged
+// as for the tile kernel. (Timed against the tile kernel on nine shapes from 896 x 128 columns to
+// 8192 x 8192: from 512 rows on this path is faster where K <= 4864, and with K = 8192 from about
+// 1024 rows; below that the decode, 2 bytes written per weight, costs more than it saves.) The
+// shape alone makes a call eligible, so workspace sizes never depend on the library; an eligible
+// call runs the fused tile kernel when hipBLASLt or an algorithm for its shape is missing, or when
+// the path is switched off (mtc_set_prefill_decode_once).
+constexpr int kDecodeOnceMinRows = 512;
 constexpr size_t kBlasWsBytes = (size_t)32 << 20;   // the GEMM's own workspace (fixed: one algorithm per shape)
 std::atomic<int> g_decode_once{1};
 
@@ -1239,7 +1241,7 @@ int64_t decode_once_ldw(const mtc_tile_desc* d) { return (int64_t)d->n_ksteps * 
 size_t decode_once_wt_bytes(const mtc_tile_desc* d) { return round256((size_t)d->N * decode_once_ldw(d) * 2); }
 
 bool decode_once_shape(const mtc_tile_desc* d, int M) {
-  return !d->col_perm && M >= kDecodeOnceMinRows && (int64_t)((M + kTM - 1) / kTM) * d->n_col_tiles >= kFillCUs;
+  return !d->col_perm && M >= std::max(kDecodeOnceMinRows, d->K / 8);
 }
 
 // Workspace of the path: Wt (N x ldw bf16), the staged X (if any), the GEMM's workspace.
@@ -1304,10 +1306,10 @@ std::map<std::tuple<int, int, int, int, int, int64_t, int64_t, int64_t>, Plan> g
 // within kBlasWsBytes of workspace, so a shape always runs the same algorithm); nullptr when
 // the library or an algorithm is missing.
 const Plan* plan_for(int M, int N, int K, int64_t ldw, int64_t ldb, int64_t ldy, int ydt) {
-  const Api& L = api();
-  if (!L.ok) return nullptr;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  const Api& L = api();
+  if (!L.ok) return nullptr;
   std::lock_guard<std::mutex> lock(g_mu);
   const auto key = std::make_tuple(dev, M, N, K, ydt, ldw, ldb, ldy);
   auto it = g_plans.find(key);
@@ -1449,6 +1451,9 @@ struct GemmBatchHeader {
   int32_t stage_rows;     // rows per LDS staging block (0: global gather)
   int32_t stage_max_k;
   int32_t tm;             // output rows per tile block (256, 128 or 64)
+  int32_t n_once;         // members on the decode-once path (a batch that does not fill the chip)
+  uint64_t once_off;      // their indices (uint32)
+  uint64_t once_ws_off;   // their shared workspace area
   uint64_t items_off;
   uint64_t blocks_off;
   uint64_t stage_off;
@@ -1496,9 +1501,23 @@ int build_gemm_batch_plan(const mtc_gemm_batch_item* items, int n, int M, int x_
   // Tile height: 256 rows when the batch fills the chip, else the shortest any item's single call
   // would use (its split is kept, so its Y stays the single call's bit for bit).
   const bool fill = total_tiles >= kFillCUs;
+  // Members that a single call would run on the decode-once path run on it here too, one after
+  // another after the tile launches, when the batch does not fill the chip (their Y then stays the
+  // single call's); a batch that fills the chip runs every member on the tile kernel.
+  std::vector<char> once(n, 0);
+  size_t once_ws = 0;
+  int n_once = 0;
+  if (!fill)
+    for (int i = 0; i < n; ++i)
+      if (decode_once_plan(items[i].desc, x_dtype, items[i].ldx, items[i].ldy, y_dtype, M)) {
+        once[i] = 1;
+        ++n_once;
+        once_ws = std::max(once_ws, decode_once_bytes(items[i].desc, M, x_dtype));
+      }
   int tm = kTM;
   if (!fill)
     for (int i = 0; i < n; ++i) {
+      if (once[i]) continue;
       int s_i = 1, tm_i = kTM;
       split_steps(items[i].desc, M, &s_i, &tm_i);
       tm = std::min(tm, tm_i);
@@ -1524,6 +1543,10 @@ int build_gemm_batch_plan(const mtc_gemm_batch_item* items, int n, int M, int x_
   std::vector<Group> groups;
   for (int i = 0; i < n; ++i) {
     const mtc_tile_desc* d = items[i].desc;
+    if (once[i]) {
+      per[i] = splits[i] = 1;
+      continue;
+    }
     int s = 1;
     per[i] = fill ? d->n_ksteps : split_steps(d, M, &s);
     splits[i] = s;
@@ -1578,7 +1601,10 @@ int build_gemm_batch_plan(const mtc_gemm_batch_item* items, int n, int M, int x_
   const size_t blocks_off = align64(items_off + (size_t)n * sizeof(GemmBatchItem));
   const size_t stage_off = align64(blocks_off + (size_t)blocks * sizeof(uint2));
   const size_t reduce_off = align64(stage_off + (size_t)n_stage * sizeof(uint32_t));
-  const size_t need = reduce_off + (size_t)n_reduce * sizeof(uint32_t);
+  const size_t once_off = align64(reduce_off + (size_t)n_reduce * sizeof(uint32_t));
+  const size_t need = once_off + (size_t)n_once * sizeof(uint32_t);
+  const size_t once_ws_off = ws;
+  ws += once_ws;
   if (plan_needed) *plan_needed = need;
   if (ws_needed) *ws_needed = ws;
   if (!plan) return ok();
@@ -1594,6 +1620,7 @@ int build_gemm_batch_plan(const mtc_gemm_batch_item* items, int n, int M, int x_
   uint2* table = reinterpret_cast<uint2*>(base + blocks_off);
   uint32_t* stage_list = reinterpret_cast<uint32_t*>(base + stage_off);
   uint32_t* reduce_list = reinterpret_cast<uint32_t*>(base + reduce_off);
+  uint32_t* once_list = reinterpret_cast<uint32_t*>(base + once_off);
   h->magic = kGemmBatchMagic;
   h->abi_version = MTC_ABI_VERSION;
   h->n_items = n;
@@ -1603,12 +1630,15 @@ int build_gemm_batch_plan(const mtc_gemm_batch_item* items, int n, int M, int x_
   h->y_dtype = y_dtype;
   h->cf = cf;
   h->tm = tm;
+  h->n_once = n_once;
+  h->once_off = once_off;
+  h->once_ws_off = once_ws_off;
   h->n_stage = n_stage;
   h->n_reduce = n_reduce;
   h->stage_blocks_x = stage_bx;
   int max_k = 0;
   for (int i = 0; i < n; ++i)
-    if (needs_staging(items[i].desc, x_dtype)) max_k = std::max(max_k, items[i].desc->K);
+    if (!once[i] && needs_staging(items[i].desc, x_dtype)) max_k = std::max(max_k, items[i].desc->K);
   h->stage_max_k = max_k;
   h->stage_rows = n_stage ? stage_rows_for(max_k, (int64_t)M * n_stage) : 0;
   h->reduce_blocks_x = reduce_bx;
@@ -1620,7 +1650,7 @@ int build_gemm_batch_plan(const mtc_gemm_batch_item* items, int n, int M, int x_
   h->ws_bytes = ws;
   h->workspace = workspace;
   char* wsp = reinterpret_cast<char*>(workspace);
-  n_stage = n_reduce = 0;
+  n_stage = n_reduce = n_once = 0;
   for (int i = 0; i < n; ++i) {
     const mtc_tile_desc* d = items[i].desc;
     GemmBatchItem& e = it[i];
@@ -1631,6 +1661,12 @@ int build_gemm_batch_plan(const mtc_gemm_batch_item* items, int n, int M, int x_
     e.ldy = items[i].ldy;
     e.steps_per_split = per[i];
     e.splits = splits[i];
+    if (once[i]) {
+      e.X = reinterpret_cast<const __bf16*>(items[i].X);
+      e.ldx = items[i].ldx;
+      once_list[n_once++] = (uint32_t)i;
+      continue;
+    }
     e.stage = needs_staging(d, x_dtype);
     if (e.stage) {
       e.X = reinterpret_cast<const __bf16*>(wsp);
@@ -1704,17 +1740,35 @@ int launch_gemm_batch(const void* host_plan, const void* device_plan, hipStream_
     if (rc) return rc;
   }
   const bool f32 = h->y_dtype == MTC_DTYPE_F32;
-  switch (h->cf) {
-    case kCellFp32:
-      return f32 ? launch_tile_batch<kCellFp32, MTC_DTYPE_F32>(h, items, blocks, reduce_list, st)
+  int rc = 0;
+  if (h->n_blocks) {
+    switch (h->cf) {
+      case kCellFp32:
+        rc = f32 ? launch_tile_batch<kCellFp32, MTC_DTYPE_F32>(h, items, blocks, reduce_list, st)
                  : launch_tile_batch<kCellFp32, MTC_DTYPE_BF16>(h, items, blocks, reduce_list, st);
-    case kCellCols:
-      return f32 ? launch_tile_batch<kCellCols, MTC_DTYPE_F32>(h, items, blocks, reduce_list, st)
+        break;
+      case kCellCols:
+        rc = f32 ? launch_tile_batch<kCellCols, MTC_DTYPE_F32>(h, items, blocks, reduce_list, st)
                  : launch_tile_batch<kCellCols, MTC_DTYPE_BF16>(h, items, blocks, reduce_list, st);
-    default:
-      return f32 ? launch_tile_batch<kCellBf16, MTC_DTYPE_F32>(h, items, blocks, reduce_list, st)
+        break;
+      default:
+        rc = f32 ? launch_tile_batch<kCellBf16, MTC_DTYPE_F32>(h, items, blocks, reduce_list, st)
                  : launch_tile_batch<kCellBf16, MTC_DTYPE_BF16>(h, items, blocks, reduce_list, st);
+    }
+    if (rc) return rc;
   }
+  // the decode-once members, from the host copy of the plan
+  const unsigned char* hp = reinterpret_cast<const unsigned char*>(host_plan);
+  const GemmBatchItem* hitems = reinterpret_cast<const GemmBatchItem*>(hp + h->items_off);
+  const uint32_t* once_list = reinterpret_cast<const uint32_t*>(hp + h->once_off);
+  for (int j = 0; j < h->n_once && !rc; ++j) {
+    const GemmBatchItem& e = hitems[once_list[j]];
+    const lt::Plan* p = decode_once_plan(&e.d, h->x_dtype, e.ldx_src, e.ldy, h->y_dtype, h->M);
+    if (!p) return fail(MTC_E_LAUNCH, "batch item %u: no GEMM plan for its decode-once path", once_list[j]);
+    rc = decode_once_call(&e.d, e.Xsrc, h->x_dtype, e.ldx_src, e.Y, h->M,
+                          reinterpret_cast<char*>(const_cast<void*>(h->workspace)) + h->once_ws_off, p, st);
+  }
+  return rc;
 }
 
 }  // namespace

@@ -287,7 +287,6 @@ class DeviceTiles:
         d.row_perm, d.col_perm = ptr(self.row_perm), ptr(self.col_perm)
         self.desc = d
         _abi.check(self.lib, "mtc_check_tile_desc", self.lib.mtc_check_tile_desc(ctypes.byref(d)))
-        self._ws: Dict[int, "object"] = {}             # HIP stream handle -> workspace tensor
 
     @property
     def K(self) -> int:
@@ -313,20 +312,16 @@ class DeviceTiles:
         d.cells, d.step_off, d.payload = ptr(other.cells), ptr(other.step_off), ptr(other.payload)
         d.row_perm, d.col_perm = ptr(other.row_perm), ptr(other.col_perm)
         other.desc = d
-        other._ws = {}
         return other
 
     def workspace(self, M: int, x_dtype: int, need: int = None):
+        """The prefill workspace of an M-row call (prefill_workspace: shared by every matrix's calls
+        on the current stream)."""
         if need is None:
             need = int(self.lib.mtc_gemm_workspace_bytes(ctypes.byref(self.desc), int(M), int(x_dtype)))
         if need == 0:
             return None, 0
-        key = current_stream_handle(self.device)       # one per stream: calls on two streams may overlap
-        ws = self._ws.get(key)
-        if ws is None or ws.numel() < need:
-            torch = _torch()
-            ws = self._ws[key] = torch.empty(need, dtype=torch.uint8, device=self.device)
-        return ws, need
+        return prefill_workspace(self.device, need), need
 
     def gemm_bf16(self, X, out=None, out_dtype=None):
         torch = _torch()
@@ -445,7 +440,22 @@ class GemmBatch:
         return self.outs
 
 
-_GROUP_WS: dict = {}
+_PREFILL_WS: dict = {}
+
+
+def prefill_workspace(device, need: int):
+    """A device buffer of at least `need` bytes for the prefill calls on the current HIP stream of
+    `device`, shared by every matrix and group: calls ordered on one stream never overlap, calls on
+    two streams may, so each stream has its own. The buffer only grows, to at least twice its last
+    size, and a buffer it outgrows is kept, never freed: a HIP graph captured earlier still
+    addresses it."""
+    torch = _torch()
+    key = (str(device), current_stream_handle(device))
+    held = _PREFILL_WS.setdefault(key, [])
+    if not held or held[-1].numel() < need:
+        size = max(int(need), 2 * held[-1].numel() if held else 0)
+        held.append(torch.empty(size, dtype=torch.uint8, device=device))
+    return held[-1]
 
 
 def gemm_bf16_group(tiles, X, outs=None, out_dtype=None):
@@ -481,10 +491,7 @@ def gemm_bf16_group(tiles, X, outs=None, out_dtype=None):
     lib = tiles[0].lib
     descs = (_abi.TileDescP * n)(*[ctypes.pointer(t.desc) for t in tiles])
     need = int(lib.mtc_gemm_group_workspace_bytes(descs, n, M, xdt))
-    key = (str(dev), current_stream_handle(dev))
-    ws = _GROUP_WS.get(key)
-    if need and (ws is None or ws.numel() < need):
-        ws = _GROUP_WS[key] = torch.empty(need, dtype=torch.uint8, device=dev)
+    ws = prefill_workspace(dev, need) if need else None
     ys = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
     lds = (ctypes.c_int64 * n)(*[_row_stride(o) for o in outs])
     rc = lib.mtc_gemm_bf16_group(descs, n, X.data_ptr(), xdt, _row_stride(X), ys, ydt, lds, M,

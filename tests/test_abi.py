@@ -181,24 +181,27 @@ def test_group_prefill_entry_rejects_bad_arguments_before_any_gpu_call(hip):
 
 
 def test_decode_once_workspace_by_shape(hip):
-    """Prefill whose 256-row output tiles fill the chip, from 1024 rows of X on and without an
-    output column permutation, takes the decode-once path: its workspace holds W_hat in bf16
-    (N x 64 * n_ksteps), the staged X and 32 MiB for the GEMM. The shape alone decides."""
+    """Prefill with at least max(512, K / 8) rows of X and no output column permutation takes the
+    decode-once path: its workspace holds W_hat in bf16 (N x 64 * n_ksteps), the staged X and
+    32 MiB for the GEMM. The shape alone decides."""
     blas = 32 << 20
     big = _tdesc(K=1024, N=4096, n_ksteps=16, n_col_tiles=16)
     wt = 4096 * 1024 * 2
     ws = lambda d, M, xdt: hip.mtc_gemm_workspace_bytes(ctypes.byref(d), M, xdt)
-    assert ws(big, 4096, 1) == wt + blas                                  # 16 x 16 tiles, bf16 X read in place
+    assert ws(big, 4096, 1) == wt + blas                                  # bf16 X read in place
     assert ws(big, 4096, 0) == wt + 4096 * 1024 * 2 + blas                # fp32 X staged as bf16
-    wide = _tdesc(K=1024, N=16384, n_ksteps=16, n_col_tiles=64)
-    assert ws(wide, 1000, 1) == 0                                         # fills the chip, but under 1024 rows
-    assert ws(wide, 1024, 1) == 16384 * 1024 * 2 + blas
+    assert ws(big, 512, 1) == wt + blas
+    short = ws(big, 511, 1)                                               # tile kernel: split-K partials only
+    assert short % (511 * 4096 * 4) == 0 and 1 <= short // (511 * 4096 * 4) <= 16
+    deep = _tdesc(K=8192, N=2048, n_ksteps=128, n_col_tiles=8)           # K / 8 = 1024 rows
+    assert ws(deep, 1024, 1) == 2048 * 8192 * 2 + blas
+    assert ws(deep, 1023, 1) % (1023 * 2048 * 4) == 0
     rows = _tdesc(K=1024, N=4096, n_ksteps=16, n_col_tiles=16, row_perm=0x2000)
     assert ws(rows, 4096, 1) == wt + 4096 * 1024 * 2 + blas               # a row permutation: X staged
     cols = _tdesc(K=1024, N=4096, n_ksteps=16, n_col_tiles=16, row_perm=0x2000, col_perm=0x3000)
     assert ws(cols, 4096, 1) == 4096 * 1024 * 2                           # a column permutation: tile kernel
     D = _abi.TileDescP
-    small = _tdesc(K=1024, n_ksteps=16)
+    small = _tdesc(K=1024, n_ksteps=16, row_perm=0x2000, col_perm=0x3000)
     descs = (D * 2)(ctypes.pointer(small), ctypes.pointer(big))
     assert hip.mtc_gemm_group_workspace_bytes(descs, 2, 4096, 1) == ws(small, 4096, 1) + wt + blas
     assert hip.mtc_set_prefill_decode_once(-1) == 1

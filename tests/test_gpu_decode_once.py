@@ -1,6 +1,6 @@
-"""Prefill on the decode-once path (run on an MI355X): calls whose 256-row output tiles fill the
-chip from 1024 rows of X on decode W_hat once into bf16 (k_tile_dequant_bf16) and multiply it
-with hipBLASLt's bf16 GEMM (fp32 accumulation).
+"""Prefill on the decode-once path (run on an MI355X): calls with at least max(512, K / 8) rows
+of X and no output column permutation decode W_hat once into bf16 (k_tile_dequant_bf16) and
+multiply it with hipBLASLt's bf16 GEMM (fp32 accumulation).
 
 Bars: the decoded bf16 W_hat bit-exact against bf16(oracle W_hat) in the stream's row order;
 Y within 2e-3 relative Frobenius of the fp64 product of the same bf16 X (the bf16 path's
@@ -25,7 +25,7 @@ from conftest import outlier_matrix
 pytestmark = pytest.mark.gpu
 
 TOL_BF16 = 2e-3
-K, N, M = 1024, 4096, 4096          # 16 x 16 output tiles of 256: eligible from 1024 rows on
+K, N, M = 1024, 4096, 4096          # eligible from 512 rows on
 
 
 def _say(*a):
@@ -115,15 +115,26 @@ def test_decode_once_bf16_output_and_strided_x(gpu, mats, xs):
     assert O.relative_frobenius_error(ref, Ys) <= TOL_BF16
 
 
+def _col_permuted_tiles(gpu, N_, seed):
+    """A QT-P matrix packed with its column permutation kept (bf16-pair cells and col_perm, not
+    gathered columns): the tile kernel at every M, since a GEMM cannot scatter Y's columns."""
+    from tensorpack_amd.device import DeviceTiles
+    from tensorpack_amd.tilestream import pack_tiles
+    Wn = outlier_matrix(seed, K, N_)
+    a = PermutedQuadtreeRD(Wn, None, (32, 16, 8, 4)).select(4.5)
+    lv = MTCMatrix.from_quadtree(a, Wn)._levels
+    ts = pack_tiles(lv.shape, lv.sizes, lv.leaf, lv.modes, lv.scales, lv.codes_of, lv.scale_format, lv.row_perm,
+                    lv.col_perm, gather_cols=False)
+    assert ts.col_perm is not None
+    return DeviceTiles(ts, gpu)
+
+
 def test_decode_once_group_members_equal_single_calls(gpu, mats, xs):
-    """A group of an eligible member and one that runs the tile kernel with split K (N = 256:
-    16 tiles): each Y equals its single call bit for bit."""
+    """A group of an eligible member and one that runs the tile kernel (a column permutation,
+    N = 256: 16 tiles, split K): each Y equals its single call bit for bit."""
     from tensorpack_amd.device import gemm_bf16_group
-    m, _ = mats["qt"]
-    Wn = outlier_matrix(74, K, 256)
-    a = QuadtreeRD(Wn, None, (32, 16, 8, 4)).select(4.5)
-    small = MTCMatrix.from_quadtree(a, Wn).device_tiles(gpu)
-    g = m.device_tiles(gpu)
+    small = _col_permuted_tiles(gpu, 256, 74)
+    g = mats["qt"][0].device_tiles(gpu)
     assert g.lib.mtc_gemm_workspace_bytes(ctypes.byref(small.desc), M, 1) < (32 << 20)   # not eligible
     _, Xb = xs
     for X in (Xb, Xb.float()):
@@ -131,3 +142,50 @@ def test_decode_once_group_members_equal_single_calls(gpu, mats, xs):
         Ys = gemm_bf16_group([small, g], X)
         assert np.array_equal(_bits(Ys[0].cpu().numpy()), _bits(small.gemm_bf16(X).cpu().numpy()))
         assert np.array_equal(_bits(Ys[1].cpu().numpy()), _bits(g.gemm_bf16(X).cpu().numpy()))
+
+
+@pytest.mark.parametrize("Mb", [512, 600])
+def test_decode_once_batch_members_equal_single_calls(gpu, mats, Mb):
+    """A batch that does not fill the chip (an eligible member from 512 rows on, and a column-
+    permuted one on the tile kernel): each member's Y equals its single call bit for bit, the
+    eligible one on the decode-once path; relaunching gives the same bits."""
+    import torch
+    from tensorpack_amd.device import GemmBatch
+    g = mats["qt"][0].device_tiles(gpu)
+    small = _col_permuted_tiles(gpu, 256, 75)
+    rng = np.random.RandomState(Mb)
+    Xs = [torch.from_numpy(rng.randn(Mb, K).astype(np.float32)).to(gpu).to(torch.bfloat16) for _ in range(2)]
+    _say("decode-once batch", Mb)
+    b = GemmBatch([g, small], Xs)
+    ys = [y.clone() for y in b.launch()]
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(ys[0].cpu().numpy()), _bits(g.gemm_bf16(Xs[0]).cpu().numpy()))
+    assert np.array_equal(_bits(ys[1].cpu().numpy()), _bits(small.gemm_bf16(Xs[1]).cpu().numpy()))
+    b.launch()
+    torch.cuda.synchronize()
+    for y0, y in zip(ys, b.outs):
+        assert torch.equal(y0, y)
+
+
+def test_decode_once_first_call_under_graph_capture(gpu, mats):
+    """The first call of a shape made while a HIP graph is captured (the GEMM plan is made
+    during the capture): every replay equals the eager call bit for bit."""
+    import torch
+    g = mats["uniform"][0].device_tiles(gpu)
+    X = torch.from_numpy(np.random.RandomState(76).randn(700, K).astype(np.float32)).to(gpu).to(torch.bfloat16)
+    out = torch.empty(700, N, device=gpu)
+    _say("decode-once first call under capture")
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            g.gemm_bf16(X, out=out)
+    torch.cuda.current_stream().wait_stream(side)
+    eager = g.gemm_bf16(X)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
