@@ -294,7 +294,8 @@ size_t mtc_gemm_workspace_bytes(const mtc_tile_desc* d, int M, int x_dtype);
  * X (M x K, fp32 or bf16, leading dim ldx) * W_hat with bf16 operands and
  * fp32 accumulation. bf16 X read in place must have 16-byte aligned rows
  * (ldx % 8 == 0). Any M >= 1.
- * Decode-once path: a call with M >= max(512, K / 8) and no col_perm decodes W_hat once
+ * Decode-once path: a call with M >= max(512, K / 8), M * K * N >= 2^28 and no col_perm
+ * decodes W_hat once
  * into bf16 in the workspace (the values the tile kernel would multiply) and runs
  * hipBLASLt's bf16 GEMM with fp32 accumulation on it, instead of the tile kernel, which
  * decodes each weight step once per 256-row tile. The same shape always runs the same GEMM

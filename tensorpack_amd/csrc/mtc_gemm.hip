@@ -1223,17 +1223,20 @@ int stage_x(const mtc_tile_desc* d, const void* X, int x_dtype, int64_t ldx, int
 }
 
 // ---- decode once, then a plain GEMM ----
-// A call with at least max(kDecodeOnceMinRows, K / 8) rows of X and no output column
-// permutation: the tile kernel would decode every weight step once per row tile (16 times at 4096
-// rows), so W_hat is decoded once into bf16 (k_tile_dequant_bf16, the bf16 values the tile
-// kernel's MFMAs read) and multiplied by hipBLASLt's bf16 GEMM with fp32 accumulation, X staged
-// as for the tile kernel. (Timed against the tile kernel on nine shapes from 896 x 128 columns to
-// 8192 x 8192: from 512 rows on this path is faster where K <= 4864, and with K = 8192 from about
-// 1024 rows; below that the decode, 2 bytes written per weight, costs more than it saves.) The
+// A call with at least max(kDecodeOnceMinRows, K / 8) rows of X, at least kDecodeOnceMinMacs
+// multiply-adds and no output column permutation: the tile kernel would decode every weight step
+// once per row tile (16 times at 4096 rows), so W_hat is decoded once into bf16
+// (k_tile_dequant_bf16, the bf16 values the tile kernel's MFMAs read) and multiplied by
+// hipBLASLt's bf16 GEMM with fp32 accumulation, X staged as for the tile kernel. (Timed against
+// the tile kernel on ten shapes from 896 x 128 to 8192 x 8192: from 512 rows on this path is
+// faster where K <= 4864, and with K = 8192 from about 1024 rows; below that the decode, 2 bytes
+// written per weight, costs more than it saves, and calls of fewer multiply-adds, such as
+// 512 x 896 x 128, are bound by their launches, of which this path has one more.) The
 // shape alone makes a call eligible, so workspace sizes never depend on the library; an eligible
 // call runs the fused tile kernel when hipBLASLt or an algorithm for its shape is missing, or when
 // the path is switched off (mtc_set_prefill_decode_once).
 constexpr int kDecodeOnceMinRows = 512;
+constexpr int64_t kDecodeOnceMinMacs = (int64_t)1 << 28;   // below: one launch more costs more than it saves
 constexpr size_t kBlasWsBytes = (size_t)32 << 20;   // the GEMM's own workspace (fixed: one algorithm per shape)
 std::atomic<int> g_decode_once{1};
 
@@ -1241,7 +1244,8 @@ int64_t decode_once_ldw(const mtc_tile_desc* d) { return (int64_t)d->n_ksteps * 
 size_t decode_once_wt_bytes(const mtc_tile_desc* d) { return round256((size_t)d->N * decode_once_ldw(d) * 2); }
 
 bool decode_once_shape(const mtc_tile_desc* d, int M) {
-  return !d->col_perm && M >= std::max(kDecodeOnceMinRows, d->K / 8);
+  return !d->col_perm && M >= std::max(kDecodeOnceMinRows, d->K / 8) &&
+         (int64_t)M * d->K * d->N >= kDecodeOnceMinMacs;
 }
 
 // Workspace of the path: Wt (N x ldw bf16), the staged X (if any), the GEMM's workspace.

@@ -181,9 +181,9 @@ def test_group_prefill_entry_rejects_bad_arguments_before_any_gpu_call(hip):
 
 
 def test_decode_once_workspace_by_shape(hip):
-    """Prefill with at least max(512, K / 8) rows of X and no output column permutation takes the
-    decode-once path: its workspace holds W_hat in bf16 (N x 64 * n_ksteps), the staged X and
-    32 MiB for the GEMM. The shape alone decides."""
+    """Prefill with at least max(512, K / 8) rows of X, 2^28 multiply-adds and no output column
+    permutation takes the decode-once path: its workspace holds W_hat in bf16 (N x 64 * n_ksteps),
+    the staged X and 32 MiB for the GEMM. The shape alone decides."""
     blas = 32 << 20
     big = _tdesc(K=1024, N=4096, n_ksteps=16, n_col_tiles=16)
     wt = 4096 * 1024 * 2
@@ -196,6 +196,9 @@ def test_decode_once_workspace_by_shape(hip):
     deep = _tdesc(K=8192, N=2048, n_ksteps=128, n_col_tiles=8)           # K / 8 = 1024 rows
     assert ws(deep, 1024, 1) == 2048 * 8192 * 2 + blas
     assert ws(deep, 1023, 1) % (1023 * 2048 * 4) == 0
+    narrow = _tdesc(K=1024, N=256, n_ksteps=16, n_col_tiles=1)            # 2^28 multiply-adds from 1024 rows
+    assert ws(narrow, 1024, 1) == 256 * 1024 * 2 + blas
+    assert ws(narrow, 1023, 1) % (1023 * 256 * 4) == 0
     rows = _tdesc(K=1024, N=4096, n_ksteps=16, n_col_tiles=16, row_perm=0x2000)
     assert ws(rows, 4096, 1) == wt + 4096 * 1024 * 2 + blas               # a row permutation: X staged
     cols = _tdesc(K=1024, N=4096, n_ksteps=16, n_col_tiles=16, row_perm=0x2000, col_perm=0x3000)
