@@ -745,81 +745,109 @@ __global__ __launch_bounds__(kStageThreads) void k_stage_x_f32(const float* __re
 }
 
 // ---- decode once: W_hat in bf16 for a plain GEMM ----
-// One block per (column tile ct, K-step ks), grid n_col_tiles x n_ksteps, 256 threads: thread t
-// decodes cells t and t + 256 of the step as the tile kernel's producers do (decode_cell: the same
-// bf16 values the MFMAs would read), into a swizzled [256][64] LDS tile, then the block writes it
-// out as whole 128-byte row pieces: Wt[n][k] (N rows of ldw bf16, ldw = 64 * n_ksteps) holds
-// W_hat[k][n] for stream row k (row_perm order, as the staged X) and column n; rows k >= K hold
-// the stream's zero padding. (Stores straight from registers, one cell per thread, ran 54 us
-// against 40 us at 8192 x 8192: a step's cells are sorted by class first, so their lines split.)
+// One block per (column tile ct, run of `spb` K-steps), grid n_col_tiles x ceil(n_ksteps / spb),
+// 256 threads: for each step thread t decodes cells t and t + 256 as the tile kernel's producers
+// do (decode_cell: the same bf16 values the MFMAs would read) into a swizzled [256][64] LDS tile,
+// then the block writes it out as whole 128-byte row pieces: Wt[n][k] (N rows of ldw bf16,
+// ldw = 64 * n_ksteps) holds W_hat[k][n] for stream row k (row_perm order, as the staged X) and
+// column n; rows k >= K hold the stream's zero padding. While a step is decoded and written, the
+// next step's payload and the descriptors of the step after it are in flight. (Stores straight
+// from registers, one cell per thread, ran 54 us against 40 us for one step per block at
+// 8192 x 8192: a step's cells are sorted by class first, so their lines split.)
 template <int kCF>
 __global__ __launch_bounds__(256) void k_tile_dequant_bf16(const mtc_tile_desc d, __bf16* __restrict__ Wt,
-                                                          int64_t ldw) {
+                                                          int64_t ldw, int spb) {
   __shared__ __attribute__((aligned(16))) unsigned char bs[kTN * kTK * 2];
   constexpr int CW = cell_words(kCF);
-  const int t = threadIdx.x;
-  const size_t step = (size_t)blockIdx.x * d.n_ksteps + blockIdx.y;
-  const __amdgpu_buffer_rsrc_t cell_r = buffer_of(d.cells + step * kCells * CW, (int64_t)kCells * CW * 4);
+  const int t = threadIdx.x, ct = blockIdx.x;
+  const int ks0 = (int)blockIdx.y * spb, nks = min(spb, d.n_ksteps - ks0);
+  const size_t step0 = (size_t)ct * d.n_ksteps + ks0;
+  const __amdgpu_buffer_rsrc_t cell_r = buffer_of(d.cells + step0 * kCells * CW, (int64_t)nks * kCells * CW * 4);
   const __amdgpu_buffer_rsrc_t pay_r = buffer_of(d.payload, d.payload_dwords * 4);
-  const uint32_t base = d.step_off[step];
-  uint32_t w[2][CW];
+  const uint32_t* step_off = d.step_off + step0;
+  auto load_desc = [&](int i, uint32_t (&w)[2][CW]) __attribute__((always_inline)) {
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const uint32_t off = (uint32_t)((t + 256 * h) * CW) * 4u;
-    if constexpr (CW == 2) {
-      const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(cell_r, off, 0, 0);
-      w[h][0] = v.x;
-      w[h][1] = v.y;
-    } else {
-#pragma unroll
-      for (int i = 0; i < CW / 4; ++i) {
-        const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(cell_r, off + 16u * i, 0, 0);
-        w[h][4 * i + 0] = v.x;
-        w[h][4 * i + 1] = v.y;
-        w[h][4 * i + 2] = v.z;
-        w[h][4 * i + 3] = v.w;
-      }
-    }
-  }
-  u32x4_t q[2][4];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const uint32_t cls = (w[h][0] >> 14) & 3u;
-    const uint32_t o = (base + (w[h][0] & 0x3FFFu)) * 4u;
-    const uint32_t n = cls == 0 ? 1u : cls == 1 ? 2u : cls == 2 ? 4u : 0u;
-#pragma unroll
-    for (uint32_t i = 0; i < 4; ++i)
-      q[h][i] = __builtin_amdgcn_raw_buffer_load_b128(pay_r, i < n ? o + 16u * i : kOutOfRange, 0, 0);
-  }
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    float st[4], sb[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if constexpr (kCF == kCellFp32) {
-        st[j] = __uint_as_float(w[h][1]);
-        sb[j] = __uint_as_float(w[h][2]);
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t off = (uint32_t)((i * kCells + t + 256 * h) * CW) * 4u;
+      if constexpr (CW == 2) {
+        const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(cell_r, off, 0, 0);
+        w[h][0] = v.x;
+        w[h][1] = v.y;
       } else {
-        const uint32_t sw = kCF == kCellCols ? w[h][1 + j] : w[h][1];
-        st[j] = __uint_as_float(sw << 16);
-        sb[j] = __uint_as_float(sw & 0xFFFF0000u);
+#pragma unroll
+        for (int j = 0; j < CW / 4; ++j) {
+          const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(cell_r, off + 16u * j, 0, 0);
+          w[h][4 * j + 0] = v.x;
+          w[h][4 * j + 1] = v.y;
+          w[h][4 * j + 2] = v.z;
+          w[h][4 * j + 3] = v.w;
+        }
       }
     }
-    const uint32_t pos = (w[h][0] >> 16) & (kCells - 1);   // (column group, row block) of the cell
-    const int col = (int)(pos >> 3) * 4, seg = (int)(pos & 7u);
-    u32x4_t o[4];
-    decode_cell<kCF == kCellCols>((w[h][0] >> 14) & 3u, q[h], st, sb, o);
+  };
+  auto load_payload = [&](uint32_t base, const uint32_t (&w)[2][CW], u32x4_t (&q)[2][4]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4_t*>(bs + swz(col + j, seg)) = o[j];
-  }
-  __syncthreads();
-  __bf16* const out = Wt + (int64_t)blockIdx.y * kTK;
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t cls = (w[h][0] >> 14) & 3u;
+      const uint32_t o = (base + (w[h][0] & 0x3FFFu)) * 4u;
+      const uint32_t n = cls == 0 ? 1u : cls == 1 ? 2u : cls == 2 ? 4u : 0u;
 #pragma unroll
-  for (int i = 0; i < kTN * 8 / 256; ++i) {
-    const int piece = t + 256 * i, row = piece >> 3, seg = piece & 7;
-    const int n = (int)blockIdx.x * kTN + row;
-    if (n < d.N)
-      *reinterpret_cast<u32x4_t*>(out + (int64_t)n * ldw + seg * 8) = *reinterpret_cast<const u32x4_t*>(bs + swz(row, seg));
+      for (uint32_t i = 0; i < 4; ++i)
+        q[h][i] = __builtin_amdgcn_raw_buffer_load_b128(pay_r, i < n ? o + 16u * i : kOutOfRange, 0, 0);
+    }
+  };
+  auto decode = [&](const uint32_t (&w)[2][CW], const u32x4_t (&q)[2][4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float st[4], sb[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (kCF == kCellFp32) {
+          st[j] = __uint_as_float(w[h][1]);
+          sb[j] = __uint_as_float(w[h][2]);
+        } else {
+          const uint32_t sw = kCF == kCellCols ? w[h][1 + j] : w[h][1];
+          st[j] = __uint_as_float(sw << 16);
+          sb[j] = __uint_as_float(sw & 0xFFFF0000u);
+        }
+      }
+      const uint32_t pos = (w[h][0] >> 16) & (kCells - 1);   // (column group, row block) of the cell
+      const int col = (int)(pos >> 3) * 4, seg = (int)(pos & 7u);
+      u32x4_t o[4];
+      decode_cell<kCF == kCellCols>((w[h][0] >> 14) & 3u, q[h], st, sb, o);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4_t*>(bs + swz(col + j, seg)) = o[j];
+    }
+  };
+  auto write_out = [&](int ks) __attribute__((always_inline)) {
+    __bf16* const out = Wt + (int64_t)ks * kTK;
+#pragma unroll
+    for (int i = 0; i < kTN * 8 / 256; ++i) {
+      const int piece = t + 256 * i, row = piece >> 3, seg = piece & 7;
+      const int n = ct * kTN + row;
+      if (n < d.N)
+        *reinterpret_cast<u32x4_t*>(out + (int64_t)n * ldw + seg * 8) =
+            *reinterpret_cast<const u32x4_t*>(bs + swz(row, seg));
+    }
+  };
+  // step i: descriptors wa, payload qa; step i + 1: descriptors wb, payload qb
+  uint32_t wa[2][CW], wb[2][CW];
+  u32x4_t qa[2][4], qb[2][4];
+  auto body = [&](int i, uint32_t (&wc)[2][CW], u32x4_t (&qc)[2][4], const uint32_t (&wn)[2][CW],
+                  u32x4_t (&qn)[2][4]) __attribute__((always_inline)) {
+    decode(wc, qc);
+    if (i + 1 < nks) load_payload(step_off[i + 1], wn, qn);
+    if (i + 2 < nks) load_desc(i + 2, wc);
+    lds_barrier();                                     // LDS only: the loads above stay in flight
+    write_out(ks0 + i);
+    lds_barrier();                                     // the tile is free for the next step
+  };
+  load_desc(0, wa);
+  if (nks > 1) load_desc(1, wb);
+  load_payload(step_off[0], wa, qa);
+  for (int i = 0; i < nks; i += 2) {
+    body(i, wa, qa, wb, qb);
+    if (i + 1 < nks) body(i + 1, wb, qb, wa, qa);
   }
 }
 
@@ -1380,17 +1408,21 @@ int decode_once_call(const mtc_tile_desc* d, const void* X, int x_dtype, int64_t
     xb = reinterpret_cast<const __bf16*>(w);
     w += round256(staging_bytes(d, M, x_dtype));
   }
-  const dim3 grid((unsigned)d->n_col_tiles, (unsigned)d->n_ksteps);
+  // K-steps per block: one while there are fewer steps than a wave of resident blocks (five per
+  // CU by LDS), up to 8 as the matrix grows (8192 x 8192: 4096 steps, 3 per block)
+  const int64_t n_steps = (int64_t)d->n_col_tiles * d->n_ksteps;
+  const int spb = (int)std::min<int64_t>(8, std::max<int64_t>(1, n_steps / (5 * kFillCUs)));
+  const dim3 grid((unsigned)d->n_col_tiles, (unsigned)((d->n_ksteps + spb - 1) / spb));
   const int64_t ldw = decode_once_ldw(d);
   switch (cell_format(d)) {
     case kCellFp32:
-      hipLaunchKernelGGL(k_tile_dequant_bf16<kCellFp32>, grid, dim3(256), 0, st, *d, Wt, ldw);
+      hipLaunchKernelGGL(k_tile_dequant_bf16<kCellFp32>, grid, dim3(256), 0, st, *d, Wt, ldw, spb);
       break;
     case kCellCols:
-      hipLaunchKernelGGL(k_tile_dequant_bf16<kCellCols>, grid, dim3(256), 0, st, *d, Wt, ldw);
+      hipLaunchKernelGGL(k_tile_dequant_bf16<kCellCols>, grid, dim3(256), 0, st, *d, Wt, ldw, spb);
       break;
     default:
-      hipLaunchKernelGGL(k_tile_dequant_bf16<kCellBf16>, grid, dim3(256), 0, st, *d, Wt, ldw);
+      hipLaunchKernelGGL(k_tile_dequant_bf16<kCellBf16>, grid, dim3(256), 0, st, *d, Wt, ldw, spb);
   }
   const int rc = check_launch("k_tile_dequant_bf16");
   if (rc) return rc;
