@@ -287,7 +287,7 @@ int mtc_check_tile_desc(const mtc_tile_desc* d);
  * splits*M*N*4 when the output has too few 256 x 256 tiles to fill the chip and the
  * K steps are split over blocks (fp32 partial tiles, summed in a fixed order).
  * For a call eligible for the decode-once path (below) at least N*64*ceil(K/64)*2
- * (W_hat in bf16) + the staged X + 32 MiB (the GEMM's own workspace). */
+ * (W_hat in bf16) + the staged X (the GEMM itself runs without a workspace). */
 size_t mtc_gemm_workspace_bytes(const mtc_tile_desc* d, int M, int x_dtype);
 
 /* bf16 MFMA path (prefill): Y (M x N, fp32 or bf16, leading dim ldy) =

@@ -1265,7 +1265,10 @@ int stage_x(const mtc_tile_desc* d, const void* X, int x_dtype, int64_t ldx, int
 // the path is switched off (mtc_set_prefill_decode_once).
 constexpr int kDecodeOnceMinRows = 512;
 constexpr int64_t kDecodeOnceMinMacs = (int64_t)1 << 28;   // below: one launch more costs more than it saves
-constexpr size_t kBlasWsBytes = (size_t)32 << 20;   // the GEMM's own workspace (fixed: one algorithm per shape)
+// The GEMM runs without a workspace: the algorithms hipBLASLt picks first for the shapes timed here
+// need none when allowed 32 MiB (and run as fast), and one without a workspace can never leave a
+// memset node in a captured graph.
+constexpr size_t kBlasWsBytes = 0;
 std::atomic<int> g_decode_once{1};
 
 int64_t decode_once_ldw(const mtc_tile_desc* d) { return (int64_t)d->n_ksteps * kTK; }
@@ -1276,7 +1279,7 @@ bool decode_once_shape(const mtc_tile_desc* d, int M) {
          (int64_t)M * d->K * d->N >= kDecodeOnceMinMacs;
 }
 
-// Workspace of the path: Wt (N x ldw bf16), the staged X (if any), the GEMM's workspace.
+// Workspace of the path: Wt (N x ldw bf16), then the staged X (if any).
 size_t decode_once_bytes(const mtc_tile_desc* d, int M, int x_dtype) {
   return decode_once_wt_bytes(d) + round256(staging_bytes(d, M, x_dtype)) + kBlasWsBytes;
 }
@@ -1335,8 +1338,8 @@ std::map<int, hipblasLtHandle_t> g_handles;                                   //
 std::map<std::tuple<int, int, int, int, int, int64_t, int64_t, int64_t>, Plan> g_plans;
 
 // The GEMM plan of a shape on the current device, made once (the heuristic's first algorithm
-// within kBlasWsBytes of workspace, so a shape always runs the same algorithm); nullptr when
-// the library or an algorithm is missing.
+// among those needing at most kBlasWsBytes of workspace, so a shape always runs the same
+// algorithm); nullptr when the library or an algorithm is missing.
 const Plan* plan_for(int M, int N, int K, int64_t ldw, int64_t ldb, int64_t ldy, int ydt) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;

@@ -8,8 +8,6 @@ bar) and within 1e-5 of the fused tile kernel's Y (the same bf16 operands, fp32 
 another order); repeated calls and group members bit-identical to single calls.
 """
 
-import ctypes
-
 import numpy as np
 import pytest
 
@@ -135,7 +133,6 @@ def test_decode_once_group_members_equal_single_calls(gpu, mats, xs):
     from tensorpack_amd.device import gemm_bf16_group
     small = _col_permuted_tiles(gpu, 256, 74)
     g = mats["qt"][0].device_tiles(gpu)
-    assert g.lib.mtc_gemm_workspace_bytes(ctypes.byref(small.desc), M, 1) < (32 << 20)   # not eligible
     _, Xb = xs
     for X in (Xb, Xb.float()):
         _say("decode-once group", X.dtype)
