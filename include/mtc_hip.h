@@ -307,8 +307,9 @@ int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, int64_t ld
 /* Switches the decode-once path of mtc_gemm_bf16 / mtc_gemm_bf16_group on (1, the default)
  * or off (0: every call runs the tile kernel) for the process; -1 only queries. Returns the
  * previous setting. No counterpart in the reference: for callers and tests that measure or
- * check the fused tile kernel at shapes the decode-once path would take. Not synchronised
- * with calls in flight on other threads. */
+ * check the fused tile kernel at shapes the decode-once path would take. A prefill batch
+ * plan keeps the choice made when it was built. Not synchronised with calls in flight on
+ * other threads. */
 int mtc_set_prefill_decode_once(int enable);
 
 /* fp32 matrix-core path over the tile stream: Y (M x N fp32, leading dim ldy) = X (M x K

@@ -1801,8 +1801,10 @@ int launch_gemm_batch(const void* host_plan, const void* device_plan, hipStream_
   const GemmBatchItem* hitems = reinterpret_cast<const GemmBatchItem*>(hp + h->items_off);
   const uint32_t* once_list = reinterpret_cast<const uint32_t*>(hp + h->once_off);
   for (int j = 0; j < h->n_once && !rc; ++j) {
+    // the plan's choice stands (made when it was built; the switch may have changed since)
     const GemmBatchItem& e = hitems[once_list[j]];
-    const lt::Plan* p = decode_once_plan(&e.d, h->x_dtype, e.ldx_src, e.ldy, h->y_dtype, h->M);
+    const lt::Plan* p = lt::plan_for(h->M, e.d.N, e.d.K, decode_once_ldw(&e.d),
+                                     needs_staging(&e.d, h->x_dtype) ? e.d.K : e.ldx_src, e.ldy, h->y_dtype);
     if (!p) return fail(MTC_E_LAUNCH, "batch item %u: no GEMM plan for its decode-once path", once_list[j]);
     rc = decode_once_call(&e.d, e.Xsrc, h->x_dtype, e.ldx_src, e.Y, h->M,
                           reinterpret_cast<char*>(const_cast<void*>(h->workspace)) + h->once_ws_off, p, st);

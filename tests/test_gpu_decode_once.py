@@ -162,6 +162,11 @@ def test_decode_once_batch_members_equal_single_calls(gpu, mats, Mb):
     torch.cuda.synchronize()
     for y0, y in zip(ys, b.outs):
         assert torch.equal(y0, y)
+    # the plan keeps the path it was built with, whatever the switch says at launch
+    _fused(lambda: b.launch())
+    torch.cuda.synchronize()
+    for y0, y in zip(ys, b.outs):
+        assert torch.equal(y0, y)
 
 
 def test_decode_once_first_call_under_graph_capture(gpu, mats):
