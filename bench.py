@@ -899,7 +899,7 @@ def main():
         from tensorpack_amd.packer import LAYOUT_MX, LAYOUT_V1
         M1_LAYOUT = {"v1": LAYOUT_V1, "mx": LAYOUT_MX}[args.m1_layout]
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+        print(f"bench.py measures one GPU only (the library has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
         sys.exit(2)
     from tensorpack_amd import workloads

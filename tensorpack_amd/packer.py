@@ -126,7 +126,7 @@ class PanelStream:
         with np.load(path, allow_pickle=False) as z:
             meta = [int(x) for x in z["meta"]]
             if meta[0] != STREAM_FORMAT:
-                raise ValueError(f"{path}: panel stream format {meta[0]}, this build reads {STREAM_FORMAT}")
+                raise ValueError(f"{path}: panel stream format {meta[0]}, this library reads {STREAM_FORMAT}")
             get = lambda k: np.array(z[k]) if k in z.files else None
             stats = dict(zip([str(k) for k in z["stats_keys"]], [float(v) for v in z["stats_vals"]]))
             ps = cls(K=meta[1], N=meta[2], chunk_rows=meta[3], payload=get("payload"), buckets=get("buckets"),

@@ -1,4 +1,4 @@
-"""The reference's import paths (`mtc.*`) resolve to this build, and the legacy uniform
+"""The reference's import paths (`mtc.*`) resolve to this package, and the legacy uniform
 constructors `MTCMatrix.from_numpy` / `from_numpy_joint` write the reference's arena bytes.
 
 CPU only: packing and byte layouts; the GPU side of these matrices is in

@@ -1,6 +1,6 @@
 """GPU parity of the HIP path against the CPU oracle (run on an MI355X).
 
-Bars (north-star): W_hat bit-exact vs the oracle's qt_dequant (-0.0 == +0.0
+Bars: W_hat bit-exact vs the oracle's qt_dequant (-0.0 == +0.0
 never arises: the quadtree W_hat has no negative zeros); Y within relative
 Frobenius 1e-5 of fp64 X @ W_hat for the fp32 path and 2e-3 for the bf16
 MFMA path (fp64 reference built from the same bf16-rounded X).
