@@ -191,3 +191,29 @@ def test_decode_once_first_call_under_graph_capture(gpu, mats):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+@pytest.mark.parametrize("K_,N_,M_", [(992, 544, 1024), (96, 4096, 1024), (2048, 288, 600)])
+def test_decode_once_ragged_shapes(gpu, K_, N_, M_):
+    """K not a multiple of 64 (the decoded rows past K hold the stream's zero padding and the GEMM
+    reads K of them), N not a multiple of 256 (the last column tile decodes columns past N that
+    are not written) and M not a multiple of any tile height: Y within the bf16 bar of the fp64
+    product, the decoded W_hat bit-exact in the workspace, the tile kernel's Y within 1e-5."""
+    import torch
+    W = outlier_matrix(K_ + N_, K_, N_)
+    a = QuadtreeRD(W, None, (32, 16, 8, 4)).select(4.5)
+    W_hat = O.qt_dequant(W, a.sizes, a.leaf, a.modes, a.scales)
+    g = MTCMatrix.from_quadtree(a, W).device_tiles(gpu)
+    assert M_ * K_ * N_ >= 1 << 28 and M_ >= max(512, K_ // 8)          # eligible
+    X = torch.from_numpy(np.random.RandomState(K_).randn(M_, K_).astype(np.float32)).to(gpu).to(torch.bfloat16)
+    _say("decode-once ragged", K_, N_, M_)
+    Y = g.gemm_bf16(X)
+    torch.cuda.synchronize()
+    ws, _ = g.workspace(M_, 1)
+    ldw = 64 * g.host.n_ksteps
+    Wt = ws[: N_ * ldw * 2].view(torch.bfloat16).view(N_, ldw).float().cpu().numpy()
+    assert np.array_equal(_bits(Wt[:, :K_]), _bits(O.bf16_round(W_hat).T + np.float32(0.0)))
+    assert not Wt[:, K_:].any()
+    Y = Y.cpu().numpy()
+    assert O.relative_frobenius_error(O.qt_gemm_f64(X.float().cpu().numpy(), W_hat), Y) <= TOL_BF16
+    assert O.relative_frobenius_error(_fused(lambda: g.gemm_bf16(X)).cpu().numpy(), Y) <= 1e-5
