@@ -304,7 +304,7 @@ size_t mtc_gemm_workspace_bytes(const mtc_tile_desc* d, int M, int x_dtype);
 int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, int64_t ldx, void* Y, int y_dtype,
                   int64_t ldy, int M, void* workspace, size_t workspace_bytes, void* hip_stream);
 
-/* Switches the decode-once path of mtc_gemm_bf16 / mtc_gemm_bf16_group on (1, the default)
+/* Switches the decode-once paths of mtc_gemm_bf16 / mtc_gemm_bf16_group / mtc_gemm_f32 on (1, the default)
  * or off (0: every call runs the tile kernel) for the process; -1 only queries. Returns the
  * previous setting. No counterpart in the reference: for callers and tests that measure or
  * check the fused tile kernel at shapes the decode-once path would take. A prefill batch
@@ -319,7 +319,12 @@ int mtc_set_prefill_decode_once(int enable);
  * the same operation as mtc_gemv_f32, for callers at 5..16 rows and beyond). X read in place
  * must have 16-byte aligned rows (ldx % 4 == 0); a stream with a row permutation gathers X
  * into the workspace first. Workspace (mtc_gemm_f32_workspace_bytes, 256-byte aligned, no
- * initialisation): the gathered X (M*K*4) and the split-K partials. */
+ * initialisation): the gathered X (M*K*4) and the split-K partials.
+ * Decode-once path: a call with M >= 256, M * K * N >= 2^32 and no col_perm decodes the exact
+ * W_hat once into fp32 in the workspace (N*64*ceil(K/64)*4 bytes, then the gathered X) and runs
+ * hipBLASLt's fp32 GEMM on it (fp32 products and sums); deterministic, one algorithm per shape;
+ * without hipBLASLt, or with the path switched off (mtc_set_prefill_decode_once), the tile
+ * kernel runs. */
 size_t mtc_gemm_f32_workspace_bytes(const mtc_tile_desc* d, int M);
 int mtc_gemm_f32(const mtc_tile_desc* d, const float* X, int64_t ldx, float* Y, int64_t ldy, int M,
                  void* workspace, size_t workspace_bytes, void* hip_stream);

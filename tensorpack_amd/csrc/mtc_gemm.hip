@@ -744,20 +744,21 @@ __global__ __launch_bounds__(kStageThreads) void k_stage_x_f32(const float* __re
   *reinterpret_cast<float4*>(Xp + m * K + k0) = make_float4(x[src.x], x[src.y], x[src.z], x[src.w]);
 }
 
-// ---- decode once: W_hat in bf16 for a plain GEMM ----
+// ---- decode once: W_hat in bf16 (or fp32) for a plain GEMM ----
 // One block per (column tile ct, run of `spb` K-steps), grid n_col_tiles x ceil(n_ksteps / spb),
 // 256 threads: for each step thread t decodes cells t and t + 256 as the tile kernel's producers
-// do (decode_cell: the same bf16 values the MFMAs would read) into a swizzled [256][64] LDS tile,
-// then the block writes it out as whole 128-byte row pieces: Wt[n][k] (N rows of ldw bf16,
-// ldw = 64 * n_ksteps) holds W_hat[k][n] for stream row k (row_perm order, as the staged X) and
-// column n; rows k >= K hold the stream's zero padding. While a step is decoded and written, the
-// next step's payload and the descriptors of the step after it are in flight. (Stores straight
-// from registers, one cell per thread, ran 54 us against 40 us for one step per block at
-// 8192 x 8192: a step's cells are sorted by class first, so their lines split.)
-template <int kCF>
-__global__ __launch_bounds__(256) void k_tile_dequant_bf16(const mtc_tile_desc d, __bf16* __restrict__ Wt,
-                                                          int64_t ldw, int spb) {
-  __shared__ __attribute__((aligned(16))) unsigned char bs[kTN * kTK * 2];
+// do (decode_cell: the same bf16 values the MFMAs would read; with F32, decode_cell_f32: the exact
+// W_hat) into a swizzled [256][64] LDS tile, then the block writes it out as whole row pieces
+// (128 bytes of bf16, 256 of fp32): Wt[n][k] (N rows of ldw elements, ldw = 64 * n_ksteps) holds
+// W_hat[k][n] for stream row k (row_perm order, as the staged X) and column n; rows k >= K hold
+// the stream's zero padding. While a step is decoded and written, the next step's payload and
+// the descriptors of the step after it are in flight. (Stores straight from registers, one cell
+// per thread, ran 54 us against 40 us for one step per block at 8192 x 8192 in bf16: a step's
+// cells are sorted by class first, so their lines split.)
+template <int kCF, bool F32>
+__device__ __forceinline__ void tile_dequant_block(const mtc_tile_desc& d, void* __restrict__ Wt, int64_t ldw,
+                                                   int spb) {
+  __shared__ __attribute__((aligned(16))) unsigned char bs[kTN * kTK * (F32 ? 4 : 2)];
   constexpr int CW = cell_words(kCF);
   const int t = threadIdx.x, ct = blockIdx.x;
   const int ks0 = (int)blockIdx.y * spb, nks = min(spb, d.n_ksteps - ks0);
@@ -813,21 +814,34 @@ __global__ __launch_bounds__(256) void k_tile_dequant_bf16(const mtc_tile_desc d
       }
       const uint32_t pos = (w[h][0] >> 16) & (kCells - 1);   // (column group, row block) of the cell
       const int col = (int)(pos >> 3) * 4, seg = (int)(pos & 7u);
-      u32x4_t o[4];
-      decode_cell<kCF == kCellCols>((w[h][0] >> 14) & 3u, q[h], st, sb, o);
+      if constexpr (F32) {
+        float o[4][8];
+        decode_cell_f32<kCF == kCellCols>((w[h][0] >> 14) & 3u, q[h], st, sb, o);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4_t*>(bs + swz(col + j, seg)) = o[j];
+        for (int j = 0; j < 4; ++j) {
+          *reinterpret_cast<f32x4_t*>(bs + swz_f32(col + j, 2 * seg)) = f32x4_t{o[j][0], o[j][1], o[j][2], o[j][3]};
+          *reinterpret_cast<f32x4_t*>(bs + swz_f32(col + j, 2 * seg + 1)) = f32x4_t{o[j][4], o[j][5], o[j][6], o[j][7]};
+        }
+      } else {
+        u32x4_t o[4];
+        decode_cell<kCF == kCellCols>((w[h][0] >> 14) & 3u, q[h], st, sb, o);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4_t*>(bs + swz(col + j, seg)) = o[j];
+      }
     }
   };
+  // 16-byte pieces of the tile's rows: 8 per row in bf16, 16 in fp32
+  constexpr int SH = F32 ? 4 : 3, EPP = F32 ? 4 : 8;   // log2 pieces per row, elements per piece
   auto write_out = [&](int ks) __attribute__((always_inline)) {
-    __bf16* const out = Wt + (int64_t)ks * kTK;
 #pragma unroll
-    for (int i = 0; i < kTN * 8 / 256; ++i) {
-      const int piece = t + 256 * i, row = piece >> 3, seg = piece & 7;
+    for (int i = 0; i < (kTN << SH) / 256; ++i) {
+      const int piece = t + 256 * i, row = piece >> SH, seg = piece & ((1 << SH) - 1);
       const int n = ct * kTN + row;
-      if (n < d.N)
-        *reinterpret_cast<u32x4_t*>(out + (int64_t)n * ldw + seg * 8) =
-            *reinterpret_cast<const u32x4_t*>(bs + swz(row, seg));
+      if (n < d.N) {
+        const int64_t e = (int64_t)n * ldw + (int64_t)ks * kTK + seg * EPP;
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(bs + (F32 ? swz_f32(row, seg) : swz(row, seg)));
+        *reinterpret_cast<u32x4_t*>(reinterpret_cast<unsigned char*>(Wt) + e * (F32 ? 4 : 2)) = v;
+      }
     }
   };
   // step i: descriptors wa, payload qa; step i + 1: descriptors wb, payload qb
@@ -849,6 +863,18 @@ __global__ __launch_bounds__(256) void k_tile_dequant_bf16(const mtc_tile_desc d
     body(i, wa, qa, wb, qb);
     if (i + 1 < nks) body(i + 1, wb, qb, wa, qa);
   }
+}
+
+template <int kCF>
+__global__ __launch_bounds__(256) void k_tile_dequant_bf16(const mtc_tile_desc d, __bf16* __restrict__ Wt,
+                                                          int64_t ldw, int spb) {
+  tile_dequant_block<kCF, false>(d, Wt, ldw, spb);
+}
+
+template <int kCF>
+__global__ __launch_bounds__(256) void k_tile_dequant_f32(const mtc_tile_desc d, float* __restrict__ Wt,
+                                                         int64_t ldw, int spb) {
+  tile_dequant_block<kCF, true>(d, Wt, ldw, spb);
 }
 
 // Up to kMaxGroup matrices that read the same X, in one launch of each kernel: member i owns
@@ -1335,18 +1361,19 @@ struct Plan {
 
 std::mutex g_mu;
 std::map<int, hipblasLtHandle_t> g_handles;                                   // per device
-std::map<std::tuple<int, int, int, int, int, int64_t, int64_t, int64_t>, Plan> g_plans;
+std::map<std::tuple<int, int, int, int, int, int64_t, int64_t, int64_t, bool>, Plan> g_plans;
 
 // The GEMM plan of a shape on the current device, made once (the heuristic's first algorithm
 // among those needing at most kBlasWsBytes of workspace, so a shape always runs the same
-// algorithm); nullptr when the library or an algorithm is missing.
-const Plan* plan_for(int M, int N, int K, int64_t ldw, int64_t ldb, int64_t ldy, int ydt) {
+// algorithm); nullptr when the library or an algorithm is missing. f32: fp32 operands (the
+// exact W_hat and fp32 X) instead of bf16 ones.
+const Plan* plan_for(int M, int N, int K, int64_t ldw, int64_t ldb, int64_t ldy, int ydt, bool f32 = false) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;
   const Api& L = api();
   if (!L.ok) return nullptr;
   std::lock_guard<std::mutex> lock(g_mu);
-  const auto key = std::make_tuple(dev, M, N, K, ydt, ldw, ldb, ldy);
+  const auto key = std::make_tuple(dev, M, N, K, ydt, ldw, ldb, ldy, f32);
   auto it = g_plans.find(key);
   if (it != g_plans.end()) return it->second.ok ? &it->second : nullptr;
   Plan& p = g_plans[key];
@@ -1363,8 +1390,8 @@ const Plan* plan_for(int M, int N, int K, int64_t ldw, int64_t ldb, int64_t ldy,
   if (L.desc_create(&p.op, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS ||
       L.desc_set(p.op, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) != HIPBLAS_STATUS_SUCCESS ||
       L.desc_set(p.op, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) != HIPBLAS_STATUS_SUCCESS ||
-      L.layout_create(&p.a, HIP_R_16BF, (uint64_t)K, (uint64_t)N, ldw) != HIPBLAS_STATUS_SUCCESS ||
-      L.layout_create(&p.b, HIP_R_16BF, (uint64_t)K, (uint64_t)M, ldb) != HIPBLAS_STATUS_SUCCESS ||
+      L.layout_create(&p.a, f32 ? HIP_R_32F : HIP_R_16BF, (uint64_t)K, (uint64_t)N, ldw) != HIPBLAS_STATUS_SUCCESS ||
+      L.layout_create(&p.b, f32 ? HIP_R_32F : HIP_R_16BF, (uint64_t)K, (uint64_t)M, ldb) != HIPBLAS_STATUS_SUCCESS ||
       L.layout_create(&p.c, yt, (uint64_t)N, (uint64_t)M, ldy) != HIPBLAS_STATUS_SUCCESS)
     return nullptr;
   hipblasLtMatmulPreference_t pref = nullptr;
@@ -1382,7 +1409,7 @@ const Plan* plan_for(int M, int N, int K, int64_t ldw, int64_t ldb, int64_t ldy,
   return p.ok ? &p : nullptr;
 }
 
-int gemm(const Plan* p, const __bf16* Wt, const __bf16* Xb, void* Y, void* ws, hipStream_t st) {
+int gemm(const Plan* p, const void* Wt, const void* Xb, void* Y, void* ws, hipStream_t st) {
   const float alpha = 1.0f, beta = 0.0f;
   const hipblasStatus_t s =
       api().matmul(p->handle, p->op, &alpha, Wt, p->a, Xb, p->b, &beta, Y, p->c, Y, p->c, &p->algo, ws, kBlasWsBytes, st);
@@ -1430,6 +1457,23 @@ int decode_once_call(const mtc_tile_desc* d, const void* X, int x_dtype, int64_t
   const int rc = check_launch("k_tile_dequant_bf16");
   if (rc) return rc;
   return lt::gemm(p, Wt, xb, Y, w, st);
+}
+
+// ---- decode once for fp32 results (mtc_gemm_f32): the exact W_hat in fp32, then hipBLASLt's
+// fp32 GEMM (fp32 products and sums, like the tile path), for calls with at least
+// kDecodeOnceF32MinRows rows, kDecodeOnceF32MinMacs multiply-adds and no output column
+// permutation (an fp32 GEMM of 4096 x 4096 x M took 75 us at M = 256 against 176 us for the fp32
+// tile kernel, and 24 against 52 us at M = 64, where writing the 64 MB W_hat costs 20 us more).
+constexpr int kDecodeOnceF32MinRows = 256;
+constexpr int64_t kDecodeOnceF32MinMacs = (int64_t)1 << 32;
+
+bool decode_once_f32_shape(const mtc_tile_desc* d, int M) {
+  return !d->col_perm && M >= kDecodeOnceF32MinRows && (int64_t)M * d->K * d->N >= kDecodeOnceF32MinMacs;
+}
+
+// Workspace of the fp32 path: Wt (N x ldw fp32), then X gathered through row_perm (M x K fp32).
+size_t decode_once_f32_bytes(const mtc_tile_desc* d, int M) {
+  return round256((size_t)d->N * decode_once_ldw(d) * 4) + (d->row_perm ? round256((size_t)M * d->K * 4) : 0);
 }
 
 // Workspace of a group: per member, its staged X (if any) then its split-K partials, each on a
@@ -1853,7 +1897,8 @@ size_t f32_ws_bytes(const mtc_tile_desc* d, int M) {
 
 MTC_API size_t mtc_gemm_f32_workspace_bytes(const mtc_tile_desc* d, int M) {
   if (check_tile_desc(d) || M <= 0) return 0;
-  return f32_ws_bytes(d, M);
+  const size_t tiles = f32_ws_bytes(d, M);
+  return decode_once_f32_shape(d, M) ? std::max(tiles, decode_once_f32_bytes(d, M)) : tiles;
 }
 
 MTC_API int mtc_gemm_f32(const mtc_tile_desc* d, const float* X, int64_t ldx, float* Y, int64_t ldy, int M,
@@ -1870,7 +1915,10 @@ MTC_API int mtc_gemm_f32(const mtc_tile_desc* d, const float* X, int64_t ldx, fl
   if ((size_t)kLdsBytesF32 > mtc::host::device_lds_limit())
     return fail(MTC_E_SHAPE, "fp32 tile kernel needs %d B of LDS per block, device has %zu", kLdsBytesF32,
                 mtc::host::device_lds_limit());
-  const size_t stage = f32_stage_bytes(d, M), need = f32_ws_bytes(d, M);
+  const lt::Plan* once = nullptr;
+  if (decode_once_f32_shape(d, M) && g_decode_once.load(std::memory_order_relaxed))
+    once = lt::plan_for(M, d->N, d->K, decode_once_ldw(d), d->row_perm ? d->K : ldx, ldy, MTC_DTYPE_F32, true);
+  const size_t stage = f32_stage_bytes(d, M), need = once ? decode_once_f32_bytes(d, M) : f32_ws_bytes(d, M);
   if (need && (!workspace || workspace_bytes < need))
     return fail(MTC_E_WORKSPACE, "fp32 tile workspace of %zu bytes needed, %zu given", need,
                 workspace ? workspace_bytes : 0);
@@ -1879,6 +1927,37 @@ MTC_API int mtc_gemm_f32(const mtc_tile_desc* d, const float* X, int64_t ldx, fl
   hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);
   const float* xa = X;
   int64_t lda = ldx;
+  if (once) {
+    // the exact W_hat in fp32, X gathered through row_perm after it, then the fp32 GEMM
+    float* const Wt = reinterpret_cast<float*>(workspace);
+    const int64_t ldw = decode_once_ldw(d);
+    if (d->row_perm) {
+      float* xp = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + round256((size_t)d->N * ldw * 4));
+      hipLaunchKernelGGL(k_stage_x_f32, dim3((unsigned)((d->K / 4 + kStageThreads - 1) / kStageThreads), (unsigned)M),
+                         dim3(kStageThreads), 0, st, X, ldx, d->row_perm, xp, d->K);
+      rc = check_launch("k_stage_x_f32");
+      if (rc) return rc;
+      xa = xp;
+      lda = d->K;
+    }
+    // K-steps per block: two blocks per CU by LDS (a 64 KB fp32 tile)
+    const int64_t n_steps = (int64_t)d->n_col_tiles * d->n_ksteps;
+    const int spb = (int)std::min<int64_t>(8, std::max<int64_t>(1, n_steps / (2 * kFillCUs)));
+    const dim3 grid((unsigned)d->n_col_tiles, (unsigned)((d->n_ksteps + spb - 1) / spb));
+    switch (cell_format(d)) {
+      case kCellFp32:
+        hipLaunchKernelGGL(k_tile_dequant_f32<kCellFp32>, grid, dim3(256), 0, st, *d, Wt, ldw, spb);
+        break;
+      case kCellCols:
+        hipLaunchKernelGGL(k_tile_dequant_f32<kCellCols>, grid, dim3(256), 0, st, *d, Wt, ldw, spb);
+        break;
+      default:
+        hipLaunchKernelGGL(k_tile_dequant_f32<kCellBf16>, grid, dim3(256), 0, st, *d, Wt, ldw, spb);
+    }
+    rc = check_launch("k_tile_dequant_f32");
+    if (rc) return rc;
+    return lt::gemm(once, Wt, xa, Y, nullptr, st);
+  }
   if (stage) {
     float* xp = reinterpret_cast<float*>(workspace);
     hipLaunchKernelGGL(k_stage_x_f32, dim3((unsigned)((d->K / 4 + kStageThreads - 1) / kStageThreads), (unsigned)M),

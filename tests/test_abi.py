@@ -207,6 +207,12 @@ def test_decode_once_workspace_by_shape(hip):
     small = _tdesc(K=1024, n_ksteps=16, row_perm=0x2000, col_perm=0x3000)
     descs = (D * 2)(ctypes.pointer(small), ctypes.pointer(big))
     assert hip.mtc_gemm_group_workspace_bytes(descs, 2, 4096, 1) == ws(small, 4096, 1) + wt
+    # the fp32 path (mtc_gemm_f32): from 256 rows and 2^32 multiply-adds, the exact W_hat in fp32
+    f32ws = lambda d, M: hip.mtc_gemm_f32_workspace_bytes(ctypes.byref(d), M)
+    assert f32ws(big, 1024) == 4096 * 1024 * 4                           # 1024 x 1024 x 4096 = 2^32
+    assert f32ws(rows, 1024) == 4096 * 1024 * 4 + 1024 * 1024 * 4         # and X gathered through row_perm
+    assert f32ws(big, 1023) == 0                                          # below: the tile kernel (1024 tiles, no split)
+    assert f32ws(cols, 1024) == 1024 * 1024 * 4                           # a column permutation: tile kernel, X gathered
     assert hip.mtc_set_prefill_decode_once(-1) == 1
     assert hip.mtc_set_prefill_decode_once(0) == 1
     assert hip.mtc_set_prefill_decode_once(-1) == 0

@@ -8,6 +8,8 @@ bar) and within 1e-5 of the fused tile kernel's Y (the same bf16 operands, fp32 
 another order); repeated calls and group members bit-identical to single calls.
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -217,3 +219,30 @@ def test_decode_once_ragged_shapes(gpu, K_, N_, M_):
     Y = Y.cpu().numpy()
     assert O.relative_frobenius_error(O.qt_gemm_f64(X.float().cpu().numpy(), W_hat), Y) <= TOL_BF16
     assert O.relative_frobenius_error(_fused(lambda: g.gemm_bf16(X)).cpu().numpy(), Y) <= 1e-5
+
+
+@pytest.mark.parametrize("name", ["qt", "qtp", "uniform"])
+def test_decode_once_f32(gpu, mats, xs, name):
+    """fp32 results (mtc_gemm_f32) from 256 rows and 2^32 multiply-adds on: the exact W_hat decoded
+    once into fp32 (bit-exact against the oracle in the stream's row order) and hipBLASLt's fp32
+    GEMM; Y within the fp32 bar (1e-5) of the fp64 product and within 1e-6 of the fp32 tile
+    kernel's Y; repeated calls bit-identical."""
+    import torch
+    m, W_hat = mats[name]
+    g = m.device_tiles(gpu)
+    Xf, _ = xs
+    X = Xf[:1024]
+    _say("decode-once fp32", name)
+    Y = g.gemm_f32(X)
+    torch.cuda.synchronize()
+    ws, _ = g.workspace(1024, 0, int(g.lib.mtc_gemm_f32_workspace_bytes(ctypes.byref(g.desc), 1024)))
+    ldw = 64 * g.host.n_ksteps
+    Wt = ws[: N * ldw * 4].view(torch.float32).view(N, ldw)[:, :K].cpu().numpy()
+    rows = g.host.row_perm if g.host.row_perm is not None else np.arange(K)
+    assert np.array_equal(_bits(Wt), _bits(W_hat[rows].T + np.float32(0.0))), name
+    Y = Y.cpu().numpy()
+    err = O.relative_frobenius_error(O.qt_gemm_f64(X.cpu().numpy(), W_hat), Y)
+    assert err <= 1e-5, (name, err)
+    assert np.array_equal(_bits(g.gemm_f32(X).cpu().numpy()), _bits(Y)), "repeat"
+    Yt = _fused(lambda: g.gemm_f32(X)).cpu().numpy()
+    assert O.relative_frobenius_error(Yt, Y) <= 1e-6, name
