@@ -1291,9 +1291,11 @@ int stage_x(const mtc_tile_desc* d, const void* X, int x_dtype, int64_t ldx, int
 // the path is switched off (mtc_set_prefill_decode_once).
 constexpr int kDecodeOnceMinRows = 512;
 constexpr int64_t kDecodeOnceMinMacs = (int64_t)1 << 28;   // below: one launch more costs more than it saves
-// The GEMM runs without a workspace: the algorithms hipBLASLt picks first for the shapes timed here
-// need none when allowed 32 MiB (and run as fast), and one without a workspace can never leave a
-// memset node in a captured graph.
+// The GEMM runs without a workspace: the algorithms hipBLASLt picks first for the bf16 shapes timed
+// here need none when allowed 32 MiB (and run as fast), and one without a workspace can neither
+// leave a memset node in a captured graph nor split K with atomic sums. (Some fp32 shapes' first
+// algorithms need one, 896 x 4864 x 1024: 4 MB; with none allowed those calls find no algorithm and
+// keep the tile kernel.)
 constexpr size_t kBlasWsBytes = 0;
 std::atomic<int> g_decode_once{1};
 
