@@ -246,3 +246,36 @@ def test_decode_once_f32(gpu, mats, xs, name):
     assert np.array_equal(_bits(g.gemm_f32(X).cpu().numpy()), _bits(Y)), "repeat"
     Yt = _fused(lambda: g.gemm_f32(X)).cpu().numpy()
     assert O.relative_frobenius_error(Yt, Y) <= 1e-6, name
+
+
+def test_decode_once_two_threads_two_streams(gpu, mats):
+    """Two host threads, each on its own HIP stream, make the first calls of new shapes at the same
+    time (plans made concurrently; one prefill workspace per stream): each Y equals the same call
+    made alone afterwards, bit for bit."""
+    import threading
+    import torch
+    tiles = [mats["qt"][0].device_tiles(gpu), mats["qtp"][0].device_tiles(gpu)]
+    Ms = (900, 1100)
+    Xs = [torch.from_numpy(np.random.RandomState(90 + i).randn(M_, K).astype(np.float32)).to(gpu).to(torch.bfloat16)
+          for i, M_ in enumerate(Ms)]
+    outs, errs = [None, None], []
+
+    def run(i):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                for _ in range(3):
+                    outs[i] = tiles[i].gemm_bf16(Xs[i])
+            s.synchronize()
+        except Exception as ex:            # reported below, in the test's own thread
+            errs.append(ex)
+
+    _say("decode-once two threads")
+    th = [threading.Thread(target=run, args=(i,)) for i in range(2)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    assert not errs, errs
+    for i in range(2):
+        assert torch.equal(outs[i], tiles[i].gemm_bf16(Xs[i])), i
