@@ -300,7 +300,9 @@ size_t mtc_gemm_workspace_bytes(const mtc_tile_desc* d, int M, int x_dtype);
  * hipBLASLt's bf16 GEMM with fp32 accumulation on it, instead of the tile kernel, which
  * decodes each weight step once per 256-row tile. The same shape always runs the same GEMM
  * algorithm, so results are deterministic. Without hipBLASLt, or with no algorithm for the
- * shape, the call runs the tile kernel. */
+ * shape, the call runs the tile kernel; so does a call made while its stream is captured into a
+ * graph before any call outside a capture has set the library up on the device (that allocates),
+ * whose graph then holds the tile kernel. */
 int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, int64_t ldx, void* Y, int y_dtype,
                   int64_t ldy, int M, void* workspace, size_t workspace_bytes, void* hip_stream);
 

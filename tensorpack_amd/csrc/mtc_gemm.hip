@@ -1365,13 +1365,26 @@ std::mutex g_mu;
 std::map<int, hipblasLtHandle_t> g_handles;                                   // per device
 std::map<std::tuple<int, int, int, int, int, int64_t, int64_t, int64_t, bool>, Plan> g_plans;
 
+// Whether work enqueued on st is being captured into a graph.
+bool capturing(hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
 // The GEMM plan of a shape on the current device, made once (the heuristic's first algorithm
 // among those needing at most kBlasWsBytes of workspace, so a shape always runs the same
 // algorithm); nullptr when the library or an algorithm is missing. f32: fp32 operands (the
-// exact W_hat and fp32 X) instead of bf16 ones.
-const Plan* plan_for(int M, int N, int K, int64_t ldw, int64_t ldb, int64_t ldy, int ydt, bool f32 = false) {
+// exact W_hat and fp32 X) instead of bf16 ones. setup: whether the library may be opened and
+// the device's handle made here, which allocates; a caller whose stream is being captured passes
+// false and gets nullptr (the tile kernel runs) until a call outside a capture has made them.
+const Plan* plan_for(int M, int N, int K, int64_t ldw, int64_t ldb, int64_t ldy, int ydt, bool f32, bool setup) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  if (!setup) {
+    std::lock_guard<std::mutex> lock(g_mu);
+    auto hit = g_handles.find(dev);
+    if (hit == g_handles.end() || !hit->second) return nullptr;
+  }
   const Api& L = api();
   if (!L.ok) return nullptr;
   std::lock_guard<std::mutex> lock(g_mu);
@@ -1421,10 +1434,12 @@ int gemm(const Plan* p, const void* Wt, const void* Xb, void* Y, void* ws, hipSt
 
 }  // namespace lt
 
-// The plan of an eligible call, or nullptr for the fused tile kernel.
-const lt::Plan* decode_once_plan(const mtc_tile_desc* d, int x_dtype, int64_t ldx, int64_t ldy, int y_dtype, int M) {
+// The plan of an eligible call, or nullptr for the fused tile kernel (setup: see lt::plan_for).
+const lt::Plan* decode_once_plan(const mtc_tile_desc* d, int x_dtype, int64_t ldx, int64_t ldy, int y_dtype, int M,
+                                 bool setup) {
   if (!decode_once_shape(d, M) || !g_decode_once.load(std::memory_order_relaxed)) return nullptr;
-  return lt::plan_for(M, d->N, d->K, decode_once_ldw(d), needs_staging(d, x_dtype) ? d->K : ldx, ldy, y_dtype);
+  return lt::plan_for(M, d->N, d->K, decode_once_ldw(d), needs_staging(d, x_dtype) ? d->K : ldx, ldy, y_dtype, false,
+                      setup);
 }
 
 // Stage X (if needed), decode W_hat into Wt, run the GEMM; ws holds decode_once_bytes.
@@ -1594,7 +1609,7 @@ int build_gemm_batch_plan(const mtc_gemm_batch_item* items, int n, int M, int x_
   int n_once = 0;
   if (!fill)
     for (int i = 0; i < n; ++i)
-      if (decode_once_plan(items[i].desc, x_dtype, items[i].ldx, items[i].ldy, y_dtype, M)) {
+      if (decode_once_plan(items[i].desc, x_dtype, items[i].ldx, items[i].ldy, y_dtype, M, true)) {
         once[i] = 1;
         ++n_once;
         once_ws = std::max(once_ws, decode_once_bytes(items[i].desc, M, x_dtype));
@@ -1850,7 +1865,8 @@ int launch_gemm_batch(const void* host_plan, const void* device_plan, hipStream_
     // the plan's choice stands (made when it was built; the switch may have changed since)
     const GemmBatchItem& e = hitems[once_list[j]];
     const lt::Plan* p = lt::plan_for(h->M, e.d.N, e.d.K, decode_once_ldw(&e.d),
-                                     needs_staging(&e.d, h->x_dtype) ? e.d.K : e.ldx_src, e.ldy, h->y_dtype);
+                                     needs_staging(&e.d, h->x_dtype) ? e.d.K : e.ldx_src, e.ldy, h->y_dtype, false,
+                                     !lt::capturing(st));
     if (!p) return fail(MTC_E_LAUNCH, "batch item %u: no GEMM plan for its decode-once path", once_list[j]);
     rc = decode_once_call(&e.d, e.Xsrc, h->x_dtype, e.ldx_src, e.Y, h->M,
                           reinterpret_cast<char*>(const_cast<void*>(h->workspace)) + h->once_ws_off, p, st);
@@ -1917,16 +1933,17 @@ MTC_API int mtc_gemm_f32(const mtc_tile_desc* d, const float* X, int64_t ldx, fl
   if ((size_t)kLdsBytesF32 > mtc::host::device_lds_limit())
     return fail(MTC_E_SHAPE, "fp32 tile kernel needs %d B of LDS per block, device has %zu", kLdsBytesF32,
                 mtc::host::device_lds_limit());
+  hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);
   const lt::Plan* once = nullptr;
   if (decode_once_f32_shape(d, M) && g_decode_once.load(std::memory_order_relaxed))
-    once = lt::plan_for(M, d->N, d->K, decode_once_ldw(d), d->row_perm ? d->K : ldx, ldy, MTC_DTYPE_F32, true);
+    once = lt::plan_for(M, d->N, d->K, decode_once_ldw(d), d->row_perm ? d->K : ldx, ldy, MTC_DTYPE_F32, true,
+                        !lt::capturing(st));
   const size_t stage = f32_stage_bytes(d, M), need = once ? decode_once_f32_bytes(d, M) : f32_ws_bytes(d, M);
   if (need && (!workspace || workspace_bytes < need))
     return fail(MTC_E_WORKSPACE, "fp32 tile workspace of %zu bytes needed, %zu given", need,
                 workspace ? workspace_bytes : 0);
   if (need && (reinterpret_cast<uintptr_t>(workspace) & 255))
     return fail(MTC_E_WORKSPACE, "workspace not 256-byte aligned");
-  hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);
   const float* xa = X;
   int64_t lda = ldx;
   if (once) {
@@ -2015,7 +2032,7 @@ MTC_API int mtc_gemm_bf16(const mtc_tile_desc* d, const void* X, int x_dtype, in
   const size_t stage = staging_bytes(d, M, x_dtype);
   if (!stage && (ldx % 8 || (reinterpret_cast<uintptr_t>(X) & 15)))
     return fail(MTC_E_SHAPE, "bf16 X read in place needs 16-byte aligned rows (ldx=%lld)", (long long)ldx);
-  const lt::Plan* once = decode_once_plan(d, x_dtype, ldx, ldy, y_dtype, M);
+  const lt::Plan* once = decode_once_plan(d, x_dtype, ldx, ldy, y_dtype, M, !lt::capturing(st));
   const size_t need = once ? decode_once_bytes(d, M, x_dtype) : stage + partial_bytes(d, M);
   if (need && (!workspace || workspace_bytes < need))
     return fail(MTC_E_WORKSPACE, "prefill workspace of %zu bytes needed, %zu given", need, workspace ? workspace_bytes : 0);
@@ -2085,7 +2102,8 @@ MTC_API int mtc_gemm_bf16_group(const mtc_tile_desc* const* descs, int n, const 
   // members that a single call would run on the decode-once path run on it here too, one after
   // another in the area past the fused members' layout; the rest share the fused launches
   const lt::Plan* once[kMaxGroup];
-  for (int i = 0; i < n; ++i) once[i] = decode_once_plan(descs[i], x_dtype, ldx, ldy[i], y_dtype, M);
+  const bool setup = !lt::capturing(st);
+  for (int i = 0; i < n; ++i) once[i] = decode_once_plan(descs[i], x_dtype, ldx, ldy[i], y_dtype, M, setup);
   GemmGroup g;
   StageGroup sg;
   ReduceGroup rg;

@@ -171,28 +171,59 @@ def test_decode_once_batch_members_equal_single_calls(gpu, mats, Mb):
         assert torch.equal(y0, y)
 
 
-def test_decode_once_first_call_under_graph_capture(gpu, mats):
-    """The first call of a shape made while a HIP graph is captured (the GEMM plan is made
-    during the capture): every replay equals the eager call bit for bit."""
+def _capture(fn, out, reps=3):
+    """Capture fn() (writing `out`) into a HIP graph on a side stream and replay it `reps` times,
+    with eager work and a synchronisation between replays; returns each replay's output."""
     import torch
-    g = mats["uniform"][0].device_tiles(gpu)
-    X = torch.from_numpy(np.random.RandomState(76).randn(700, K).astype(np.float32)).to(gpu).to(torch.bfloat16)
-    out = torch.empty(700, N, device=gpu)
-    _say("decode-once first call under capture")
     graph = torch.cuda.CUDAGraph()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
         with torch.cuda.graph(graph, stream=side):
-            g.gemm_bf16(X, out=out)
+            fn()
     torch.cuda.current_stream().wait_stream(side)
-    eager = g.gemm_bf16(X)
-    torch.cuda.synchronize()
-    for _ in range(3):
+    res = []
+    for _ in range(reps):
         out.zero_()
         graph.replay()
         torch.cuda.synchronize()
-        assert torch.equal(out, eager)
+        res.append(out.clone())
+    return res
+
+
+def _first_call_under_capture(fn, out, eager_fn, tol):
+    """A shape's first call made while a graph is captured. If nothing has set up the library in
+    this process outside a capture, the graph holds the tile kernel (the library is never set up
+    during a capture); either way its replays agree with each other, and with the eager call within
+    `tol`. A second capture, after the eager call, equals the eager call bit for bit."""
+    import torch
+    first = _capture(fn, out)
+    eager = eager_fn()
+    torch.cuda.synchronize()
+    for r in first[1:]:
+        assert torch.equal(r, first[0])
+    assert O.relative_frobenius_error(eager.cpu().numpy(), first[0].cpu().numpy()) <= tol
+    for r in _capture(fn, out):
+        assert torch.equal(r, eager)
+
+
+def test_decode_once_first_call_under_graph_capture(gpu, mats):
+    import torch
+    g = mats["uniform"][0].device_tiles(gpu)
+    X = torch.from_numpy(np.random.RandomState(76).randn(700, K).astype(np.float32)).to(gpu).to(torch.bfloat16)
+    out = torch.empty(700, N, device=gpu)
+    _say("decode-once first call under capture")
+    _first_call_under_capture(lambda: g.gemm_bf16(X, out=out), out, lambda: g.gemm_bf16(X), 1e-5)
+
+
+def test_decode_once_f32_first_call_under_graph_capture(gpu, mats):
+    import torch
+    g = mats["qtp"][0].device_tiles(gpu)
+    M_ = 1100                                          # 1100 x 1024 x 4096 >= 2^32: the fp32 path
+    X = torch.from_numpy(np.random.RandomState(95).randn(M_, K).astype(np.float32)).to(gpu)
+    out = torch.empty(M_, N, device=gpu)
+    _say("decode-once fp32 first call under capture")
+    _first_call_under_capture(lambda: g.gemm_f32(X, out=out), out, lambda: g.gemm_f32(X), 1e-6)
 
 
 @pytest.mark.parametrize("K_,N_,M_", [(992, 544, 1024), (96, 4096, 1024), (2048, 288, 600)])
@@ -279,3 +310,4 @@ def test_decode_once_two_threads_two_streams(gpu, mats):
     assert not errs, errs
     for i in range(2):
         assert torch.equal(outs[i], tiles[i].gemm_bf16(Xs[i])), i
+
